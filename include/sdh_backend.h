@@ -1,0 +1,190 @@
+/*
+ * sdh_backend.h - C ABI of backend_hip, the MI355X (gfx950) backend for the
+ * elementwise / reduction / broadcast ops of StableDiffusion-cpp's tensor
+ * library.
+ *
+ * It replaces the non-GEMM part of the reference's GPU boundary,
+ * src/backend_cuda.h (namespace sd::cuda, raw device pointers + int64 sizes).
+ * Each entry point keeps the parameters of the function it replaces, in the
+ * same order and with the same meaning; the comment on each cites that
+ * declaration. Differences, all at the ABI level:
+ *   - plain C: every function returns an int status (SDH_OK = 0) instead of
+ *     throwing; sdh_last_error() gives the message of the calling thread's
+ *     last failure. bool parameters are int.
+ *   - memory comes from a device arena owned by the library; op outputs are
+ *     NOT zero-filled (the reference's Tensor(shape, Device) zero-fills,
+ *     tensor.cpp:55-63; every op here writes its whole output).
+ *   - every pointer argument of an op must lie, with the extent the op
+ *     touches, inside one live allocation of this library (sdh_malloc) or a
+ *     range registered with sdh_register_external; otherwise the call fails
+ *     with SDH_ERR_INVALID before anything is launched.
+ *   - all work is queued in order on one HIP stream owned by the library.
+ *     Ops return as soon as the work is queued; sdh_download and
+ *     sdh_synchronize wait for it (backend_cuda.h:12-13 semantics).
+ *   - additive entry points (marked FUSED) have no single reference
+ *     function; their comment names the reference composition they equal.
+ *
+ * Thread safety: calls may come from any thread; the allocator is
+ * mutex-guarded; ops on one stream are serialised in call order.
+ */
+#ifndef SDH_BACKEND_H
+#define SDH_BACKEND_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ------------------------------------------------------------ */
+#define SDH_OK 0
+#define SDH_ERR_UNAVAILABLE 1 /* no HIP device, or the CPU-only stub library */
+#define SDH_ERR_INVALID 2     /* bad argument: size, shape or pointer range */
+#define SDH_ERR_OOM 3         /* device arena exhausted */
+#define SDH_ERR_HIP 4         /* HIP runtime error (message has the HIP string) */
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* sdh_last_error(void);
+
+/* ---- device ------------------------------------------------------------ */
+/* backend_cuda.h:24 available(): 1 if built with HIP and a device is present. */
+int sdh_available(void);
+/* backend_cuda.h:26 device_name(): name of device 0, "" if unavailable. */
+const char* sdh_device_name(void);
+/* backend_cuda.h:27 device_memory(): bytes of device 0, 0 if unavailable. */
+size_t sdh_device_memory(void);
+/* No reference counterpart (the reference probes lazily, backend_cuda.cu:50-89):
+ * explicit initialisation. Creates the stream, the staging buffers and a first
+ * arena segment of arena_bytes (0 = SDH_ARENA_MB from the environment, else
+ * 1024 MiB). Called implicitly by the first call that needs the device. */
+int sdh_init(size_t arena_bytes);
+/* Frees every device and pinned allocation of the library. */
+int sdh_shutdown(void);
+
+/* ---- memory (backend_cuda.h:29-36) -------------------------------------- */
+/* backend_cuda.h:30 malloc(): *out = device block of `bytes` (256-byte aligned,
+ * uninitialised). bytes == 0 gives *out = NULL and SDH_OK. */
+int sdh_malloc(size_t bytes, void** out);
+/* backend_cuda.h:31 free(): returns a block to the arena (NULL is a no-op). */
+int sdh_free(void* p);
+/* backend_cuda.h:32 upload(): host -> device. Staged through pinned buffers
+ * with hipMemcpyAsync; the host buffer may be reused when the call returns. */
+int sdh_upload(void* dst, const void* src, size_t bytes);
+/* backend_cuda.h:33 download(): device -> host; waits for all queued work. */
+int sdh_download(void* dst, const void* src, size_t bytes);
+/* backend_cuda.h:34 copy(): device -> device, asynchronous. */
+int sdh_copy(void* dst, const void* src, size_t bytes);
+/* backend_cuda.h:35 zero(): fills with zero bytes, asynchronous. */
+int sdh_zero(void* dst, size_t bytes);
+/* backend_cuda.h:36 synchronize(): waits for all queued work. */
+int sdh_synchronize(void);
+/* No reference counterpart: lets ops accept device memory that the library did
+ * not allocate (for example a framework's tensor). The range must stay valid
+ * until sdh_unregister_external. */
+int sdh_register_external(void* p, size_t bytes);
+int sdh_unregister_external(void* p);
+/* No reference counterpart: arena statistics (bytes reserved from HIP, bytes
+ * handed out to live blocks). */
+int sdh_memory_stats(size_t* reserved, size_t* in_use);
+
+/* ---- norms -------------------------------------------------------------- */
+/* backend_cuda.h:48 group_norm(); tensor.h:166. x, y [N, C, HW]; gamma, beta
+ * [C]; C % groups == 0. y may equal x. */
+int sdh_group_norm(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups, const float* gamma,
+                   const float* beta, float eps);
+/* backend_cuda.h:50 layer_norm(); tensor.h:170. x, y [rows, C]; gamma, beta
+ * [C] or NULL. y may equal x. */
+int sdh_layer_norm(const float* x, float* y, int64_t rows, int64_t C, const float* gamma, const float* beta,
+                   float eps);
+/* backend_cuda.h:51 rms_norm(); tensor.h:177. x, y [rows, C]; gamma [C] or
+ * NULL. y may equal x. */
+int sdh_rms_norm(const float* x, float* y, int64_t rows, int64_t C, const float* gamma, float eps);
+/* backend_cuda.h:52 rms_norm_heads(); tensor.h:180. In place on x
+ * [groups, dim]; gamma [dim] or NULL. */
+int sdh_rms_norm_heads(float* x, int64_t groups, int64_t dim, const float* gamma, float eps);
+
+/* ---- rotary -------------------------------------------------------------- */
+/* backend_cuda.h:54 rope(); tensor.h:188. In place on x [N, S, inner],
+ * inner % dim == 0, dim even; cos, sin [S, dim]. interleaved = 1: pairs
+ * (2i, 2i+1) rotated by cos/sin[s, 2i]; 0: pairs (i, i + dim/2) as
+ * tensor.cpp:721-725. */
+int sdh_rope(float* x, int64_t N, int64_t S, int64_t inner, int64_t dim, const float* cos, const float* sin,
+             int interleaved);
+/* FUSED: rope() on q [N, S, inner_q] and on k [N, S, inner_k] in one launch;
+ * equals rope_(q, ...) then rope_(k, ...) (zimage.cpp:119-120). */
+int sdh_rope_qk(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
+                const float* cos, const float* sin, int interleaved);
+
+/* ---- softmax ------------------------------------------------------------- */
+/* backend_cuda.h:56 softmax_rows(); tensor.h:236. In place on x [rows, cols]:
+ * p = exp(x*scale - max) / sum over the valid columns; causal keeps columns
+ * 0..r of row r and zeroes the rest. */
+int sdh_softmax_rows(float* x, int64_t rows, int64_t cols, float scale, int causal);
+/* As sdh_softmax_rows, with the causal row index taken modulo `period` (a
+ * stack of [period, cols] score matrices, as the reference's attention launch
+ * at backend_cuda.cu:578). */
+int sdh_softmax_rows_batched(float* x, int64_t rows, int64_t cols, float scale, int causal, int64_t period);
+
+/* ---- activations ----------------------------------------------------------- */
+/* backend_cuda.h:61 swiglu(); tensor.h:191. y = gate / (1 + exp(-gate)) * up. */
+int sdh_swiglu(const float* gate, const float* up, float* y, int64_t n);
+/* backend_cuda.h:60 geglu(); tensor.h:217. x [rows, 2D] -> y [rows, D]. */
+int sdh_geglu(const float* x, float* y, int64_t rows, int64_t D);
+/* backend_cuda.h:64 silu(), :65 tanh(), :66 gelu(), :67 quick_gelu(): in place. */
+int sdh_silu(float* x, int64_t n);
+int sdh_tanh(float* x, int64_t n);
+int sdh_gelu(float* x, int64_t n);
+int sdh_quick_gelu(float* x, int64_t n);
+
+/* ---- broadcasts / residual ------------------------------------------------- */
+/* backend_cuda.h:68 add(): a += b. */
+int sdh_add(float* a, const float* b, int64_t n);
+/* backend_cuda.h:69 scale(): x *= s. */
+int sdh_scale(float* x, float s, int64_t n);
+/* backend_cuda.h:70 affine(): x = x * a + b. */
+int sdh_affine(float* x, float a, float b, int64_t n);
+/* backend_cuda.h:71 mul_rows(): x[r, :] *= v[:]. */
+int sdh_mul_rows(float* x, const float* v, int64_t rows, int64_t dim);
+/* backend_cuda.h:72 add_rows_scaled(): x[r, :] += g[:] * y[r, :]. */
+int sdh_add_rows_scaled(float* x, const float* y, const float* g, int64_t rows, int64_t dim);
+/* backend_cuda.h:73 add_channel_bias(): x[n, c, :] += b[n, c]. */
+int sdh_add_channel_bias(float* x, const float* b, int64_t N, int64_t C, int64_t HW);
+/* x[r, :] += v[:] (row-vector bias / adaLN shift). The reference has this only
+ * inside linear's bias epilogue (k_add_bias_cols, backend_cuda.cu:239-241);
+ * on the CPU it equals add_rows_scaled_(x, ones, v). */
+int sdh_add_rows(float* x, const float* v, int64_t rows, int64_t dim);
+
+/* ---- fused ------------------------------------------------------------------ */
+/* FUSED: x += r; y = rms_norm(x, gamma, eps). Equals add_(x, r) then
+ * rms_norm(x, gamma, eps) (the residual -> norm order of zimage.cpp:123-128).
+ * x, r, y [rows, C]; gamma [C] or NULL. */
+int sdh_add_rms_norm(float* x, const float* r, float* y, int64_t rows, int64_t C, const float* gamma, float eps);
+/* FUSED: y = silu(group_norm(x)). Equals group_norm then silu_
+ * (modules.cpp:34-35, vae.cpp:48-49, unet.cpp:120-121). y may equal x. */
+int sdh_group_norm_silu(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups, const float* gamma,
+                        const float* beta, float eps);
+/* FUSED adaLN: y = layer_norm(x, no affine, eps) * (1 + scale) + shift;
+ * res += tanh(gate) * y. Equals layer_norm -> affine_(scale, 1, 1) ->
+ * tanh_(gate) -> mul_rows_(y, 1+scale) -> add_rows_scaled_(y, ones, shift) ->
+ * add_rows_scaled_(res, y, tanh(gate)) (zimage.cpp:104-107, :221-224).
+ * x, res [rows, C]; scale, gate [C]; shift [C] or NULL; y_out [rows, C] or
+ * NULL (y is then not stored). */
+int sdh_ln_modulate_gate(const float* x, float* res, const float* scale, const float* shift, const float* gate,
+                         float* y_out, int64_t rows, int64_t C, float eps);
+
+/* ---- measurement helpers (no reference counterpart) -------------------------- */
+/* Fills x[0..n) on the device with N(mean, std) values of the library's
+ * seeded counter-based generator (splitmix64 + Box-Muller); for synthetic
+ * benchmark inputs. */
+int sdh_fill_normal(float* x, int64_t n, uint64_t seed, float mean, float std);
+/* Records timer slot `slot` (0..15) on the library stream. */
+int sdh_timer_record(int slot);
+/* Milliseconds between two recorded slots; waits for the second. */
+int sdh_timer_elapsed(int start_slot, int end_slot, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SDH_BACKEND_H */

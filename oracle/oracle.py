@@ -1,0 +1,464 @@
+"""ctypes bindings of the parity checkers. TEST INFRASTRUCTURE ONLY.
+
+Two libraries live here, both built by ``oracle/Makefile``:
+
+* ``liboracle.so`` -- the C restatement of the reference's ops (sd_oracle.c).
+  ``Oracle`` wraps it with numpy arrays in, numpy arrays out.
+* ``_ref/libsdref.so`` -- the reference's own ``src/tensor.cpp`` compiled from
+  /root/reference.  ``Reference`` wraps it the same way, and also exposes the
+  handle API used to time the reference CPU path as it is called.
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's cpu_baseline leg may
+import this module, and only as the checker: the product never routes a
+computation through it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libsdref.so")
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_i64 = C.c_int64
+_fl = C.c_float
+_vp = C.c_void_p
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class _NullableF32:
+    """ctypes argtype accepting a float32 array or None."""
+
+    @classmethod
+    def from_param(cls, obj):
+        if obj is None:
+            return None
+        if not (isinstance(obj, np.ndarray) and obj.dtype == np.float32 and obj.flags.c_contiguous):
+            raise TypeError("expected a C-contiguous float32 array or None")
+        return obj.ctypes.data_as(C.c_void_p)
+
+
+class Oracle:
+    """numpy-level wrapper of liboracle.so (the C restatement)."""
+
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (run make -C oracle)")
+        L = self.lib = C.CDLL(path)
+        N = _NullableF32
+        sig = {
+            "orc_set_threads": (None, [C.c_int]),
+            "orc_num_threads": (C.c_int, []),
+            "orc_plant_mistake": (None, [C.c_int]),
+            "orc_fill_normal": (None, [_f32p, _i64, C.c_uint64, C.c_double, C.c_double]),
+            "orc_group_norm": (None, [_f32p, _f32p, _i64, _i64, _i64, C.c_int, _f32p, _f32p, _fl]),
+            "orc_group_norm_silu": (None, [_f32p, _f32p, _i64, _i64, _i64, C.c_int, _f32p, _f32p, _fl]),
+            "orc_layer_norm": (None, [_f32p, _f32p, _i64, _i64, N, N, _fl]),
+            "orc_rms_norm": (None, [_f32p, _f32p, _i64, _i64, N, _fl]),
+            "orc_rms_norm_heads": (None, [_f32p, _i64, _i64, N, _fl]),
+            "orc_rope": (None, [_f32p, _i64, _i64, _i64, _i64, _f32p, _f32p, C.c_int]),
+            "orc_rope_tables_3axis": (None, [_i32p, _i64, _i32p, _i64, C.c_double, _f32p, _f32p]),
+            "orc_rope_tables_half": (None, [_i64, _i64, C.c_double, _f32p, _f32p]),
+            "orc_swiglu": (None, [_f32p, _f32p, _f32p, _i64]),
+            "orc_geglu": (None, [_f32p, _f32p, _i64, _i64]),
+            "orc_silu": (None, [_f32p, _i64]),
+            "orc_tanh": (None, [_f32p, _i64]),
+            "orc_gelu": (None, [_f32p, _i64]),
+            "orc_quick_gelu": (None, [_f32p, _i64]),
+            "orc_softmax_rows": (None, [_f32p, _i64, _i64, _fl, C.c_int]),
+            "orc_softmax_rows_period": (None, [_f32p, _i64, _i64, _fl, C.c_int, _i64]),
+            "orc_add": (None, [_f32p, _f32p, _i64]),
+            "orc_scale": (None, [_f32p, _fl, _i64]),
+            "orc_affine": (None, [_f32p, _fl, _fl, _i64]),
+            "orc_mul_rows": (None, [_f32p, _f32p, _i64, _i64]),
+            "orc_add_rows_scaled": (None, [_f32p, _f32p, _f32p, _i64, _i64]),
+            "orc_add_channel_bias": (None, [_f32p, _f32p, _i64, _i64, _i64]),
+            "orc_add_rms_norm": (None, [_f32p, _f32p, _f32p, _i64, _i64, N, _fl]),
+            "orc_ln_modulate_gate": (None, [_f32p, _f32p, _f32p, N, _f32p, N, _i64, _i64, _fl]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+
+    # -- control --
+    def set_threads(self, n: int):
+        self.lib.orc_set_threads(n)
+
+    def num_threads(self) -> int:
+        return self.lib.orc_num_threads()
+
+    def plant(self, which: int):
+        self.lib.orc_plant_mistake(which)
+
+    # -- generator --
+    def randn(self, shape, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+        n = int(np.prod(shape)) if len(shape) else 1
+        out = np.empty(n, np.float32)
+        self.lib.orc_fill_normal(out, n, seed, mean, std)
+        return out.reshape(shape)
+
+    # -- ops (inputs are never modified; in-place ops return a new array) --
+    def group_norm(self, x, groups, gamma, beta, eps, silu=False):
+        x = _f32(x)
+        N, Cc = x.shape[0], x.shape[1]
+        HW = x.size // (N * Cc)
+        y = np.empty_like(x)
+        fn = self.lib.orc_group_norm_silu if silu else self.lib.orc_group_norm
+        fn(x, y, N, Cc, HW, groups, _f32(gamma), _f32(beta), eps)
+        return y
+
+    def layer_norm(self, x, gamma, beta, eps):
+        x = _f32(x)
+        Cc = x.shape[-1]
+        y = np.empty_like(x)
+        self.lib.orc_layer_norm(x, y, x.size // Cc, Cc, None if gamma is None else _f32(gamma),
+                                None if beta is None else _f32(beta), eps)
+        return y
+
+    def rms_norm(self, x, gamma, eps):
+        x = _f32(x)
+        Cc = x.shape[-1]
+        y = np.empty_like(x)
+        self.lib.orc_rms_norm(x, y, x.size // Cc, Cc, None if gamma is None else _f32(gamma), eps)
+        return y
+
+    def rms_norm_heads(self, x, dim, gamma, eps):
+        y = _f32(x).copy()
+        self.lib.orc_rms_norm_heads(y, y.size // dim, dim, None if gamma is None else _f32(gamma), eps)
+        return y
+
+    def rope(self, x, dim, cos_t, sin_t, interleaved):
+        """x [..., S, inner] rotated in a copy; cos/sin [S, dim]."""
+        y = _f32(x).copy()
+        inner, S = y.shape[-1], y.shape[-2]
+        N = y.size // (S * inner)
+        self.lib.orc_rope(y, N, S, inner, dim, _f32(cos_t), _f32(sin_t), int(bool(interleaved)))
+        return y
+
+    def rope_tables_3axis(self, pos, axes_dims, dim, theta):
+        pos = np.ascontiguousarray(pos, dtype=np.int32)
+        S = pos.shape[0]
+        c = np.empty((S, dim), np.float32)
+        s = np.empty((S, dim), np.float32)
+        self.lib.orc_rope_tables_3axis(pos, S, np.ascontiguousarray(axes_dims, dtype=np.int32), dim, theta, c, s)
+        return c, s
+
+    def rope_tables_half(self, S, dim, theta):
+        c = np.empty((S, dim), np.float32)
+        s = np.empty((S, dim), np.float32)
+        self.lib.orc_rope_tables_half(S, dim, theta, c, s)
+        return c, s
+
+    def swiglu(self, g, u):
+        g, u = _f32(g), _f32(u)
+        y = np.empty_like(g)
+        self.lib.orc_swiglu(g, u, y, g.size)
+        return y
+
+    def geglu(self, x):
+        x = _f32(x)
+        D = x.shape[-1] // 2
+        y = np.empty(x.shape[:-1] + (D,), np.float32)
+        self.lib.orc_geglu(x, y, x.size // (2 * D), D)
+        return y
+
+    def _unary(self, fn, x):
+        y = _f32(x).copy()
+        fn(y, y.size)
+        return y
+
+    def silu(self, x):
+        return self._unary(self.lib.orc_silu, x)
+
+    def tanh(self, x):
+        return self._unary(self.lib.orc_tanh, x)
+
+    def gelu(self, x):
+        return self._unary(self.lib.orc_gelu, x)
+
+    def quick_gelu(self, x):
+        return self._unary(self.lib.orc_quick_gelu, x)
+
+    def softmax_rows(self, x, scale, causal=False, period=None):
+        y = _f32(x).copy()
+        cols = y.shape[-1]
+        rows = y.size // cols
+        if period is None:
+            self.lib.orc_softmax_rows(y, rows, cols, scale, int(bool(causal)))
+        else:
+            self.lib.orc_softmax_rows_period(y, rows, cols, scale, int(bool(causal)), period)
+        return y
+
+    def add(self, a, b):
+        y = _f32(a).copy()
+        self.lib.orc_add(y, _f32(b), y.size)
+        return y
+
+    def scale(self, x, s):
+        y = _f32(x).copy()
+        self.lib.orc_scale(y, s, y.size)
+        return y
+
+    def affine(self, x, a, b):
+        y = _f32(x).copy()
+        self.lib.orc_affine(y, a, b, y.size)
+        return y
+
+    def mul_rows(self, x, v):
+        y = _f32(x).copy()
+        dim = y.shape[-1]
+        self.lib.orc_mul_rows(y, _f32(v), y.size // dim, dim)
+        return y
+
+    def add_rows_scaled(self, x, yv, g):
+        o = _f32(x).copy()
+        dim = o.shape[-1]
+        self.lib.orc_add_rows_scaled(o, _f32(yv), _f32(g), o.size // dim, dim)
+        return o
+
+    def add_channel_bias(self, x, b):
+        y = _f32(x).copy()
+        N, Cc = y.shape[0], y.shape[1]
+        self.lib.orc_add_channel_bias(y, _f32(b), N, Cc, y.size // (N * Cc))
+        return y
+
+    def add_rms_norm(self, x, r, gamma, eps):
+        """Returns (x + r, rms_norm(x + r) * gamma)."""
+        s = _f32(x).copy()
+        y = np.empty_like(s)
+        Cc = s.shape[-1]
+        self.lib.orc_add_rms_norm(s, _f32(r), y, s.size // Cc, Cc, None if gamma is None else _f32(gamma), eps)
+        return s, y
+
+    def ln_modulate_gate(self, x, res, scale, shift, gate, eps):
+        """Returns (res + tanh(gate) * y, y) with y = LN(x) * (1 + scale) + shift."""
+        x = _f32(x)
+        r = _f32(res).copy()
+        y = np.empty_like(x)
+        Cc = x.shape[-1]
+        self.lib.orc_ln_modulate_gate(x, r, _f32(scale), None if shift is None else _f32(shift), _f32(gate), y,
+                                      x.size // Cc, Cc, eps)
+        return r, y
+
+
+class Reference:
+    """numpy-level wrapper of the compiled reference tensor library."""
+
+    def __init__(self, path: str = REF_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (run make -C oracle ref where /root/reference exists)")
+        L = self.lib = C.CDLL(path)
+        sig = {
+            "ref_last_error": (C.c_char_p, []),
+            "ref_set_threads": (None, [C.c_int]),
+            "ref_num_threads": (C.c_int, []),
+            "ref_tensor_new": (_vp, [C.POINTER(C.c_int64), C.c_int]),
+            "ref_tensor_data": (C.POINTER(C.c_float), [_vp]),
+            "ref_tensor_numel": (C.c_int64, [_vp]),
+            "ref_tensor_free": (None, [_vp]),
+            "ref_group_norm": (_vp, [_vp, C.c_int, _vp, _vp, _fl]),
+            "ref_layer_norm": (_vp, [_vp, _vp, _vp, _fl]),
+            "ref_rms_norm": (_vp, [_vp, _vp, _fl]),
+            "ref_swiglu": (_vp, [_vp, _vp]),
+            "ref_geglu": (_vp, [_vp]),
+            "ref_rms_norm_heads_": (C.c_int, [_vp, _i64, _vp, _fl]),
+            "ref_rope_": (C.c_int, [_vp, _i64, _vp, _vp, C.c_int]),
+            "ref_softmax_rows_": (C.c_int, [_vp, _i64, _i64, _fl, C.c_int]),
+            "ref_silu_": (C.c_int, [_vp]),
+            "ref_tanh_": (C.c_int, [_vp]),
+            "ref_gelu_": (C.c_int, [_vp]),
+            "ref_quick_gelu_": (C.c_int, [_vp]),
+            "ref_add_": (C.c_int, [_vp, _vp]),
+            "ref_scale_": (C.c_int, [_vp, _fl]),
+            "ref_affine_": (C.c_int, [_vp, _fl, _fl]),
+            "ref_mul_rows_": (C.c_int, [_vp, _vp]),
+            "ref_add_rows_scaled_": (C.c_int, [_vp, _vp, _vp]),
+            "ref_add_channel_bias_": (C.c_int, [_vp, _vp]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+
+    # -- handles --
+    def new(self, shape, data=None):
+        shp = (C.c_int64 * len(shape))(*[int(s) for s in shape])
+        h = self.lib.ref_tensor_new(shp, len(shape))
+        if not h:
+            raise RuntimeError(self.lib.ref_last_error().decode())
+        if data is not None:
+            self.view(h)[...] = np.asarray(data, np.float32).reshape(-1)
+        return h
+
+    def view(self, h) -> np.ndarray:
+        n = self.lib.ref_tensor_numel(h)
+        return np.ctypeslib.as_array(self.lib.ref_tensor_data(h), shape=(n,))
+
+    def take(self, h, shape) -> np.ndarray:
+        out = self.view(h).copy().reshape(shape)
+        self.lib.ref_tensor_free(h)
+        return out
+
+    def free(self, *hs):
+        for h in hs:
+            if h:
+                self.lib.ref_tensor_free(h)
+
+    def _chk(self, rc):
+        if rc:
+            raise RuntimeError(self.lib.ref_last_error().decode())
+
+    def _ptr(self, h):
+        if not h:
+            raise RuntimeError(self.lib.ref_last_error().decode())
+        return h
+
+    # -- numpy-level ops (same meaning as Oracle's) --
+    def group_norm(self, x, groups, gamma, beta, eps, silu=False):
+        x = _f32(x)
+        hx, hg, hb = self.new(x.shape, x), self.new(gamma.shape, gamma), self.new(beta.shape, beta)
+        hy = self._ptr(self.lib.ref_group_norm(hx, groups, hg, hb, eps))
+        if silu:
+            self._chk(self.lib.ref_silu_(hy))
+        self.free(hx, hg, hb)
+        return self.take(hy, x.shape)
+
+    def layer_norm(self, x, gamma, beta, eps):
+        x = _f32(x)
+        hx = self.new(x.shape, x)
+        hg = self.new(gamma.shape, gamma) if gamma is not None else None
+        hb = self.new(beta.shape, beta) if beta is not None else None
+        hy = self._ptr(self.lib.ref_layer_norm(hx, hg, hb, eps))
+        self.free(hx, hg, hb)
+        return self.take(hy, x.shape)
+
+    def rms_norm(self, x, gamma, eps):
+        x = _f32(x)
+        hx = self.new(x.shape, x)
+        hg = self.new(gamma.shape, gamma) if gamma is not None else None
+        hy = self._ptr(self.lib.ref_rms_norm(hx, hg, eps))
+        self.free(hx, hg)
+        return self.take(hy, x.shape)
+
+    def rms_norm_heads(self, x, dim, gamma, eps):
+        x = _f32(x)
+        hx = self.new(x.shape, x)
+        hg = self.new(gamma.shape, gamma) if gamma is not None else None
+        self._chk(self.lib.ref_rms_norm_heads_(hx, dim, hg, eps))
+        self.free(hg)
+        return self.take(hx, x.shape)
+
+    def rope(self, x, dim, cos_t, sin_t, interleaved):
+        x = _f32(x)
+        hx, hc, hs = self.new(x.shape, x), self.new(cos_t.shape, cos_t), self.new(sin_t.shape, sin_t)
+        self._chk(self.lib.ref_rope_(hx, dim, hc, hs, int(bool(interleaved))))
+        self.free(hc, hs)
+        return self.take(hx, x.shape)
+
+    def swiglu(self, g, u):
+        g = _f32(g)
+        hg, hu = self.new(g.shape, g), self.new(u.shape, u)
+        hy = self._ptr(self.lib.ref_swiglu(hg, hu))
+        self.free(hg, hu)
+        return self.take(hy, g.shape)
+
+    def geglu(self, x):
+        x = _f32(x)
+        hx = self.new(x.shape, x)
+        hy = self._ptr(self.lib.ref_geglu(hx))
+        self.free(hx)
+        return self.take(hy, x.shape[:-1] + (x.shape[-1] // 2,))
+
+    def _unary(self, fn, x):
+        x = _f32(x)
+        hx = self.new(x.shape, x)
+        self._chk(fn(hx))
+        return self.take(hx, x.shape)
+
+    def silu(self, x):
+        return self._unary(self.lib.ref_silu_, x)
+
+    def tanh(self, x):
+        return self._unary(self.lib.ref_tanh_, x)
+
+    def gelu(self, x):
+        return self._unary(self.lib.ref_gelu_, x)
+
+    def quick_gelu(self, x):
+        return self._unary(self.lib.ref_quick_gelu_, x)
+
+    def softmax_rows(self, x, scale, causal=False):
+        x = _f32(x)
+        hx = self.new(x.shape, x)
+        cols = x.shape[-1]
+        self._chk(self.lib.ref_softmax_rows_(hx, x.size // cols, cols, scale, int(bool(causal))))
+        return self.take(hx, x.shape)
+
+    def add(self, a, b):
+        a = _f32(a)
+        ha, hb = self.new(a.shape, a), self.new(b.shape, b)
+        self._chk(self.lib.ref_add_(ha, hb))
+        self.free(hb)
+        return self.take(ha, a.shape)
+
+    def scale(self, x, s):
+        x = _f32(x)
+        hx = self.new(x.shape, x)
+        self._chk(self.lib.ref_scale_(hx, s))
+        return self.take(hx, x.shape)
+
+    def affine(self, x, a, b):
+        x = _f32(x)
+        hx = self.new(x.shape, x)
+        self._chk(self.lib.ref_affine_(hx, a, b))
+        return self.take(hx, x.shape)
+
+    def mul_rows(self, x, v):
+        x = _f32(x)
+        hx, hv = self.new(x.shape, x), self.new(v.shape, v)
+        self._chk(self.lib.ref_mul_rows_(hx, hv))
+        self.free(hv)
+        return self.take(hx, x.shape)
+
+    def add_rows_scaled(self, x, yv, g):
+        x = _f32(x)
+        hx, hy, hg = self.new(x.shape, x), self.new(yv.shape, yv), self.new(g.shape, g)
+        self._chk(self.lib.ref_add_rows_scaled_(hx, hy, hg))
+        self.free(hy, hg)
+        return self.take(hx, x.shape)
+
+    def add_channel_bias(self, x, b):
+        x = _f32(x)
+        hx, hb = self.new(x.shape, x), self.new(b.shape, b)
+        self._chk(self.lib.ref_add_channel_bias_(hx, hb))
+        self.free(hb)
+        return self.take(hx, x.shape)
+
+    # -- compositions, exactly as the reference's callers chain the ops --
+    def add_rms_norm(self, x, r, gamma, eps):
+        s = self.add(x, r)
+        return s, self.rms_norm(s, gamma, eps)
+
+    def ln_modulate_gate(self, x, res, scale, shift, gate, eps):
+        Cc = x.shape[-1]
+        y = self.layer_norm(x, None, None, eps)
+        s1 = self.affine(scale, 1.0, 1.0)
+        tg = self.tanh(gate)
+        y = self.mul_rows(y, s1)
+        if shift is not None:
+            y = self.add_rows_scaled(y, np.ones_like(y), shift)
+        out = self.add_rows_scaled(res, y, tg)
+        assert out.shape[-1] == Cc
+        return out, y
+
+
+def have_reference() -> bool:
+    return os.path.exists(REF_SO)

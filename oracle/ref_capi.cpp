@@ -1,0 +1,100 @@
+// ref_capi.cpp - C entry points over the REFERENCE's own tensor library, for
+// use as a checker and CPU baseline. TEST INFRASTRUCTURE ONLY.
+//
+// Built by oracle/Makefile together with /root/reference/src/tensor.cpp and
+// /root/reference/src/backend_cuda_stub.cpp, compiled where they lie (nothing
+// of the reference is copied into this repository), into oracle/_ref/.
+//
+// The API is handle based so that a caller can time an op exactly as the
+// reference calls it (output allocation included, tensor.h:58) without the
+// cost of copying inputs into sd::Tensor objects inside the timed region.
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "tensor.h"
+
+using sd::Tensor;
+
+namespace {
+thread_local std::string g_err;
+
+template <class F>
+void* guard_ptr(F&& f) {
+    try {
+        g_err.clear();
+        return f();
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return nullptr;
+    }
+}
+template <class F>
+int guard(F&& f) {
+    try {
+        g_err.clear();
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return 1;
+    }
+}
+Tensor* T(void* h) { return static_cast<Tensor*>(h); }
+const Tensor* opt(void* h) { return h ? static_cast<Tensor*>(h) : nullptr; }
+void* wrap(Tensor&& t) { return new Tensor(std::move(t)); }
+}  // namespace
+
+extern "C" {
+
+const char* ref_last_error(void) { return g_err.c_str(); }
+void ref_set_threads(int n) { sd::set_num_threads(n); }
+int ref_num_threads(void) { return sd::num_threads(); }
+
+void* ref_tensor_new(const int64_t* shape, int ndim) {
+    return guard_ptr([&] { return wrap(Tensor(std::vector<int64_t>(shape, shape + ndim))); });
+}
+float* ref_tensor_data(void* h) { return T(h)->ptr(); }
+int64_t ref_tensor_numel(void* h) { return T(h)->numel(); }
+void ref_tensor_free(void* h) { delete T(h); }
+
+// ---- ops returning a new tensor ----
+void* ref_group_norm(void* x, int groups, void* g, void* b, float eps) {
+    return guard_ptr([&] { return wrap(sd::group_norm(*T(x), groups, *T(g), *T(b), eps)); });
+}
+void* ref_layer_norm(void* x, void* g, void* b, float eps) {
+    return guard_ptr([&] { return wrap(sd::layer_norm(*T(x), opt(g), opt(b), eps)); });
+}
+void* ref_rms_norm(void* x, void* g, float eps) {
+    return guard_ptr([&] { return wrap(sd::rms_norm(*T(x), opt(g), eps)); });
+}
+void* ref_swiglu(void* g, void* u) {
+    return guard_ptr([&] { return wrap(sd::swiglu(*T(g), *T(u))); });
+}
+void* ref_geglu(void* x) {
+    return guard_ptr([&] { return wrap(sd::geglu(*T(x))); });
+}
+
+// ---- in-place ops ----
+int ref_rms_norm_heads_(void* x, int64_t dim, void* g, float eps) {
+    return guard([&] { sd::rms_norm_heads_(*T(x), dim, opt(g), eps); });
+}
+int ref_rope_(void* x, int64_t dim, void* c, void* s, int interleaved) {
+    return guard([&] { sd::rope_(*T(x), dim, *T(c), *T(s), interleaved != 0); });
+}
+int ref_softmax_rows_(void* x, int64_t rows, int64_t cols, float scale, int causal) {
+    return guard([&] { sd::softmax_rows_(T(x)->ptr(), rows, cols, scale, causal != 0); });
+}
+int ref_silu_(void* x) { return guard([&] { sd::silu_(*T(x)); }); }
+int ref_tanh_(void* x) { return guard([&] { sd::tanh_(*T(x)); }); }
+int ref_gelu_(void* x) { return guard([&] { sd::gelu_(*T(x)); }); }
+int ref_quick_gelu_(void* x) { return guard([&] { sd::quick_gelu_(*T(x)); }); }
+int ref_add_(void* a, void* b) { return guard([&] { sd::add_(*T(a), *T(b)); }); }
+int ref_scale_(void* x, float s) { return guard([&] { sd::scale_(*T(x), s); }); }
+int ref_affine_(void* x, float a, float b) { return guard([&] { sd::affine_(*T(x), a, b); }); }
+int ref_mul_rows_(void* x, void* v) { return guard([&] { sd::mul_rows_(*T(x), *T(v)); }); }
+int ref_add_rows_scaled_(void* x, void* y, void* g) { return guard([&] { sd::add_rows_scaled_(*T(x), *T(y), *T(g)); }); }
+int ref_add_channel_bias_(void* x, void* b) { return guard([&] { sd::add_channel_bias_(*T(x), *T(b)); }); }
+
+}  // extern "C"

@@ -1,0 +1,69 @@
+// backend_stub.cpp - CPU-only stand-in for libsdh (the role
+// src/backend_cuda_stub.cpp plays for the reference, :14-56): it exports every
+// entry point of sdh_backend.h, sdh_available() is 0 and every other call
+// fails with SDH_ERR_UNAVAILABLE and a message, so a host without a GPU can
+// build and link the C++ side and a mistake is loud rather than silent.
+// It computes nothing: there is no CPU fallback behind the C ABI.
+#include "sdh_backend.h"
+
+namespace {
+const char* g_msg = "";
+int unavailable() {
+    g_msg = "backend_hip not built for this host (CPU-only stub library)";
+    return SDH_ERR_UNAVAILABLE;
+}
+}  // namespace
+
+#define STUB(decl) \
+    decl { return unavailable(); }
+
+extern "C" {
+
+const char* sdh_last_error(void) { return g_msg; }
+int sdh_available(void) { return 0; }
+const char* sdh_device_name(void) { return ""; }
+size_t sdh_device_memory(void) { return 0; }
+STUB(int sdh_init(size_t))
+int sdh_shutdown(void) { return SDH_OK; }
+
+STUB(int sdh_malloc(size_t, void**))
+int sdh_free(void* p) { return p ? unavailable() : SDH_OK; }
+STUB(int sdh_upload(void*, const void*, size_t))
+STUB(int sdh_download(void*, const void*, size_t))
+STUB(int sdh_copy(void*, const void*, size_t))
+STUB(int sdh_zero(void*, size_t))
+int sdh_synchronize(void) { return SDH_OK; }
+STUB(int sdh_register_external(void*, size_t))
+STUB(int sdh_unregister_external(void*))
+STUB(int sdh_memory_stats(size_t*, size_t*))
+
+STUB(int sdh_group_norm(const float*, float*, int64_t, int64_t, int64_t, int, const float*, const float*, float))
+STUB(int sdh_layer_norm(const float*, float*, int64_t, int64_t, const float*, const float*, float))
+STUB(int sdh_rms_norm(const float*, float*, int64_t, int64_t, const float*, float))
+STUB(int sdh_rms_norm_heads(float*, int64_t, int64_t, const float*, float))
+STUB(int sdh_rope(float*, int64_t, int64_t, int64_t, int64_t, const float*, const float*, int))
+STUB(int sdh_rope_qk(float*, int64_t, float*, int64_t, int64_t, int64_t, int64_t, const float*, const float*, int))
+STUB(int sdh_softmax_rows(float*, int64_t, int64_t, float, int))
+STUB(int sdh_softmax_rows_batched(float*, int64_t, int64_t, float, int, int64_t))
+STUB(int sdh_swiglu(const float*, const float*, float*, int64_t))
+STUB(int sdh_geglu(const float*, float*, int64_t, int64_t))
+STUB(int sdh_silu(float*, int64_t))
+STUB(int sdh_tanh(float*, int64_t))
+STUB(int sdh_gelu(float*, int64_t))
+STUB(int sdh_quick_gelu(float*, int64_t))
+STUB(int sdh_add(float*, const float*, int64_t))
+STUB(int sdh_scale(float*, float, int64_t))
+STUB(int sdh_affine(float*, float, float, int64_t))
+STUB(int sdh_mul_rows(float*, const float*, int64_t, int64_t))
+STUB(int sdh_add_rows_scaled(float*, const float*, const float*, int64_t, int64_t))
+STUB(int sdh_add_channel_bias(float*, const float*, int64_t, int64_t, int64_t))
+STUB(int sdh_add_rows(float*, const float*, int64_t, int64_t))
+STUB(int sdh_add_rms_norm(float*, const float*, float*, int64_t, int64_t, const float*, float))
+STUB(int sdh_group_norm_silu(const float*, float*, int64_t, int64_t, int64_t, int, const float*, const float*, float))
+STUB(int sdh_ln_modulate_gate(const float*, float*, const float*, const float*, const float*, float*, int64_t,
+                              int64_t, float))
+STUB(int sdh_fill_normal(float*, int64_t, uint64_t, float, float))
+STUB(int sdh_timer_record(int))
+STUB(int sdh_timer_elapsed(int, int, float*))
+
+}  // extern "C"

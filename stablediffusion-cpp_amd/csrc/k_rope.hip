@@ -1,0 +1,153 @@
+// k_rope.hip - in-place rotary embedding (tensor.cpp:698-730), for one
+// tensor or for Q and K in one launch.
+//
+// x is [N, S, inner] with inner = heads * dim; the tables are [S, dim].
+// A workgroup owns one token row (one (n, s)) of one tensor: blockIdx.x is the
+// row, blockIdx.y picks Q or K. Its threads sweep the row in float4 steps, so
+// every HBM access is a coalesced 128-bit load/store and each table row is
+// fetched once per token and reused from cache by all heads.
+//   interleaved: float4 (a0, b0, a1, b1) holds pairs (2i, 2i+1), (2i+2, 2i+3),
+//                rotated by cos/sin[s, 2i] and [s, 2i+2] (the even entries, as
+//                tensor.cpp:717-718 uses c[i] and sn[i] for both outputs).
+//   rotate_half: the float4 at head offset i < dim/2 pairs with the float4 at
+//                i + dim/2 (tensor.cpp:722-724); one thread updates both.
+#include "sdh_internal.hpp"
+
+namespace sdh {
+namespace {
+
+using dev::f4;
+
+constexpr int kThreads = 256;
+
+struct RopeArgs {
+    float* x[2];
+    int64_t inner[2];
+};
+
+__global__ __launch_bounds__(kThreads) void k_rope_interleaved(RopeArgs a, int64_t S, int dim,
+                                                              const float* __restrict__ cs,
+                                                              const float* __restrict__ sn) {
+    const int t = blockIdx.y;
+    const int64_t ns = blockIdx.x;
+    const int64_t inner = a.inner[t];
+    const int64_t s = ns % S;
+    f4* row = (f4*)(a.x[t] + ns * inner);
+    const f4* c4 = (const f4*)(cs + s * dim);
+    const f4* s4 = (const f4*)(sn + s * dim);
+    const int n4 = (int)(inner >> 2), d4 = dim >> 2;
+    for (int i = threadIdx.x; i < n4; i += kThreads) {
+        const int h = i % d4;  // float4 index inside the head
+        const f4 v = dev::ld_stream(row + i);
+        const f4 c = c4[h], sv = s4[h];
+        f4 o;
+        o.x = v.x * c.x - v.y * sv.x;
+        o.y = v.y * c.x + v.x * sv.x;
+        o.z = v.z * c.z - v.w * sv.z;
+        o.w = v.w * c.z + v.z * sv.z;
+        dev::st_stream(row + i, o);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_rope_half(RopeArgs a, int64_t S, int dim, const float* __restrict__ cs,
+                                                       const float* __restrict__ sn) {
+    const int t = blockIdx.y;
+    const int64_t ns = blockIdx.x;
+    const int64_t inner = a.inner[t];
+    const int64_t s = ns % S;
+    f4* row = (f4*)(a.x[t] + ns * inner);
+    const f4* c4 = (const f4*)(cs + s * dim);
+    const f4* s4 = (const f4*)(sn + s * dim);
+    const int h4 = dim >> 3;                    // float4 per half head
+    const int pairs = (int)(inner / dim) * h4;  // float4 pairs per row
+    for (int i = threadIdx.x; i < pairs; i += kThreads) {
+        const int head = i / h4, k = i - head * h4;
+        f4* lo = row + head * (dim >> 2) + k;
+        f4* hi = lo + h4;
+        const f4 a0 = dev::ld_stream(lo), b0 = dev::ld_stream(hi);
+        const f4 cl = c4[k], sl = s4[k], ch = c4[k + h4], shh = s4[k + h4];
+        dev::st_stream(lo, a0 * cl - b0 * sl);
+        dev::st_stream(hi, b0 * ch + a0 * shh);
+    }
+}
+
+// Scalar fallback for any shape/alignment: one thread per pair.
+__global__ __launch_bounds__(kThreads) void k_rope_scalar(RopeArgs a, int64_t NS, int64_t S, int64_t dim,
+                                                         const float* __restrict__ cs, const float* __restrict__ sn,
+                                                         int interleaved) {
+    const int t = blockIdx.y;
+    const int64_t inner = a.inner[t];
+    const int64_t half = dim / 2, heads = inner / dim;
+    const int64_t total = NS * heads * half;
+    for (int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * kThreads) {
+        const int64_t i = idx % half, h = (idx / half) % heads, ns = idx / (half * heads), s = ns % S;
+        float* p = a.x[t] + ns * inner + h * dim;
+        const float* c = cs + s * dim;
+        const float* sv = sn + s * dim;
+        if (interleaved) {
+            const float x0 = p[2 * i], x1 = p[2 * i + 1];
+            p[2 * i] = x0 * c[2 * i] - x1 * sv[2 * i];
+            p[2 * i + 1] = x1 * c[2 * i] + x0 * sv[2 * i];
+        } else {
+            const float x0 = p[i], x1 = p[i + half];
+            p[i] = x0 * c[i] - x1 * sv[i];
+            p[i + half] = x1 * c[i + half] + x0 * sv[i + half];
+        }
+    }
+}
+
+void run_rope(const char* op, float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
+              const float* cs, const float* sn, int interleaved) {
+    need(N >= 0 && S >= 0 && inner_q >= 0 && inner_k >= 0, op, "negative size");
+    need(dim > 0 && dim % 2 == 0, op, "dim must be positive and even");
+    need(inner_q % dim == 0 && inner_k % dim == 0, op, "inner must be a multiple of dim");
+    const int nt = k ? 2 : 1;
+    if (N == 0 || S == 0 || (inner_q == 0 && (!k || inner_k == 0))) return;
+    need(N * S <= 0x7fffffffLL, op, "too many token rows");
+    ensure_init();
+    check_range(q, (size_t)(N * S * inner_q) * 4, op, "x/q");
+    if (k) check_range(k, (size_t)(N * S * inner_k) * 4, op, "k");
+    check_range(cs, (size_t)(S * dim) * 4, op, "cos");
+    check_range(sn, (size_t)(S * dim) * 4, op, "sin");
+    RopeArgs a;
+    a.x[0] = q;
+    a.inner[0] = inner_q;
+    a.x[1] = k ? k : q;
+    a.inner[1] = k ? inner_k : inner_q;
+    const bool al = aligned16(q) && (!k || aligned16(k)) && aligned16(cs) && aligned16(sn);
+    if (interleaved && al && dim % 4 == 0 && inner_q % 4 == 0 && inner_k % 4 == 0) {
+        k_rope_interleaved<<<dim3((unsigned)(N * S), nt), kThreads, 0, stream()>>>(a, S, (int)dim, cs, sn);
+    } else if (!interleaved && al && dim % 8 == 0) {
+        k_rope_half<<<dim3((unsigned)(N * S), nt), kThreads, 0, stream()>>>(a, S, (int)dim, cs, sn);
+    } else {
+        const int64_t total = N * S * (std::max(inner_q, inner_k) / dim) * (dim / 2);
+        const int64_t want = (total + kThreads - 1) / kThreads;
+        const unsigned gx = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, (int64_t)num_cus() * 16));
+        k_rope_scalar<<<dim3(gx, nt), kThreads, 0, stream()>>>(a, N * S, S, dim, cs, sn, interleaved);
+    }
+    launched(op);
+}
+
+}  // namespace
+}  // namespace sdh
+
+using namespace sdh;
+
+extern "C" {
+
+int sdh_rope(float* x, int64_t N, int64_t S, int64_t inner, int64_t dim, const float* cos, const float* sin,
+             int interleaved) {
+    return guarded([&] { run_rope("sdh_rope", x, inner, nullptr, 0, N, S, dim, cos, sin, interleaved); });
+}
+
+int sdh_rope_qk(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
+                const float* cos, const float* sin, int interleaved) {
+    return guarded([&] {
+        need(k != nullptr, "sdh_rope_qk", "k is NULL");
+        need(k != q, "sdh_rope_qk", "q and k must be distinct tensors");
+        run_rope("sdh_rope_qk", q, inner_q, k, inner_k, N, S, dim, cos, sin, interleaved);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,528 @@
+// k_rownorm.hip - per-row reductions: rms_norm, layer_norm, the fused
+// residual-add + rms_norm, the fused adaLN chain (layer_norm -> (1+scale) ->
+// +shift -> res += tanh(gate) * y) and per-head rms_norm (QK-norm).
+//
+// Layout and mapping (gfx950, wave64):
+//   * One wave owns one row at a time. A row of C floats is held in
+//     registers as V float4 per lane (lane l holds float4 l, l+64, ...), so
+//     HBM sees exactly one read of every input and one write of every output;
+//     the statistics pass and the apply pass both run on registers.
+//   * Reductions are wave-only (DPP + readlane, sdh_internal.hpp); no LDS and
+//     no barrier, except the adaLN kernel, which stages its three column
+//     vectors in LDS once per workgroup.
+//   * Waves are persistent: the grid is sized to the chip and each wave walks
+//     rows r, r + waves, ... so per-column constants (gamma) are loaded once
+//     per wave, not once per row.
+// Statistics: the reference accumulates in double (tensor.cpp:640-648,
+// :672-674, :690-692). Here each lane accumulates its <= 4V values in fp32,
+// the wave tree adds 64 partials in fp32, and the final mean / rstd are
+// formed in double; the relative error of the sums stays below ~1e-6.
+// Rows whose length is not a multiple of 4, unaligned rows or rows longer
+// than 64 * 4 * 32 floats take the generic kernel (same arithmetic, strided
+// scalar loops that re-read the row from cache).
+#include "sdh_internal.hpp"
+
+namespace sdh {
+namespace {
+
+using dev::f4;
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+enum Mode { M_LN = 0, M_RMS = 1 };
+
+__device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
+
+// rstd as the reference forms it: (float)(1 / sqrt(stat / C + eps)) in double.
+__device__ __forceinline__ float rstd_of(float stat, int64_t C, float eps) {
+    return (float)(1.0 / sqrt((double)stat / (double)C + (double)eps));
+}
+
+// y = layer_norm / rms_norm of each row of x (tensor.cpp:628-679).
+template <int V, int MODE, bool HAS_G, bool HAS_B>
+__global__ __launch_bounds__(kThreads) void k_rownorm(const float* __restrict__ x, float* __restrict__ y,
+                                                     int64_t rows, int C, const float* __restrict__ gamma,
+                                                     const float* __restrict__ beta, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int n4 = C >> 2;
+    f4 g[V], b[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * j;
+        if constexpr (HAS_G) g[j] = idx < n4 ? ((const f4*)gamma)[idx] : zero4();
+        if constexpr (HAS_B) b[j] = idx < n4 ? ((const f4*)beta)[idx] : zero4();
+    }
+    const int64_t stride = (int64_t)gridDim.x * kWaves;
+    for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows; row += stride) {
+        const f4* xr = (const f4*)(x + row * C);
+        f4* yr = (f4*)(y + row * C);
+        f4 v[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int idx = lane + 64 * j;
+            v[j] = idx < n4 ? dev::ld_stream(xr + idx) : zero4();
+        }
+        float mean = 0.f, rstd;
+        if constexpr (MODE == M_LN) {
+            float s = 0.f;
+#pragma unroll
+            for (int j = 0; j < V; ++j) s += dev::hsum(v[j]);
+            mean = (float)((double)dev::wave_sum(s) / (double)C);
+            float q = 0.f;
+#pragma unroll
+            for (int j = 0; j < V; ++j) {
+                if (lane + 64 * j < n4) {
+                    const f4 d = v[j] - mean;
+                    q += dev::hsum(d * d);
+                }
+            }
+            rstd = rstd_of(dev::wave_sum(q), C, eps);
+        } else {
+            float q = 0.f;
+#pragma unroll
+            for (int j = 0; j < V; ++j) q += dev::hsum(v[j] * v[j]);
+            rstd = rstd_of(dev::wave_sum(q), C, eps);
+        }
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int idx = lane + 64 * j;
+            if (idx < n4) {
+                f4 o;
+                if constexpr (MODE == M_LN) {
+                    // (x - mean) * rstd, then * gamma, then + beta, each rounded
+                    // on its own as tensor.cpp:650-652 does.
+                    o = (v[j] - mean) * rstd;
+                    if constexpr (HAS_G) o = f4{__fmul_rn(o.x, g[j].x), __fmul_rn(o.y, g[j].y),
+                                                __fmul_rn(o.z, g[j].z), __fmul_rn(o.w, g[j].w)};
+                    if constexpr (HAS_B) o = f4{__fadd_rn(o.x, b[j].x), __fadd_rn(o.y, b[j].y),
+                                                __fadd_rn(o.z, b[j].z), __fadd_rn(o.w, b[j].w)};
+                } else {
+                    o = v[j] * rstd;  // x * rstd * gamma (tensor.cpp:675)
+                    if constexpr (HAS_G) o = o * g[j];
+                }
+                dev::st_stream(yr + idx, o);
+            }
+        }
+    }
+}
+
+// x += r; y = rms_norm(x) * gamma  (add_ then rms_norm, tensor.cpp:876, :673-675).
+template <int V, bool HAS_G>
+__global__ __launch_bounds__(kThreads) void k_add_rms(float* __restrict__ x, const float* __restrict__ r,
+                                                     float* __restrict__ y, int64_t rows, int C,
+                                                     const float* __restrict__ gamma, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int n4 = C >> 2;
+    f4 g[V];
+    if constexpr (HAS_G) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int idx = lane + 64 * j;
+            g[j] = idx < n4 ? ((const f4*)gamma)[idx] : zero4();
+        }
+    }
+    const int64_t stride = (int64_t)gridDim.x * kWaves;
+    for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows; row += stride) {
+        f4* xr = (f4*)(x + row * C);
+        const f4* rr = (const f4*)(r + row * C);
+        f4* yr = (f4*)(y + row * C);
+        f4 v[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int idx = lane + 64 * j;
+            if (idx < n4) {
+                v[j] = dev::ld_stream(xr + idx) + dev::ld_stream(rr + idx);
+            } else {
+                v[j] = zero4();
+            }
+        }
+        float q = 0.f;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int idx = lane + 64 * j;
+            if (idx < n4) dev::st_stream(xr + idx, v[j]);
+            q += dev::hsum(v[j] * v[j]);
+        }
+        const float rstd = rstd_of(dev::wave_sum(q), C, eps);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int idx = lane + 64 * j;
+            if (idx < n4) {
+                f4 o = v[j] * rstd;
+                if constexpr (HAS_G) o = o * g[j];
+                dev::st_stream(yr + idx, o);
+            }
+        }
+    }
+}
+
+// Fused adaLN chain (see sdh_ln_modulate_gate). The workgroup first writes
+// 1 + scale, shift and tanh(gate) for all C columns into LDS (the affine_ /
+// tanh_ prologue of zimage.cpp:104-107), then its waves walk rows.
+template <int V, bool HAS_SHIFT, bool STORE_Y>
+__global__ __launch_bounds__(kThreads) void k_ln_mod_gate(const float* __restrict__ x, float* __restrict__ res,
+                                                         const float* __restrict__ scale,
+                                                         const float* __restrict__ shift,
+                                                         const float* __restrict__ gate, float* __restrict__ yout,
+                                                         int64_t rows, int C, float eps) {
+    extern __shared__ f4 lds[];  // [3][n4]: 1+scale | shift | tanh(gate)
+    const int lane = threadIdx.x & 63;
+    const int n4 = C >> 2;
+    f4* s1 = lds;
+    f4* sh = lds + n4;
+    f4* tg = lds + 2 * n4;
+    for (int i = threadIdx.x; i < n4; i += kThreads) {
+        const f4 sc = ((const f4*)scale)[i];
+        s1[i] = sc * 1.0f + 1.0f;  // affine_(scale, 1, 1): x * 1 + 1
+        if constexpr (HAS_SHIFT) sh[i] = ((const f4*)shift)[i];
+        const f4 gt = ((const f4*)gate)[i];
+        tg[i] = f4{tanhf(gt.x), tanhf(gt.y), tanhf(gt.z), tanhf(gt.w)};
+    }
+    __syncthreads();
+    const int64_t stride = (int64_t)gridDim.x * kWaves;
+    for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows; row += stride) {
+        const f4* xr = (const f4*)(x + row * C);
+        f4* rr = (f4*)(res + row * C);
+        f4 v[V], rv[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int idx = lane + 64 * j;
+            v[j] = idx < n4 ? dev::ld_stream(xr + idx) : zero4();
+            rv[j] = idx < n4 ? dev::ld_stream(rr + idx) : zero4();
+        }
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < V; ++j) s += dev::hsum(v[j]);
+        const float mean = (float)((double)dev::wave_sum(s) / (double)C);
+        float q = 0.f;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            if (lane + 64 * j < n4) {
+                const f4 d = v[j] - mean;
+                q += dev::hsum(d * d);
+            }
+        }
+        const float rstd = rstd_of(dev::wave_sum(q), C, eps);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int idx = lane + 64 * j;
+            if (idx < n4) {
+                const f4 ln = (v[j] - mean) * rstd;  // layer_norm, no affine
+                const f4 m = s1[idx];
+                f4 yv = f4{__fmul_rn(ln.x, m.x), __fmul_rn(ln.y, m.y), __fmul_rn(ln.z, m.z), __fmul_rn(ln.w, m.w)};
+                if constexpr (HAS_SHIFT) yv = yv + sh[idx];  // add_rows_scaled_(y, ones, shift)
+                if constexpr (STORE_Y) dev::st_stream((f4*)(yout + row * C) + idx, yv);
+                dev::st_stream(rr + idx, rv[j] + tg[idx] * yv);  // res += tanh(gate) * y
+            }
+        }
+    }
+}
+
+// In-place per-group RMS norm over groups of dim = L * 4 floats, L lanes per
+// group (L = 4 .. 64), 64 / L groups per wave step (tensor.cpp:687-695).
+template <int L, bool HAS_G>
+__global__ __launch_bounds__(kThreads) void k_heads(float* __restrict__ x, int64_t groups, int dim,
+                                                   const float* __restrict__ gamma, float eps) {
+    constexpr int GPW = 64 / L;  // groups per wave step
+    const int lane = threadIdx.x & 63;
+    const int sub = lane % L;
+    f4 g = zero4();
+    if constexpr (HAS_G) g = ((const f4*)gamma)[sub];
+    const int64_t wave = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int64_t nwaves = (int64_t)gridDim.x * kWaves;
+    for (int64_t base = wave * GPW; base < groups; base += nwaves * GPW) {
+        const int64_t grp = base + lane / L;
+        const bool ok = grp < groups;
+        f4* p = (f4*)(x + grp * dim) + sub;
+        const f4 v = ok ? dev::ld_stream(p) : zero4();
+        const float q = dev::group_sum<L>(dev::hsum(v * v));
+        const float rstd = rstd_of(q, dim, eps);
+        f4 o = v * rstd;
+        if constexpr (HAS_G) o = o * g;
+        if (ok) dev::st_stream(p, o);
+    }
+}
+
+// Generic fallback: one wave per row, strided scalar loops; handles any C
+// and any alignment. MODE: LN or RMS. Also used for in-place QK-norm of odd
+// group sizes (y == x).
+template <int MODE>
+__global__ __launch_bounds__(kThreads) void k_rownorm_generic(const float* x, float* y, int64_t rows, int64_t C,
+                                                             const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t stride = (int64_t)gridDim.x * kWaves;
+    for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows; row += stride) {
+        const float* p = x + row * C;
+        float* q = y + row * C;
+        float mean = 0.f;
+        if constexpr (MODE == M_LN) {
+            float s = 0.f;
+            for (int64_t i = lane; i < C; i += 64) s += p[i];
+            mean = (float)((double)dev::wave_sum(s) / (double)C);
+        }
+        float ss = 0.f;
+        for (int64_t i = lane; i < C; i += 64) {
+            const float d = p[i] - mean;
+            ss += d * d;
+        }
+        const float rstd = rstd_of(dev::wave_sum(ss), C, eps);
+        for (int64_t i = lane; i < C; i += 64) {
+            if constexpr (MODE == M_LN) {
+                float o = (p[i] - mean) * rstd;
+                if (gamma) o = __fmul_rn(o, gamma[i]);
+                if (beta) o = __fadd_rn(o, beta[i]);
+                q[i] = o;
+            } else {
+                q[i] = p[i] * rstd * (gamma ? gamma[i] : 1.0f);
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_add_rms_generic(float* x, const float* r, float* y, int64_t rows,
+                                                             int64_t C, const float* __restrict__ gamma, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t stride = (int64_t)gridDim.x * kWaves;
+    for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows; row += stride) {
+        float* p = x + row * C;
+        const float* rp = r + row * C;
+        float* q = y + row * C;
+        float ss = 0.f;
+        for (int64_t i = lane; i < C; i += 64) {
+            const float s = p[i] + rp[i];
+            p[i] = s;
+            ss += s * s;
+        }
+        const float rstd = rstd_of(dev::wave_sum(ss), C, eps);
+        for (int64_t i = lane; i < C; i += 64) q[i] = p[i] * rstd * (gamma ? gamma[i] : 1.0f);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_ln_mod_gate_generic(const float* x, float* res,
+                                                                 const float* __restrict__ scale,
+                                                                 const float* __restrict__ shift,
+                                                                 const float* __restrict__ gate, float* yout,
+                                                                 int64_t rows, int64_t C, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t stride = (int64_t)gridDim.x * kWaves;
+    for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows; row += stride) {
+        const float* p = x + row * C;
+        float* rp = res + row * C;
+        float s = 0.f;
+        for (int64_t i = lane; i < C; i += 64) s += p[i];
+        const float mean = (float)((double)dev::wave_sum(s) / (double)C);
+        float ss = 0.f;
+        for (int64_t i = lane; i < C; i += 64) {
+            const float d = p[i] - mean;
+            ss += d * d;
+        }
+        const float rstd = rstd_of(dev::wave_sum(ss), C, eps);
+        for (int64_t i = lane; i < C; i += 64) {
+            float yv = __fmul_rn((p[i] - mean) * rstd, scale[i] * 1.0f + 1.0f);
+            if (shift) yv = yv + shift[i];
+            if (yout) yout[row * C + i] = yv;
+            rp[i] = rp[i] + tanhf(gate[i]) * yv;
+        }
+    }
+}
+
+// ---- dispatch helpers ------------------------------------------------------
+constexpr int kMaxV = 32;
+
+// Smallest supported V with 64 * V >= n4, or 0 if n4 is too large.
+int pick_v(int64_t n4) {
+    static const int vs[] = {1, 2, 4, 8, 12, 15, 16, 24, 32};
+    for (int v : vs)
+        if (64 * (int64_t)v >= n4) return v;
+    return 0;
+}
+
+unsigned row_grid(int64_t rows, int waves_per_cu) {
+    const int64_t want = (rows + kWaves - 1) / kWaves;
+    const int64_t cap = (int64_t)num_cus() * waves_per_cu / kWaves;
+    return (unsigned)std::max<int64_t>(1, std::min(want, std::max<int64_t>(cap, 1)));
+}
+
+// Calls f(std::integral_constant<int, V>) for the runtime V.
+template <class F>
+void with_v(int v, F&& f) {
+    switch (v) {
+        case 1: f(std::integral_constant<int, 1>()); break;
+        case 2: f(std::integral_constant<int, 2>()); break;
+        case 4: f(std::integral_constant<int, 4>()); break;
+        case 8: f(std::integral_constant<int, 8>()); break;
+        case 12: f(std::integral_constant<int, 12>()); break;
+        case 15: f(std::integral_constant<int, 15>()); break;
+        case 16: f(std::integral_constant<int, 16>()); break;
+        case 24: f(std::integral_constant<int, 24>()); break;
+        case 32: f(std::integral_constant<int, 32>()); break;
+        default: fail(SDH_ERR_INVALID, "internal: unsupported row width");
+    }
+}
+
+bool vec_ok(int64_t C, std::initializer_list<const void*> ptrs) {
+    if (C % 4 != 0 || pick_v(C / 4) == 0 || C > (int64_t)64 * 4 * kMaxV) return false;
+    for (const void* p : ptrs)
+        if (p && !aligned16(p)) return false;
+    return true;
+}
+
+void run_rownorm(const char* op, int mode, const float* x, float* y, int64_t rows, int64_t C, const float* gamma,
+                 const float* beta, float eps) {
+    need(rows >= 0 && C >= 0, op, "negative size");
+    if (rows == 0 || C == 0) return;
+    ensure_init();
+    const size_t bytes = (size_t)(rows * C) * 4;
+    check_range(x, bytes, op, "x");
+    check_range(y, bytes, op, "y");
+    if (gamma) check_range(gamma, (size_t)C * 4, op, "gamma");
+    if (beta) check_range(beta, (size_t)C * 4, op, "beta");
+    if (vec_ok(C, {x, y, gamma, beta})) {
+        const int v = pick_v(C / 4);
+        const unsigned grid = row_grid(rows, 16);
+        with_v(v, [&](auto vc) {
+            constexpr int V = decltype(vc)::value;
+            if (mode == M_RMS) {
+                if (gamma)
+                    k_rownorm<V, M_RMS, true, false><<<grid, kThreads, 0, stream()>>>(x, y, rows, (int)C, gamma, beta, eps);
+                else
+                    k_rownorm<V, M_RMS, false, false><<<grid, kThreads, 0, stream()>>>(x, y, rows, (int)C, gamma, beta, eps);
+            } else {
+                if (gamma && beta)
+                    k_rownorm<V, M_LN, true, true><<<grid, kThreads, 0, stream()>>>(x, y, rows, (int)C, gamma, beta, eps);
+                else if (gamma)
+                    k_rownorm<V, M_LN, true, false><<<grid, kThreads, 0, stream()>>>(x, y, rows, (int)C, gamma, beta, eps);
+                else if (beta)
+                    k_rownorm<V, M_LN, false, true><<<grid, kThreads, 0, stream()>>>(x, y, rows, (int)C, gamma, beta, eps);
+                else
+                    k_rownorm<V, M_LN, false, false><<<grid, kThreads, 0, stream()>>>(x, y, rows, (int)C, gamma, beta, eps);
+            }
+        });
+    } else {
+        const unsigned grid = row_grid(rows, 32);
+        if (mode == M_RMS)
+            k_rownorm_generic<M_RMS><<<grid, kThreads, 0, stream()>>>(x, y, rows, C, gamma, beta, eps);
+        else
+            k_rownorm_generic<M_LN><<<grid, kThreads, 0, stream()>>>(x, y, rows, C, gamma, beta, eps);
+    }
+    launched(op);
+}
+
+}  // namespace
+}  // namespace sdh
+
+using namespace sdh;
+
+extern "C" {
+
+int sdh_rms_norm(const float* x, float* y, int64_t rows, int64_t C, const float* gamma, float eps) {
+    return guarded([&] { run_rownorm("sdh_rms_norm", M_RMS, x, y, rows, C, gamma, nullptr, eps); });
+}
+
+int sdh_layer_norm(const float* x, float* y, int64_t rows, int64_t C, const float* gamma, const float* beta,
+                   float eps) {
+    return guarded([&] { run_rownorm("sdh_layer_norm", M_LN, x, y, rows, C, gamma, beta, eps); });
+}
+
+int sdh_add_rms_norm(float* x, const float* r, float* y, int64_t rows, int64_t C, const float* gamma, float eps) {
+    return guarded([&] {
+        const char* op = "sdh_add_rms_norm";
+        need(rows >= 0 && C >= 0, op, "negative size");
+        if (rows == 0 || C == 0) return;
+        ensure_init();
+        const size_t bytes = (size_t)(rows * C) * 4;
+        check_range(x, bytes, op, "x");
+        check_range(r, bytes, op, "r");
+        check_range(y, bytes, op, "y");
+        if (gamma) check_range(gamma, (size_t)C * 4, op, "gamma");
+        if (vec_ok(C, {x, r, y, gamma})) {
+            const unsigned grid = row_grid(rows, 16);
+            with_v(pick_v(C / 4), [&](auto vc) {
+                constexpr int V = decltype(vc)::value;
+                if (gamma)
+                    k_add_rms<V, true><<<grid, kThreads, 0, stream()>>>(x, r, y, rows, (int)C, gamma, eps);
+                else
+                    k_add_rms<V, false><<<grid, kThreads, 0, stream()>>>(x, r, y, rows, (int)C, gamma, eps);
+            });
+        } else {
+            k_add_rms_generic<<<row_grid(rows, 32), kThreads, 0, stream()>>>(x, r, y, rows, C, gamma, eps);
+        }
+        launched(op);
+    });
+}
+
+int sdh_ln_modulate_gate(const float* x, float* res, const float* scale, const float* shift, const float* gate,
+                         float* y_out, int64_t rows, int64_t C, float eps) {
+    return guarded([&] {
+        const char* op = "sdh_ln_modulate_gate";
+        need(rows >= 0 && C >= 0, op, "negative size");
+        if (rows == 0 || C == 0) return;
+        ensure_init();
+        const size_t bytes = (size_t)(rows * C) * 4;
+        check_range(x, bytes, op, "x");
+        check_range(res, bytes, op, "res");
+        check_range(scale, (size_t)C * 4, op, "scale");
+        check_range(gate, (size_t)C * 4, op, "gate");
+        if (shift) check_range(shift, (size_t)C * 4, op, "shift");
+        if (y_out) check_range(y_out, bytes, op, "y_out");
+        const size_t lds = (size_t)3 * C * 4;
+        if (vec_ok(C, {x, res, scale, shift, gate, y_out}) && lds <= 64 * 1024) {
+            const unsigned grid = row_grid(rows, 8);
+            with_v(pick_v(C / 4), [&](auto vc) {
+                constexpr int V = decltype(vc)::value;
+                if (shift && y_out)
+                    k_ln_mod_gate<V, true, true><<<grid, kThreads, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
+                else if (shift)
+                    k_ln_mod_gate<V, true, false><<<grid, kThreads, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
+                else if (y_out)
+                    k_ln_mod_gate<V, false, true><<<grid, kThreads, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
+                else
+                    k_ln_mod_gate<V, false, false><<<grid, kThreads, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
+            });
+        } else {
+            k_ln_mod_gate_generic<<<row_grid(rows, 32), kThreads, 0, stream()>>>(x, res, scale, shift, gate, y_out,
+                                                                                rows, C, eps);
+        }
+        launched(op);
+    });
+}
+
+int sdh_rms_norm_heads(float* x, int64_t groups, int64_t dim, const float* gamma, float eps) {
+    return guarded([&] {
+        const char* op = "sdh_rms_norm_heads";
+        need(groups >= 0 && dim >= 0, op, "negative size");
+        if (groups == 0 || dim == 0) return;
+        ensure_init();
+        check_range(x, (size_t)(groups * dim) * 4, op, "x");
+        if (gamma) check_range(gamma, (size_t)dim * 4, op, "gamma");
+        const int64_t L = dim / 4;
+        const bool vec = dim % 4 == 0 && (L == 4 || L == 8 || L == 16 || L == 32 || L == 64) && aligned16(x) &&
+                         (!gamma || aligned16(gamma));
+        if (vec) {
+            const int64_t steps = (groups + (64 / L) - 1) / (64 / L);
+            const unsigned grid = row_grid(steps, 16);
+            auto go = [&](auto lc) {
+                constexpr int LL = decltype(lc)::value;
+                if (gamma)
+                    k_heads<LL, true><<<grid, kThreads, 0, stream()>>>(x, groups, (int)dim, gamma, eps);
+                else
+                    k_heads<LL, false><<<grid, kThreads, 0, stream()>>>(x, groups, (int)dim, gamma, eps);
+            };
+            switch (L) {
+                case 4: go(std::integral_constant<int, 4>()); break;
+                case 8: go(std::integral_constant<int, 8>()); break;
+                case 16: go(std::integral_constant<int, 16>()); break;
+                case 32: go(std::integral_constant<int, 32>()); break;
+                default: go(std::integral_constant<int, 64>()); break;
+            }
+        } else {
+            k_rownorm_generic<M_RMS><<<row_grid(groups, 32), kThreads, 0, stream()>>>(x, x, groups, dim, gamma,
+                                                                                     nullptr, eps);
+        }
+        launched(op);
+    });
+}
+
+}  // extern "C"

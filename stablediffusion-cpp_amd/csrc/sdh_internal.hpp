@@ -1,0 +1,153 @@
+// sdh_internal.hpp - shared internals of backend_hip: error plumbing, the
+// runtime singleton's interface, launch helpers and wave64 device primitives
+// for gfx950 (CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "sdh_backend.h"
+
+namespace sdh {
+
+// ---------------------------------------------------------------------------
+// Errors: internal code throws Error; every extern "C" entry point catches it
+// (and any std::exception), records the message for sdh_last_error() and
+// returns the status. Nothing crosses the C ABI as an exception.
+// ---------------------------------------------------------------------------
+struct Error : std::runtime_error {
+    int status;
+    Error(int s, const std::string& m) : std::runtime_error(m), status(s) {}
+};
+
+[[noreturn]] void fail(int status, const std::string& msg);
+void hip_check(hipError_t e, const char* what);
+void set_last_error(const char* msg);
+
+template <class F>
+int guarded(F&& f) noexcept {
+    try {
+        f();
+        set_last_error("");
+        return SDH_OK;
+    } catch (const Error& e) {
+        set_last_error(e.what());
+        return e.status;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return SDH_ERR_HIP;
+    } catch (...) {
+        set_last_error("unknown error");
+        return SDH_ERR_HIP;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Runtime (runtime.hip)
+// ---------------------------------------------------------------------------
+void ensure_init();
+hipStream_t stream();
+int num_cus();
+// Throws SDH_ERR_INVALID unless [p, p + bytes) lies inside one live arena
+// block or one registered external range. `what` names the argument.
+void check_range(const void* p, size_t bytes, const char* op, const char* what);
+// Per-call device scratch of at least `bytes`, owned by the library, valid
+// until the next call that asks for scratch (ops are serialised on one stream).
+void* scratch(size_t bytes);
+// Zero-initialised per-library device counters (uint32), persistent across
+// calls; kernels that use them leave them at zero when they finish.
+unsigned* counters(size_t count);
+void launched(const char* op);
+// Queues a zero fill of [p, p + bytes) on the library stream (a kernel, not a memset).
+void zero_device(void* p, size_t bytes);
+
+// Argument helpers shared by the op entry points.
+inline void need(bool ok, const char* op, const char* msg) {
+    if (!ok) fail(SDH_ERR_INVALID, std::string(op) + ": " + msg);
+}
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline unsigned blocks_for(int64_t items, int64_t per_block) {
+    int64_t b = (items + per_block - 1) / per_block;
+    return (unsigned)(b < 1 ? 1 : b);
+}
+
+}  // namespace sdh
+
+// ---------------------------------------------------------------------------
+// Device primitives (wave64)
+// ---------------------------------------------------------------------------
+namespace sdh {
+namespace dev {
+
+constexpr int kWave = 64;
+
+// Native 128-bit vector of 4 floats (one global_load_dwordx4 per lane).
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// DPP lane moves within a row of 16 lanes. Controls (GCN/CDNA DPP encoding):
+// quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E, row_half_mirror =
+// 0x141, row_mirror = 0x140. Every lane reads a valid lane for these.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over aligned groups of W lanes (W = 4, 8, 16, 32, 64); every lane of a
+// group receives the group's sum. All 64 lanes must be active.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    if constexpr (W >= 8) v += dpp<0x141>(v);
+    if constexpr (W >= 16) v += dpp<0x140>(v);
+    if constexpr (W == 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (W == 64) {
+        // Row sums are uniform within each row of 16; combine the 4 rows
+        // through scalar reads so the result is bitwise identical in all lanes.
+        const float a = readlane(v, 0), b = readlane(v, 16), c = readlane(v, 32), d = readlane(v, 48);
+        v = (a + b) + (c + d);
+    }
+    return v;
+}
+
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+    static_assert(W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "group width");
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    if constexpr (W >= 8) v = fmaxf(v, dpp<0x141>(v));
+    if constexpr (W >= 16) v = fmaxf(v, dpp<0x140>(v));
+    if constexpr (W == 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+    if constexpr (W == 64) {
+        const float a = readlane(v, 0), b = readlane(v, 16), c = readlane(v, 32), d = readlane(v, 48);
+        v = fmaxf(fmaxf(a, b), fmaxf(c, d));
+    }
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
+
+__device__ __forceinline__ float hsum(const f4& v) { return (v.x + v.y) + (v.z + v.w); }
+
+// Streaming accesses: data touched exactly once per launch is loaded and
+// stored non-temporally so it does not displace reusable lines in L2/MALL.
+__device__ __forceinline__ f4 ld_stream(const f4* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void st_stream(f4* p, f4 v) { __builtin_nontemporal_store(v, p); }
+
+// Reference-order activations (tensor.cpp:745, :847, :859, :866, :830).
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+__device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+__device__ __forceinline__ float quick_gelu(float v) { return v / (1.0f + expf(-1.702f * v)); }
+
+}  // namespace dev
+}  // namespace sdh

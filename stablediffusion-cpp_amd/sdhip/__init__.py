@@ -1,0 +1,299 @@
+"""Python bindings of backend_hip's C ABI (include/sdh_backend.h), via ctypes.
+
+This is a thin host-side mirror used by the parity tests and the benchmark:
+``Backend`` loads ``libsdh.so`` (built in-tree by ``__graft_entry__.build()``)
+and exposes every entry point with numpy-friendly helpers. Device memory comes
+from the library's own arena (``DArray``); no other framework is involved.
+
+There is deliberately no CPU fallback: if the library or the device is
+missing, constructing ``Backend`` raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "libsdh.so")
+STUB_PATH = os.path.join(PKG_DIR, "libsdh_stub.so")
+
+SDH_OK = 0
+SDH_ERR_UNAVAILABLE = 1
+SDH_ERR_INVALID = 2
+SDH_ERR_OOM = 3
+SDH_ERR_HIP = 4
+
+_STATUS = {1: "UNAVAILABLE", 2: "INVALID", 3: "OOM", 4: "HIP"}
+
+
+class SdhError(RuntimeError):
+    """A non-zero status from the C ABI, with the library's message."""
+
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"[{_STATUS.get(status, status)}] {msg}")
+        self.status = status
+
+
+_i64, _fl, _vp, _int = C.c_int64, C.c_float, C.c_void_p, C.c_int
+
+# name -> argtypes (all return int status unless listed in _RESTYPES)
+SIGNATURES = {
+    "sdh_last_error": [],
+    "sdh_available": [],
+    "sdh_device_name": [],
+    "sdh_device_memory": [],
+    "sdh_init": [C.c_size_t],
+    "sdh_shutdown": [],
+    "sdh_malloc": [C.c_size_t, C.POINTER(C.c_void_p)],
+    "sdh_free": [_vp],
+    "sdh_upload": [_vp, _vp, C.c_size_t],
+    "sdh_download": [_vp, _vp, C.c_size_t],
+    "sdh_copy": [_vp, _vp, C.c_size_t],
+    "sdh_zero": [_vp, C.c_size_t],
+    "sdh_synchronize": [],
+    "sdh_register_external": [_vp, C.c_size_t],
+    "sdh_unregister_external": [_vp],
+    "sdh_memory_stats": [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)],
+    "sdh_group_norm": [_vp, _vp, _i64, _i64, _i64, _int, _vp, _vp, _fl],
+    "sdh_layer_norm": [_vp, _vp, _i64, _i64, _vp, _vp, _fl],
+    "sdh_rms_norm": [_vp, _vp, _i64, _i64, _vp, _fl],
+    "sdh_rms_norm_heads": [_vp, _i64, _i64, _vp, _fl],
+    "sdh_rope": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _int],
+    "sdh_rope_qk": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _int],
+    "sdh_softmax_rows": [_vp, _i64, _i64, _fl, _int],
+    "sdh_softmax_rows_batched": [_vp, _i64, _i64, _fl, _int, _i64],
+    "sdh_swiglu": [_vp, _vp, _vp, _i64],
+    "sdh_geglu": [_vp, _vp, _i64, _i64],
+    "sdh_silu": [_vp, _i64],
+    "sdh_tanh": [_vp, _i64],
+    "sdh_gelu": [_vp, _i64],
+    "sdh_quick_gelu": [_vp, _i64],
+    "sdh_add": [_vp, _vp, _i64],
+    "sdh_scale": [_vp, _fl, _i64],
+    "sdh_affine": [_vp, _fl, _fl, _i64],
+    "sdh_mul_rows": [_vp, _vp, _i64, _i64],
+    "sdh_add_rows_scaled": [_vp, _vp, _vp, _i64, _i64],
+    "sdh_add_channel_bias": [_vp, _vp, _i64, _i64, _i64],
+    "sdh_add_rows": [_vp, _vp, _i64, _i64],
+    "sdh_add_rms_norm": [_vp, _vp, _vp, _i64, _i64, _vp, _fl],
+    "sdh_group_norm_silu": [_vp, _vp, _i64, _i64, _i64, _int, _vp, _vp, _fl],
+    "sdh_ln_modulate_gate": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _fl],
+    "sdh_fill_normal": [_vp, _i64, C.c_uint64, _fl, _fl],
+    "sdh_timer_record": [_int],
+    "sdh_timer_elapsed": [_int, _int, C.POINTER(C.c_float)],
+}
+_RESTYPES = {
+    "sdh_last_error": C.c_char_p,
+    "sdh_device_name": C.c_char_p,
+    "sdh_device_memory": C.c_size_t,
+}
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    """Loads a backend_hip shared library and declares every signature."""
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built; run __graft_entry__.build() (or make -C "
+                                f"stablediffusion-cpp_amd/csrc)")
+    lib = C.CDLL(path)
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPES.get(name, C.c_int)
+    return lib
+
+
+def _p(x) -> Optional[int]:
+    """Device address of a DArray (or None)."""
+    if x is None:
+        return None
+    if isinstance(x, DArray):
+        return x.ptr
+    if isinstance(x, int):
+        return x
+    raise TypeError(f"expected DArray, int address or None, got {type(x).__name__}")
+
+
+class DArray:
+    """A float32 array in the backend's device arena."""
+
+    def __init__(self, backend: "Backend", shape: Sequence[int], ptr: Optional[int] = None, owned: bool = True):
+        self.be = backend
+        self.shape = tuple(int(s) for s in shape)
+        self.size = int(np.prod(self.shape)) if self.shape else 1
+        self.nbytes = self.size * 4
+        self.owned = owned
+        if ptr is None:
+            ptr = backend.malloc(self.nbytes)
+        self.ptr = ptr
+
+    def upload(self, a: np.ndarray) -> "DArray":
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        if a.size != self.size:
+            raise ValueError(f"upload size {a.size} != {self.size}")
+        self.be.upload(self.ptr, a)
+        return self
+
+    def download(self) -> np.ndarray:
+        out = np.empty(self.shape, np.float32)
+        self.be.download(out, self.ptr)
+        return out
+
+    def free(self):
+        if self.owned and self.ptr:
+            self.be.free(self.ptr)
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            if self.owned and self.ptr:
+                self.be.free(self.ptr)
+        except Exception:
+            pass
+
+
+class Backend:
+    """The loaded library plus numpy-level helpers for every entry point."""
+
+    def __init__(self, path: str = LIB_PATH, require_device: bool = True, arena_bytes: int = 0):
+        self.lib = load_library(path)
+        self.path = path
+        if require_device:
+            if not self.lib.sdh_available():
+                raise SdhError(SDH_ERR_UNAVAILABLE, "no HIP device visible to backend_hip")
+            self.check(self.lib.sdh_init(arena_bytes))
+
+    # -- plumbing --
+    def last_error(self) -> str:
+        return (self.lib.sdh_last_error() or b"").decode()
+
+    def check(self, rc: int):
+        if rc != SDH_OK:
+            raise SdhError(rc, self.last_error())
+
+    def call(self, name: str, *args):
+        self.check(getattr(self.lib, name)(*args))
+
+    def available(self) -> bool:
+        return bool(self.lib.sdh_available())
+
+    def device_name(self) -> str:
+        return self.lib.sdh_device_name().decode()
+
+    def malloc(self, nbytes: int) -> int:
+        p = C.c_void_p()
+        self.check(self.lib.sdh_malloc(nbytes, C.byref(p)))
+        return p.value or 0
+
+    def free(self, ptr: int):
+        self.check(self.lib.sdh_free(ptr))
+
+    def upload(self, ptr: int, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        self.check(self.lib.sdh_upload(ptr, a.ctypes.data, a.nbytes))
+
+    def download(self, out: np.ndarray, ptr: int):
+        assert out.flags.c_contiguous
+        self.check(self.lib.sdh_download(out.ctypes.data, ptr, out.nbytes))
+
+    def synchronize(self):
+        self.check(self.lib.sdh_synchronize())
+
+    def memory_stats(self):
+        r, u = C.c_size_t(), C.c_size_t()
+        self.check(self.lib.sdh_memory_stats(C.byref(r), C.byref(u)))
+        return r.value, u.value
+
+    def empty(self, shape) -> DArray:
+        return DArray(self, shape)
+
+    def array(self, a: np.ndarray) -> DArray:
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        return DArray(self, a.shape).upload(a)
+
+    def randn(self, shape, seed: int, mean: float = 0.0, std: float = 1.0) -> DArray:
+        d = DArray(self, shape)
+        self.check(self.lib.sdh_fill_normal(d.ptr, d.size, seed, mean, std))
+        return d
+
+    def timer_record(self, slot: int):
+        self.check(self.lib.sdh_timer_record(slot))
+
+    def timer_elapsed(self, a: int, b: int) -> float:
+        ms = C.c_float()
+        self.check(self.lib.sdh_timer_elapsed(a, b, C.byref(ms)))
+        return ms.value
+
+    # -- ops on DArrays (argument meaning as include/sdh_backend.h) --
+    def group_norm(self, x, y, N, Cc, HW, groups, gamma, beta, eps, silu=False):
+        self.call("sdh_group_norm_silu" if silu else "sdh_group_norm", _p(x), _p(y), N, Cc, HW, groups, _p(gamma),
+                  _p(beta), eps)
+
+    def layer_norm(self, x, y, rows, Cc, gamma, beta, eps):
+        self.call("sdh_layer_norm", _p(x), _p(y), rows, Cc, _p(gamma), _p(beta), eps)
+
+    def rms_norm(self, x, y, rows, Cc, gamma, eps):
+        self.call("sdh_rms_norm", _p(x), _p(y), rows, Cc, _p(gamma), eps)
+
+    def rms_norm_heads(self, x, groups, dim, gamma, eps):
+        self.call("sdh_rms_norm_heads", _p(x), groups, dim, _p(gamma), eps)
+
+    def rope(self, x, N, S, inner, dim, cos_t, sin_t, interleaved):
+        self.call("sdh_rope", _p(x), N, S, inner, dim, _p(cos_t), _p(sin_t), int(bool(interleaved)))
+
+    def rope_qk(self, q, inner_q, k, inner_k, N, S, dim, cos_t, sin_t, interleaved):
+        self.call("sdh_rope_qk", _p(q), inner_q, _p(k), inner_k, N, S, dim, _p(cos_t), _p(sin_t),
+                  int(bool(interleaved)))
+
+    def softmax_rows(self, x, rows, cols, scale, causal=False, period=None):
+        if period is None:
+            self.call("sdh_softmax_rows", _p(x), rows, cols, scale, int(bool(causal)))
+        else:
+            self.call("sdh_softmax_rows_batched", _p(x), rows, cols, scale, int(bool(causal)), period)
+
+    def swiglu(self, g, u, y, n):
+        self.call("sdh_swiglu", _p(g), _p(u), _p(y), n)
+
+    def geglu(self, x, y, rows, D):
+        self.call("sdh_geglu", _p(x), _p(y), rows, D)
+
+    def silu(self, x, n):
+        self.call("sdh_silu", _p(x), n)
+
+    def tanh(self, x, n):
+        self.call("sdh_tanh", _p(x), n)
+
+    def gelu(self, x, n):
+        self.call("sdh_gelu", _p(x), n)
+
+    def quick_gelu(self, x, n):
+        self.call("sdh_quick_gelu", _p(x), n)
+
+    def add(self, a, b, n):
+        self.call("sdh_add", _p(a), _p(b), n)
+
+    def scale(self, x, s, n):
+        self.call("sdh_scale", _p(x), s, n)
+
+    def affine(self, x, a, b, n):
+        self.call("sdh_affine", _p(x), a, b, n)
+
+    def mul_rows(self, x, v, rows, dim):
+        self.call("sdh_mul_rows", _p(x), _p(v), rows, dim)
+
+    def add_rows_scaled(self, x, y, g, rows, dim):
+        self.call("sdh_add_rows_scaled", _p(x), _p(y), _p(g), rows, dim)
+
+    def add_rows(self, x, v, rows, dim):
+        self.call("sdh_add_rows", _p(x), _p(v), rows, dim)
+
+    def add_channel_bias(self, x, b, N, Cc, HW):
+        self.call("sdh_add_channel_bias", _p(x), _p(b), N, Cc, HW)
+
+    def add_rms_norm(self, x, r, y, rows, Cc, gamma, eps):
+        self.call("sdh_add_rms_norm", _p(x), _p(r), _p(y), rows, Cc, _p(gamma), eps)
+
+    def ln_modulate_gate(self, x, res, scale, shift, gate, y_out, rows, Cc, eps):
+        self.call("sdh_ln_modulate_gate", _p(x), _p(res), _p(scale), _p(shift), _p(gate), _p(y_out), rows, Cc, eps)

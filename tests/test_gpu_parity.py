@@ -1,0 +1,341 @@
+"""GPU parity: every backend_hip entry point vs the CPU oracle (and, where it
+was built, vs the compiled reference itself), through the C ABI.
+
+Inputs come from the oracle's seeded generator, are uploaded once, and the
+same host arrays feed the oracle, so both sides see identical bits. Shapes:
+the reference's own test_ops shapes (tests/test_ops.cpp:389-463), odd and
+unaligned shapes that force the generic kernels, and the BASELINE config
+shapes (Z-Image 1024^2: T=4096 tokens, D=3840, F=10240; FLUX-VAE and SD 1.5
+GroupNorm shapes). Tolerances are defined in tolerances.py.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import sdhip
+from tolerances import assert_elementwise, assert_reduction, assert_softmax
+
+pytestmark = pytest.mark.gpu
+
+T, D, F = 4096, 3840, 10240
+
+
+def _seed(*parts):
+    h = 1469598103934665603
+    for p in parts:
+        for ch in str(p):
+            h = ((h ^ ord(ch)) * 1099511628211) % (1 << 64)
+    return h
+
+
+# ---------------------------------------------------------------- elementwise
+@pytest.mark.parametrize("n", [1, 3, 1000, 4097, 1 << 20, T * F])
+def test_swiglu(be, orc, n):
+    g = orc.randn((n,), _seed("sw_g", n), 0.0, 1.5)
+    u = orc.randn((n,), _seed("sw_u", n), 0.0, 1.5)
+    dg, du, dy = be.array(g), be.array(u), be.empty((n,))
+    be.swiglu(dg, du, dy, n)
+    assert_elementwise(dy.download(), orc.swiglu(g, u), f"swiglu n={n}")
+
+
+@pytest.mark.parametrize("op", ["silu", "tanh", "gelu", "quick_gelu"])
+@pytest.mark.parametrize("n", [1000, 1 << 18, 12345])
+def test_unary(be, orc, op, n):
+    x = orc.randn((n,), _seed(op, n), 0.0, 3.0)
+    dx = be.array(x)
+    getattr(be, op)(dx, n)
+    assert_elementwise(dx.download(), getattr(orc, op)(x), f"{op} n={n}")
+
+
+@pytest.mark.parametrize("n", [1000, 1 << 20, 7])
+def test_add_scale_affine(be, orc, n):
+    a = orc.randn((n,), _seed("a", n))
+    b = orc.randn((n,), _seed("b", n))
+    da, db = be.array(a), be.array(b)
+    be.add(da, db, n)
+    want = orc.add(a, b)
+    assert_elementwise(da.download(), want, "add")
+    be.scale(da, 0.37, n)
+    want = orc.scale(want, 0.37)
+    assert_elementwise(da.download(), want, "scale")
+    be.affine(da, 1.5, -0.25, n)
+    want = orc.affine(want, 1.5, -0.25)
+    assert_elementwise(da.download(), want, "affine")
+
+
+@pytest.mark.parametrize("rows,D2", [(6, 40), (33, 1280 * 2), (4, 7 * 2)])
+def test_geglu(be, orc, rows, D2):
+    x = orc.randn((rows, D2), _seed("geglu", rows, D2))
+    dx, dy = be.array(x), be.empty((rows, D2 // 2))
+    be.geglu(dx, dy, rows, D2 // 2)
+    assert_elementwise(dy.download(), orc.geglu(x), "geglu")
+
+
+# ---------------------------------------------------------------- broadcasts
+@pytest.mark.parametrize("rows,dim", [(4, 6), (T, D), (37, 64), (5, 7)])
+def test_row_broadcasts(be, orc, rows, dim):
+    x = orc.randn((rows, dim), _seed("rb_x", rows, dim))
+    y = orc.randn((rows, dim), _seed("rb_y", rows, dim))
+    v = orc.randn((dim,), _seed("rb_v", rows, dim), 0.0, 0.2)
+    dx, dy, dv = be.array(x), be.array(y), be.array(v)
+    be.mul_rows(dx, dv, rows, dim)
+    want = orc.mul_rows(x, v)
+    assert_elementwise(dx.download(), want, "mul_rows")
+    be.add_rows_scaled(dx, dy, dv, rows, dim)
+    want = orc.add_rows_scaled(want, y, v)
+    assert_elementwise(dx.download(), want, "add_rows_scaled")
+    be.add_rows(dx, dv, rows, dim)
+    want = orc.add_rows_scaled(want, np.ones_like(want), v)  # += v as the CPU composes it
+    assert_elementwise(dx.download(), want, "add_rows")
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 4, 5), (2, 320, 64, 64), (1, 7, 3, 3)])
+def test_add_channel_bias(be, orc, shape):
+    x = orc.randn(shape, _seed("cb_x", *shape))
+    b = orc.randn(shape[:2], _seed("cb_b", *shape))
+    dx, db = be.array(x), be.array(b)
+    N, Cc = shape[0], shape[1]
+    be.add_channel_bias(dx, db, N, Cc, x.size // (N * Cc))
+    assert_elementwise(dx.download(), orc.add_channel_bias(x, b), "add_channel_bias")
+
+
+# ---------------------------------------------------------------- norms
+@pytest.mark.parametrize("rows,C", [(21, 64), (T, D), (5, 24), (3, 70), (2, 9000), (130, 5), (1, 1)])
+@pytest.mark.parametrize("affine", [True, False])
+def test_rms_norm(be, orc, rows, C, affine):
+    x = orc.randn((rows, C), _seed("rms", rows, C))
+    w = orc.randn((C,), _seed("rms_w", C), 1.0, 0.1) if affine else None
+    dx, dy = be.array(x), be.empty((rows, C))
+    dw = be.array(w) if affine else None
+    be.rms_norm(dx, dy, rows, C, dw, 1e-6)
+    assert_reduction(dy.download(), orc.rms_norm(x, w, 1e-6), f"rms_norm [{rows},{C}]")
+
+
+@pytest.mark.parametrize("rows,C", [(21, 64), (T, D), (3, 70), (2, 9000), (33, 320)])
+@pytest.mark.parametrize("gb", ["both", "none", "gamma", "beta"])
+def test_layer_norm(be, orc, rows, C, gb):
+    x = orc.randn((rows, C), _seed("ln", rows, C), 2.0, 3.0)
+    g = orc.randn((C,), _seed("ln_g", C), 1.0, 0.1) if gb in ("both", "gamma") else None
+    b = orc.randn((C,), _seed("ln_b", C), 0.0, 0.1) if gb in ("both", "beta") else None
+    dx, dy = be.array(x), be.empty((rows, C))
+    be.layer_norm(dx, dy, rows, C, be.array(g) if g is not None else None, be.array(b) if b is not None else None,
+                  1e-5)
+    assert_reduction(dy.download(), orc.layer_norm(x, g, b, 1e-5), f"layer_norm [{rows},{C}] {gb}")
+
+
+@pytest.mark.parametrize("groups,dim", [(15, 8), (T * 30, 128), (37, 64), (10, 256), (9, 30), (4, 16)])
+@pytest.mark.parametrize("affine", [True, False])
+def test_rms_norm_heads(be, orc, groups, dim, affine):
+    x = orc.randn((groups, dim), _seed("qk", groups, dim))
+    w = orc.randn((dim,), _seed("qk_w", dim), 1.0, 0.1) if affine else None
+    dx = be.array(x)
+    be.rms_norm_heads(dx, groups, dim, be.array(w) if affine else None, 1e-5)
+    assert_reduction(dx.download(), orc.rms_norm_heads(x, dim, w, 1e-5), f"rms_norm_heads [{groups},{dim}]")
+
+
+@pytest.mark.parametrize("rows,C", [(T, D), (7, 64), (3, 70), (1, 9000)])
+@pytest.mark.parametrize("affine", [True, False])
+def test_add_rms_norm(be, orc, rows, C, affine):
+    """Config 1: fused residual add + RMSNorm vs add_ then rms_norm."""
+    x = orc.randn((rows, C), _seed("arn_x", rows, C))
+    r = orc.randn((rows, C), _seed("arn_r", rows, C))
+    w = orc.randn((C,), _seed("arn_w", C), 1.0, 0.1) if affine else None
+    dx, dr, dy = be.array(x), be.array(r), be.empty((rows, C))
+    be.add_rms_norm(dx, dr, dy, rows, C, be.array(w) if affine else None, 1e-6)
+    s_ref, y_ref = orc.add_rms_norm(x, r, w, 1e-6)
+    assert_elementwise(dx.download(), s_ref, "add_rms_norm sum")
+    assert_reduction(dy.download(), y_ref, "add_rms_norm norm")
+
+
+@pytest.mark.parametrize("rows,C", [(T, D), (9, 64), (3, 70), (2, 9000)])
+@pytest.mark.parametrize("shift", [True, False])
+@pytest.mark.parametrize("store_y", [True, False])
+def test_ln_modulate_gate(be, orc, rows, C, shift, store_y):
+    """Config 5a: y = LN(x)(1+scale)+shift; res += tanh(gate) y."""
+    x = orc.randn((rows, C), _seed("lmg_x", rows, C))
+    res = orc.randn((rows, C), _seed("lmg_r", rows, C))
+    sc = orc.randn((C,), _seed("lmg_s", C), 0.0, 0.2)
+    sh = orc.randn((C,), _seed("lmg_h", C), 0.0, 0.2) if shift else None
+    gt = orc.randn((C,), _seed("lmg_g", C), 0.0, 0.2)
+    dx, dres = be.array(x), be.array(res)
+    dy = be.empty((rows, C)) if store_y else None
+    be.ln_modulate_gate(dx, dres, be.array(sc), be.array(sh) if shift else None, be.array(gt), dy, rows, C, 1e-6)
+    r_ref, y_ref = orc.ln_modulate_gate(x, res, sc, sh, gt, 1e-6)
+    assert_reduction(dres.download(), r_ref, "ln_modulate_gate res")
+    if store_y:
+        assert_reduction(dy.download(), y_ref, "ln_modulate_gate y")
+
+
+GN_SHAPES = [
+    ((2, 64, 5, 7), 32, 1e-6),          # test_ops.cpp:391-392
+    ((1, 512, 128, 128), 32, 1e-6),     # config 4a (FLUX VAE)
+    ((1, 128, 1024, 1024), 32, 1e-6),   # config 4b (FLUX VAE norm_out)
+    ((2, 320, 64, 64), 32, 1e-5),       # config 4c (SD 1.5)
+    ((2, 1280, 8, 8), 32, 1e-5),        # config 4d (SD 1.5)
+    ((1, 96, 33, 17), 32, 1e-6),        # odd plane: generic kernel
+    ((3, 8, 4, 4), 4, 1e-6),
+]
+
+
+@pytest.mark.parametrize("shape,groups,eps", GN_SHAPES)
+@pytest.mark.parametrize("silu", [True, False])
+def test_group_norm(be, orc, shape, groups, eps, silu):
+    x = orc.randn(shape, _seed("gn", *shape), 0.0, 2.0)
+    Cc = shape[1]
+    g = orc.randn((Cc,), _seed("gn_g", Cc), 1.0, 0.1)
+    b = orc.randn((Cc,), _seed("gn_b", Cc), 0.0, 0.1)
+    dx, dy = be.array(x), be.empty(shape)
+    N = shape[0]
+    be.group_norm(dx, dy, N, Cc, x.size // (N * Cc), groups, be.array(g), be.array(b), eps, silu=silu)
+    assert_reduction(dy.download(), orc.group_norm(x, groups, g, b, eps, silu=silu), f"group_norm{'+silu' if silu else ''} {shape}")
+
+
+def test_group_norm_inplace_and_repeat(be, orc):
+    """y == x is allowed; repeated calls re-arm the split kernel's counters."""
+    shape = (1, 64, 256, 256)
+    x = orc.randn(shape, 77, 1.0, 2.0)
+    g = orc.randn((64,), 78, 1.0, 0.1)
+    b = orc.randn((64,), 79, 0.0, 0.1)
+    want = orc.group_norm(x, 32, g, b, 1e-6, silu=True)
+    dg, db = be.array(g), be.array(b)
+    for _ in range(3):
+        dx = be.array(x)
+        be.group_norm(dx, dx, 1, 64, 256 * 256, 32, dg, db, 1e-6, silu=True)
+        assert_reduction(dx.download(), want, "group_norm_silu in place")
+
+
+# ---------------------------------------------------------------- softmax
+@pytest.mark.parametrize("rows,cols", [(9, 9), (64, 4096), (100, 100), (5, 4128), (3, 9000), (7, 1)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_softmax(be, orc, rows, cols, causal):
+    x = orc.randn((rows, cols), _seed("sm", rows, cols), 0.0, 3.0)
+    scale = 1.0 / math.sqrt(128.0)
+    dx = be.array(x)
+    be.softmax_rows(dx, rows, cols, scale, causal)
+    assert_softmax(dx.download(), orc.softmax_rows(x, scale, causal), f"softmax [{rows},{cols}] causal={causal}")
+
+
+def test_softmax_batched_period(be, orc):
+    rows, cols, period = 3 * 37, 37, 37
+    x = orc.randn((rows, cols), 91, 0.0, 3.0)
+    dx = be.array(x)
+    be.softmax_rows(dx, rows, cols, 0.25, True, period)
+    assert_softmax(dx.download(), orc.softmax_rows(x, 0.25, True, period), "softmax batched causal")
+
+
+def test_softmax_config_5b(be, orc):
+    """Config 5b at full size: [30 heads, 4096, 4096], scale 1/sqrt(128)."""
+    rows, cols = 30 * T, T
+    x = orc.randn((rows, cols), _seed("sm5b"), 0.0, 3.0)
+    scale = 1.0 / math.sqrt(128.0)
+    dx = be.array(x)
+    be.softmax_rows(dx, rows, cols, scale, False)
+    got = dx.download()
+    want = orc.softmax_rows(x, scale, False)
+    assert_softmax(got, want, "softmax config 5b")
+    # size-independent property: every row sums to 1
+    assert float(np.max(np.abs(got.sum(axis=1, dtype=np.float64) - 1.0))) < 1e-5
+
+
+# ---------------------------------------------------------------- rotary
+def _zimage_tables(orc, S, side):
+    pos = np.array([[0, h, w] for h in range(side) for w in range(side)], np.int32)[:S]
+    return orc.rope_tables_3axis(pos, [32, 48, 48], 128, 256.0)
+
+
+@pytest.mark.parametrize("interleaved", [True, False])
+@pytest.mark.parametrize("N,S,heads,dim", [(1, 5, 3, 8), (2, 7, 4, 16), (1, 64, 30, 128), (1, 9, 2, 6)])
+def test_rope(be, orc, interleaved, N, S, heads, dim):
+    x = orc.randn((N, S, heads * dim), _seed("rope", N, S, heads, dim))
+    ang = orc.randn((S, dim), _seed("rope_t", S, dim), 0.0, 1.0)
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)  # arbitrary, non-paired tables
+    dx = be.array(x)
+    be.rope(dx, N, S, heads * dim, dim, be.array(cs), be.array(sn), interleaved)
+    assert_elementwise(dx.download(), orc.rope(x, dim, cs, sn, interleaved), f"rope inter={interleaved}")
+
+
+def test_rope_qk_config_3(be, orc):
+    """Config 3: 3-axis interleaved RoPE on Q and K [4096, 30*128], one launch."""
+    cs, sn = _zimage_tables(orc, T, 64)
+    q = orc.randn((1, T, 30 * 128), _seed("q3"))
+    k = orc.randn((1, T, 30 * 128), _seed("k3"))
+    dq, dk, dc, ds = be.array(q), be.array(k), be.array(cs), be.array(sn)
+    be.rope_qk(dq, 30 * 128, dk, 30 * 128, 1, T, 128, dc, ds, True)
+    assert_elementwise(dq.download(), orc.rope(q, 128, cs, sn, True), "rope_qk q")
+    assert_elementwise(dk.download(), orc.rope(k, 128, cs, sn, True), "rope_qk k")
+
+
+def test_rope_qk_gqa_half(be, orc):
+    """rotate_half with fewer K heads (Qwen3-style tables, qwen3.cpp:46-53)."""
+    S, dim = 37, 128
+    cs, sn = orc.rope_tables_half(S, dim, 1e6)
+    q = orc.randn((2, S, 8 * dim), 5)
+    k = orc.randn((2, S, 2 * dim), 6)
+    dq, dk = be.array(q), be.array(k)
+    be.rope_qk(dq, 8 * dim, dk, 2 * dim, 2, S, dim, be.array(cs), be.array(sn), False)
+    assert_elementwise(dq.download(), orc.rope(q, dim, cs, sn, False), "rope_qk half q")
+    assert_elementwise(dk.download(), orc.rope(k, dim, cs, sn, False), "rope_qk half k")
+
+
+# ---------------------------------------------------------------- vs the compiled reference itself
+def test_against_compiled_reference(be, ref, orc):
+    """The same checks against oracle/_ref (the reference's tensor.cpp)."""
+    x = orc.randn((3, 7, 64), 1)
+    g = orc.randn((64,), 2, 1.0, 0.1)
+    b = orc.randn((64,), 3, 0.0, 0.1)
+    dy = be.empty((3, 7, 64))
+    be.layer_norm(be.array(x), dy, 21, 64, be.array(g), be.array(b), 1e-5)
+    assert_reduction(dy.download(), ref.layer_norm(x, g, b, 1e-5), "ref layer_norm")
+    be.rms_norm(be.array(x), dy, 21, 64, be.array(g), 1e-6)
+    assert_reduction(dy.download(), ref.rms_norm(x, g, 1e-6), "ref rms_norm")
+    img = orc.randn((2, 64, 5, 7), 4, 0.0, 2.0)
+    dyi = be.empty(img.shape)
+    be.group_norm(be.array(img), dyi, 2, 64, 35, 32, be.array(g), be.array(b), 1e-6, silu=True)
+    assert_reduction(dyi.download(), ref.group_norm(img, 32, g, b, 1e-6, silu=True), "ref group_norm+silu")
+    sm = orc.randn((9, 9), 5, 0.0, 3.0)
+    dsm = be.array(sm)
+    be.softmax_rows(dsm, 9, 9, 0.3, True)
+    assert_softmax(dsm.download(), ref.softmax_rows(sm, 0.3, True), "ref softmax causal")
+    u = orc.randn((1, 5, 24), 6)
+    dsw = be.empty((1, 5, 24))
+    be.swiglu(be.array(x.reshape(-1)[:120]), be.array(u), dsw, 120)
+    assert_elementwise(dsw.download().reshape(-1), ref.swiglu(x.reshape(-1)[:120], u.reshape(-1)), "ref swiglu")
+
+
+# ---------------------------------------------------------------- errors and memory
+def test_invalid_arguments_fail_cleanly(be):
+    d = be.empty((16,))
+    with pytest.raises(sdhip.SdhError) as e:
+        be.swiglu(d, d, d, 17)  # extent beyond the block
+    assert e.value.status == sdhip.SDH_ERR_INVALID
+    with pytest.raises(sdhip.SdhError) as e:
+        be.group_norm(d, d, 1, 6, 2, 4, d, d, 1e-6)  # C % groups != 0
+    assert e.value.status == sdhip.SDH_ERR_INVALID
+    host = np.zeros(16, np.float32)
+    with pytest.raises(sdhip.SdhError) as e:
+        be.silu(host.ctypes.data, 16)  # host pointer
+    assert e.value.status == sdhip.SDH_ERR_INVALID
+    with pytest.raises(sdhip.SdhError):
+        be.rope(d, 1, 2, 8, 3, d, d, True)  # odd dim
+    # nothing was launched: the block still holds what we put there
+    d.upload(np.arange(16, dtype=np.float32))
+    assert np.array_equal(d.download(), np.arange(16, dtype=np.float32))
+
+
+def test_zero_and_copy(be):
+    a = be.array(np.arange(1001, dtype=np.float32))
+    b = be.empty((1001,))
+    be.check(be.lib.sdh_copy(b.ptr, a.ptr, 1001 * 4))
+    assert np.array_equal(b.download(), np.arange(1001, dtype=np.float32))
+    be.check(be.lib.sdh_zero(b.ptr + 4, 999 * 4))
+    got = b.download()
+    assert got[0] == 0.0 and got[1000] == 1000.0 and not np.any(got[1:1000])
+
+
+def test_arena_reuse(be):
+    before = be.memory_stats()[1]
+    for _ in range(5):
+        d = be.empty((1 << 20,))
+        d.free()
+    assert be.memory_stats()[1] == before
