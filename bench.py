@@ -1,0 +1,542 @@
+#!/usr/bin/env python3
+"""Benchmark of backend_hip's elementwise / reduction / broadcast path on one
+MI355X, against the HBM roofline, with the reference's CPU path timed beside it.
+
+Metric: achieved HBM GB/s (% of peak) per op at Z-Image 1024^2
+shapes; speedup vs CPU. The headline line is the SwiGLU configuration
+(configs[1]: gate, up [4096, 10240] fp32); every other BASELINE config is
+measured too and reported in the same JSON line under "ops".
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+                  [--no-cpu] [--cpu-all] [--list]
+
+A step is one call of the op over one batch of synthetic input that is already
+resident in HBM. Inputs are rotated over the fewest buffer sets (at least
+two) that hold at least 512 MB of distinct data (2x the 256 MB Infinity
+Cache), so repeated steps read HBM, not cache. Larger rotations are not "more honest": measured on
+MI355X, streaming kernels lose ~15 points of HBM peak once the buffers touched
+between two uses of the same set exceed ~0.6-0.9 GB (GPU TLB reach), which is
+a property of the benchmark loop, not of the kernel. GB/s = algorithmic bytes (each input read once, each output written
+once) / time. Kernel time comes from HIP events recorded on the library's
+stream around the timed steps; ms_per_step from the host clock around the same
+steps (both bracketed by a device synchronize).
+
+The CPU baseline is the reference's own tensor.cpp (oracle/_ref, compiled from
+/root/reference) timed in this process on the host's cores; if it is absent,
+the C restatement (oracle/liboracle.so) is timed instead ("port").
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "stablediffusion-cpp_amd"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "achieved HBM GB/s (% of peak) per op at Z-Image 1024² shapes; speedup vs CPU"
+T, D, F = 4096, 3840, 10240
+MIN_ROTATION_BYTES = 512_000_000  # 2x the 256 MB Infinity Cache
+MAX_SETS = 32
+
+
+# ------------------------------------------------------------------ workloads
+class Workload:
+    """One BASELINE config: how to make a buffer set, run one step, and the
+    reference CPU composition of the same step."""
+
+    name = ""
+    desc = ""
+    kernel = ""  # substring of the dominant kernel's name (for rocprof)
+    algo_bytes = 0
+
+    def make(self, be, i):
+        raise NotImplementedError
+
+    def step(self, be, s):
+        raise NotImplementedError
+
+
+def _tables_3axis(S, side):
+    """Z-Image interleaved cos/sin [S, 128] for positions (0, h, w) (zimage.cpp:71-88)."""
+    pos = np.array([[0, h, w] for h in range(side) for w in range(side)], np.int64)[:S]
+    cs = np.empty((S, 128), np.float32)
+    sn = np.empty((S, 128), np.float32)
+    off = 0
+    for a, da in enumerate((32, 48, 48)):
+        freq = 1.0 / np.power(256.0, np.arange(da // 2) * 2.0 / da)
+        ang = (pos[:, a:a + 1].astype(np.float64) * freq).astype(np.float32)
+        c, s = np.cos(ang.astype(np.float64)).astype(np.float32), np.sin(ang.astype(np.float64)).astype(np.float32)
+        cs[:, off:off + da:2], cs[:, off + 1:off + da:2] = c, c
+        sn[:, off:off + da:2], sn[:, off + 1:off + da:2] = s, s
+        off += da
+    return cs, sn
+
+
+class AddRmsNorm(Workload):
+    name, kernel = "add_rms_norm", "k_add_rms"
+    desc = "config 1: x += r; y = rms_norm(x) * w; x, r [4096,3840], w [3840], eps 1e-6"
+    algo_bytes = 4 * T * D * 4 + D * 4
+
+    def make(self, be, i):
+        return dict(x=be.randn((T, D), 1000 + i), r=be.randn((T, D), 2000 + i), w=be.randn((D,), 3000 + i, 1.0, 0.1),
+                    y=be.empty((T, D)))
+
+    def step(self, be, s):
+        be.add_rms_norm(s["x"], s["r"], s["y"], T, D, s["w"], 1e-6)
+
+    def cpu(self, R, orc):
+        x, r = orc.randn((T, D), 1), orc.randn((T, D), 2)
+        w = orc.randn((D,), 3, 1.0, 0.1)
+        hx, hr, hw = R.new(x.shape, x), R.new(r.shape, r), R.new(w.shape, w)
+
+        def run():
+            R._chk(R.lib.ref_add_(hx, hr))
+            return [R._ptr(R.lib.ref_rms_norm(hx, hw, 1e-6))]
+
+        return run, [hx, hr, hw]
+
+
+class SwiGLU(Workload):
+    name, kernel = "swiglu", "k_swiglu"
+    desc = "config 2: y = silu(g) * u; g, u [4096,10240] ~N(0,1.5)"
+    algo_bytes = 3 * T * F * 4
+
+    def make(self, be, i):
+        return dict(g=be.randn((T, F), 4000 + i, 0.0, 1.5), u=be.randn((T, F), 5000 + i, 0.0, 1.5), y=be.empty((T, F)))
+
+    def step(self, be, s):
+        be.swiglu(s["g"], s["u"], s["y"], T * F)
+
+    def cpu(self, R, orc):
+        g, u = orc.randn((T, F), 4, 0.0, 1.5), orc.randn((T, F), 5, 0.0, 1.5)
+        hg, hu = R.new(g.shape, g), R.new(u.shape, u)
+        return (lambda: [R._ptr(R.lib.ref_swiglu(hg, hu))]), [hg, hu]
+
+
+class RopeQK(Workload):
+    name, kernel = "rope_qk", "k_rope_interleaved"
+    desc = ("config 3: 3-axis interleaved RoPE in place on q and k [4096,30*128] in one launch, axes (32,48,48), "
+            "theta 256, reference-format duplicated cos/sin tables [4096,128]")
+    algo_bytes = 4 * T * D * 4 + 2 * T * 128 * 4
+
+    def __init__(self):
+        self.cs, self.sn = _tables_3axis(T, 64)
+
+    def make(self, be, i):
+        return dict(q=be.randn((T, D), 6000 + i), k=be.randn((T, D), 7000 + i), c=be.array(self.cs), s=be.array(self.sn))
+
+    def step(self, be, s):
+        be.rope_qk(s["q"], D, s["k"], D, 1, T, 128, s["c"], s["s"], True)
+
+    def cpu(self, R, orc):
+        q, k = orc.randn((1, T, D), 6), orc.randn((1, T, D), 7)
+        hq, hk = R.new(q.shape, q), R.new(k.shape, k)
+        hc, hs = R.new(self.cs.shape, self.cs), R.new(self.sn.shape, self.sn)
+
+        def run():
+            R._chk(R.lib.ref_rope_(hq, 128, hc, hs, 1))
+            R._chk(R.lib.ref_rope_(hk, 128, hc, hs, 1))
+            return []
+
+        return run, [hq, hk, hc, hs]
+
+
+class GNSiLU(Workload):
+    kernel = "k_gn_"
+
+    def __init__(self, tag, shape, eps, note):
+        self.shape, self.eps = shape, eps
+        self.name = f"group_norm_silu_{tag}"
+        self.desc = f"config {note}: y = silu(group_norm(x, 32 groups, eps {eps:g})), x {list(shape)} ~N(0,2)"
+        n = int(np.prod(shape))
+        self.algo_bytes = 2 * n * 4 + 2 * shape[1] * 4
+
+    def make(self, be, i):
+        Cc = self.shape[1]
+        return dict(x=be.randn(self.shape, 8000 + i, 0.0, 2.0), y=be.empty(self.shape),
+                    g=be.randn((Cc,), 9000 + i, 1.0, 0.1), b=be.randn((Cc,), 9500 + i, 0.0, 0.1))
+
+    def step(self, be, s):
+        N, Cc = self.shape[0], self.shape[1]
+        HW = int(np.prod(self.shape[2:]))
+        be.group_norm(s["x"], s["y"], N, Cc, HW, 32, s["g"], s["b"], self.eps, silu=True)
+
+    def cpu(self, R, orc):
+        x = orc.randn(self.shape, 8, 0.0, 2.0)
+        Cc = self.shape[1]
+        g, b = orc.randn((Cc,), 9, 1.0, 0.1), orc.randn((Cc,), 10, 0.0, 0.1)
+        hx, hg, hb = R.new(x.shape, x), R.new(g.shape, g), R.new(b.shape, b)
+
+        def run():
+            h = R._ptr(R.lib.ref_group_norm(hx, 32, hg, hb, self.eps))
+            R._chk(R.lib.ref_silu_(h))
+            return [h]
+
+        return run, [hx, hg, hb]
+
+
+class LNModGate(Workload):
+    name, kernel = "ln_modulate_gate", "k_ln_mod_gate"
+    desc = ("config 5a: y = layer_norm(x)*(1+scale)+shift; res += tanh(gate)*y (y not stored); x, res [4096,3840]; "
+            "scale, shift, gate [3840] ~N(0,0.2); eps 1e-6")
+    algo_bytes = 3 * T * D * 4 + 3 * D * 4
+
+    def make(self, be, i):
+        return dict(x=be.randn((T, D), 10000 + i), res=be.randn((T, D), 11000 + i),
+                    sc=be.randn((D,), 12000 + i, 0.0, 0.2), sh=be.randn((D,), 13000 + i, 0.0, 0.2),
+                    gt=be.randn((D,), 14000 + i, 0.0, 0.2))
+
+    def step(self, be, s):
+        be.ln_modulate_gate(s["x"], s["res"], s["sc"], s["sh"], s["gt"], None, T, D, 1e-6)
+
+    def cpu(self, R, orc):
+        x, res = orc.randn((T, D), 10), orc.randn((T, D), 11)
+        sc, sh, gt = (orc.randn((D,), 12 + i, 0.0, 0.2) for i in range(3))
+        hx, hr = R.new(x.shape, x), R.new(res.shape, res)
+        hsc, hsh, hgt = R.new((D,), sc), R.new((D,), sh), R.new((D,), gt)
+        hones = R.new((T, D), np.ones((T, D), np.float32))
+
+        def run():
+            y = R._ptr(R.lib.ref_layer_norm(hx, None, None, 1e-6))
+            R._chk(R.lib.ref_affine_(hsc, 1.0, 1.0))
+            R._chk(R.lib.ref_tanh_(hgt))
+            R._chk(R.lib.ref_mul_rows_(y, hsc))
+            R._chk(R.lib.ref_add_rows_scaled_(y, hones, hsh))
+            R._chk(R.lib.ref_add_rows_scaled_(hr, y, hgt))
+            return [y]
+
+        return run, [hx, hr, hsc, hsh, hgt, hones]
+
+
+class Softmax(Workload):
+    name, kernel = "softmax_rows", "k_softmax"
+    desc = "config 5b: in-place row softmax of scores [30,4096,4096] ~N(0,3), scale 1/sqrt(128), non-causal"
+    algo_bytes = 2 * 30 * T * T * 4
+
+    def make(self, be, i):
+        return dict(x=be.randn((30 * T, T), 15000 + i, 0.0, 3.0))
+
+    def step(self, be, s):
+        be.softmax_rows(s["x"], 30 * T, T, 1.0 / math.sqrt(128.0), False)
+
+    def cpu(self, R, orc):
+        x = orc.randn((30 * T, T), 15, 0.0, 3.0)
+        hx = R.new(x.shape, x)
+        del x
+
+        def run():
+            R._chk(R.lib.ref_softmax_rows_(hx, 30 * T, T, 1.0 / math.sqrt(128.0), 0))
+            return []
+
+        return run, [hx]
+
+
+class CopyCalibration(Workload):
+    """Not a BASELINE config: an in-place x *= 1 stream over [4096,10240]
+    (one read + one write of 168 MB), the plain-copy reference for what HBM
+    streaming reaches on this box and the calibration for the traffic counters."""
+
+    name, kernel = "copy_calibration", "k_unary"
+    desc = "calibration (not a config): in-place x *= 1.0 over [4096,10240] fp32, 1 read + 1 write"
+    algo_bytes = 2 * T * F * 4
+
+    def make(self, be, i):
+        return dict(x=be.randn((T, F), 16000 + i))
+
+    def step(self, be, s):
+        be.scale(s["x"], 1.0, T * F)
+
+
+def all_workloads():
+    return [
+        CopyCalibration(),
+        AddRmsNorm(),
+        SwiGLU(),
+        RopeQK(),
+        GNSiLU("4a", (1, 512, 128, 128), 1e-6, "4a (FLUX VAE)"),
+        GNSiLU("4b", (1, 128, 1024, 1024), 1e-6, "4b (FLUX VAE norm_out)"),
+        GNSiLU("4c", (2, 320, 64, 64), 1e-5, "4c (SD 1.5, reported only)"),
+        GNSiLU("4d", (2, 1280, 8, 8), 1e-5, "4d (SD 1.5, reported only)"),
+        LNModGate(),
+        Softmax(),
+    ]
+
+
+# ------------------------------------------------------------------ GPU timing
+def measure_gpu(be, w, steps, warmup):
+    first = w.make(be, 0)
+    footprint = sum(a.nbytes for a in first.values())
+    nsets = max(2, min(MAX_SETS, math.ceil(MIN_ROTATION_BYTES / max(footprint, 1))))
+    sets = [first] + [w.make(be, i) for i in range(1, nsets)]
+    be.synchronize()
+    for i in range(warmup):
+        w.step(be, sets[i % nsets])
+    be.synchronize()
+    t0 = time.perf_counter()
+    be.timer_record(0)
+    for i in range(steps):
+        w.step(be, sets[i % nsets])
+    be.timer_record(1)
+    be.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = be.timer_elapsed(0, 1)
+    for s in sets:
+        for a in s.values():
+            a.free()
+    return dict(nsets=nsets, footprint=footprint * nsets, wall_ms=wall * 1e3 / steps, event_ms=ev_ms / steps)
+
+
+# ------------------------------------------------------------------ CPU baseline
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except Exception:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def measure_cpu(w, reps):
+    """Times the reference's CPU composition of one step (median of reps)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle import Oracle, Reference, have_reference
+
+    if not hasattr(w, "cpu"):
+        return None
+    orc = Oracle()
+    threads = cpu_threads()
+    orc.set_threads(threads)
+    if not have_reference():
+        return measure_cpu_port(w, orc, reps, threads)
+    R = Reference()
+    R.lib.ref_set_threads(threads)
+    run, handles = w.cpu(R, orc)
+    times = []
+    for i in range(reps + 1):
+        t0 = time.perf_counter()
+        outs = run()
+        dt = time.perf_counter() - t0
+        R.free(*outs)
+        if i:
+            times.append(dt)
+    R.free(*handles)
+    return dict(ms=statistics.median(times) * 1e3, reps=reps, threads=threads, kind="reference")
+
+
+def measure_cpu_port(w, orc, reps, threads):
+    """Fallback when oracle/_ref is absent: the C restatement of the same
+    step (SwiGLU only; other configs report no CPU time then)."""
+    if not isinstance(w, SwiGLU):
+        return None
+    g, u = orc.randn((T, F), 4, 0.0, 1.5), orc.randn((T, F), 5, 0.0, 1.5)
+    times = []
+    for i in range(reps + 1):
+        t0 = time.perf_counter()
+        orc.swiglu(g, u)
+        if i:
+            times.append(time.perf_counter() - t0)
+    return dict(ms=statistics.median(times) * 1e3, reps=reps, threads=threads, kind="port")
+
+
+# ------------------------------------------------------------------ traffic (rocprof pmc)
+def read_traffic(name):
+    """HBM bytes per launch from profiles/hbm_traffic.txt (rocprofv3 --pmc
+    FETCH_SIZE and WRITE_SIZE runs, scaled by the plain-copy calibration)."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        m = re.match(r"^\s*" + re.escape(name) + r"\s+.*traffic_bytes=(\d+)", line)
+        if m:
+            return int(m.group(1))
+    return None
+
+
+# ------------------------------------------------------------------ rocprofv3 summaries
+KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
+    "k_unary<4>": "copy_calibration", "k_add_rms": "add_rms_norm", "k_swiglu": "swiglu",
+    "k_rope_interleaved": "rope_qk", "k_ln_mod_gate": "ln_modulate_gate", "k_softmax_block": "softmax_rows",
+}
+
+
+def _kernel_key(full_name):
+    m = re.search(r"(k_\w+)(<[^>]*>)?\(", full_name)
+    return (m.group(1) + (m.group(2) or "")) if m else full_name
+
+
+def rocprof_summary(trace_dir, fetch_dir=None, write_dir=None):
+    """Markdown summary of a `rocprofv3 --kernel-trace --stats --output-format
+    csv` run of this script (and, optionally, of its --pmc FETCH_SIZE and
+    WRITE_SIZE runs). Traffic is calibrated against the in-place copy kernel
+    (copy_calibration: known 1 read + 1 write of [4096,10240] fp32)."""
+    import collections
+    import csv
+    import glob
+
+    def rows_of(d, suffix):
+        files = glob.glob(os.path.join(d, "*" + suffix))
+        return list(csv.DictReader(open(files[0]))) if files else []
+
+    trace = rows_of(trace_dir, "_kernel_trace.csv")
+    dur = collections.defaultdict(list)
+    for r in trace:
+        k = (_kernel_key(r["Kernel_Name"]), int(r["Grid_Size_X"]) * int(r.get("Grid_Size_Y", 1) or 1))
+        dur[k].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    out = ["| kernel | grid (work-items) | dispatches | avg us | median us | min us |", "|---|---|---|---|---|---|"]
+    for (k, g), v in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
+        if k.startswith("k_fill_normal") or k.startswith("k_zero"):
+            continue
+        v = sorted(v)
+        out.append(f"| `{k}` | {g} | {len(v)} | {statistics.mean(v):.2f} | {v[len(v) // 2]:.2f} | {v[0]:.2f} |")
+    text = "\n".join(out) + "\n"
+    traffic_lines = []
+    if fetch_dir and write_dir:
+        def counters(d):
+            agg = collections.defaultdict(list)
+            for r in rows_of(d, "_counter_collection.csv"):
+                k = (_kernel_key(r["Kernel_Name"]), int(r["Grid_Size"]))
+                agg[k].append(float(r["Counter_Value"]))
+            return {k: statistics.median(v) for k, v in agg.items()}
+
+        f, w = counters(fetch_dir), counters(write_dir)
+        cal = [k for k in f if k[0] == "k_unary<4>" and k[1] == T * F // 4]
+        copy_kib = T * F * 4 / 1024.0
+        ff = copy_kib / f[cal[0]] if cal else 1.0
+        wf = copy_kib / w[cal[0]] if cal else 1.0
+        text += (f"\nCalibration (in-place copy, {copy_kib:.0f} KiB read + {copy_kib:.0f} KiB written): "
+                 f"FETCH_SIZE factor {ff:.3f}, WRITE_SIZE factor {wf:.3f}.\n\n")
+        text += "| kernel | grid | FETCH_SIZE KiB | WRITE_SIZE KiB | calibrated HBM bytes per dispatch |\n|---|---|---|---|---|\n"
+        for k in sorted(f, key=lambda k: -f[k]):
+            if k[0].startswith("k_fill_normal") or k[0].startswith("k_zero"):
+                continue
+            tb = int(round((f[k] * ff + w.get(k, 0.0) * wf) * 1024))
+            text += f"| `{k[0]}` | {k[1]} | {f[k]:.0f} | {w.get(k, 0.0):.0f} | {tb:,} |\n"
+            wl = next((v for kk, v in KERNEL_OF.items() if k[0].startswith(kk)), None)
+            if wl:
+                traffic_lines.append(f"{wl} kernel={k[0]} grid={k[1]} fetch_kib={f[k]:.1f} write_kib={w.get(k, 0.0):.1f} "
+                                     f"fetch_factor={ff:.4f} write_factor={wf:.4f} traffic_bytes={tb}")
+    return text, traffic_lines
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="swiglu", help="headline workload (default: swiglu = configs[1])")
+    ap.add_argument("--only", default=None, help="comma list: measure only these workloads (profiling runs)")
+    ap.add_argument("--op-steps", type=int, default=20, help="timed steps per op in the per-op table")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-all", action="store_true", help="time the reference CPU path for every config")
+    ap.add_argument("--cpu-reps", type=int, default=5)
+    ap.add_argument("--list", action="store_true")
+    ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR",
+                    help="print a markdown summary of rocprofv3 csv output: TRACE_DIR [FETCH_DIR WRITE_DIR]")
+    args = ap.parse_args()
+
+    if args.rocprof_summary:
+        d = args.rocprof_summary
+        text, lines = rocprof_summary(d[0], d[1] if len(d) > 2 else None, d[2] if len(d) > 2 else None)
+        print(text)
+        if lines:
+            print("traffic lines (profiles/hbm_traffic.txt format):")
+            print("\n".join(lines))
+        return 0
+
+    wls = {w.name: w for w in all_workloads()}
+    if args.list:
+        for w in wls.values():
+            print(f"{w.name:24s} {w.algo_bytes:>14,d} B  {w.desc}")
+        return 0
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU only: every op shards by rows with no exchange "
+                                   "(see DESIGN.md); run with --gpus 1"}), flush=True)
+        return 2
+    if args.workload not in wls:
+        print(f"unknown workload {args.workload}; --list shows them", file=sys.stderr)
+        return 2
+
+    import sdhip
+
+    be = sdhip.Backend()
+    head = wls[args.workload]
+    names = [n.strip() for n in args.only.split(",")] if args.only else list(wls)
+
+    ops = []
+    head_res = None
+    for n in names:
+        w = wls[n]
+        steps = args.steps if w is head else args.op_steps
+        warm = args.warmup if w is head else 3
+        r = measure_gpu(be, w, steps, warm)
+        gbs = w.algo_bytes / (r["event_ms"] * 1e-3) / 1e9
+        entry = dict(op=w.name, desc=w.desc, algo_bytes=w.algo_bytes, us_per_op=round(r["event_ms"] * 1e3, 2),
+                     GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1), rotation_sets=r["nsets"],
+                     rotation_MB=round(r["footprint"] / 2**20))
+        if args.cpu_all and not args.no_cpu:
+            c = measure_cpu(w, 3 if w.algo_bytes > (1 << 30) else args.cpu_reps)
+            if c:
+                entry.update(cpu_ms=round(c["ms"], 3), cpu_threads=c["threads"],
+                             speedup_vs_cpu=round(c["ms"] / (r["event_ms"]), 1))
+        ops.append(entry)
+        print(f"# {w.name:22s} {entry['us_per_op']:10.2f} us  {entry['GBps']:8.1f} GB/s  "
+              f"{entry['pct_hbm_peak']:5.1f}% of 8 TB/s" + (f"  cpu {entry['cpu_ms']:.2f} ms" if 'cpu_ms' in entry else ""),
+              file=sys.stderr, flush=True)
+        if w is head:
+            head_res = r
+
+    if head_res is None:
+        print(json.dumps({"ops": ops}), flush=True)
+        return 0
+
+    achieved = head.algo_bytes / (head_res["event_ms"] * 1e-3) / 1e9
+    traffic = read_traffic(head.name)
+    cpu = None
+    if not args.no_cpu:
+        c = measure_cpu(head, args.cpu_reps)
+        if c:
+            cpu = dict(value=round(head.algo_bytes / (c["ms"] * 1e-3) / 1e9, 2), unit="GB/s", cores=c["threads"],
+                       kind=c["kind"],
+                       sample=f"the full {head.name} step at the config shape through "
+                              + ("the reference's tensor.cpp (compiled from /root/reference)" if c["kind"] == "reference"
+                                 else "the C restatement of tensor.cpp")
+                              + f", output allocation included, median of {c['reps']} runs after 1 warm-up: "
+                              f"{c['ms']:.2f} ms per step",
+                       ms_per_step=round(c["ms"], 3))
+    value = head.algo_bytes / (head_res["wall_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head_res["wall_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(mu,sigma) fp32 inputs generated on the device, resident in HBM)",
+        "config": {"workload": head.desc, "algorithmic_bytes": head.algo_bytes,
+                   "rotation_sets": head_res["nsets"], "rotation_MB": round(head_res["footprint"] / 2**20)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": head.kernel, "kernel_us": round(head_res["event_ms"] * 1e3, 3)},
+        "cpu_baseline": cpu,
+        "speedup_vs_cpu": round(cpu["ms_per_step"] / head_res["wall_ms"], 1) if cpu else None,
+        "ops": ops,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

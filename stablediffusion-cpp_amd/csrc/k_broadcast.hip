@@ -5,11 +5,10 @@
 //                                             backend_cuda.cu:239-241)
 //   add_channel_bias x[n, c, :] += b[n, c]   (tensor.cpp:919-929)
 // HBM-bound. When the row length is a multiple of 4 and the pointers are
-// 16-byte aligned, a thread handles 128-bit vectors of one column group and
-// walks several rows with the column vector held in registers, so the
-// broadcast operand costs one load per thread instead of one per element
-// and no per-element 64-bit division is needed (the reference's kernels
-// compute i % dim for every element, backend_cuda.cu:394-402).
+// 16-byte aligned, each thread handles one 128-bit vector, the grid covers
+// the tensor exactly, and the broadcast operand (a [dim] vector, resident in
+// L2) is indexed with a 32-bit column computed once per vector instead of a
+// 64-bit i % dim per element (backend_cuda.cu:394-402).
 #include "sdh_internal.hpp"
 
 namespace sdh {
@@ -21,26 +20,19 @@ constexpr int kThreads = 256;
 
 enum BKind { B_MUL, B_ADD_SCALED, B_ADD };
 
-// 2D mapping: blockIdx.x covers 256 float4 columns, blockIdx.y covers
-// `rows_per_block` rows.
 template <int K>
 __global__ __launch_bounds__(kThreads) void k_rows_vec(f4* __restrict__ x, const f4* __restrict__ y,
-                                                      const f4* __restrict__ v, int64_t rows, int dim4,
-                                                      int rows_per_block) {
-    const int c = blockIdx.x * kThreads + threadIdx.x;
-    if (c >= dim4) return;
+                                                      const f4* __restrict__ v, int64_t n4, unsigned dim4) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n4) return;
+    const unsigned c = n4 <= 0xffffffffLL ? (unsigned)i % dim4 : (unsigned)(i % dim4);
     const f4 vv = v[c];
-    const int64_t r0 = (int64_t)blockIdx.y * rows_per_block;
-    const int64_t r1 = r0 + rows_per_block < rows ? r0 + rows_per_block : rows;
-    for (int64_t r = r0; r < r1; ++r) {
-        f4* p = x + r * dim4 + c;
-        const f4 xv = dev::ld_stream(p);
-        f4 o;
-        if constexpr (K == B_MUL) o = xv * vv;
-        if constexpr (K == B_ADD_SCALED) o = xv + vv * dev::ld_stream(y + r * dim4 + c);
-        if constexpr (K == B_ADD) o = xv + vv;
-        dev::st_stream(p, o);
-    }
+    const f4 xv = x[i];
+    f4 o;
+    if constexpr (K == B_MUL) o = xv * vv;
+    if constexpr (K == B_ADD_SCALED) o = xv + vv * y[i];
+    if constexpr (K == B_ADD) o = xv + vv;
+    dev::st_stream(x + i, o);
 }
 
 template <int K>
@@ -84,19 +76,12 @@ void run_rows(const char* op, float* x, const float* y, const float* v, int64_t 
     check_range(x, (size_t)(rows * dim) * 4, op, "x");
     if (K == B_ADD_SCALED) check_range(y, (size_t)(rows * dim) * 4, op, "y");
     check_range(v, (size_t)dim * 4, op, K == B_ADD_SCALED ? "g" : "v");
-    const bool vec = dim % 4 == 0 && dim / 4 <= 0x7fffffff && aligned16(x) && aligned16(v) &&
+    const bool vec = dim % 4 == 0 && rows * dim / 4 <= 0x7fffffffLL * kThreads && aligned16(x) && aligned16(v) &&
                      (K != B_ADD_SCALED || aligned16(y));
     if (vec) {
-        const int dim4 = (int)(dim / 4);
-        const unsigned gx = blocks_for(dim4, kThreads);
-        // 8 rows per block keeps enough blocks to fill the chip while each
-        // thread reuses its column vector; grid.y stays within 65535
-        const int64_t rpb64 = std::max<int64_t>(8, (rows + 65534) / 65535);
-        need(rpb64 <= 0x7fffffffLL, op, "too many rows");
-        const int rpb = (int)rpb64;
-        const int64_t gy = (rows + rpb - 1) / rpb;
-        k_rows_vec<K><<<dim3(gx, (unsigned)gy), kThreads, 0, stream()>>>((f4*)x, (const f4*)y, (const f4*)v, rows,
-                                                                          dim4, rpb);
+        const int64_t n4 = rows * dim / 4;
+        k_rows_vec<K><<<blocks_for(n4, kThreads), kThreads, 0, stream()>>>((f4*)x, (const f4*)y, (const f4*)v, n4,
+                                                                            (unsigned)(dim / 4));
     } else {
         k_rows_scalar<K><<<stride_grid(rows * dim), kThreads, 0, stream()>>>(x, y, v, rows, dim);
     }

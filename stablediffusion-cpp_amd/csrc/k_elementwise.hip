@@ -2,9 +2,11 @@
 // quick_gelu, add, scale, affine, geglu, the device zero fill and the seeded
 // normal generator.
 //
-// Roofline: HBM-bound (well under 1 flop per byte). Each lane moves 128-bit
-// vectors, UNROLL of them per launch slot, with the slots of one instruction
-// contiguous across the wave (1 KiB per wave per instruction). Arithmetic
+// Roofline: HBM-bound (well under 1 flop per byte). Each thread moves one
+// 128-bit vector per operand and the grid covers the tensor exactly (no
+// persistent loop): on MI355X many small workgroups with non-temporal loads
+// and stores stream best (measured: a plain copy reaches ~81% of the 8 TB/s
+// peak this way, against ~74% with four vectors per thread). Arithmetic
 // follows the reference's expression order (tensor.cpp:745, :847, :852,
 // :859, :866, :876, :881, :886, :830) with ROCm's device libm (expf, tanhf,
 // erff).
@@ -16,7 +18,7 @@ namespace {
 using dev::f4;
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 1;
 constexpr int64_t kPerBlock = (int64_t)kThreads * kUnroll;  // float4 per block
 
 enum UnaryKind { U_SILU, U_TANH, U_GELU, U_QGELU, U_SCALE, U_AFFINE };
@@ -135,6 +137,18 @@ __global__ __launch_bounds__(kThreads) void k_geglu(const float* __restrict__ x,
     }
 }
 
+// Vectorised GEGLU for D % 4 == 0: one float4 of the output per thread.
+__global__ __launch_bounds__(kThreads) void k_geglu_vec(const f4* __restrict__ x, f4* __restrict__ y, int64_t n4,
+                                                       int64_t D4) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n4) return;
+    const int64_t r = i / D4, c = i - r * D4;
+    const f4 a = dev::ld_stream(x + r * 2 * D4 + c);
+    const f4 g = dev::ld_stream(x + r * 2 * D4 + D4 + c);
+    auto one = [](float av, float gg) { return av * 0.5f * gg * (1.0f + erff(gg * 0.70710678118654752f)); };
+    dev::st_stream(y + i, f4{one(a.x, g.x), one(a.y, g.y), one(a.z, g.z), one(a.w, g.w)});
+}
+
 // Zero fill (used instead of hipMemsetAsync so the library queues no memset
 // nodes into a stream a caller might capture into a graph).
 __global__ __launch_bounds__(kThreads) void k_zero(f4* __restrict__ p, int64_t n4) {
@@ -240,7 +254,12 @@ int sdh_geglu(const float* x, float* y, int64_t rows, int64_t D) {
         ensure_init();
         check_range(x, (size_t)(rows * 2 * D) * 4, op, "x");
         check_range(y, (size_t)(rows * D) * 4, op, "y");
-        k_geglu<<<stride_grid(rows * D), kThreads, 0, stream()>>>(x, y, rows, D);
+        if (D % 4 == 0 && aligned16(x) && aligned16(y)) {
+            const int64_t n4 = rows * D / 4;
+            k_geglu_vec<<<blocks_for(n4, kThreads), kThreads, 0, stream()>>>((const f4*)x, (f4*)y, n4, D / 4);
+        } else {
+            k_geglu<<<stride_grid(rows * D), kThreads, 0, stream()>>>(x, y, rows, D);
+        }
         launched(op);
     });
 }

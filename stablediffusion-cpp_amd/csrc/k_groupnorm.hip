@@ -8,21 +8,30 @@
 // a = rstd * gamma[c], then SiLU as x / (1 + exp(-x)).
 //
 // Two schedules:
-//   * single: one workgroup per segment when the segment fits in the
-//     workgroup's registers (<= 256 threads x 16 float4). One HBM read, one
-//     write. Used by the SD 1.5 mid-block shapes.
+//   * single: one workgroup (256 or 1024 threads) per segment when the
+//     segment fits in its registers (<= 65536 floats). One HBM read, one
+//     write. Used by the SD 1.5 shapes.
 //   * split: the segment is cut into chunks of kChunk floats.
 //       pass A (k_gn_partial): one workgroup per chunk computes the chunk's
 //         sum and its M2 around the chunk mean from registers and stores the
-//         pair; it then bumps the segment's arrival counter, and the last
-//         arriving workgroup merges all chunk pairs in double
-//         (M2 = sum M2_i + n_i (mean_i - mean)^2, the exact pairwise identity),
-//         writes (mean, rstd) and re-arms the counter to zero. No workgroup
-//         ever waits for another.
-//       pass B (k_gn_apply): one workgroup per chunk applies the affine (and
-//         SiLU), walking the chunks in the reverse of pass A's order so that
-//         its first reads find the most recently read data still in the
-//         last-level (Infinity) cache.
+//         pair. No atomics: cross-workgroup publication through device-scope
+//         release/acquire would write back and invalidate the per-XCD L2s
+//         from every workgroup; the kernel boundary publishes instead.
+//       finalize (k_gn_finalize): one workgroup per segment merges the
+//         segment's chunk pairs in double in a fixed order (M2 = sum M2_i +
+//         n_i (mean_i - mean)^2, the exact pairwise identity) into
+//         (mean, rstd). A separate tiny launch measured faster than merging
+//         inside every pass-B workgroup, which puts a dependent L2 round trip
+//         and two reductions in front of each workgroup's stores.
+//       pass B (k_gn_apply): one workgroup per chunk, with the same
+//         workgroup -> chunk mapping as pass A, so each chunk is re-read on
+//         the XCD whose L2 read it in pass A (tensors up to the 32 MB of
+//         total L2 are mostly re-read from cache); it applies the affine (and
+//         SiLU).
+//     Measured on MI355X the Infinity Cache does not keep streamed reads
+//     (re-reading 64-512 MB is no faster than the first read), so for
+//     tensors much larger than L2 this schedule moves three streams (x, x,
+//     y) against the two of the algorithmic minimum.
 #include "sdh_internal.hpp"
 
 namespace sdh {
@@ -34,23 +43,11 @@ constexpr int kThreads = 256;
 constexpr int kChunkV = 8;                               // float4 per thread per chunk
 constexpr int64_t kChunk = (int64_t)kThreads * 4 * kChunkV;  // floats per chunk (8192)
 
-struct SegStat {
-    double mean;
-    float rstd;
-    float pad;
-};
-
-// Block-wide sum of 4 waves: wave DPP reduction, then 4 partials via LDS.
-__device__ __forceinline__ float block_sum4(float v, float* sh) {
-    v = dev::wave_sum(v);
-    const int w = threadIdx.x >> 6;
-    __syncthreads();  // sh may still be read from a previous call
-    if ((threadIdx.x & 63) == 0) sh[w] = v;
-    __syncthreads();
-    return (sh[0] + sh[1]) + (sh[2] + sh[3]);
-}
-
-__device__ __forceinline__ float silu1(float v) { return v / (1.0f + expf(-v)); }
+// SiLU on the hardware exp2 and reciprocal: x * rcp(1 + 2^(-x log2 e)). Its
+// error against the correctly rounded x / (1 + expf(-x)) is a few ulp (the
+// exp argument's rounding contributes |x| 2^-24 relatively, v_exp_f32 and
+// v_rcp_f32 1 ulp each), far inside the 1e-4 relative bound of this op.
+__device__ __forceinline__ float silu1(float v) { return dev::silu_fast(v); }
 
 template <bool SILU>
 __device__ __forceinline__ f4 apply4(f4 v, float a, float b) {
@@ -60,11 +57,24 @@ __device__ __forceinline__ f4 apply4(f4 v, float a, float b) {
 }
 
 // ---- single-workgroup schedule ---------------------------------------------
-template <int V, bool SILU>
-__global__ __launch_bounds__(kThreads) void k_gn_single(const float* __restrict__ x, float* __restrict__ y, int C,
-                                                       int HW, int groups, const float* __restrict__ gamma,
-                                                       const float* __restrict__ beta, float eps) {
-    __shared__ float sh[4];
+template <int TPB>
+__device__ __forceinline__ float block_sum(float v, float* sh) {
+    constexpr int W = TPB / 64;
+    v = dev::wave_sum(v);
+    __syncthreads();  // sh may still be read by the previous reduction
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = sh[0];
+#pragma unroll
+    for (int k = 1; k < W; ++k) t += sh[k];
+    return t;
+}
+
+template <int TPB, int V, bool SILU>
+__global__ __launch_bounds__(TPB) void k_gn_single(const float* __restrict__ x, float* __restrict__ y, int C, int HW,
+                                                  int groups, const float* __restrict__ gamma,
+                                                  const float* __restrict__ beta, float eps) {
+    __shared__ float sh[TPB / 64];
     const int64_t seg = blockIdx.x;
     const int n = (int)(seg / groups), g = (int)(seg % groups);
     const int cg = C / groups;
@@ -75,26 +85,26 @@ __global__ __launch_bounds__(kThreads) void k_gn_single(const float* __restrict_
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-        const int idx = threadIdx.x + kThreads * j;
+        const int idx = threadIdx.x + TPB * j;
         v[j] = idx < n4 ? dev::ld_stream(p + idx) : f4{0.f, 0.f, 0.f, 0.f};
         s += dev::hsum(v[j]);
     }
-    const double mean = (double)block_sum4(s, sh) / (double)L;
+    const double mean = (double)block_sum<TPB>(s, sh) / (double)L;
     const float meanf = (float)mean;
     float m2 = 0.f;
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-        const int idx = threadIdx.x + kThreads * j;
+        const int idx = threadIdx.x + TPB * j;
         if (idx < n4) {
             const f4 d = v[j] - meanf;
             m2 += dev::hsum(d * d);
         }
     }
-    const double var = (double)block_sum4(m2, sh);
+    const double var = (double)block_sum<TPB>(m2, sh);
     const float rstd = (float)(1.0 / sqrt(var / (double)L + (double)eps));
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-        const int idx = threadIdx.x + kThreads * j;
+        const int idx = threadIdx.x + TPB * j;
         if (idx < n4) {
             const int ch = g * cg + (idx * 4) / HW;
             const float a = rstd * gamma[ch];
@@ -105,12 +115,11 @@ __global__ __launch_bounds__(kThreads) void k_gn_single(const float* __restrict_
 }
 
 // ---- split schedule -----------------------------------------------------------
-// grid = (chunks per segment, segments)
+// Pass A. grid = (chunks per segment, segments). Ordinary (cache-allocating)
+// loads, so pass B can re-read from L2.
 __global__ __launch_bounds__(kThreads) void k_gn_partial(const float* __restrict__ x, int64_t L, int64_t nchunks,
-                                                        float2* __restrict__ part, SegStat* __restrict__ stats,
-                                                        unsigned* __restrict__ counter, float eps) {
-    __shared__ float sh[4];
-    __shared__ unsigned last;
+                                                        float2* __restrict__ part) {
+    __shared__ float sh[kThreads / 64];
     const int64_t seg = blockIdx.y, chunk = blockIdx.x;
     const int64_t off = chunk * kChunk;
     const int64_t cnt = L - off < kChunk ? L - off : kChunk;
@@ -121,10 +130,10 @@ __global__ __launch_bounds__(kThreads) void k_gn_partial(const float* __restrict
 #pragma unroll
     for (int j = 0; j < kChunkV; ++j) {
         const int idx = threadIdx.x + kThreads * j;
-        v[j] = idx < n4 ? dev::ld_stream(p + idx) : f4{0.f, 0.f, 0.f, 0.f};
+        v[j] = idx < n4 ? p[idx] : f4{0.f, 0.f, 0.f, 0.f};
         s += dev::hsum(v[j]);
     }
-    const float sum = block_sum4(s, sh);
+    const float sum = block_sum<kThreads>(s, sh);
     const float mc = sum / (float)cnt;
     float m2 = 0.f;
 #pragma unroll
@@ -135,20 +144,16 @@ __global__ __launch_bounds__(kThreads) void k_gn_partial(const float* __restrict
             m2 += dev::hsum(d * d);
         }
     }
-    const float M2 = block_sum4(m2, sh);
-    if (threadIdx.x == 0) {
-        part[seg * nchunks + chunk] = make_float2(sum, M2);
-        // release our partial, then count ourselves in
-        const unsigned prev =
-            __hip_atomic_fetch_add(counter + seg, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last = (prev == (unsigned)(nchunks - 1)) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!last) return;
-    // Last arrival for this segment: merge the chunk pairs in double, in
-    // chunk order (deterministic whichever workgroup arrives last).
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const float M2 = block_sum<kThreads>(m2, sh);
+    if (threadIdx.x == 0) part[seg * nchunks + chunk] = make_float2(sum, M2);
+}
+
+// Merge of one segment's chunk pairs in double, in chunk order (fixed tree):
+// M2 = sum_i M2_i + n_i (mean_i - mean)^2. grid = segments.
+__global__ __launch_bounds__(kThreads) void k_gn_finalize(const float2* __restrict__ part, int64_t L, int64_t nchunks,
+                                                         float2* __restrict__ stats, float eps) {
     __shared__ double dsh[kThreads];
+    const int64_t seg = blockIdx.x;
     const float2* pp = part + seg * nchunks;
     double tot = 0.0;
     for (int64_t i = threadIdx.x; i < nchunks; i += kThreads) tot += (double)pp[i].x;
@@ -173,56 +178,54 @@ __global__ __launch_bounds__(kThreads) void k_gn_partial(const float* __restrict
         if ((int)threadIdx.x < w) dsh[threadIdx.x] += dsh[threadIdx.x + w];
         __syncthreads();
     }
-    if (threadIdx.x == 0) {
-        SegStat st;
-        st.mean = mean;
-        st.rstd = (float)(1.0 / sqrt(dsh[0] / (double)L + (double)eps));
-        st.pad = 0.f;
-        stats[seg] = st;
-        counter[seg] = 0u;  // re-arm for the next call (ordered before the next kernel)
-    }
+    if (threadIdx.x == 0) stats[seg] = make_float2((float)mean, (float)(1.0 / sqrt(dsh[0] / (double)L + (double)eps)));
 }
 
-// grid = (chunks per segment, segments), walked in reverse.
-template <bool SILU>
+// Pass B. grid = (chunks per segment, segments), same mapping as pass A.
+// UNIFORM: HW % kChunk == 0, so every chunk is full and lies inside one
+// channel (channel = chunk / (HW / kChunk)): no masks, one set of affine
+// coefficients per workgroup. Otherwise each vector finds its channel with
+// 32-bit arithmetic (a vector never straddles channels since HW % 4 == 0;
+// segments are < 2^31 floats on this path). Index math stays 32-bit: a
+// 64-bit division here expands into a software routine that doubled the
+// kernel's VGPR count and cost a third of its bandwidth.
+template <bool SILU, bool UNIFORM>
 __global__ __launch_bounds__(kThreads) void k_gn_apply(const float* __restrict__ x, float* __restrict__ y, int64_t L,
-                                                      int64_t HW, int cg, int groups, int64_t nchunks,
-                                                      const SegStat* __restrict__ stats,
+                                                      int HW, int chunks_per_ch, int cg, int groups, int nchunks,
+                                                      const float2* __restrict__ stats,
                                                       const float* __restrict__ gamma,
                                                       const float* __restrict__ beta) {
-    const int64_t seg = (int64_t)gridDim.y - 1 - blockIdx.y;
-    const int64_t chunk = nchunks - 1 - blockIdx.x;
-    const int64_t off = chunk * kChunk;
-    const int64_t cnt = L - off < kChunk ? L - off : kChunk;
-    const int n4 = (int)(cnt >> 2);
-    const SegStat st = stats[seg];
-    const float meanf = (float)st.mean;
-    const int g = (int)(seg % groups);
-    const f4* p = (const f4*)(x + seg * L + off);
-    f4* q = (f4*)(y + seg * L + off);
-    const int64_t c_first = off / HW, c_last = (off + cnt - 1) / HW;
-    f4 v[kChunkV];
+    const int seg = blockIdx.y, chunk = blockIdx.x;
+    const int off = chunk * (int)kChunk;
+    const f4* p = (const f4*)(x + (int64_t)seg * L + off);
+    f4* q = (f4*)(y + (int64_t)seg * L + off);
+    const float2 st = stats[seg];
+    const float meanf = st.x, rstd = st.y;
+    const int gc = (seg % groups) * cg;
+    if constexpr (UNIFORM) {
+        f4 v[kChunkV];
 #pragma unroll
-    for (int j = 0; j < kChunkV; ++j) {
-        const int idx = threadIdx.x + kThreads * j;
-        if (idx < n4) v[j] = dev::ld_stream(p + idx);
-    }
-    if (c_first == c_last) {
-        const int ch = g * cg + (int)c_first;
-        const float a = st.rstd * gamma[ch];
+        for (int j = 0; j < kChunkV; ++j) v[j] = dev::ld_stream(p + threadIdx.x + kThreads * j);
+        const int ch = gc + chunk / chunks_per_ch;
+        const float a = rstd * gamma[ch];
         const float b = beta[ch] - meanf * a;
+#pragma unroll
+        for (int j = 0; j < kChunkV; ++j) dev::st_stream(q + threadIdx.x + kThreads * j, apply4<SILU>(v[j], a, b));
+    } else {
+        const int cnt = (int)(L - off < kChunk ? L - off : kChunk);
+        const int n4 = cnt >> 2;
+        f4 v[kChunkV];
 #pragma unroll
         for (int j = 0; j < kChunkV; ++j) {
             const int idx = threadIdx.x + kThreads * j;
-            if (idx < n4) dev::st_stream(q + idx, apply4<SILU>(v[j], a, b));
+            if (idx < n4) v[j] = dev::ld_stream(p + idx);
         }
-    } else {
 #pragma unroll
         for (int j = 0; j < kChunkV; ++j) {
             const int idx = threadIdx.x + kThreads * j;
             if (idx < n4) {
-                const int ch = g * cg + (int)((off + (int64_t)idx * 4) / HW);
-                const float a = st.rstd * gamma[ch];
+                const int ch = gc + (int)((unsigned)(off + idx * 4) / (unsigned)HW);
+                const float a = rstd * gamma[ch];
                 const float b = beta[ch] - meanf * a;
                 dev::st_stream(q + idx, apply4<SILU>(v[j], a, b));
             }
@@ -274,18 +277,6 @@ __global__ __launch_bounds__(kThreads) void k_gn_generic(const float* x, float* 
     }
 }
 
-template <class F>
-void with_v(int v, F&& f) {
-    switch (v) {
-        case 1: f(std::integral_constant<int, 1>()); break;
-        case 2: f(std::integral_constant<int, 2>()); break;
-        case 4: f(std::integral_constant<int, 4>()); break;
-        case 8: f(std::integral_constant<int, 8>()); break;
-        case 16: f(std::integral_constant<int, 16>()); break;
-        default: fail(SDH_ERR_INVALID, "internal: unsupported group width");
-    }
-}
-
 void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups,
             const float* gamma, const float* beta, float eps) {
     need(N >= 0 && C >= 0 && HW >= 0, op, "negative size");
@@ -300,36 +291,50 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
     check_range(beta, (size_t)C * 4, op, "beta");
     const int64_t cg = C / groups, L = cg * HW, nseg = N * groups;
     const bool vec = HW % 4 == 0 && aligned16(x) && aligned16(y) && L < (1LL << 31);
-    if (vec && L <= (int64_t)kThreads * 4 * 16 && nseg <= 0x7fffffffLL) {
-        const int64_t per_thread = (L / 4 + kThreads - 1) / kThreads;
-        const int v = per_thread <= 1 ? 1 : per_thread <= 2 ? 2 : per_thread <= 4 ? 4 : per_thread <= 8 ? 8 : 16;
-        with_v(v, [&](auto vc) {
-            constexpr int V = decltype(vc)::value;
+    if (vec && L <= (int64_t)1024 * 4 * 16 && nseg <= 0x7fffffffLL) {
+        const int64_t n4 = L / 4;
+        auto go = [&](auto tc, auto vc) {
+            constexpr int TPB = decltype(tc)::value, V = decltype(vc)::value;
             if (silu)
-                k_gn_single<V, true><<<(unsigned)nseg, kThreads, 0, stream()>>>(x, y, (int)C, (int)HW, groups, gamma,
+                k_gn_single<TPB, V, true><<<(unsigned)nseg, TPB, 0, stream()>>>(x, y, (int)C, (int)HW, groups, gamma,
                                                                                beta, eps);
             else
-                k_gn_single<V, false><<<(unsigned)nseg, kThreads, 0, stream()>>>(x, y, (int)C, (int)HW, groups, gamma,
+                k_gn_single<TPB, V, false><<<(unsigned)nseg, TPB, 0, stream()>>>(x, y, (int)C, (int)HW, groups, gamma,
                                                                                 beta, eps);
-        });
+        };
+        using I = std::integral_constant<int, 256>;
+        using K = std::integral_constant<int, 1024>;
+        if (n4 <= 256) go(I(), std::integral_constant<int, 1>());
+        else if (n4 <= 512) go(I(), std::integral_constant<int, 2>());
+        else if (n4 <= 1024) go(I(), std::integral_constant<int, 4>());
+        else if (n4 <= 2048) go(I(), std::integral_constant<int, 8>());
+        else if (n4 <= 4096) go(K(), std::integral_constant<int, 4>());
+        else if (n4 <= 8192) go(K(), std::integral_constant<int, 8>());
+        else if (n4 <= 12288) go(K(), std::integral_constant<int, 12>());
+        else go(K(), std::integral_constant<int, 16>());
     } else if (vec && nseg <= 65535) {
         const int64_t nchunks = (L + kChunk - 1) / kChunk;
         need(nchunks <= 0x7fffffffLL, op, "segment too large");
-        const size_t part_bytes = (size_t)(nseg * nchunks) * sizeof(float2);
-        const size_t stat_off = (part_bytes + 255) / 256 * 256;
-        char* scr = (char*)scratch(stat_off + (size_t)nseg * sizeof(SegStat));
+        const size_t part_bytes = ((size_t)(nseg * nchunks) * sizeof(float2) + 255) / 256 * 256;
+        char* scr = (char*)scratch(part_bytes + (size_t)nseg * sizeof(float2));
         float2* part = (float2*)scr;
-        SegStat* stats = (SegStat*)(scr + stat_off);
-        unsigned* cnt = counters((size_t)nseg);
+        float2* stats = (float2*)(scr + part_bytes);
         const dim3 grid((unsigned)nchunks, (unsigned)nseg);
-        k_gn_partial<<<grid, kThreads, 0, stream()>>>(x, L, nchunks, part, stats, cnt, eps);
+        k_gn_partial<<<grid, kThreads, 0, stream()>>>(x, L, nchunks, part);
         launched(op);
-        if (silu)
-            k_gn_apply<true><<<grid, kThreads, 0, stream()>>>(x, y, L, HW, (int)cg, groups, nchunks, stats, gamma,
-                                                            beta);
-        else
-            k_gn_apply<false><<<grid, kThreads, 0, stream()>>>(x, y, L, HW, (int)cg, groups, nchunks, stats, gamma,
-                                                             beta);
+        k_gn_finalize<<<(unsigned)nseg, kThreads, 0, stream()>>>(part, L, nchunks, stats, eps);
+        launched(op);
+        const bool uniform = HW % kChunk == 0;
+        const int cpc = uniform ? (int)(HW / kChunk) : 1;
+        auto apply = [&](auto sc, auto uc) {
+            constexpr bool S = decltype(sc)::value, U = decltype(uc)::value;
+            k_gn_apply<S, U><<<grid, kThreads, 0, stream()>>>(x, y, L, (int)HW, cpc, (int)cg, groups, (int)nchunks,
+                                                              stats, gamma, beta);
+        };
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        if (silu) uniform ? apply(T_(), T_()) : apply(T_(), F_());
+        else uniform ? apply(F_(), T_()) : apply(F_(), F_());
     } else {
         need(nseg <= 0x7fffffffLL, op, "too many groups");
         if (silu)

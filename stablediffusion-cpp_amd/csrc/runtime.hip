@@ -52,7 +52,8 @@ struct Arena {
     std::vector<Seg> segs;
     std::map<uintptr_t, size_t> free_by_addr;          // addr -> size
     std::multimap<size_t, uintptr_t> free_by_size;     // size -> addr
-    std::map<uintptr_t, size_t> live;                  // addr -> size
+    std::map<uintptr_t, size_t> live;                  // addr -> rounded size
+    std::map<uintptr_t, size_t> requested;             // addr -> bytes asked for
     size_t reserved = 0, in_use = 0, limit = 0;        // limit 0 = none
 
     int seg_of(uintptr_t a) const {
@@ -122,6 +123,7 @@ struct Arena {
         erase_free(a, fsz);
         if (fsz > sz) insert_free(a + sz, fsz - sz);
         live[a] = sz;
+        requested[a] = bytes;
         in_use += sz;
         return (void*)a;
     }
@@ -130,6 +132,7 @@ struct Arena {
         if (it == live.end()) return false;
         const size_t sz = it->second;
         live.erase(it);
+        requested.erase((uintptr_t)p);
         in_use -= sz;
         insert_free((uintptr_t)p, sz);
         return true;
@@ -140,6 +143,7 @@ struct Arena {
         free_by_addr.clear();
         free_by_size.clear();
         live.clear();
+        requested.clear();
         reserved = in_use = 0;
     }
 };
@@ -215,7 +219,8 @@ void range_check_locked(Runtime& r, const void* p, size_t bytes, const char* op,
         --it;
         return a >= it->first && a - it->first <= it->second && bytes <= it->second - (a - it->first);
     };
-    if (inside(r.arena.live) || inside(r.external)) return;
+    // exact extents: the bytes the caller asked for, not the rounded block
+    if (inside(r.arena.requested) || inside(r.external)) return;
     fail(SDH_ERR_INVALID, std::string(op) + ": " + what + " (" + std::to_string(bytes) +
                               " bytes) is not inside a live backend_hip allocation");
 }

@@ -144,6 +144,13 @@ __device__ __forceinline__ float hsum(const f4& v) { return (v.x + v.y) + (v.z +
 __device__ __forceinline__ f4 ld_stream(const f4* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_stream(f4* p, f4 v) { __builtin_nontemporal_store(v, p); }
 
+// exp(x) as 2^(x log2 e) on the hardware exp2 (v_exp_f32). Relative error
+// about |x| 2^-24 (from rounding x log2 e) plus 1 ulp; for ops whose bound
+// is relative 1e-4, not for the max-abs 1e-5 elementwise ops.
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+// x / (1 + exp(-x)) with the hardware reciprocal (v_rcp_f32, 1 ulp).
+__device__ __forceinline__ float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(1.0f + exp_fast(-x)); }
+
 // Reference-order activations (tensor.cpp:745, :847, :859, :866, :830).
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 __device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }

@@ -1,0 +1,94 @@
+"""The oracle (C restatement) against the compiled reference tensor library
+(oracle/_ref, the reference's own src/tensor.cpp): bit-for-bit equality on
+seeded random inputs, for every op on the path, at tiny, odd and mid-size
+shapes. Skipped where oracle/_ref was not built.
+"""
+import numpy as np
+import pytest
+
+
+def _eq(a, b, what):
+    assert a.shape == b.shape, what
+    assert np.array_equal(a, b), f"{what}: max diff {np.max(np.abs(a - b)):.3e}"
+
+
+@pytest.mark.parametrize("rows,C", [(21, 64), (3, 70), (37, 3840), (1, 1)])
+def test_norms_bitexact(orc, ref, rows, C):
+    x = orc.randn((rows, C), 100 + C, 1.0, 2.0)
+    g = orc.randn((C,), 200 + C, 1.0, 0.1)
+    b = orc.randn((C,), 300 + C, 0.0, 0.1)
+    _eq(orc.rms_norm(x, g, 1e-6), ref.rms_norm(x, g, 1e-6), "rms_norm")
+    _eq(orc.rms_norm(x, None, 1e-5), ref.rms_norm(x, None, 1e-5), "rms_norm no gamma")
+    for gg, bb in ((g, b), (None, None), (g, None), (None, b)):
+        _eq(orc.layer_norm(x, gg, bb, 1e-5), ref.layer_norm(x, gg, bb, 1e-5), "layer_norm")
+    s1, y1 = orc.add_rms_norm(x, x[::-1].copy(), g, 1e-6)
+    s2, y2 = ref.add_rms_norm(x, x[::-1].copy(), g, 1e-6)
+    _eq(s1, s2, "add_rms_norm sum")
+    _eq(y1, y2, "add_rms_norm norm")
+
+
+@pytest.mark.parametrize("groups,dim", [(15, 8), (64, 128), (9, 30)])
+def test_rms_norm_heads_bitexact(orc, ref, groups, dim):
+    x = orc.randn((groups, dim), 7 + dim)
+    g = orc.randn((dim,), 8 + dim, 1.0, 0.1)
+    _eq(orc.rms_norm_heads(x, dim, g, 1e-5), ref.rms_norm_heads(x, dim, g, 1e-5), "rms_norm_heads")
+
+
+@pytest.mark.parametrize("shape,groups", [((2, 64, 5, 7), 32), ((1, 128, 32, 32), 32), ((2, 96, 7, 3), 8)])
+def test_group_norm_bitexact(orc, ref, shape, groups):
+    x = orc.randn(shape, 11, 0.0, 2.0)
+    g = orc.randn((shape[1],), 12, 1.0, 0.1)
+    b = orc.randn((shape[1],), 13, 0.0, 0.1)
+    _eq(orc.group_norm(x, groups, g, b, 1e-6), ref.group_norm(x, groups, g, b, 1e-6), "group_norm")
+    _eq(orc.group_norm(x, groups, g, b, 1e-5, silu=True), ref.group_norm(x, groups, g, b, 1e-5, silu=True),
+        "group_norm+silu")
+
+
+@pytest.mark.parametrize("rows,cols", [(9, 9), (40, 37), (16, 4096)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_softmax_bitexact(orc, ref, rows, cols, causal):
+    x = orc.randn((rows, cols), 21 + cols, 0.0, 3.0)
+    _eq(orc.softmax_rows(x, 0.0883883, causal), ref.softmax_rows(x, 0.0883883, causal), "softmax")
+
+
+@pytest.mark.parametrize("interleaved", [True, False])
+def test_rope_bitexact(orc, ref, interleaved):
+    S = 64
+    pos = np.array([[0, h, w] for h in range(8) for w in range(8)], np.int32)
+    if interleaved:
+        cs, sn = orc.rope_tables_3axis(pos, [32, 48, 48], 128, 256.0)
+    else:
+        cs, sn = orc.rope_tables_half(S, 128, 1e6)
+    x = orc.randn((2, S, 3 * 128), 31)
+    _eq(orc.rope(x, 128, cs, sn, interleaved), ref.rope(x, 128, cs, sn, interleaved), "rope")
+
+
+def test_elementwise_bitexact(orc, ref):
+    x = orc.randn((33, 100), 41, 0.0, 3.0)
+    u = orc.randn((33, 100), 42, 0.0, 1.5)
+    v = orc.randn((100,), 43, 0.0, 0.2)
+    _eq(orc.swiglu(x, u), ref.swiglu(x, u), "swiglu")
+    _eq(orc.geglu(x), ref.geglu(x), "geglu")
+    for op in ("silu", "tanh", "gelu", "quick_gelu"):
+        _eq(getattr(orc, op)(x), getattr(ref, op)(x), op)
+    _eq(orc.add(x, u), ref.add(x, u), "add")
+    _eq(orc.scale(x, 0.37), ref.scale(x, 0.37), "scale")
+    _eq(orc.affine(x, 1.5, -0.25), ref.affine(x, 1.5, -0.25), "affine")
+    _eq(orc.mul_rows(x, v), ref.mul_rows(x, v), "mul_rows")
+    _eq(orc.add_rows_scaled(x, u, v), ref.add_rows_scaled(x, u, v), "add_rows_scaled")
+    img = orc.randn((2, 3, 4, 5), 44)
+    b = orc.randn((2, 3), 45)
+    _eq(orc.add_channel_bias(img, b), ref.add_channel_bias(img, b), "add_channel_bias")
+
+
+@pytest.mark.parametrize("shift", [True, False])
+def test_ln_modulate_gate_bitexact(orc, ref, shift):
+    x = orc.randn((12, 3840), 51)
+    r = orc.randn((12, 3840), 52)
+    sc = orc.randn((3840,), 53, 0.0, 0.2)
+    sh = orc.randn((3840,), 54, 0.0, 0.2) if shift else None
+    gt = orc.randn((3840,), 55, 0.0, 0.2)
+    a = orc.ln_modulate_gate(x, r, sc, sh, gt, 1e-6)
+    b = ref.ln_modulate_gate(x, r, sc, sh, gt, 1e-6)
+    _eq(a[0], b[0], "res")
+    _eq(a[1], b[1], "y")
