@@ -1,0 +1,125 @@
+// sd_hip.hpp - C++17 face of backend_hip for the reference's tensor library.
+//
+// This header is the drop-in for the elementwise / reduction / broadcast half
+// of src/backend_cuda.h: namespace sd::hip has the functions of namespace
+// sd::cuda (backend_cuda.h:23-80) with the same parameter lists, so
+// tensor.cpp's `if (x.is_cuda()) cuda::op(...)` branches become
+// `if (x.is_hip()) hip::op(...)` with no other change. Each function calls the
+// C ABI (include/sdh_backend.h) and turns a non-zero status into
+// std::runtime_error carrying sdh_last_error(), which is how the reference's
+// backend reports failures (check()/launched(), backend_cuda.cu:41-48, and the
+// stub's throw, backend_cuda_stub.cpp:14).
+//
+// GEMM, conv2d, attention and the layout copies stay with their existing
+// implementations; they are not part of this backend.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "sdh_backend.h"
+
+namespace sd {
+namespace hip {
+
+namespace detail {
+inline void check(int status, const char* what) {
+    if (status != SDH_OK) throw std::runtime_error(std::string(what) + ": " + sdh_last_error());
+}
+}  // namespace detail
+
+// backend_cuda.h:24-27
+inline bool available() { return sdh_available() != 0; }
+inline const char* device_name() { return sdh_device_name(); }
+inline size_t device_memory() { return sdh_device_memory(); }
+
+// backend_cuda.h:30-36
+inline void* malloc(size_t bytes) {
+    void* p = nullptr;
+    detail::check(sdh_malloc(bytes, &p), "hip::malloc");
+    return p;
+}
+inline void free(void* p) { detail::check(sdh_free(p), "hip::free"); }
+inline void upload(void* dst, const void* src, size_t bytes) { detail::check(sdh_upload(dst, src, bytes), "hip::upload"); }
+inline void download(void* dst, const void* src, size_t bytes) {
+    detail::check(sdh_download(dst, src, bytes), "hip::download");
+}
+inline void copy(void* dst, const void* src, size_t bytes) { detail::check(sdh_copy(dst, src, bytes), "hip::copy"); }
+inline void zero(void* dst, size_t bytes) { detail::check(sdh_zero(dst, bytes), "hip::zero"); }
+inline void synchronize() { detail::check(sdh_synchronize(), "hip::synchronize"); }
+
+// backend_cuda.h:48-52
+inline void group_norm(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups, const float* gamma,
+                       const float* beta, float eps) {
+    detail::check(sdh_group_norm(x, y, N, C, HW, groups, gamma, beta, eps), "hip::group_norm");
+}
+inline void layer_norm(const float* x, float* y, int64_t rows, int64_t C, const float* gamma, const float* beta,
+                       float eps) {
+    detail::check(sdh_layer_norm(x, y, rows, C, gamma, beta, eps), "hip::layer_norm");
+}
+inline void rms_norm(const float* x, float* y, int64_t rows, int64_t C, const float* gamma, float eps) {
+    detail::check(sdh_rms_norm(x, y, rows, C, gamma, eps), "hip::rms_norm");
+}
+inline void rms_norm_heads(float* x, int64_t groups, int64_t dim, const float* gamma, float eps) {
+    detail::check(sdh_rms_norm_heads(x, groups, dim, gamma, eps), "hip::rms_norm_heads");
+}
+// backend_cuda.h:54-56
+inline void rope(float* x, int64_t N, int64_t S, int64_t inner, int64_t dim, const float* cos, const float* sin,
+                 bool interleaved) {
+    detail::check(sdh_rope(x, N, S, inner, dim, cos, sin, interleaved ? 1 : 0), "hip::rope");
+}
+inline void softmax_rows(float* x, int64_t rows, int64_t cols, float scale, bool causal) {
+    detail::check(sdh_softmax_rows(x, rows, cols, scale, causal ? 1 : 0), "hip::softmax_rows");
+}
+// backend_cuda.h:60-61
+inline void geglu(const float* x, float* y, int64_t rows, int64_t D) {
+    detail::check(sdh_geglu(x, y, rows, D), "hip::geglu");
+}
+inline void swiglu(const float* gate, const float* up, float* y, int64_t n) {
+    detail::check(sdh_swiglu(gate, up, y, n), "hip::swiglu");
+}
+// backend_cuda.h:64-73
+inline void silu(float* x, int64_t n) { detail::check(sdh_silu(x, n), "hip::silu"); }
+inline void tanh(float* x, int64_t n) { detail::check(sdh_tanh(x, n), "hip::tanh"); }
+inline void gelu(float* x, int64_t n) { detail::check(sdh_gelu(x, n), "hip::gelu"); }
+inline void quick_gelu(float* x, int64_t n) { detail::check(sdh_quick_gelu(x, n), "hip::quick_gelu"); }
+inline void add(float* a, const float* b, int64_t n) { detail::check(sdh_add(a, b, n), "hip::add"); }
+inline void scale(float* x, float s, int64_t n) { detail::check(sdh_scale(x, s, n), "hip::scale"); }
+inline void affine(float* x, float a, float b, int64_t n) { detail::check(sdh_affine(x, a, b, n), "hip::affine"); }
+inline void mul_rows(float* x, const float* v, int64_t rows, int64_t dim) {
+    detail::check(sdh_mul_rows(x, v, rows, dim), "hip::mul_rows");
+}
+inline void add_rows_scaled(float* x, const float* y, const float* g, int64_t rows, int64_t dim) {
+    detail::check(sdh_add_rows_scaled(x, y, g, rows, dim), "hip::add_rows_scaled");
+}
+inline void add_channel_bias(float* x, const float* b, int64_t N, int64_t C, int64_t HW) {
+    detail::check(sdh_add_channel_bias(x, b, N, C, HW), "hip::add_channel_bias");
+}
+
+// Additive entry points (no single backend_cuda.h counterpart).
+inline void add_rows(float* x, const float* v, int64_t rows, int64_t dim) {
+    detail::check(sdh_add_rows(x, v, rows, dim), "hip::add_rows");
+}
+inline void softmax_rows_batched(float* x, int64_t rows, int64_t cols, float scale, bool causal, int64_t period) {
+    detail::check(sdh_softmax_rows_batched(x, rows, cols, scale, causal ? 1 : 0, period), "hip::softmax_rows_batched");
+}
+inline void rope_qk(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
+                    const float* cos, const float* sin, bool interleaved) {
+    detail::check(sdh_rope_qk(q, inner_q, k, inner_k, N, S, dim, cos, sin, interleaved ? 1 : 0), "hip::rope_qk");
+}
+inline void add_rms_norm(float* x, const float* r, float* y, int64_t rows, int64_t C, const float* gamma, float eps) {
+    detail::check(sdh_add_rms_norm(x, r, y, rows, C, gamma, eps), "hip::add_rms_norm");
+}
+inline void group_norm_silu(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups,
+                            const float* gamma, const float* beta, float eps) {
+    detail::check(sdh_group_norm_silu(x, y, N, C, HW, groups, gamma, beta, eps), "hip::group_norm_silu");
+}
+inline void ln_modulate_gate(const float* x, float* res, const float* scale, const float* shift, const float* gate,
+                             float* y_out, int64_t rows, int64_t C, float eps) {
+    detail::check(sdh_ln_modulate_gate(x, res, scale, shift, gate, y_out, rows, C, eps), "hip::ln_modulate_gate");
+}
+
+}  // namespace hip
+}  // namespace sd

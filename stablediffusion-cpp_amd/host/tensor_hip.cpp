@@ -1,0 +1,311 @@
+// tensor_hip.cpp - device branch of the tensor.h operators over backend_hip.
+// Shape checks and their messages follow src/tensor.cpp (lines cited per op);
+// the arithmetic is backend_hip's (include/sdh_backend.h).
+#include "tensor_hip.h"
+
+#include <sstream>
+#include <stdexcept>
+
+#include "sd_hip.hpp"
+
+namespace sdh {
+
+struct DeviceBuffer {
+    void* p = nullptr;
+    size_t bytes = 0;
+    explicit DeviceBuffer(size_t n) : bytes(n) { p = n ? sd::hip::malloc(n) : nullptr; }
+    ~DeviceBuffer() {
+        if (p) sdh_free(p);  // never throws from a destructor
+    }
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+};
+
+const char* device_name(Device d) { return d == Device::HIP ? "hip" : "cpu"; }
+
+// tensor.cpp:45-53 with "hip" for "cuda".
+Device parse_device(const std::string& s) {
+    if (s == "cpu") return Device::CPU;
+    if (s == "hip") {
+        if (!sd::hip::available()) throw std::runtime_error("HIP requested but not available (no MI355X visible)");
+        return Device::HIP;
+    }
+    if (s == "auto") return sd::hip::available() ? Device::HIP : Device::CPU;
+    throw std::runtime_error("unknown device '" + s + "' (use cpu, hip or auto)");
+}
+
+int64_t Tensor::numel_of(const std::vector<int64_t>& s) {
+    int64_t n = 1;
+    for (int64_t d : s) n *= d;
+    return n;
+}
+
+Tensor::Tensor(std::vector<int64_t> s) : shape(std::move(s)), data((size_t)numel_of(shape), 0.0f) {}
+
+Tensor::Tensor(std::vector<int64_t> s, Device d) : shape(std::move(s)), device(d) {
+    if (d == Device::CPU) {
+        data.assign((size_t)numel_of(shape), 0.0f);
+    } else {
+        const size_t bytes = (size_t)numel_of(shape) * sizeof(float);
+        dev = std::make_shared<DeviceBuffer>(bytes);
+        if (bytes) sd::hip::zero(dev->p, bytes);
+    }
+}
+
+Tensor Tensor::empty(std::vector<int64_t> s, Device d) {
+    if (d == Device::CPU) return Tensor(std::move(s));
+    Tensor t;
+    t.shape = std::move(s);
+    t.device = d;
+    t.dev = std::make_shared<DeviceBuffer>((size_t)numel_of(t.shape) * sizeof(float));
+    return t;
+}
+
+float* Tensor::dptr() { return is_hip() && dev ? (float*)dev->p : nullptr; }
+const float* Tensor::dptr() const { return is_hip() && dev ? (const float*)dev->p : nullptr; }
+
+float* Tensor::ptr() {
+    if (is_hip()) throw std::runtime_error("tensor is on the GPU; host pointer requested " + shape_str());
+    return data.data();
+}
+const float* Tensor::ptr() const {
+    if (is_hip()) throw std::runtime_error("tensor is on the GPU; host pointer requested " + shape_str());
+    return data.data();
+}
+
+Tensor Tensor::to(Device d) const {
+    if (d == device) return *this;
+    Tensor t;
+    t.shape = shape;
+    t.device = d;
+    const size_t bytes = (size_t)numel() * sizeof(float);
+    if (d == Device::HIP) {
+        t.dev = std::make_shared<DeviceBuffer>(bytes);
+        if (bytes) sd::hip::upload(t.dev->p, data.data(), bytes);
+    } else {
+        t.data.resize((size_t)numel());
+        if (bytes) sd::hip::download(t.data.data(), dev->p, bytes);
+    }
+    return t;
+}
+
+Tensor& Tensor::reshape(std::vector<int64_t> s) {
+    if (numel_of(s) != numel()) throw std::runtime_error("reshape: element count mismatch for " + shape_str());
+    shape = std::move(s);
+    return *this;
+}
+
+std::string Tensor::shape_str() const {
+    std::ostringstream os;
+    os << "[";
+    for (size_t i = 0; i < shape.size(); ++i) os << (i ? ", " : "") << shape[i];
+    os << "]";
+    return os.str();
+}
+
+namespace {
+
+// The CPU branch of every op is the reference's tensor.cpp; this library
+// only implements the device branch.
+void need_hip(const Tensor& t, const char* op) {
+    if (!t.is_hip())
+        throw std::runtime_error(std::string(op) +
+                                 ": host tensor; backend_hip implements the HIP device path only (the CPU path is "
+                                 "the reference's tensor.cpp)");
+}
+// tensor.cpp:97-99
+void same_device(const Tensor& a, const Tensor& b, const char* op) {
+    if (a.device != b.device) throw std::runtime_error(std::string(op) + ": tensors on different devices");
+}
+const float* opt(const Tensor* t) { return t ? t->dptr() : nullptr; }
+
+}  // namespace
+
+// tensor.cpp:592-600
+Tensor group_norm(const Tensor& x, int groups, const Tensor& gamma, const Tensor& beta, float eps) {
+    need_hip(x, "group_norm");
+    same_device(x, gamma, "group_norm");
+    same_device(x, beta, "group_norm");
+    const int64_t N = x.dim(0), C = x.dim(1), HW = x.numel() / (N * C);
+    if (C % groups != 0) throw std::runtime_error("group_norm: channels not divisible by groups");
+    Tensor y = Tensor::empty(x.shape, Device::HIP);
+    sd::hip::group_norm(x.dptr(), y.dptr(), N, C, HW, groups, gamma.dptr(), beta.dptr(), eps);
+    return y;
+}
+
+// tensor.cpp:628-634
+Tensor layer_norm(const Tensor& x, const Tensor* gamma, const Tensor* beta, float eps) {
+    need_hip(x, "layer_norm");
+    if (gamma) same_device(x, *gamma, "layer_norm");
+    if (beta) same_device(x, *beta, "layer_norm");
+    const int64_t C = x.dim(-1), rows = x.numel() / C;
+    Tensor y = Tensor::empty(x.shape, Device::HIP);
+    sd::hip::layer_norm(x.dptr(), y.dptr(), rows, C, opt(gamma), opt(beta), eps);
+    return y;
+}
+
+// tensor.cpp:660-666
+Tensor rms_norm(const Tensor& x, const Tensor* gamma, float eps) {
+    need_hip(x, "rms_norm");
+    if (gamma) same_device(x, *gamma, "rms_norm");
+    const int64_t C = x.dim(-1), rows = x.numel() / C;
+    Tensor y = Tensor::empty(x.shape, Device::HIP);
+    sd::hip::rms_norm(x.dptr(), y.dptr(), rows, C, opt(gamma), eps);
+    return y;
+}
+
+// tensor.cpp:681-686
+void rms_norm_heads_(Tensor& x, int64_t dim, const Tensor* gamma, float eps) {
+    need_hip(x, "rms_norm_heads_");
+    if (gamma) same_device(x, *gamma, "rms_norm_heads_");
+    sd::hip::rms_norm_heads(x.dptr(), x.numel() / dim, dim, opt(gamma), eps);
+}
+
+// tensor.cpp:698-705
+void rope_(Tensor& x, int64_t dim, const Tensor& cos, const Tensor& sin, bool interleaved) {
+    need_hip(x, "rope_");
+    const int64_t inner = x.dim(-1), S = x.dim(-2), N = x.numel() / (S * inner);
+    if (cos.dim(0) < S || cos.dim(1) != dim) throw std::runtime_error("rope_: table shape mismatch");
+    same_device(x, cos, "rope_");
+    same_device(x, sin, "rope_");
+    sd::hip::rope(x.dptr(), N, S, inner, dim, cos.dptr(), sin.dptr(), interleaved);
+}
+
+// tensor.cpp:732-738
+Tensor swiglu(const Tensor& gate, const Tensor& up) {
+    if (gate.numel() != up.numel()) throw std::runtime_error("swiglu: shape mismatch");
+    same_device(gate, up, "swiglu");
+    need_hip(gate, "swiglu");
+    Tensor y = Tensor::empty(gate.shape, Device::HIP);
+    sd::hip::swiglu(gate.dptr(), up.dptr(), y.dptr(), y.numel());
+    return y;
+}
+
+// tensor.cpp:813-821
+Tensor geglu(const Tensor& x) {
+    need_hip(x, "geglu");
+    const int64_t D2 = x.dim(-1), D = D2 / 2, rows = x.numel() / D2;
+    std::vector<int64_t> oshape = x.shape;
+    oshape.back() = D;
+    Tensor y = Tensor::empty(oshape, Device::HIP);
+    sd::hip::geglu(x.dptr(), y.dptr(), rows, D);
+    return y;
+}
+
+// tensor.cpp:843-868
+void silu_(Tensor& x) {
+    need_hip(x, "silu_");
+    sd::hip::silu(x.dptr(), x.numel());
+}
+void tanh_(Tensor& x) {
+    need_hip(x, "tanh_");
+    sd::hip::tanh(x.dptr(), x.numel());
+}
+void gelu_(Tensor& x) {
+    need_hip(x, "gelu_");
+    sd::hip::gelu(x.dptr(), x.numel());
+}
+void quick_gelu_(Tensor& x) {
+    need_hip(x, "quick_gelu_");
+    sd::hip::quick_gelu(x.dptr(), x.numel());
+}
+
+// tensor.cpp:869-887
+void add_(Tensor& a, const Tensor& b) {
+    if (a.numel() != b.numel()) throw std::runtime_error("add_: " + a.shape_str() + " vs " + b.shape_str());
+    same_device(a, b, "add_");
+    need_hip(a, "add_");
+    sd::hip::add(a.dptr(), b.dptr(), a.numel());
+}
+void scale_(Tensor& x, float s) {
+    need_hip(x, "scale_");
+    sd::hip::scale(x.dptr(), s, x.numel());
+}
+void affine_(Tensor& x, float a, float b) {
+    need_hip(x, "affine_");
+    sd::hip::affine(x.dptr(), a, b, x.numel());
+}
+
+// tensor.cpp:889-893
+void mul_rows_(Tensor& x, const Tensor& v) {
+    const int64_t dim = x.dim(-1), rows = x.numel() / dim;
+    if (v.numel() != dim) throw std::runtime_error("mul_rows_: vector size mismatch");
+    same_device(x, v, "mul_rows_");
+    need_hip(x, "mul_rows_");
+    sd::hip::mul_rows(x.dptr(), v.dptr(), rows, dim);
+}
+
+// tensor.cpp:903-908
+void add_rows_scaled_(Tensor& x, const Tensor& y, const Tensor& g) {
+    const int64_t dim = x.dim(-1), rows = x.numel() / dim;
+    if (y.numel() != x.numel() || g.numel() != dim) throw std::runtime_error("add_rows_scaled_: shape mismatch");
+    same_device(x, y, "add_rows_scaled_");
+    same_device(x, g, "add_rows_scaled_");
+    need_hip(x, "add_rows_scaled_");
+    sd::hip::add_rows_scaled(x.dptr(), y.dptr(), g.dptr(), rows, dim);
+}
+
+// tensor.cpp:919-923
+void add_channel_bias_(Tensor& x, const Tensor& b) {
+    const int64_t N = x.dim(0), C = x.dim(1), HW = x.numel() / (N * C);
+    if (b.numel() != N * C) throw std::runtime_error("add_channel_bias_: expected [N, C] bias");
+    same_device(x, b, "add_channel_bias_");
+    need_hip(x, "add_channel_bias_");
+    sd::hip::add_channel_bias(x.dptr(), b.dptr(), N, C, HW);
+}
+
+// tensor.cpp:752 (device pointer)
+void softmax_rows_(float* x, int64_t rows, int64_t cols, float scale, bool causal) {
+    sd::hip::softmax_rows(x, rows, cols, scale, causal);
+}
+void softmax_rows_(Tensor& x, float scale, bool causal) {
+    need_hip(x, "softmax_rows_");
+    const int64_t cols = x.dim(-1);
+    sd::hip::softmax_rows(x.dptr(), x.numel() / cols, cols, scale, causal);
+}
+
+// ---- fused ----
+Tensor add_rms_norm_(Tensor& x, const Tensor& r, const Tensor* gamma, float eps) {
+    if (x.numel() != r.numel()) throw std::runtime_error("add_: " + x.shape_str() + " vs " + r.shape_str());
+    same_device(x, r, "add_rms_norm_");
+    need_hip(x, "add_rms_norm_");
+    const int64_t C = x.dim(-1), rows = x.numel() / C;
+    Tensor y = Tensor::empty(x.shape, Device::HIP);
+    sd::hip::add_rms_norm(x.dptr(), r.dptr(), y.dptr(), rows, C, opt(gamma), eps);
+    return y;
+}
+
+Tensor group_norm_silu(const Tensor& x, int groups, const Tensor& gamma, const Tensor& beta, float eps) {
+    need_hip(x, "group_norm_silu");
+    same_device(x, gamma, "group_norm_silu");
+    same_device(x, beta, "group_norm_silu");
+    const int64_t N = x.dim(0), C = x.dim(1), HW = x.numel() / (N * C);
+    if (C % groups != 0) throw std::runtime_error("group_norm: channels not divisible by groups");
+    Tensor y = Tensor::empty(x.shape, Device::HIP);
+    sd::hip::group_norm_silu(x.dptr(), y.dptr(), N, C, HW, groups, gamma.dptr(), beta.dptr(), eps);
+    return y;
+}
+
+void ln_modulate_gate_(const Tensor& x, Tensor& res, const Tensor& scale, const Tensor* shift, const Tensor& gate,
+                       float eps, Tensor* y_out) {
+    need_hip(x, "ln_modulate_gate_");
+    same_device(x, res, "ln_modulate_gate_");
+    const int64_t C = x.dim(-1), rows = x.numel() / C;
+    if (res.numel() != x.numel() || scale.numel() != C || gate.numel() != C || (shift && shift->numel() != C))
+        throw std::runtime_error("ln_modulate_gate_: shape mismatch");
+    if (y_out && (y_out->numel() != x.numel() || !y_out->is_hip()))
+        throw std::runtime_error("ln_modulate_gate_: y_out must be a device tensor shaped like x");
+    sd::hip::ln_modulate_gate(x.dptr(), res.dptr(), scale.dptr(), opt(shift), gate.dptr(),
+                              y_out ? y_out->dptr() : nullptr, rows, C, eps);
+}
+
+void rope_qk_(Tensor& q, Tensor& k, int64_t dim, const Tensor& cos, const Tensor& sin, bool interleaved) {
+    need_hip(q, "rope_qk_");
+    same_device(q, k, "rope_qk_");
+    const int64_t S = q.dim(-2), N = q.numel() / (S * q.dim(-1));
+    if (k.dim(-2) != S || k.numel() / (S * k.dim(-1)) != N) throw std::runtime_error("rope_qk_: q/k token mismatch");
+    if (cos.dim(0) < S || cos.dim(1) != dim) throw std::runtime_error("rope_: table shape mismatch");
+    sd::hip::rope_qk(q.dptr(), q.dim(-1), k.dptr(), k.dim(-1), N, S, dim, cos.dptr(), sin.dptr(), interleaved);
+}
+
+}  // namespace sdh

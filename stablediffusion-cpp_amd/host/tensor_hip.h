@@ -1,0 +1,104 @@
+// tensor_hip.h - the reference's tensor.h operator API for HIP device tensors.
+//
+// sdh::Tensor mirrors sd::Tensor (src/tensor.h:48-95) for fp32 data: a shape
+// plus storage that lives either on the host (std::vector<float>) or on the
+// MI355X (a backend_hip arena block). The free functions below keep the
+// names, parameters, return conventions (new tensor vs in-place `_` ops) and
+// error messages of the tensor.h declarations they cite, and run on the
+// device through backend_hip. They implement the device branch only: the
+// CPU branch of every op is the reference's own tensor.cpp, so passing a host
+// tensor to an op throws rather than computing anything on the CPU.
+//
+// Additive fused ops (add_rms_norm_, group_norm_silu, ln_modulate_gate_,
+// rope_qk_) equal the reference compositions named in their comments.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace sdh {
+
+// tensor.h:32, with HIP in place of CUDA.
+enum class Device { CPU, HIP };
+const char* device_name(Device d);          // "cpu" / "hip"
+Device parse_device(const std::string& s);  // "cpu", "hip", or "auto" (hip if available)
+
+struct DeviceBuffer;  // one backend_hip arena block
+
+struct Tensor {
+    std::vector<int64_t> shape;
+    std::vector<float> data;            // host storage when device == CPU
+    Device device = Device::CPU;
+    std::shared_ptr<DeviceBuffer> dev;  // device storage when device == HIP
+
+    Tensor() = default;
+    // Zero-filled host tensor (tensor.h:58).
+    explicit Tensor(std::vector<int64_t> s);
+    // Zero-filled tensor on the given device (tensor.h:60, tensor.cpp:55-63).
+    Tensor(std::vector<int64_t> s, Device d);
+    // Device tensor whose contents are left uninitialised; ops use it for
+    // outputs they overwrite completely (no zero-fill pass).
+    static Tensor empty(std::vector<int64_t> s, Device d);
+
+    static int64_t numel_of(const std::vector<int64_t>& s);
+    int64_t numel() const { return numel_of(shape); }
+    bool is_hip() const { return device == Device::HIP; }
+    Tensor to(Device d) const;  // tensor.cpp:72-93
+    float* dptr();
+    const float* dptr() const;
+    int ndim() const { return (int)shape.size(); }
+    int64_t dim(int i) const { return shape[i < 0 ? i + ndim() : i]; }
+    float* ptr();  // host only
+    const float* ptr() const;
+    Tensor& reshape(std::vector<int64_t> s);
+    std::string shape_str() const;
+};
+
+// ---- norms (tensor.h:166-180) ----
+Tensor group_norm(const Tensor& x, int groups, const Tensor& gamma, const Tensor& beta, float eps);
+Tensor layer_norm(const Tensor& x, const Tensor* gamma, const Tensor* beta, float eps);
+inline Tensor layer_norm(const Tensor& x, const Tensor& gamma, const Tensor& beta, float eps) {
+    return layer_norm(x, &gamma, &beta, eps);
+}
+Tensor rms_norm(const Tensor& x, const Tensor* gamma, float eps);
+void rms_norm_heads_(Tensor& x, int64_t dim, const Tensor* gamma, float eps);
+
+// ---- rotary, activations (tensor.h:188-191, :217-228) ----
+void rope_(Tensor& x, int64_t dim, const Tensor& cos, const Tensor& sin, bool interleaved);
+Tensor swiglu(const Tensor& gate, const Tensor& up);
+Tensor geglu(const Tensor& x);
+void silu_(Tensor& x);
+void tanh_(Tensor& x);
+void gelu_(Tensor& x);
+void quick_gelu_(Tensor& x);
+
+// ---- broadcasts / residual (tensor.h:195-198, :230-232) ----
+void affine_(Tensor& x, float a, float b);
+void mul_rows_(Tensor& x, const Tensor& v);
+void add_rows_scaled_(Tensor& x, const Tensor& y, const Tensor& g);
+void add_channel_bias_(Tensor& x, const Tensor& b);
+void add_(Tensor& a, const Tensor& b);
+void scale_(Tensor& x, float s);
+
+// ---- softmax (tensor.h:236) ----
+// Same parameters as the reference; x is a DEVICE pointer here (rows x cols
+// floats inside a backend_hip block).
+void softmax_rows_(float* x, int64_t rows, int64_t cols, float scale, bool causal);
+// Convenience: the whole tensor viewed as [numel / last dim, last dim].
+void softmax_rows_(Tensor& x, float scale, bool causal);
+
+// ---- fused (no single tensor.h counterpart) ----
+// add_(x, r); return rms_norm(x, gamma, eps)   (zimage.cpp:123-128 order)
+Tensor add_rms_norm_(Tensor& x, const Tensor& r, const Tensor* gamma, float eps);
+// group_norm then silu_   (modules.cpp:34-35, vae.cpp:48-49)
+Tensor group_norm_silu(const Tensor& x, int groups, const Tensor& gamma, const Tensor& beta, float eps);
+// y = layer_norm(x, no affine) * (1 + scale) + shift; res += tanh(gate) * y
+// (zimage.cpp:104-107, :221-224). shift and y_out may be null.
+void ln_modulate_gate_(const Tensor& x, Tensor& res, const Tensor& scale, const Tensor* shift, const Tensor& gate,
+                       float eps, Tensor* y_out = nullptr);
+// rope_(q, ...) then rope_(k, ...) in one launch (zimage.cpp:119-120)
+void rope_qk_(Tensor& q, Tensor& k, int64_t dim, const Tensor& cos, const Tensor& sin, bool interleaved);
+
+}  // namespace sdh
