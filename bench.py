@@ -480,7 +480,7 @@ def main():
         gbs = w.algo_bytes / (r["event_ms"] * 1e-3) / 1e9
         entry = dict(op=w.name, desc=w.desc, algo_bytes=w.algo_bytes, us_per_op=round(r["event_ms"] * 1e3, 2),
                      GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1), rotation_sets=r["nsets"],
-                     rotation_MB=round(r["footprint"] / 2**20))
+                     rotation_MB=round(r["footprint"] / 2**20), traffic_bytes=read_traffic(w.name))
         if args.cpu_all and not args.no_cpu:
             c = measure_cpu(w, 3 if w.algo_bytes > (1 << 30) else args.cpu_reps)
             if c:

@@ -8,14 +8,16 @@
 //     HBM sees exactly one read of every input and one write of every output;
 //     the statistics pass and the apply pass both run on registers.
 //   * Reductions are wave-only (DPP + readlane, sdh_internal.hpp); no LDS and
-//     no barrier, except the adaLN kernel, which stages its three column
-//     vectors in LDS once per 8 rows.
+//     no barrier, except the adaLN kernel (two waves per row, column vectors
+//     staged in LDS once per 4 rows).
 //   * The grid covers the rows exactly (4 rows per 256-thread workgroup, no
 //     persistent loop): measured on MI355X, letting the dispatcher refill CUs
 //     with fresh workgroups streams ~10 points of peak better than persistent
-//     waves. Row data is loaded with ordinary loads, per-column vectors
-//     (gamma, beta, scale, shift) come from L2, and every store is
-//     non-temporal.
+//     waves. Row data is loaded and stored non-temporally; per-column vectors
+//     (gamma, beta, scale, shift) come from L2. Measured: with ordinary
+//     (allocating) row loads the same kernels gain ~7 points when the
+//     benchmark rotates few buffer sets and lose ~8 points when it rotates
+//     many; non-temporal loads give the same bandwidth either way.
 // Statistics: the reference accumulates in double (tensor.cpp:640-648,
 // :672-674, :690-692). Here each lane accumulates its <= 4V values in fp32,
 // the wave tree adds 64 partials in fp32, and the final mean / rstd are
@@ -57,7 +59,7 @@ __global__ __launch_bounds__(kThreads) void k_rownorm(const float* __restrict__ 
 #pragma unroll
     for (int j = 0; j < V; ++j) {
         const int idx = lane + 64 * j;
-        v[j] = idx < n4 ? xr[idx] : zero4();
+        v[j] = idx < n4 ? dev::ld_stream(xr + idx) : zero4();
     }
     float mean = 0.f, rstd;
     if constexpr (MODE == M_LN) {
@@ -122,7 +124,7 @@ __global__ __launch_bounds__(kThreads) void k_add_rms(float* __restrict__ x, con
 #pragma unroll
     for (int j = 0; j < V; ++j) {
         const int idx = lane + 64 * j;
-        v[j] = idx < n4 ? xr[idx] + rr[idx] : zero4();
+        v[j] = idx < n4 ? dev::ld_stream(xr + idx) + dev::ld_stream(rr + idx) : zero4();
     }
     float q = 0.f;
 #pragma unroll
@@ -144,63 +146,71 @@ __global__ __launch_bounds__(kThreads) void k_add_rms(float* __restrict__ x, con
 }
 
 // Fused adaLN chain (see sdh_ln_modulate_gate). A 512-thread workgroup owns
-// kModRows rows, one per wave. It first issues its rows' loads, then stages
-// 1 + scale (affine_(scale, 1, 1)), shift and tanh(gate) for all C columns
-// in LDS (the affine_ / tanh_ prologue of zimage.cpp:104-107, done once per
-// kModRows rows), then each wave finishes its row from registers + LDS.
-// Measured on MI355X: 8 rows per workgroup beats both 4 (prologue cost) and
-// 16 (one workgroup per CU, no refill) and the variant that reads the three
-// vectors per element from L2.
-constexpr int kModRows = 8;
+// kModRows = 4 rows, two waves (128 threads, V float4 each) per row. It first
+// issues its rows' loads, then stages 1 + scale (affine_(scale, 1, 1)), shift
+// and tanh(gate) for all C columns in LDS (the affine_ / tanh_ prologue of
+// zimage.cpp:104-107, once per 4 rows), combines each row's two wave
+// partials through LDS, and finishes from registers + LDS. Two waves per row
+// halve the live registers per lane against one wave per row (168 -> ~90
+// VGPRs), doubling the waves in flight; measured the fastest of the variants
+// tried (1 wave/row with 8 rows per block, L2 gathers of the vectors, 2 or 8
+// rows per block).
+constexpr int kModRows = 4;
+constexpr int kModThreads = kModRows * 128;
 
 template <int V, bool HAS_SHIFT, bool STORE_Y>
-__global__ __launch_bounds__(kModRows * 64) void k_ln_mod_gate(const float* __restrict__ x, float* __restrict__ res,
-                                                              const float* __restrict__ scale,
-                                                              const float* __restrict__ shift,
-                                                              const float* __restrict__ gate,
-                                                              float* __restrict__ yout, int64_t rows, int C,
-                                                              float eps) {
+__global__ __launch_bounds__(kModThreads) void k_ln_mod_gate(const float* __restrict__ x, float* __restrict__ res,
+                                                            const float* __restrict__ scale,
+                                                            const float* __restrict__ shift,
+                                                            const float* __restrict__ gate, float* __restrict__ yout,
+                                                            int64_t rows, int C, float eps) {
     extern __shared__ f4 lds[];  // [3][n4]: 1+scale | shift | tanh(gate)
-    const int lane = threadIdx.x & 63;
+    __shared__ float red[2 * kModRows * 2];
     const int n4 = C >> 2;
     f4* s1 = lds;
     f4* sh = lds + n4;
     f4* tg = lds + 2 * n4;
-    const int64_t row = (int64_t)blockIdx.x * kModRows + (threadIdx.x >> 6);
+    const int sub = threadIdx.x >> 7, t = threadIdx.x & 127, w = threadIdx.x >> 6;
+    const int64_t row = (int64_t)blockIdx.x * kModRows + sub;
     const bool ok = row < rows;
     const f4* xr = (const f4*)(x + row * C);
     f4* rr = (f4*)(res + row * C);
     f4 v[V], rv[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-        const int idx = lane + 64 * j;
-        v[j] = (ok && idx < n4) ? xr[idx] : zero4();
-        rv[j] = (ok && idx < n4) ? rr[idx] : zero4();
+        const int idx = t + 128 * j;
+        v[j] = (ok && idx < n4) ? dev::ld_stream(xr + idx) : zero4();
+        rv[j] = (ok && idx < n4) ? dev::ld_stream(rr + idx) : zero4();
     }
-    for (int i = threadIdx.x; i < n4; i += kModRows * 64) {
+    for (int i = threadIdx.x; i < n4; i += kModThreads) {
         s1[i] = ((const f4*)scale)[i] * 1.0f + 1.0f;
         if constexpr (HAS_SHIFT) sh[i] = ((const f4*)shift)[i];
         const f4 gt = ((const f4*)gate)[i];
         tg[i] = f4{tanhf(gt.x), tanhf(gt.y), tanhf(gt.z), tanhf(gt.w)};
     }
-    __syncthreads();
-    if (!ok) return;
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < V; ++j) s += dev::hsum(v[j]);
-    const float mean = (float)((double)dev::wave_sum(s) / (double)C);
+    s = dev::wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[w] = s;
+    __syncthreads();  // also publishes the staged vectors
+    const float mean = (float)((double)(red[2 * sub] + red[2 * sub + 1]) / (double)C);
     float q = 0.f;
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-        if (lane + 64 * j < n4) {
+        if (t + 128 * j < n4) {
             const f4 d = v[j] - mean;
             q += dev::hsum(d * d);
         }
     }
-    const float rstd = rstd_of(dev::wave_sum(q), C, eps);
+    q = dev::wave_sum(q);
+    if ((threadIdx.x & 63) == 0) red[2 * kModRows + w] = q;
+    __syncthreads();
+    if (!ok) return;
+    const float rstd = rstd_of(red[2 * kModRows + 2 * sub] + red[2 * kModRows + 2 * sub + 1], C, eps);
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-        const int idx = lane + 64 * j;
+        const int idx = t + 128 * j;
         if (idx < n4) {
             const f4 ln = (v[j] - mean) * rstd;  // layer_norm, no affine
             const f4 m = s1[idx];
@@ -462,22 +472,31 @@ int sdh_ln_modulate_gate(const float* x, float* res, const float* scale, const f
         if (shift) check_range(shift, (size_t)C * 4, op, "shift");
         if (y_out) check_range(y_out, bytes, op, "y_out");
         const size_t lds = (size_t)3 * C * 4;
-        if (vec_ok(C, {x, res, scale, shift, gate, y_out}) && lds <= 64 * 1024) {
+        const int64_t n4 = C / 4;
+        const int v = n4 <= 128 ? 1 : n4 <= 256 ? 2 : n4 <= 512 ? 4 : n4 <= 1024 ? 8 : n4 <= 1536 ? 12 : n4 <= 2048 ? 16 : 0;
+        if (vec_ok(C, {x, res, scale, shift, gate, y_out}) && lds <= 64 * 1024 && v) {
             const int64_t blocks = (rows + kModRows - 1) / kModRows;
             need(blocks <= 0x7fffffffLL, op, "too many rows for one launch");
             const unsigned grid = (unsigned)blocks;
-            const unsigned tpb = kModRows * 64;
-            with_v(pick_v(C / 4), [&](auto vc) {
+            auto go = [&](auto vc) {
                 constexpr int V = decltype(vc)::value;
                 if (shift && y_out)
-                    k_ln_mod_gate<V, true, true><<<grid, tpb, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
+                    k_ln_mod_gate<V, true, true><<<grid, kModThreads, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
                 else if (shift)
-                    k_ln_mod_gate<V, true, false><<<grid, tpb, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
+                    k_ln_mod_gate<V, true, false><<<grid, kModThreads, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
                 else if (y_out)
-                    k_ln_mod_gate<V, false, true><<<grid, tpb, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
+                    k_ln_mod_gate<V, false, true><<<grid, kModThreads, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
                 else
-                    k_ln_mod_gate<V, false, false><<<grid, tpb, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
-            });
+                    k_ln_mod_gate<V, false, false><<<grid, kModThreads, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
+            };
+            switch (v) {
+                case 1: go(std::integral_constant<int, 1>()); break;
+                case 2: go(std::integral_constant<int, 2>()); break;
+                case 4: go(std::integral_constant<int, 4>()); break;
+                case 8: go(std::integral_constant<int, 8>()); break;
+                case 12: go(std::integral_constant<int, 12>()); break;
+                default: go(std::integral_constant<int, 16>()); break;
+            }
         } else {
             k_ln_mod_gate_generic<<<row_grid(rows, 32), kThreads, 0, stream()>>>(x, res, scale, shift, gate, y_out,
                                                                                 rows, C, eps);
