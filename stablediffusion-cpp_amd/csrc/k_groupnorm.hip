@@ -32,6 +32,9 @@
 //     (re-reading 64-512 MB is no faster than the first read), so for
 //     tensors much larger than L2 this schedule moves three streams (x, x,
 //     y) against the two of the algorithmic minimum.
+#include <algorithm>
+#include <cstdlib>
+
 #include "sdh_internal.hpp"
 
 namespace sdh {
@@ -42,6 +45,7 @@ using dev::f4;
 constexpr int kThreads = 256;
 constexpr int kChunkV = 8;                               // float4 per thread per chunk
 constexpr int64_t kChunk = (int64_t)kThreads * 4 * kChunkV;  // floats per chunk (8192)
+constexpr int64_t kGnBlockMB = 0;
 
 // SiLU on the hardware exp2 and reciprocal: x * rcp(1 + 2^(-x log2 e)). Its
 // error against the correctly rounded x / (1 + expf(-x)) is a few ulp (the
@@ -186,7 +190,7 @@ __global__ __launch_bounds__(64) void k_gn_finalize(const float2* __restrict__ p
 // kernel's VGPR count and cost a third of its bandwidth.
 template <bool SILU, bool UNIFORM>
 __global__ __launch_bounds__(kThreads) void k_gn_apply(const float* __restrict__ x, float* __restrict__ y, int64_t L,
-                                                      int HW, int chunks_per_ch, int cg, int groups, int nchunks,
+                                                      int HW, int chunks_per_ch, int cg, int groups, int seg0,
                                                       const float2* __restrict__ stats,
                                                       const float* __restrict__ gamma,
                                                       const float* __restrict__ beta) {
@@ -196,7 +200,7 @@ __global__ __launch_bounds__(kThreads) void k_gn_apply(const float* __restrict__
     f4* q = (f4*)(y + (int64_t)seg * L + off);
     const float2 st = stats[seg];
     const float meanf = st.x, rstd = st.y;
-    const int gc = (seg % groups) * cg;
+    const int gc = ((seg0 + seg) % groups) * cg;
     if constexpr (UNIFORM) {
         f4 v[kChunkV];
 #pragma unroll
@@ -272,6 +276,23 @@ __global__ __launch_bounds__(kThreads) void k_gn_generic(const float* x, float* 
     }
 }
 
+// Bytes of input per block of the split schedule (SDH_GN_BLOCK_MB; 0 = the
+// whole tensor in one block, the default). Blocks exist for the grid's
+// 65535-segment limit; smaller blocks, so that the apply pass would re-read
+// a block from cache, measured slower on MI355X at every size from 8 to 128
+// MB (4b: 249 us whole, 258-431 us blocked), so the knob serves tests of the
+// multi-block path at small sizes.
+int64_t gn_block_bytes() {
+    static const int64_t v = [] {
+        const char* e = std::getenv("SDH_GN_BLOCK_MB");
+        if (!e || !*e) return (int64_t)kGnBlockMB << 20;
+        char* end = nullptr;
+        const long long mb = std::strtoll(e, &end, 10);
+        return (end && *end == 0 && mb >= 0) ? (int64_t)mb << 20 : (int64_t)kGnBlockMB << 20;
+    }();
+    return v;
+}
+
 void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups,
             const float* gamma, const float* beta, float eps) {
     need(N >= 0 && C >= 0 && HW >= 0, op, "negative size");
@@ -307,29 +328,41 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
         else if (n4 <= 8192) go(K(), std::integral_constant<int, 8>());
         else if (n4 <= 12288) go(K(), std::integral_constant<int, 12>());
         else go(K(), std::integral_constant<int, 16>());
-    } else if (vec && nseg <= 65535) {
+    } else if (vec) {
         const int64_t nchunks = (L + kChunk - 1) / kChunk;
-        need(nchunks <= 0x7fffffffLL, op, "segment too large");
-        const size_t part_bytes = ((size_t)(nseg * nchunks) * sizeof(float2) + 255) / 256 * 256;
-        char* scr = (char*)scratch(part_bytes + (size_t)nseg * sizeof(float2));
+        // segments per block: the apply pass re-reads a block right after
+        // the partial pass read it, while it is still cached
+        int64_t sb = nseg;
+        const int64_t budget = gn_block_bytes();
+        if (budget > 0) sb = std::max<int64_t>(1, std::min<int64_t>(nseg, budget / (L * 4)));
+        sb = std::min<int64_t>(sb, 65535);
+        const size_t part_bytes = ((size_t)(sb * nchunks) * sizeof(float2) + 255) / 256 * 256;
+        char* scr = (char*)scratch(part_bytes + (size_t)sb * sizeof(float2));
         float2* part = (float2*)scr;
         float2* stats = (float2*)(scr + part_bytes);
-        const dim3 grid((unsigned)nchunks, (unsigned)nseg);
-        k_gn_partial<<<grid, kThreads, 0, stream()>>>(x, L, nchunks, part);
-        launched(op);
-        k_gn_finalize<<<(unsigned)nseg, 64, 0, stream()>>>(part, L, nchunks, stats, eps);
-        launched(op);
         const bool uniform = HW % kChunk == 0;
         const int cpc = uniform ? (int)(HW / kChunk) : 1;
-        auto apply = [&](auto sc, auto uc) {
-            constexpr bool S = decltype(sc)::value, U = decltype(uc)::value;
-            k_gn_apply<S, U><<<grid, kThreads, 0, stream()>>>(x, y, L, (int)HW, cpc, (int)cg, groups, (int)nchunks,
-                                                              stats, gamma, beta);
-        };
-        using T_ = std::true_type;
-        using F_ = std::false_type;
-        if (silu) uniform ? apply(T_(), T_()) : apply(T_(), F_());
-        else uniform ? apply(F_(), T_()) : apply(F_(), F_());
+        for (int64_t s0 = 0; s0 < nseg; s0 += sb) {
+            const int64_t k = std::min<int64_t>(sb, nseg - s0);
+            const float* xb = x + s0 * L;
+            float* yb = y + s0 * L;
+            const dim3 grid((unsigned)nchunks, (unsigned)k);
+            k_gn_partial<<<grid, kThreads, 0, stream()>>>(xb, L, nchunks, part);
+            launched(op);
+            k_gn_finalize<<<(unsigned)k, 64, 0, stream()>>>(part, L, nchunks, stats, eps);
+            launched(op);
+            const int seg0 = (int)(s0 % groups);
+            auto apply = [&](auto sc, auto uc) {
+                constexpr bool S = decltype(sc)::value, U = decltype(uc)::value;
+                k_gn_apply<S, U><<<grid, kThreads, 0, stream()>>>(xb, yb, L, (int)HW, cpc, (int)cg, groups, seg0,
+                                                                  stats, gamma, beta);
+            };
+            using T_ = std::true_type;
+            using F_ = std::false_type;
+            if (silu) uniform ? apply(T_(), T_()) : apply(T_(), F_());
+            else uniform ? apply(F_(), T_()) : apply(F_(), F_());
+            if (s0 + sb < nseg) launched(op);
+        }
     } else {
         need(nseg <= 0x7fffffffLL, op, "too many groups");
         if (silu)

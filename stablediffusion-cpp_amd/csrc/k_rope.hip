@@ -3,14 +3,20 @@
 //
 // x is [N, S, inner] with inner = heads * dim; the tables are [S, dim].
 // A workgroup owns one token row (one (n, s)) of one tensor: blockIdx.x is the
-// row, blockIdx.y picks Q or K. Its threads sweep the row in float4 steps, so
+// row, blockIdx.y picks Q or K. Its threads cover the row in float4 steps, so
 // every HBM access is a coalesced 128-bit load/store and each table row is
-// fetched once per token and reused from cache by all heads.
+// fetched once per token and reused from cache by all heads. Rows of up to
+// 8 float4 per thread (16 interleaved / 4 rotate_half pairs when the head size
+// divides the workgroup, 2 pairs otherwise) are held in registers, all loads
+// before any store; wider rows use the looping kernels.
 //   interleaved: float4 (a0, b0, a1, b1) holds pairs (2i, 2i+1), (2i+2, 2i+3),
 //                rotated by cos/sin[s, 2i] and [s, 2i+2] (the even entries, as
 //                tensor.cpp:717-718 uses c[i] and sn[i] for both outputs).
 //   rotate_half: the float4 at head offset i < dim/2 pairs with the float4 at
 //                i + dim/2 (tensor.cpp:722-724); one thread updates both.
+#include <algorithm>
+#include <type_traits>
+
 #include "sdh_internal.hpp"
 
 namespace sdh {
@@ -24,6 +30,108 @@ struct RopeArgs {
     float* x[2];
     int64_t inner[2];
 };
+
+// Row in registers: RV float4 per thread, every load of the row issued before
+// any store (the in-place stores would otherwise order each step's loads
+// behind the previous step's stores). HINV: the head size divides the
+// workgroup, so a thread's position inside the head, and with it its table
+// entries, is the same at every step and the table is loaded once.
+template <int RV, bool HINV>
+__global__ __launch_bounds__(kThreads) void k_rope_il_reg(RopeArgs a, int64_t S, int dim,
+                                                         const float* __restrict__ cs,
+                                                         const float* __restrict__ sn) {
+    const int t = blockIdx.y;
+    const int64_t ns = blockIdx.x;
+    const int64_t inner = a.inner[t];
+    const int64_t s = ns % S;
+    f4* row = (f4*)(a.x[t] + ns * inner);
+    const f4* c4 = (const f4*)(cs + s * dim);
+    const f4* s4 = (const f4*)(sn + s * dim);
+    const int n4 = (int)(inner >> 2), d4 = dim >> 2;
+    f4 v[RV], c[HINV ? 1 : RV], sv[HINV ? 1 : RV];
+#pragma unroll
+    for (int j = 0; j < RV; ++j) {
+        const int i = threadIdx.x + kThreads * j;
+        if (i < n4) v[j] = dev::ld_stream(row + i);
+    }
+    if constexpr (HINV) {
+        const int h = threadIdx.x % d4;
+        c[0] = c4[h];
+        sv[0] = s4[h];
+    } else {
+#pragma unroll
+        for (int j = 0; j < RV; ++j) {
+            const int i = threadIdx.x + kThreads * j;
+            if (i < n4) {
+                c[j] = c4[i % d4];
+                sv[j] = s4[i % d4];
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < RV; ++j) {
+        const int i = threadIdx.x + kThreads * j;
+        if (i < n4) {
+            const f4 cc = c[HINV ? 0 : j], ss = sv[HINV ? 0 : j];
+            f4 o;
+            o.x = v[j].x * cc.x - v[j].y * ss.x;
+            o.y = v[j].y * cc.x + v[j].x * ss.x;
+            o.z = v[j].z * cc.z - v[j].w * ss.z;
+            o.w = v[j].w * cc.z + v[j].z * ss.z;
+            dev::st_stream(row + i, o);
+        }
+    }
+}
+
+template <int RV, bool HINV>
+__global__ __launch_bounds__(kThreads) void k_rope_half_reg(RopeArgs a, int64_t S, int dim,
+                                                           const float* __restrict__ cs,
+                                                           const float* __restrict__ sn) {
+    const int t = blockIdx.y;
+    const int64_t ns = blockIdx.x;
+    const int64_t inner = a.inner[t];
+    const int64_t s = ns % S;
+    f4* row = (f4*)(a.x[t] + ns * inner);
+    const f4* c4 = (const f4*)(cs + s * dim);
+    const f4* s4 = (const f4*)(sn + s * dim);
+    const int h4 = dim >> 3;                    // float4 per half head
+    const int pairs = (int)(inner / dim) * h4;  // float4 pairs per row
+    f4 lo[RV], hi[RV];
+    constexpr int TB = HINV ? 1 : RV;
+    f4 cl[TB], sl[TB], ch[TB], sh[TB];
+#pragma unroll
+    for (int j = 0; j < RV; ++j) {
+        const int i = threadIdx.x + kThreads * j;
+        if (i < pairs) {
+            const int head = i / h4, k = i - head * h4;
+            f4* p = row + head * (dim >> 2) + k;
+            lo[j] = dev::ld_stream(p);
+            hi[j] = dev::ld_stream(p + h4);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < TB; ++j) {
+        const int i = threadIdx.x + kThreads * j;
+        if (HINV || i < pairs) {
+            const int k = i % h4;
+            cl[j] = c4[k];
+            sl[j] = s4[k];
+            ch[j] = c4[k + h4];
+            sh[j] = s4[k + h4];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < RV; ++j) {
+        const int i = threadIdx.x + kThreads * j;
+        if (i < pairs) {
+            const int head = i / h4, k = i - head * h4;
+            f4* p = row + head * (dim >> 2) + k;
+            const int b = HINV ? 0 : j;
+            dev::st_stream(p, lo[j] * cl[b] - hi[j] * sl[b]);
+            dev::st_stream(p + h4, hi[j] * ch[b] + lo[j] * sh[b]);
+        }
+    }
+}
 
 __global__ __launch_bounds__(kThreads) void k_rope_interleaved(RopeArgs a, int64_t S, int dim,
                                                               const float* __restrict__ cs,
@@ -116,10 +224,35 @@ void run_rope(const char* op, float* q, int64_t inner_q, float* k, int64_t inner
     a.x[1] = k ? k : q;
     a.inner[1] = k ? inner_k : inner_q;
     const bool al = aligned16(q) && (!k || aligned16(k)) && aligned16(cs) && aligned16(sn);
+    const dim3 grid((unsigned)(N * S), nt);
+    const int64_t inner_max = std::max(inner_q, k ? inner_k : inner_q);
     if (interleaved && al && dim % 4 == 0 && inner_q % 4 == 0 && inner_k % 4 == 0) {
-        k_rope_interleaved<<<dim3((unsigned)(N * S), nt), kThreads, 0, stream()>>>(a, S, (int)dim, cs, sn);
+        // float4 per thread of the widest row
+        const int64_t steps = (inner_max / 4 + kThreads - 1) / kThreads;
+        const bool hinv = kThreads % (dim / 4) == 0;
+        auto go = [&](auto rc) {
+            constexpr int RV = decltype(rc)::value;
+            if (hinv) k_rope_il_reg<RV, true><<<grid, kThreads, 0, stream()>>>(a, S, (int)dim, cs, sn);
+            else k_rope_il_reg<RV, false><<<grid, kThreads, 0, stream()>>>(a, S, (int)dim, cs, sn);
+        };
+        if (steps <= 1) go(std::integral_constant<int, 1>());
+        else if (steps <= 2) go(std::integral_constant<int, 2>());
+        else if (steps <= 4) go(std::integral_constant<int, 4>());
+        else if (steps <= 8) go(std::integral_constant<int, 8>());
+        else if (steps <= 16 && hinv) k_rope_il_reg<16, true><<<grid, kThreads, 0, stream()>>>(a, S, (int)dim, cs, sn);
+        else k_rope_interleaved<<<grid, kThreads, 0, stream()>>>(a, S, (int)dim, cs, sn);
     } else if (!interleaved && al && dim % 8 == 0) {
-        k_rope_half<<<dim3((unsigned)(N * S), nt), kThreads, 0, stream()>>>(a, S, (int)dim, cs, sn);
+        const int64_t steps = ((inner_max / dim) * (dim / 8) + kThreads - 1) / kThreads;
+        const bool hinv = kThreads % (dim / 8) == 0;
+        auto go = [&](auto rc) {
+            constexpr int RV = decltype(rc)::value;
+            if (hinv) k_rope_half_reg<RV, true><<<grid, kThreads, 0, stream()>>>(a, S, (int)dim, cs, sn);
+            else k_rope_half_reg<RV, false><<<grid, kThreads, 0, stream()>>>(a, S, (int)dim, cs, sn);
+        };
+        if (steps <= 1) go(std::integral_constant<int, 1>());
+        else if (steps <= 2) go(std::integral_constant<int, 2>());
+        else if (steps <= 4 && hinv) k_rope_half_reg<4, true><<<grid, kThreads, 0, stream()>>>(a, S, (int)dim, cs, sn);
+        else k_rope_half<<<grid, kThreads, 0, stream()>>>(a, S, (int)dim, cs, sn);
     } else {
         const int64_t total = N * S * (std::max(inner_q, inner_k) / dim) * (dim / 2);
         const int64_t want = (total + kThreads - 1) / kThreads;

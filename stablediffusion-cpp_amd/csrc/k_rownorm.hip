@@ -146,9 +146,9 @@ __global__ __launch_bounds__(kThreads) void k_add_rms(float* __restrict__ x, con
 }
 
 // Fused adaLN chain (see sdh_ln_modulate_gate). A 512-thread workgroup owns
-// kModRows = 4 rows, two waves (128 threads, V float4 each) per row. It first
-// issues its rows' loads, then stages 1 + scale (affine_(scale, 1, 1)), shift
-// and tanh(gate) for all C columns in LDS (the affine_ / tanh_ prologue of
+// kModRows = 4 rows, two waves (128 threads, V float4 each) per row. It
+// stages 1 + scale (affine_(scale, 1, 1)), shift and tanh(gate) for all C
+// columns in LDS (the affine_ / tanh_ prologue of
 // zimage.cpp:104-107, once per 4 rows), combines each row's two wave
 // partials through LDS, and finishes from registers + LDS. Two waves per row
 // halve the live registers per lane against one wave per row (168 -> ~90
@@ -175,18 +175,40 @@ __global__ __launch_bounds__(kModThreads) void k_ln_mod_gate(const float* __rest
     const bool ok = row < rows;
     const f4* xr = (const f4*)(x + row * C);
     f4* rr = (f4*)(res + row * C);
+    // Issue order: the column vectors (L2 hits) first, then x, then res.
+    // Loads complete in order, so the staging below waits only for the
+    // vectors while the row loads are in flight, and the mean only for x.
+    constexpr int SV = (V + 3) / 4;  // staged float4 per thread: n4 <= 128 V
+    f4 ssc[SV], ssh[SV], sgt[SV];
+#pragma unroll
+    for (int k = 0; k < SV; ++k) {
+        const int i = threadIdx.x + kModThreads * k;
+        if (i < n4) {
+            ssc[k] = ((const f4*)scale)[i];
+            if constexpr (HAS_SHIFT) ssh[k] = ((const f4*)shift)[i];
+            sgt[k] = ((const f4*)gate)[i];
+        }
+    }
     f4 v[V], rv[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {
         const int idx = t + 128 * j;
         v[j] = (ok && idx < n4) ? dev::ld_stream(xr + idx) : zero4();
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = t + 128 * j;
         rv[j] = (ok && idx < n4) ? dev::ld_stream(rr + idx) : zero4();
     }
-    for (int i = threadIdx.x; i < n4; i += kModThreads) {
-        s1[i] = ((const f4*)scale)[i] * 1.0f + 1.0f;
-        if constexpr (HAS_SHIFT) sh[i] = ((const f4*)shift)[i];
-        const f4 gt = ((const f4*)gate)[i];
-        tg[i] = f4{tanhf(gt.x), tanhf(gt.y), tanhf(gt.z), tanhf(gt.w)};
+#pragma unroll
+    for (int k = 0; k < SV; ++k) {
+        const int i = threadIdx.x + kModThreads * k;
+        if (i < n4) {
+            s1[i] = ssc[k] * 1.0f + 1.0f;
+            if constexpr (HAS_SHIFT) sh[i] = ssh[k];
+            sgt[k] = f4{tanhf(sgt[k].x), tanhf(sgt[k].y), tanhf(sgt[k].z), tanhf(sgt[k].w)};
+            tg[i] = sgt[k];
+        }
     }
     float s = 0.f;
 #pragma unroll

@@ -9,6 +9,9 @@ shapes (Z-Image 1024^2: T=4096 tokens, D=3840, F=10240; FLUX-VAE and SD 1.5
 GroupNorm shapes). Tolerances are defined in tolerances.py.
 """
 import math
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -19,6 +22,9 @@ from tolerances import assert_elementwise, assert_reduction, assert_softmax
 pytestmark = pytest.mark.gpu
 
 T, D, F = 4096, 3840, 10240
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG_DIR = os.path.join(ROOT, "stablediffusion-cpp_amd")
+ORACLE_DIR = os.path.join(ROOT, "oracle")
 
 
 def _seed(*parts):
@@ -205,6 +211,50 @@ def test_group_norm_inplace_and_repeat(be, orc):
         assert_reduction(dx.download(), want, "group_norm_silu in place")
 
 
+def test_group_norm_interleaved_shapes(be, orc):
+    """Consecutive calls with different shapes and schedules, in place,
+    each checked (scratch partials and statistics are reused across calls)."""
+    cases = [((1, 512, 128, 128), 1e-6), ((2, 320, 64, 64), 1e-5), ((1, 64, 256, 256), 1e-6)]
+    data = []
+    for i, (shape, eps) in enumerate(cases):
+        x = orc.randn(shape, 300 + i, 0.5, 2.0)
+        g = orc.randn((shape[1],), 310 + i, 1.0, 0.1)
+        b = orc.randn((shape[1],), 320 + i, 0.0, 0.1)
+        data.append((shape, eps, x, be.array(g), be.array(b), orc.group_norm(x, 32, g, b, eps, silu=True)))
+    for rep in range(2):
+        for shape, eps, x, dg, db, want in data + data[::-1]:
+            dx = be.array(x)
+            N, Cc = shape[0], shape[1]
+            be.group_norm(dx, dx, N, Cc, x.size // (N * Cc), 32, dg, db, eps, silu=True)
+            assert_reduction(dx.download(), want, f"group_norm_silu {shape} rep {rep}")
+
+
+def test_group_norm_segment_blocks():
+    """The split schedule run block by block (SDH_GN_BLOCK_MB=2, in a child
+    process): blocks that start inside a sample's groups (channel offset),
+    one-segment blocks, and a plane that is not a whole number of chunks."""
+    code = (
+        "import sys; sys.path[:0] = [%r, %r]\n"
+        "import numpy as np, sdhip\n"
+        "from oracle import Oracle\n"
+        "be, orc = sdhip.Backend(), Oracle()\n"
+        "for shape, groups, eps in (((2, 64, 256, 256), 32, 1e-6), ((1, 32, 300, 300), 8, 1e-5), ((1, 512, 128, 128), 32, 1e-6)):\n"
+        "    for silu in (True, False):\n"
+        "        x = orc.randn(shape, 5, 0.5, 2.0); g = orc.randn((shape[1],), 6, 1.0, 0.1); b = orc.randn((shape[1],), 7, 0.0, 0.1)\n"
+        "        d, o = be.array(x), be.empty(shape); N, C = shape[0], shape[1]\n"
+        "        be.group_norm(d, o, N, C, x.size // (N * C), groups, be.array(g), be.array(b), eps, silu=silu)\n"
+        "        want = orc.group_norm(x, groups, g, b, eps, silu=silu)\n"
+        "        err = float(np.max(np.abs(o.download() - want) / np.maximum(np.abs(want), 1.0)))\n"
+        "        print(shape, silu, err, flush=True)\n"
+        "        assert err <= 1e-4, (shape, silu, err)\n"
+        "print('blocks ok')\n"
+    ) % (PKG_DIR, ORACLE_DIR)
+    env = dict(os.environ, SDH_GN_BLOCK_MB="2")
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=180, env=env)
+    print(r.stdout)
+    assert r.returncode == 0 and "blocks ok" in r.stdout, r.stdout + r.stderr
+
+
 # ---------------------------------------------------------------- softmax
 @pytest.mark.parametrize("rows,cols", [(9, 9), (64, 4096), (100, 100), (5, 4128), (3, 9000), (7, 1)])
 @pytest.mark.parametrize("causal", [False, True])
@@ -253,6 +303,28 @@ def test_rope(be, orc, interleaved, N, S, heads, dim):
     dx = be.array(x)
     be.rope(dx, N, S, heads * dim, dim, be.array(cs), be.array(sn), interleaved)
     assert_elementwise(dx.download(), orc.rope(x, dim, cs, sn, interleaved), f"rope inter={interleaved}")
+
+
+# (heads, dim) chosen to reach every register-resident form: 1/2/4/8/16 float4
+# per thread (interleaved) and 1/2/4 pairs (rotate_half), with head sizes that
+# divide the 256-thread workgroup (table loaded once) and that do not (dim 24),
+# plus rows too wide for registers (the looping kernels).
+ROPE_DISPATCH = [
+    (True, 40, 24), (True, 100, 24), (True, 200, 24), (True, 350, 24),
+    (True, 60, 128), (True, 120, 128), (True, 140, 128),
+    (False, 30, 128), (False, 60, 128), (False, 70, 128), (False, 40, 24), (False, 150, 24), (False, 200, 24),
+]
+
+
+@pytest.mark.parametrize("interleaved,heads,dim", ROPE_DISPATCH)
+def test_rope_dispatch(be, orc, interleaved, heads, dim):
+    N, S = 1, 3
+    x = orc.randn((N, S, heads * dim), _seed("ropd", heads, dim))
+    ang = orc.randn((S, dim), _seed("ropd_t", dim), 0.0, 1.0)
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    dx = be.array(x)
+    be.rope(dx, N, S, heads * dim, dim, be.array(cs), be.array(sn), interleaved)
+    assert_elementwise(dx.download(), orc.rope(x, dim, cs, sn, interleaved), f"rope inter={interleaved} {heads}x{dim}")
 
 
 def test_rope_qk_config_3(be, orc):
