@@ -123,7 +123,7 @@ class SwiGLU(Workload):
 
 
 class RopeQK(Workload):
-    name, kernel = "rope_qk", "k_rope_interleaved"
+    name, kernel = "rope_qk", "k_rope_il_reg"
     desc = ("config 3: 3-axis interleaved RoPE in place on q and k [4096,30*128] in one launch, axes (32,48,48), "
             "theta 256, reference-format duplicated cos/sin tables [4096,128]")
     algo_bytes = 4 * T * D * 4 + 2 * T * 128 * 4
@@ -363,8 +363,25 @@ def read_traffic(name):
 # ------------------------------------------------------------------ rocprofv3 summaries
 KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
     "k_unary<4>": "copy_calibration", "k_add_rms": "add_rms_norm", "k_swiglu": "swiglu",
-    "k_rope_interleaved": "rope_qk", "k_ln_mod_gate": "ln_modulate_gate", "k_softmax_block": "softmax_rows",
+    "k_rope_il_reg": "rope_qk", "k_ln_mod_gate": "ln_modulate_gate", "k_softmax_block": "softmax_rows",
 }
+
+
+def gn_dispatches(shape, groups=32):
+    """(kernel prefix, grid work-items) of the launches that carry a GroupNorm
+    workload's HBM traffic, following run_gn's choice of schedule: one
+    k_gn_single launch for segments up to 65536 floats, else k_gn_partial and
+    k_gn_apply over 8192-float chunks (k_gn_finalize moves a few KB and is
+    left out)."""
+    N, Cc = shape[0], shape[1]
+    HW = int(np.prod(shape[2:]))
+    L, nseg = Cc // groups * HW, N * groups
+    if L <= 65536:
+        n4 = L // 4
+        tpb = 256 if n4 <= 2048 else 1024
+        return [("k_gn_single", nseg * tpb)]
+    grid = (L + 8191) // 8192 * 256 * nseg
+    return [("k_gn_partial", grid), ("k_gn_apply", grid)]
 
 
 def _kernel_key(full_name):
@@ -422,6 +439,16 @@ def rocprof_summary(trace_dir, fetch_dir=None, write_dir=None):
             wl = next((v for kk, v in KERNEL_OF.items() if k[0].startswith(kk)), None)
             if wl:
                 traffic_lines.append(f"{wl} kernel={k[0]} grid={k[1]} fetch_kib={f[k]:.1f} write_kib={w.get(k, 0.0):.1f} "
+                                     f"fetch_factor={ff:.4f} write_factor={wf:.4f} traffic_bytes={tb}")
+        for wl in all_workloads():
+            if not isinstance(wl, GNSiLU):
+                continue
+            ks = [k for pre, g in gn_dispatches(wl.shape) for k in f if k[0].startswith(pre) and k[1] == g]
+            if ks:
+                fk, wk = sum(f[k] for k in ks), sum(w.get(k, 0.0) for k in ks)
+                tb = int(round((fk * ff + wk * wf) * 1024))
+                names = "+".join(k[0] for k in ks)
+                traffic_lines.append(f"{wl.name} kernel={names} grid={ks[0][1]} fetch_kib={fk:.1f} write_kib={wk:.1f} "
                                      f"fetch_factor={ff:.4f} write_factor={wf:.4f} traffic_bytes={tb}")
     return text, traffic_lines
 
