@@ -240,6 +240,66 @@ class Softmax(Workload):
         return run, [hx]
 
 
+class Layout(Workload):
+    """Layout ops of the tensor library (tensor.cpp:931-1099) at the shapes
+    their callers use: bit-exact copies, HBM-bound at (read + write) bytes."""
+
+    SPECS = {
+        # name: (description, input shapes, output shape, kernel)
+        "upsample_nearest2x": ("VAE decoder upsample (vae.cpp:46): x [1,512,256,256] -> [1,512,512,512]",
+                               [(1, 512, 256, 256)], (1, 512, 512, 512), "k_upsample2x_vec"),
+        "nchw_to_nlc": ("VAE attention input (modules.cpp:136): [1,512,128,128] -> [1,16384,512]",
+                        [(1, 512, 128, 128)], (1, 16384, 512), "k_transpose_vec"),
+        "nlc_to_nchw": ("VAE attention output (modules.cpp:138): [1,16384,512] -> [1,512,128,128]",
+                        [(1, 16384, 512)], (1, 512, 128, 128), "k_transpose_vec"),
+        "concat_channels": ("SD 1.5 UNet skip concat (unet.cpp:113): [2,640,64,64] ++ [2,320,64,64]",
+                            [(2, 640, 64, 64), (2, 320, 64, 64)], (2, 960, 64, 64), "k_concat_vec"),
+        "patchify2d": ("Z-Image latent to tokens (zimage.cpp:165): [1,16,128,128], p 2 -> [4096,64]",
+                       [(1, 16, 128, 128)], (4096, 64), "k_patchify"),
+    }
+
+    def __init__(self, name):
+        self.name = name
+        self.desc, self.ins, self.out, self.kernel = self.SPECS[name]
+        n_in = sum(int(np.prod(s)) for s in self.ins)
+        self.algo_bytes = 4 * (n_in + int(np.prod(self.out)))
+
+    def make(self, be, i):
+        d = {f"x{k}": be.randn(s, 16000 + 100 * k + i) for k, s in enumerate(self.ins)}
+        d["y"] = be.empty(self.out)
+        return d
+
+    def step(self, be, s):
+        a, y = s["x0"], s["y"]
+        if self.name == "upsample_nearest2x":
+            N, Cc, H, W = self.ins[0]
+            be.upsample_nearest2x(a, y, N * Cc, H, W)
+        elif self.name == "nchw_to_nlc":
+            N, Cc, H, W = self.ins[0]
+            be.nchw_to_nlc(a, y, N, Cc, H * W)
+        elif self.name == "nlc_to_nchw":
+            N, HW, Cc = self.ins[0]
+            be.nlc_to_nchw(a, y, N, Cc, HW)
+        elif self.name == "concat_channels":
+            (N, Ca, H, W), (_, Cb, _, _) = self.ins
+            be.concat_channels(a, s["x1"], y, N, Ca, Cb, H * W)
+        else:
+            _, Cc, H, W = self.ins[0]
+            be.patchify(a, y, Cc, H, W, 2)
+
+    def cpu(self, R, orc):
+        xs = [orc.randn(sh, 16 + k) for k, sh in enumerate(self.ins)]
+        hs = [R.new(x.shape, x) for x in xs]
+        del xs
+        L = R.lib
+        fn = {"upsample_nearest2x": lambda: L.ref_upsample_nearest2x(hs[0]),
+              "nchw_to_nlc": lambda: L.ref_nchw_to_nlc(hs[0]),
+              "nlc_to_nchw": lambda: L.ref_nlc_to_nchw(hs[0], 128, 128),
+              "concat_channels": lambda: L.ref_concat_channels(hs[0], hs[1]),
+              "patchify2d": lambda: L.ref_patchify2d(hs[0], 2)}[self.name]
+        return (lambda: [R._ptr(fn())]), hs
+
+
 class CopyCalibration(Workload):
     """Not a BASELINE config: an in-place x *= 1 stream over [4096,10240]
     (one read + one write of 168 MB), the plain-copy reference for what HBM
@@ -268,7 +328,7 @@ def all_workloads():
         GNSiLU("4d", (2, 1280, 8, 8), 1e-5, "4d (SD 1.5, reported only)"),
         LNModGate(),
         Softmax(),
-    ]
+    ] + [Layout(n) for n in Layout.SPECS]
 
 
 # ------------------------------------------------------------------ GPU timing
@@ -364,6 +424,7 @@ def read_traffic(name):
 KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
     "k_unary<4>": "copy_calibration", "k_add_rms": "add_rms_norm", "k_swiglu": "swiglu",
     "k_rope_il_reg": "rope_qk", "k_ln_mod_gate": "ln_modulate_gate", "k_softmax_block": "softmax_rows",
+    "k_upsample2x_vec": "upsample_nearest2x", "k_concat_vec": "concat_channels", "k_patchify": "patchify2d",
 }
 
 

@@ -155,6 +155,25 @@ int sdh_add_channel_bias(float* x, const float* b, int64_t N, int64_t C, int64_t
  * on the CPU it equals add_rows_scaled_(x, ones, v). */
 int sdh_add_rows(float* x, const float* v, int64_t rows, int64_t dim);
 
+/* ---- layout (bit-exact copies; the output must not overlap an input) --------- */
+/* backend_cuda.h:74 upsample_nearest2x(); tensor.h:238. x [NC, H, W] ->
+ * y [NC, 2H, 2W], each input element repeated into a 2 x 2 block. */
+int sdh_upsample_nearest2x(const float* x, float* y, int64_t NC, int64_t H, int64_t W);
+/* backend_cuda.h:75 concat_channels(); tensor.h:240. a [N, Ca, HW] and
+ * b [N, Cb, HW] -> y [N, Ca + Cb, HW]. */
+int sdh_concat_channels(const float* a, const float* b, float* y, int64_t N, int64_t Ca, int64_t Cb, int64_t HW);
+/* backend_cuda.h:76 nchw_to_nlc(); tensor.h:244. x [N, C, HW] -> y [N, HW, C]. */
+int sdh_nchw_to_nlc(const float* x, float* y, int64_t N, int64_t C, int64_t HW);
+/* backend_cuda.h:77 nlc_to_nchw(); tensor.h:246. x [N, HW, C] -> y [N, C, HW]. */
+int sdh_nlc_to_nchw(const float* x, float* y, int64_t N, int64_t C, int64_t HW);
+/* backend_cuda.h:79 patchify(); tensor.h:200. x [C, H, W] -> y [(H/p)(W/p),
+ * p*p*C], features ordered (ph, pw, c). H and W must be multiples of p. */
+int sdh_patchify(const float* x, float* y, int64_t C, int64_t H, int64_t W, int p);
+/* backend_cuda.h:80 unpatchify(); tensor.h:201. The inverse of sdh_patchify:
+ * x [(H/p)(W/p), p*p*C] -> y [C, H, W]. H and W must be multiples of p (the
+ * reference's kernel would read past the tokens otherwise). */
+int sdh_unpatchify(const float* x, float* y, int64_t C, int64_t H, int64_t W, int p);
+
 /* ---- fused ------------------------------------------------------------------ */
 /* FUSED: x += r; y = rms_norm(x, gamma, eps). Equals add_(x, r) then
  * rms_norm(x, gamma, eps) (the residual -> norm order of zimage.cpp:123-128).

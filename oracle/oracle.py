@@ -82,6 +82,12 @@ class Oracle:
             "orc_add_channel_bias": (None, [_f32p, _f32p, _i64, _i64, _i64]),
             "orc_add_rms_norm": (None, [_f32p, _f32p, _f32p, _i64, _i64, N, _fl]),
             "orc_ln_modulate_gate": (None, [_f32p, _f32p, _f32p, N, _f32p, N, _i64, _i64, _fl]),
+            "orc_upsample_nearest2x": (None, [_f32p, _f32p, _i64, _i64, _i64]),
+            "orc_concat_channels": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64]),
+            "orc_nchw_to_nlc": (None, [_f32p, _f32p, _i64, _i64, _i64]),
+            "orc_nlc_to_nchw": (None, [_f32p, _f32p, _i64, _i64, _i64]),
+            "orc_patchify": (None, [_f32p, _f32p, _i64, _i64, _i64, C.c_int]),
+            "orc_unpatchify": (None, [_f32p, _f32p, _i64, _i64, _i64, C.c_int]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -248,6 +254,52 @@ class Oracle:
                                       x.size // Cc, Cc, eps)
         return r, y
 
+    # -- layout (tensor.cpp:931-1099) --
+    def upsample_nearest2x(self, x):
+        x = _f32(x)
+        N, Cc, H, W = x.shape
+        y = np.empty((N, Cc, 2 * H, 2 * W), np.float32)
+        self.lib.orc_upsample_nearest2x(x, y, N * Cc, H, W)
+        return y
+
+    def concat_channels(self, a, b):
+        a, b = _f32(a), _f32(b)
+        N, Ca, Cb = a.shape[0], a.shape[1], b.shape[1]
+        HW = a.size // (N * Ca) if Ca else b.size // (N * Cb)
+        y = np.empty((N, Ca + Cb) + a.shape[2:], np.float32)
+        self.lib.orc_concat_channels(a, b, y, N, Ca, Cb, HW)
+        return y
+
+    def nchw_to_nlc(self, x):
+        x = _f32(x)
+        N, Cc = x.shape[0], x.shape[1]
+        HW = x.size // (N * Cc)
+        y = np.empty((N, HW, Cc), np.float32)
+        self.lib.orc_nchw_to_nlc(x, y, N, Cc, HW)
+        return y
+
+    def nlc_to_nchw(self, x, H, W):
+        x = _f32(x)
+        N, HW, Cc = x.shape
+        assert HW == H * W
+        y = np.empty((N, Cc, H, W), np.float32)
+        self.lib.orc_nlc_to_nchw(x, y, N, Cc, HW)
+        return y
+
+    def patchify(self, x, p):
+        """x [1, C, H, W] (or [C, H, W]) -> tokens [(H/p)(W/p), p*p*C]."""
+        x = _f32(x)
+        Cc, H, W = x.shape[-3:]
+        y = np.empty(((H // p) * (W // p), p * p * Cc), np.float32)
+        self.lib.orc_patchify(x, y, Cc, H, W, p)
+        return y
+
+    def unpatchify(self, tokens, Cc, H, W, p):
+        """tokens [(H/p)(W/p), p*p*C] -> [1, C, H, W] (uncovered rows/columns 0)."""
+        y = np.zeros((1, Cc, H, W), np.float32)
+        self.lib.orc_unpatchify(_f32(tokens), y, Cc, H, W, p)
+        return y
+
 
 class Reference:
     """numpy-level wrapper of the compiled reference tensor library."""
@@ -282,6 +334,16 @@ class Reference:
             "ref_mul_rows_": (C.c_int, [_vp, _vp]),
             "ref_add_rows_scaled_": (C.c_int, [_vp, _vp, _vp]),
             "ref_add_channel_bias_": (C.c_int, [_vp, _vp]),
+            "ref_patchify2d": (_vp, [_vp, C.c_int]),
+            "ref_unpatchify2d": (_vp, [_vp, _i64, _i64, _i64, C.c_int]),
+            "ref_slice_rows": (_vp, [_vp, _i64, _i64]),
+            "ref_upsample_nearest2x": (_vp, [_vp]),
+            "ref_concat_channels": (_vp, [_vp, _vp]),
+            "ref_concat_batch": (_vp, [_vp, _vp]),
+            "ref_nchw_to_nlc": (_vp, [_vp]),
+            "ref_nlc_to_nchw": (_vp, [_vp, _i64, _i64]),
+            "ref_slice_batch": (_vp, [_vp, _i64]),
+            "ref_repeat_batch": (_vp, [_vp, _i64]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -441,6 +503,57 @@ class Reference:
         self._chk(self.lib.ref_add_channel_bias_(hx, hb))
         self.free(hb)
         return self.take(hx, x.shape)
+
+    # -- layout --
+    def _new_op(self, fn, inputs, out_shape, *args):
+        hs = [self.new(a.shape, a) for a in inputs]
+        try:
+            h = self._ptr(fn(*hs, *args))
+        finally:
+            self.free(*hs)
+        return self.take(h, out_shape)
+
+    def upsample_nearest2x(self, x):
+        x = _f32(x)
+        N, Cc, H, W = x.shape
+        return self._new_op(self.lib.ref_upsample_nearest2x, [x], (N, Cc, 2 * H, 2 * W))
+
+    def concat_channels(self, a, b):
+        a, b = _f32(a), _f32(b)
+        return self._new_op(self.lib.ref_concat_channels, [a, b], (a.shape[0], a.shape[1] + b.shape[1]) + a.shape[2:])
+
+    def concat_batch(self, a, b):
+        a, b = _f32(a), _f32(b)
+        return self._new_op(self.lib.ref_concat_batch, [a, b], (a.shape[0] + b.shape[0],) + a.shape[1:])
+
+    def nchw_to_nlc(self, x):
+        x = _f32(x)
+        N, Cc = x.shape[0], x.shape[1]
+        return self._new_op(self.lib.ref_nchw_to_nlc, [x], (N, x.size // (N * Cc), Cc))
+
+    def nlc_to_nchw(self, x, H, W):
+        x = _f32(x)
+        return self._new_op(self.lib.ref_nlc_to_nchw, [x], (x.shape[0], x.shape[2], H, W), H, W)
+
+    def patchify(self, x, p):
+        x = _f32(x)
+        Cc, H, W = x.shape[-3:]
+        return self._new_op(self.lib.ref_patchify2d, [x.reshape(1, Cc, H, W)], ((H // p) * (W // p), p * p * Cc), p)
+
+    def unpatchify(self, tokens, Cc, H, W, p):
+        return self._new_op(self.lib.ref_unpatchify2d, [_f32(tokens)], (1, Cc, H, W), Cc, H, W, p)
+
+    def slice_rows(self, x, a, b):
+        x = _f32(x)
+        return self._new_op(self.lib.ref_slice_rows, [x], (b - a, x.shape[-1]), a, b)
+
+    def slice_batch(self, x, i):
+        x = _f32(x)
+        return self._new_op(self.lib.ref_slice_batch, [x], (1,) + x.shape[1:], i)
+
+    def repeat_batch(self, x, times):
+        x = _f32(x)
+        return self._new_op(self.lib.ref_repeat_batch, [x], (x.shape[0] * times,) + x.shape[1:], times)
 
     # -- compositions, exactly as the reference's callers chain the ops --
     def add_rms_norm(self, x, r, gamma, eps):

@@ -97,4 +97,26 @@ int ref_mul_rows_(void* x, void* v) { return guard([&] { sd::mul_rows_(*T(x), *T
 int ref_add_rows_scaled_(void* x, void* y, void* g) { return guard([&] { sd::add_rows_scaled_(*T(x), *T(y), *T(g)); }); }
 int ref_add_channel_bias_(void* x, void* b) { return guard([&] { sd::add_channel_bias_(*T(x), *T(b)); }); }
 
+// ---- layout ops (new tensors) ----
+void* ref_patchify2d(void* x, int p) { return guard_ptr([&] { return wrap(sd::patchify2d(*T(x), p)); }); }
+void* ref_unpatchify2d(void* t, int64_t C, int64_t H, int64_t W, int p) {
+    return guard_ptr([&] { return wrap(sd::unpatchify2d(*T(t), C, H, W, p)); });
+}
+void* ref_slice_rows(void* x, int64_t from, int64_t to) {
+    return guard_ptr([&] { return wrap(sd::slice_rows(*T(x), from, to)); });
+}
+void* ref_upsample_nearest2x(void* x) { return guard_ptr([&] { return wrap(sd::upsample_nearest2x(*T(x))); }); }
+void* ref_concat_channels(void* a, void* b) {
+    return guard_ptr([&] { return wrap(sd::concat_channels(*T(a), *T(b))); });
+}
+void* ref_concat_batch(void* a, void* b) { return guard_ptr([&] { return wrap(sd::concat_batch(*T(a), *T(b))); }); }
+void* ref_nchw_to_nlc(void* x) { return guard_ptr([&] { return wrap(sd::nchw_to_nlc(*T(x))); }); }
+void* ref_nlc_to_nchw(void* x, int64_t H, int64_t W) {
+    return guard_ptr([&] { return wrap(sd::nlc_to_nchw(*T(x), H, W)); });
+}
+void* ref_slice_batch(void* x, int64_t b) { return guard_ptr([&] { return wrap(sd::slice_batch(*T(x), b)); }); }
+void* ref_repeat_batch(void* x, int64_t times) {
+    return guard_ptr([&] { return wrap(sd::repeat_batch(*T(x), times)); });
+}
+
 }  // extern "C"

@@ -16,6 +16,7 @@
 #include <math.h>
 #include <stddef.h>
 #include <stdlib.h>
+#include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
 #endif
@@ -491,6 +492,79 @@ static void add_channel_bias_body(void* vctx, int64_t nc, int64_t nce) {
 void orc_add_channel_bias(float* x, const float* b, int64_t N, int64_t C, int64_t HW) {
     ew_ctx c = {b, NULL, x, 0, 0, HW};
     items(N * C, add_channel_bias_body, &c);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Layout (tensor.cpp:931-1099): copies, in the reference's loop order       */
+/* ------------------------------------------------------------------------ */
+void orc_upsample_nearest2x(const float* x, float* y, int64_t NC, int64_t H, int64_t W) {
+    for (int64_t nc = 0; nc < NC; ++nc) {
+        const float* p = x + nc * H * W;
+        float* q = y + nc * 4 * H * W;
+        for (int64_t i = 0; i < H; ++i) {
+            float* r0 = q + (2 * i) * 2 * W;
+            float* r1 = r0 + 2 * W;
+            for (int64_t j = 0; j < W; ++j) {
+                const float v = p[i * W + j];
+                r0[2 * j] = r0[2 * j + 1] = v;
+                r1[2 * j] = r1[2 * j + 1] = v;
+            }
+        }
+    }
+}
+
+void orc_concat_channels(const float* a, const float* b, float* y, int64_t N, int64_t Ca, int64_t Cb, int64_t HW) {
+    for (int64_t n = 0; n < N; ++n) {
+        memcpy(y + n * (Ca + Cb) * HW, a + n * Ca * HW, (size_t)(Ca * HW) * sizeof(float));
+        memcpy(y + (n * (Ca + Cb) + Ca) * HW, b + n * Cb * HW, (size_t)(Cb * HW) * sizeof(float));
+    }
+}
+
+void orc_nchw_to_nlc(const float* x, float* y, int64_t N, int64_t C, int64_t HW) {
+    for (int64_t nc = 0; nc < N * C; ++nc) {
+        const int64_t n = nc / C, c = nc % C;
+        const float* p = x + nc * HW;
+        float* q = y + n * HW * C + c;
+        for (int64_t i = 0; i < HW; ++i) q[i * C] = p[i];
+    }
+}
+
+void orc_nlc_to_nchw(const float* x, float* y, int64_t N, int64_t C, int64_t HW) {
+    for (int64_t nc = 0; nc < N * C; ++nc) {
+        const int64_t n = nc / C, c = nc % C;
+        if (g_plant == 7) { /* plant 7: input read as if it were already NCHW (no transpose) */
+            memcpy(y + nc * HW, x + (n * C + c) * HW, (size_t)HW * sizeof(float));
+            continue;
+        }
+        const float* p = x + n * HW * C + c;
+        float* q = y + nc * HW;
+        for (int64_t i = 0; i < HW; ++i) q[i] = p[i * C];
+    }
+}
+
+void orc_patchify(const float* x, float* y, int64_t C, int64_t H, int64_t W, int p) {
+    const int64_t Ht = H / p, Wt = W / p;
+    for (int64_t h = 0; h < Ht; ++h)
+        for (int64_t w = 0; w < Wt; ++w) {
+            float* tok = y + (h * Wt + w) * p * p * C;
+            for (int64_t ph = 0; ph < p; ++ph)
+                for (int64_t pw = 0; pw < p; ++pw)
+                    for (int64_t c = 0; c < C; ++c) {
+                        const int64_t f = (g_plant == 6) ? (pw * p + ph) : (ph * p + pw); /* plant 6: ph/pw swapped */
+                        tok[f * C + c] = x[(c * H + h * p + ph) * W + w * p + pw];
+                    }
+        }
+}
+
+void orc_unpatchify(const float* x, float* y, int64_t C, int64_t H, int64_t W, int p) {
+    const int64_t Ht = H / p, Wt = W / p;
+    for (int64_t h = 0; h < Ht; ++h)
+        for (int64_t w = 0; w < Wt; ++w) {
+            const float* tok = x + (h * Wt + w) * p * p * C;
+            for (int64_t ph = 0; ph < p; ++ph)
+                for (int64_t pw = 0; pw < p; ++pw)
+                    for (int64_t c = 0; c < C; ++c) y[(c * H + h * p + ph) * W + w * p + pw] = tok[(ph * p + pw) * C + c];
+        }
 }
 
 /* ------------------------------------------------------------------------ */

@@ -87,6 +87,21 @@ void orc_group_norm_silu(const float* x, float* y, int64_t N, int64_t C, int64_t
 void orc_ln_modulate_gate(const float* x, float* res, const float* scale, const float* shift, const float* gate,
                           float* y_out, int64_t rows, int64_t C, float eps);
 
+/* ---- layout (tensor.cpp:931-1099); y never overlaps the inputs ---- */
+/* tensor.cpp:982-1004: x [NC, H, W] -> y [NC, 2H, 2W]. */
+void orc_upsample_nearest2x(const float* x, float* y, int64_t NC, int64_t H, int64_t W);
+/* tensor.cpp:1006-1023: a [N, Ca, HW], b [N, Cb, HW] -> y [N, Ca + Cb, HW]. */
+void orc_concat_channels(const float* a, const float* b, float* y, int64_t N, int64_t Ca, int64_t Cb, int64_t HW);
+/* tensor.cpp:1041-1056: x [N, C, HW] -> y [N, HW, C]. */
+void orc_nchw_to_nlc(const float* x, float* y, int64_t N, int64_t C, int64_t HW);
+/* tensor.cpp:1058-1074: x [N, HW, C] -> y [N, C, HW]. */
+void orc_nlc_to_nchw(const float* x, float* y, int64_t N, int64_t C, int64_t HW);
+/* tensor.cpp:931-949: x [C, H, W] -> y [(H/p)(W/p), p*p*C], features (ph, pw, c). */
+void orc_patchify(const float* x, float* y, int64_t C, int64_t H, int64_t W, int p);
+/* tensor.cpp:951-968: tokens [(H/p)(W/p), p*p*C] -> y [C, H, W]; rows/columns
+ * beyond (H/p)p, (W/p)p are left untouched (the reference zero-allocates y). */
+void orc_unpatchify(const float* x, float* y, int64_t C, int64_t H, int64_t W, int p);
+
 /* Planted-mistake switch for the oracle's own pin tests (0 = none). The pins
  * must fail when a mistake is planted; see tests/test_oracle_pins.py. */
 void orc_plant_mistake(int which);

@@ -62,6 +62,12 @@ STUB(int sdh_add_rms_norm(float*, const float*, float*, int64_t, int64_t, const 
 STUB(int sdh_group_norm_silu(const float*, float*, int64_t, int64_t, int64_t, int, const float*, const float*, float))
 STUB(int sdh_ln_modulate_gate(const float*, float*, const float*, const float*, const float*, float*, int64_t,
                               int64_t, float))
+STUB(int sdh_upsample_nearest2x(const float*, float*, int64_t, int64_t, int64_t))
+STUB(int sdh_concat_channels(const float*, const float*, float*, int64_t, int64_t, int64_t, int64_t))
+STUB(int sdh_nchw_to_nlc(const float*, float*, int64_t, int64_t, int64_t))
+STUB(int sdh_nlc_to_nchw(const float*, float*, int64_t, int64_t, int64_t))
+STUB(int sdh_patchify(const float*, float*, int64_t, int64_t, int64_t, int))
+STUB(int sdh_unpatchify(const float*, float*, int64_t, int64_t, int64_t, int))
 STUB(int sdh_fill_normal(float*, int64_t, uint64_t, float, float))
 STUB(int sdh_timer_record(int))
 STUB(int sdh_timer_elapsed(int, int, float*))

@@ -97,6 +97,25 @@ inline void add_rows_scaled(float* x, const float* y, const float* g, int64_t ro
 inline void add_channel_bias(float* x, const float* b, int64_t N, int64_t C, int64_t HW) {
     detail::check(sdh_add_channel_bias(x, b, N, C, HW), "hip::add_channel_bias");
 }
+// backend_cuda.h:74-80 layout ops
+inline void upsample_nearest2x(const float* x, float* y, int64_t NC, int64_t H, int64_t W) {
+    detail::check(sdh_upsample_nearest2x(x, y, NC, H, W), "hip::upsample_nearest2x");
+}
+inline void concat_channels(const float* a, const float* b, float* y, int64_t N, int64_t Ca, int64_t Cb, int64_t HW) {
+    detail::check(sdh_concat_channels(a, b, y, N, Ca, Cb, HW), "hip::concat_channels");
+}
+inline void nchw_to_nlc(const float* x, float* y, int64_t N, int64_t C, int64_t HW) {
+    detail::check(sdh_nchw_to_nlc(x, y, N, C, HW), "hip::nchw_to_nlc");
+}
+inline void nlc_to_nchw(const float* x, float* y, int64_t N, int64_t C, int64_t HW) {
+    detail::check(sdh_nlc_to_nchw(x, y, N, C, HW), "hip::nlc_to_nchw");
+}
+inline void patchify(const float* x, float* y, int64_t C, int64_t H, int64_t W, int p) {
+    detail::check(sdh_patchify(x, y, C, H, W, p), "hip::patchify");
+}
+inline void unpatchify(const float* x, float* y, int64_t C, int64_t H, int64_t W, int p) {
+    detail::check(sdh_unpatchify(x, y, C, H, W, p), "hip::unpatchify");
+}
 
 // Additive entry points (no single backend_cuda.h counterpart).
 inline void add_rows(float* x, const float* v, int64_t rows, int64_t dim) {

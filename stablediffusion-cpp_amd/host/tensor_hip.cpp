@@ -3,6 +3,7 @@
 // the arithmetic is backend_hip's (include/sdh_backend.h).
 #include "tensor_hip.h"
 
+#include <algorithm>
 #include <sstream>
 #include <stdexcept>
 
@@ -252,6 +253,121 @@ void add_channel_bias_(Tensor& x, const Tensor& b) {
     same_device(x, b, "add_channel_bias_");
     need_hip(x, "add_channel_bias_");
     sd::hip::add_channel_bias(x.dptr(), b.dptr(), N, C, HW);
+}
+
+// ---- layout ----------------------------------------------------------------
+
+// tensor.cpp:931-949
+Tensor patchify2d(const Tensor& x, int p) {
+    need_hip(x, "patchify2d");
+    const int64_t C = x.dim(1), H = x.dim(2), W = x.dim(3), Ht = H / p, Wt = W / p;
+    if (x.dim(0) != 1 || H % p || W % p) throw std::runtime_error("patchify2d: bad shape " + x.shape_str());
+    Tensor y = Tensor::empty({Ht * Wt, (int64_t)p * p * C}, Device::HIP);
+    sd::hip::patchify(x.dptr(), y.dptr(), C, H, W, p);
+    return y;
+}
+
+// tensor.cpp:951-968. The device path needs whole patches: the reference's
+// kernel (backend_cuda.cu:438-445) reads past the tokens otherwise.
+Tensor unpatchify2d(const Tensor& tokens, int64_t C, int64_t H, int64_t W, int p) {
+    need_hip(tokens, "unpatchify2d");
+    const int64_t Ht = H / p, Wt = W / p;
+    if (tokens.numel() < Ht * Wt * p * p * C) throw std::runtime_error("unpatchify2d: too few tokens");
+    if (H % p || W % p) throw std::runtime_error("unpatchify2d: H and W must be multiples of the patch size");
+    Tensor y = Tensor::empty({1, C, H, W}, Device::HIP);
+    sd::hip::unpatchify(tokens.dptr(), y.dptr(), C, H, W, p);
+    return y;
+}
+
+// tensor.cpp:970-980
+Tensor slice_rows(const Tensor& x, int64_t from, int64_t to) {
+    need_hip(x, "slice_rows");
+    const int64_t D = x.dim(-1), rows = x.numel() / D;
+    if (from < 0 || to > rows || from > to) throw std::runtime_error("slice_rows: range out of bounds");
+    Tensor y = Tensor::empty({to - from, D}, Device::HIP);
+    const size_t bytes = (size_t)((to - from) * D) * sizeof(float);
+    if (bytes) sd::hip::copy(y.dptr(), x.dptr() + from * D, bytes);
+    return y;
+}
+
+// tensor.cpp:982-1004
+Tensor upsample_nearest2x(const Tensor& x) {
+    need_hip(x, "upsample_nearest2x");
+    const int64_t N = x.dim(0), C = x.dim(1), H = x.dim(2), W = x.dim(3);
+    Tensor y = Tensor::empty({N, C, 2 * H, 2 * W}, Device::HIP);
+    sd::hip::upsample_nearest2x(x.dptr(), y.dptr(), N * C, H, W);
+    return y;
+}
+
+// tensor.cpp:1006-1023
+Tensor concat_channels(const Tensor& a, const Tensor& b) {
+    const int64_t N = a.dim(0), Ca = a.dim(1), Cb = b.dim(1), H = a.dim(2), W = a.dim(3);
+    if (b.dim(0) != N || b.dim(2) != H || b.dim(3) != W)
+        throw std::runtime_error("concat_channels: " + a.shape_str() + " vs " + b.shape_str());
+    same_device(a, b, "concat_channels");
+    need_hip(a, "concat_channels");
+    Tensor y = Tensor::empty({N, Ca + Cb, H, W}, Device::HIP);
+    sd::hip::concat_channels(a.dptr(), b.dptr(), y.dptr(), N, Ca, Cb, H * W);
+    return y;
+}
+
+// tensor.cpp:1025-1039: y takes a's shape with the batches added, then a's
+// and b's elements are copied in order. Like the reference, a b with other
+// trailing dimensions is copied flat and any tail it leaves stays zero
+// (test_ops.cpp:467 relies on that); a b that would overrun y is an error.
+Tensor concat_batch(const Tensor& a, const Tensor& b) {
+    same_device(a, b, "concat_batch");
+    need_hip(a, "concat_batch");
+    std::vector<int64_t> s = a.shape;
+    s[0] += b.dim(0);
+    const int64_t n = Tensor::numel_of(s);
+    if (a.numel() + b.numel() > n) throw std::runtime_error("concat_batch: " + a.shape_str() + " vs " + b.shape_str());
+    Tensor y = a.numel() + b.numel() == n ? Tensor::empty(s, Device::HIP) : Tensor(s, Device::HIP);
+    if (a.numel()) sd::hip::copy(y.dptr(), a.dptr(), a.numel() * sizeof(float));
+    if (b.numel()) sd::hip::copy(y.dptr() + a.numel(), b.dptr(), b.numel() * sizeof(float));
+    return y;
+}
+
+// tensor.cpp:1041-1056
+Tensor nchw_to_nlc(const Tensor& x) {
+    need_hip(x, "nchw_to_nlc");
+    const int64_t N = x.dim(0), C = x.dim(1), HW = x.dim(2) * x.dim(3);
+    Tensor y = Tensor::empty({N, HW, C}, Device::HIP);
+    sd::hip::nchw_to_nlc(x.dptr(), y.dptr(), N, C, HW);
+    return y;
+}
+
+// tensor.cpp:1058-1074
+Tensor nlc_to_nchw(const Tensor& x, int64_t H, int64_t W) {
+    need_hip(x, "nlc_to_nchw");
+    const int64_t N = x.dim(0), HW = x.dim(1), C = x.dim(2);
+    if (HW != H * W) throw std::runtime_error("nlc_to_nchw: bad spatial size");
+    Tensor y = Tensor::empty({N, C, H, W}, Device::HIP);
+    sd::hip::nlc_to_nchw(x.dptr(), y.dptr(), N, C, HW);
+    return y;
+}
+
+// tensor.cpp:1076-1086
+Tensor slice_batch(const Tensor& x, int64_t b) {
+    need_hip(x, "slice_batch");
+    if (b < 0 || b >= x.dim(0)) throw std::runtime_error("slice_batch: index out of range");
+    std::vector<int64_t> s = x.shape;
+    s[0] = 1;
+    Tensor y = Tensor::empty(s, Device::HIP);
+    const int64_t per = x.numel() / x.dim(0);
+    if (per) sd::hip::copy(y.dptr(), x.dptr() + b * per, per * sizeof(float));
+    return y;
+}
+
+// tensor.cpp:1088-1099
+Tensor repeat_batch(const Tensor& x, int64_t times) {
+    need_hip(x, "repeat_batch");
+    std::vector<int64_t> s = x.shape;
+    s[0] = x.dim(0) * times;
+    Tensor y = Tensor::empty(s, Device::HIP);
+    for (int64_t t = 0; t < times; ++t)
+        if (x.numel()) sd::hip::copy(y.dptr() + t * x.numel(), x.dptr(), x.numel() * sizeof(float));
+    return y;
 }
 
 // tensor.cpp:752 (device pointer)

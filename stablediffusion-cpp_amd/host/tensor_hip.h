@@ -82,6 +82,18 @@ void add_channel_bias_(Tensor& x, const Tensor& b);
 void add_(Tensor& a, const Tensor& b);
 void scale_(Tensor& x, float s);
 
+// ---- layout (tensor.h:200-203, :238-250); outputs are new device tensors ----
+Tensor patchify2d(const Tensor& x, int p);  // x [1, C, H, W] -> [(H/p)(W/p), p*p*C]
+Tensor unpatchify2d(const Tensor& tokens, int64_t C, int64_t H, int64_t W, int p);
+Tensor slice_rows(const Tensor& x, int64_t from, int64_t to);
+Tensor upsample_nearest2x(const Tensor& x);
+Tensor concat_channels(const Tensor& a, const Tensor& b);
+Tensor concat_batch(const Tensor& a, const Tensor& b);
+Tensor nchw_to_nlc(const Tensor& x);
+Tensor nlc_to_nchw(const Tensor& x, int64_t H, int64_t W);
+Tensor slice_batch(const Tensor& x, int64_t b);
+Tensor repeat_batch(const Tensor& x, int64_t times);
+
 // ---- softmax (tensor.h:236) ----
 // Same parameters as the reference; x is a DEVICE pointer here (rows x cols
 // floats inside a backend_hip block).

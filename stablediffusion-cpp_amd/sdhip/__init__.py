@@ -78,6 +78,12 @@ SIGNATURES = {
     "sdh_add_rows_scaled": [_vp, _vp, _vp, _i64, _i64],
     "sdh_add_channel_bias": [_vp, _vp, _i64, _i64, _i64],
     "sdh_add_rows": [_vp, _vp, _i64, _i64],
+    "sdh_upsample_nearest2x": [_vp, _vp, _i64, _i64, _i64],
+    "sdh_concat_channels": [_vp, _vp, _vp, _i64, _i64, _i64, _i64],
+    "sdh_nchw_to_nlc": [_vp, _vp, _i64, _i64, _i64],
+    "sdh_nlc_to_nchw": [_vp, _vp, _i64, _i64, _i64],
+    "sdh_patchify": [_vp, _vp, _i64, _i64, _i64, C.c_int],
+    "sdh_unpatchify": [_vp, _vp, _i64, _i64, _i64, C.c_int],
     "sdh_add_rms_norm": [_vp, _vp, _vp, _i64, _i64, _vp, _fl],
     "sdh_group_norm_silu": [_vp, _vp, _i64, _i64, _i64, _int, _vp, _vp, _fl],
     "sdh_ln_modulate_gate": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _fl],
@@ -291,6 +297,25 @@ class Backend:
 
     def add_channel_bias(self, x, b, N, Cc, HW):
         self.call("sdh_add_channel_bias", _p(x), _p(b), N, Cc, HW)
+
+    # layout (tensor.cpp:931-1099)
+    def upsample_nearest2x(self, x, y, NC, H, W):
+        self.call("sdh_upsample_nearest2x", _p(x), _p(y), NC, H, W)
+
+    def concat_channels(self, a, b, y, N, Ca, Cb, HW):
+        self.call("sdh_concat_channels", _p(a), _p(b), _p(y), N, Ca, Cb, HW)
+
+    def nchw_to_nlc(self, x, y, N, Cc, HW):
+        self.call("sdh_nchw_to_nlc", _p(x), _p(y), N, Cc, HW)
+
+    def nlc_to_nchw(self, x, y, N, Cc, HW):
+        self.call("sdh_nlc_to_nchw", _p(x), _p(y), N, Cc, HW)
+
+    def patchify(self, x, y, Cc, H, W, p):
+        self.call("sdh_patchify", _p(x), _p(y), Cc, H, W, p)
+
+    def unpatchify(self, x, y, Cc, H, W, p):
+        self.call("sdh_unpatchify", _p(x), _p(y), Cc, H, W, p)
 
     def add_rms_norm(self, x, r, y, rows, Cc, gamma, eps):
         self.call("sdh_add_rms_norm", _p(x), _p(r), _p(y), rows, Cc, _p(gamma), eps)

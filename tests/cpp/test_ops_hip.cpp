@@ -6,6 +6,7 @@
 // compositions, at the reference's tiny shapes and at the Z-Image config
 // shapes. Exit status is non-zero if any check fails; without a GPU the
 // device section is skipped, as the reference's test does (test_ops.cpp:357-360).
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <functional>
@@ -163,6 +164,50 @@ static void test_hip() {
         sdh::add_channel_bias_(imgg, bias.to(G));
         hip_check_op("add_channel_bias_", img, imgg, 1e-6);
     }
+    // shape ops (test_ops.cpp:464-476): exact copies, tolerance 0
+    {
+        Tensor img = randn_t({2, 3, 4, 5}), img2 = randn_t({2, 2, 4, 5}), x = randn_t({4, 6});
+        Tensor ig = img.to(G), ig2 = img2.to(G);
+        Tensor up({2, 3, 8, 10});
+        orc_upsample_nearest2x(img.data.data(), up.data.data(), 6, 4, 5);
+        hip_check_op("upsample_nearest2x", up, sdh::upsample_nearest2x(ig), 0.0);
+        Tensor cc({2, 5, 4, 5});
+        orc_concat_channels(img.data.data(), img2.data.data(), cc.data.data(), 2, 3, 2, 20);
+        hip_check_op("concat_channels", cc, sdh::concat_channels(ig, ig2), 0.0);
+        Tensor cb({4, 3, 4, 5});  // a's shape with the batches added; b's 80 floats leave a zero tail
+        std::copy(img.data.begin(), img.data.end(), cb.data.begin());
+        std::copy(img2.data.begin(), img2.data.end(), cb.data.begin() + img.numel());
+        hip_check_op("concat_batch", cb, sdh::concat_batch(ig, ig2), 0.0);
+        Tensor nlc({2, 20, 3}), back({2, 3, 4, 5});
+        orc_nchw_to_nlc(img.data.data(), nlc.data.data(), 2, 3, 20);
+        hip_check_op("nchw_to_nlc", nlc, sdh::nchw_to_nlc(ig), 0.0);
+        orc_nlc_to_nchw(nlc.data.data(), back.data.data(), 2, 3, 20);
+        hip_check_op("nlc_to_nchw", back, sdh::nlc_to_nchw(sdh::nchw_to_nlc(ig), 4, 5), 0.0);
+        Tensor sb({1, 3, 4, 5});
+        std::copy(img.data.begin() + 60, img.data.begin() + 120, sb.data.begin());
+        hip_check_op("slice_batch", sb, sdh::slice_batch(ig, 1), 0.0);
+        Tensor rb({6, 3, 4, 5});
+        for (int t = 0; t < 3; ++t) std::copy(img.data.begin(), img.data.end(), rb.data.begin() + t * 120);
+        hip_check_op("repeat_batch", rb, sdh::repeat_batch(ig, 3), 0.0);
+        Tensor sr({2, 6});
+        std::copy(x.data.begin() + 6, x.data.begin() + 18, sr.data.begin());
+        hip_check_op("slice_rows", sr, sdh::slice_rows(x.to(G), 1, 3), 0.0);
+        Tensor lat = randn_t({1, 16, 6, 8});
+        Tensor tok({12, 64}), un({1, 16, 6, 8});
+        orc_patchify(lat.data.data(), tok.data.data(), 16, 6, 8, 2);
+        hip_check_op("patchify2d", tok, sdh::patchify2d(lat.to(G), 2), 0.0);
+        orc_unpatchify(tok.data.data(), un.data.data(), 16, 6, 8, 2);
+        hip_check_op("unpatchify2d", un, sdh::unpatchify2d(tok.to(G), 16, 6, 8, 2), 0.0);
+        // the Z-Image 1024^2 latent and the VAE attention layout, at full size
+        Tensor zl = randn_t({1, 16, 128, 128});
+        Tensor ztok({4096, 64});
+        orc_patchify(zl.data.data(), ztok.data.data(), 16, 128, 128, 2);
+        hip_check_op("patchify2d Z-Image latent", ztok, sdh::patchify2d(zl.to(G), 2), 0.0);
+        Tensor va = randn_t({1, 512, 128, 128});
+        Tensor vnlc({1, 16384, 512});
+        orc_nchw_to_nlc(va.data.data(), vnlc.data.data(), 1, 512, 16384);
+        hip_check_op("nchw_to_nlc VAE attention", vnlc, sdh::nchw_to_nlc(va.to(G)), 0.0);
+    }
     // fused ops vs their reference compositions, tiny and Z-Image shapes
     for (int64_t rows : {7, 4096}) {
         const int64_t C = rows == 7 ? 64 : 3840;
@@ -224,6 +269,10 @@ static void test_hip() {
         bad += !throws([&] { sdh::silu_(host); });                               // host tensor: no CPU path here
         Tensor x6 = Tensor({1, 6, 2, 2}).to(G), g6 = Tensor({6}).to(G);
         bad += !throws([&] { sdh::group_norm(x6, 4, g6, g6, 1e-6f); });        // tensor.cpp:594
+        Tensor odd = Tensor({1, 2, 5, 6}).to(G);
+        bad += !throws([&] { sdh::patchify2d(odd, 2); });                      // tensor.cpp:933
+        bad += !throws([&] { sdh::slice_rows(a, 2, 5); });                     // tensor.cpp:972
+        bad += !throws([&] { sdh::nlc_to_nchw(Tensor({1, 6, 2}).to(G), 4, 2); });  // tensor.cpp:1060
         check("shape/device errors throw", (double)bad, 0.0);
     }
 }

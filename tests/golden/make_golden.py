@@ -3,7 +3,7 @@
 (oracle/_ref/libsdref.so = /root/reference/src/tensor.cpp, built by
 oracle/Makefile). Run where /root/reference is mounted:
 
-    make -C oracle all ref && python tests/golden/make_golden.py
+    make -C oracle all ref && python tests/golden/make_golden.py [--small-only]
 
 Outputs (data only: inputs are regenerated from their seeds by the oracle's
 portable generator, expected outputs come from the reference):
@@ -82,6 +82,19 @@ def small_cases(orc, ref):
     lgt = rnd("lgt", (64,), 34, 0.0, 0.2)
     out["ln_modulate_gate_res"], out["ln_modulate_gate_y"] = ref.ln_modulate_gate(lx, lr, lsc, lsh, lgt, 1e-6)
     out["add_rms_norm_sum"], out["add_rms_norm_y"] = ref.add_rms_norm(lx, lr, g64, 1e-6)
+    # layout ops, on the shapes of the reference's own GPU test (test_ops.cpp:462-476)
+    img2 = rnd("img2", (2, 2, 4, 5), 35)
+    out["upsample_nearest2x"] = ref.upsample_nearest2x(cimg)
+    out["concat_channels"] = ref.concat_channels(cimg, img2)
+    out["concat_batch"] = ref.concat_batch(cimg, img2)  # shapes differ: the reference leaves a zero tail
+    out["nchw_to_nlc"] = ref.nchw_to_nlc(cimg)
+    out["nlc_to_nchw"] = ref.nlc_to_nchw(out["nchw_to_nlc"], 4, 5)
+    out["slice_batch"] = ref.slice_batch(cimg, 1)
+    out["repeat_batch"] = ref.repeat_batch(cimg, 3)
+    out["slice_rows"] = ref.slice_rows(m, 1, 3)
+    lat = rnd("lat", (1, 16, 6, 8), 36)
+    out["patchify2d"] = ref.patchify(lat, 2)
+    out["unpatchify2d"] = ref.unpatchify(out["patchify2d"], 16, 6, 8, 2)
     return out
 
 
@@ -134,9 +147,12 @@ def main():
     orc, ref = Oracle(), Reference()
     small = small_cases(orc, ref)
     np.savez_compressed(os.path.join(HERE, "ops_small.npz"), **small)
-    cfg = config_cases(orc, ref)
-    np.savez_compressed(os.path.join(HERE, "configs.npz"), **cfg)
-    for f in ("ops_small.npz", "configs.npz"):
+    files = ["ops_small.npz"]
+    if "--small-only" not in sys.argv:  # the config summaries take a few minutes of CPU
+        cfg = config_cases(orc, ref)
+        np.savez_compressed(os.path.join(HERE, "configs.npz"), **cfg)
+        files.append("configs.npz")
+    for f in files:
         print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")
 
 

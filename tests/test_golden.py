@@ -55,6 +55,22 @@ def oracle_outputs(orc, small):
     o["ln_modulate_gate_res"], o["ln_modulate_gate_y"] = orc.ln_modulate_gate(i["lx"], i["lr"], i["lsc"], i["lsh"],
                                                                               i["lgt"], 1e-6)
     o["add_rms_norm_sum"], o["add_rms_norm_y"] = orc.add_rms_norm(i["lx"], i["lr"], i["g64"], 1e-6)
+    # layout ops: the oracle's restatements, and for the pure memcpy ops
+    # (tensor.cpp:970-980, :1025-1039, :1076-1099) their numpy equivalent
+    img, img2 = i["cimg"], i["img2"]
+    o["upsample_nearest2x"] = orc.upsample_nearest2x(img)
+    o["concat_channels"] = orc.concat_channels(img, img2)
+    cb = np.zeros((img.shape[0] + img2.shape[0],) + img.shape[1:], np.float32)
+    cb.reshape(-1)[:img.size] = img.reshape(-1)
+    cb.reshape(-1)[img.size:img.size + img2.size] = img2.reshape(-1)
+    o["concat_batch"] = cb
+    o["nchw_to_nlc"] = orc.nchw_to_nlc(img)
+    o["nlc_to_nchw"] = orc.nlc_to_nchw(o["nchw_to_nlc"], 4, 5)
+    o["slice_batch"] = img[1:2].copy()
+    o["repeat_batch"] = np.concatenate([img] * 3, axis=0)
+    o["slice_rows"] = i["m"][1:3].copy()
+    o["patchify2d"] = orc.patchify(i["lat"], 2)
+    o["unpatchify2d"] = orc.unpatchify(o["patchify2d"], 16, 6, 8, 2)
     return o
 
 

@@ -98,11 +98,26 @@ def test_small_ops_vs_reference(be, orc, small):
     be.add_rms_norm(xs, A(i["lr"]), y, 7, 64, A(i["g64"]), 1e-6)
     got["add_rms_norm_sum"], got["add_rms_norm_y"] = xs.download(), y.download()
 
+    img, img2 = A(i["cimg"]), A(i["img2"])
+    got["upsample_nearest2x"] = run_new(lambda y: be.upsample_nearest2x(img, y, 6, 4, 5), (2, 3, 8, 10))
+    got["concat_channels"] = run_new(lambda y: be.concat_channels(img, img2, y, 2, 3, 2, 20), (2, 5, 4, 5))
+    nlc = be.empty((2, 20, 3))
+    be.nchw_to_nlc(img, nlc, 2, 3, 20)
+    got["nchw_to_nlc"] = nlc.download()
+    got["nlc_to_nchw"] = run_new(lambda y: be.nlc_to_nchw(nlc, y, 2, 3, 20), (2, 3, 4, 5))
+    tok = be.empty((12, 64))
+    be.patchify(A(i["lat"]), tok, 16, 6, 8, 2)
+    got["patchify2d"] = tok.download()
+    got["unpatchify2d"] = run_new(lambda y: be.unpatchify(tok, y, 16, 6, 8, 2), (1, 16, 6, 8))
+    exact = {"upsample_nearest2x", "concat_channels", "nchw_to_nlc", "nlc_to_nchw", "patchify2d", "unpatchify2d"}
+
     reductions = {"rms_norm", "layer_norm", "layer_norm_noaffine", "group_norm", "group_norm_silu", "rms_norm_heads",
                   "ln_modulate_gate_res", "ln_modulate_gate_y", "add_rms_norm_y"}
     for k, v in got.items():
         want = small[k]
-        if k.startswith("softmax"):
+        if k in exact:
+            assert v.shape == want.shape and np.array_equal(v, want), k
+        elif k.startswith("softmax"):
             assert_softmax(v, want, k)
         elif k in reductions:
             assert_reduction(v, want, k)

@@ -350,6 +350,86 @@ def test_rope_qk_gqa_half(be, orc):
     assert_elementwise(dk.download(), orc.rope(k, dim, cs, sn, False), "rope_qk half k")
 
 
+# ---------------------------------------------------------------- layout (bit-exact copies)
+def _exact(got, want, what):
+    assert got.shape == want.shape, what
+    assert np.array_equal(got, want), f"{what}: {int(np.sum(got != want))} elements differ"
+
+
+# (2,3,4,5): the reference test's image (scalar path, odd W); (2,3,4,8) and
+# (1,2,3,6): vector path; (1,512,64,64): a VAE decoder upsample input;
+# (1,1,1,1): minimal.
+@pytest.mark.parametrize("shape", [(2, 3, 4, 5), (2, 3, 4, 8), (1, 2, 3, 6), (1, 512, 64, 64), (1, 1, 1, 1)])
+def test_upsample_nearest2x(be, orc, shape):
+    x = orc.randn(shape, _seed("up", *shape))
+    N, Cc, H, W = shape
+    y = be.empty((N, Cc, 2 * H, 2 * W))
+    be.upsample_nearest2x(be.array(x), y, N * Cc, H, W)
+    _exact(y.download(), orc.upsample_nearest2x(x), f"upsample {shape}")
+
+
+# vector path (C*HW % 4 == 0), the SD 1.5 UNet skip concat, scalar path (HW = 9),
+# and an empty first operand.
+@pytest.mark.parametrize("sa,sb", [((2, 3, 4, 5), (2, 2, 4, 5)), ((2, 640, 64, 64), (2, 320, 64, 64)),
+                                   ((2, 3, 3, 3), (2, 2, 3, 3)), ((2, 0, 4, 4), (2, 5, 4, 4))])
+def test_concat_channels(be, orc, sa, sb):
+    a = orc.randn(sa, _seed("cca", *sa))
+    b = orc.randn(sb, _seed("ccb", *sb))
+    N, Ca, Cb = sa[0], sa[1], sb[1]
+    HW = sb[2] * sb[3]
+    y = be.empty((N, Ca + Cb) + sb[2:])
+    da = be.array(a) if a.size else be.empty((1,))
+    be.concat_channels(da, be.array(b), y, N, Ca, Cb, HW)
+    _exact(y.download(), orc.concat_channels(a, b), f"concat_channels {sa} {sb}")
+
+
+# tile-aligned (VAE attention [1,512,128x128], SD 1.5 [2,320,64x64]), partial
+# edge tiles (100 x 100), and the scalar path (C = 3).
+@pytest.mark.parametrize("shape", [(1, 512, 128, 128), (2, 320, 64, 64), (1, 100, 10, 10), (2, 3, 4, 5), (3, 8, 1, 12)])
+def test_nchw_nlc_round_trip(be, orc, shape):
+    x = orc.randn(shape, _seed("nlc", *shape))
+    N, Cc, H, W = shape
+    dx, dn, db = be.array(x), be.empty((N, H * W, Cc)), be.empty(shape)
+    be.nchw_to_nlc(dx, dn, N, Cc, H * W)
+    nlc = dn.download()
+    _exact(nlc, orc.nchw_to_nlc(x), f"nchw_to_nlc {shape}")
+    be.nlc_to_nchw(dn, db, N, Cc, H * W)
+    _exact(db.download(), orc.nlc_to_nchw(nlc, H, W), f"nlc_to_nchw {shape}")
+    _exact(db.download(), x, f"round trip {shape}")
+
+
+# the reference test's latent (16 x 6 x 8, p 2), the Z-Image 1024^2 latent
+# (16 x 128 x 128, p 2), p = 3 and p = 1.
+@pytest.mark.parametrize("Cc,H,W,p", [(16, 6, 8, 2), (16, 128, 128, 2), (3, 9, 12, 3), (5, 4, 7, 1)])
+def test_patchify_round_trip(be, orc, Cc, H, W, p):
+    x = orc.randn((1, Cc, H, W), _seed("pat", Cc, H, W, p))
+    ntok, F_ = (H // p) * (W // p), p * p * Cc
+    dx, dt, dy = be.array(x), be.empty((ntok, F_)), be.empty((1, Cc, H, W))
+    be.patchify(dx, dt, Cc, H, W, p)
+    tok = dt.download()
+    _exact(tok, orc.patchify(x, p), f"patchify {Cc}x{H}x{W} p{p}")
+    be.unpatchify(dt, dy, Cc, H, W, p)
+    _exact(dy.download(), orc.unpatchify(tok, Cc, H, W, p), f"unpatchify {Cc}x{H}x{W} p{p}")
+    _exact(dy.download(), x, "round trip")
+
+
+def test_layout_invalid_arguments(be):
+    d = be.empty((2 * 4 * 6,))
+    o = be.empty((2 * 4 * 6,))
+    with pytest.raises(sdhip.SdhError) as e:
+        be.patchify(d, o, 2, 4, 6, 4)  # W not a multiple of p
+    assert e.value.status == sdhip.SDH_ERR_INVALID
+    with pytest.raises(sdhip.SdhError) as e:
+        be.unpatchify(d, o, 2, 4, 6, 0)  # p = 0
+    assert e.value.status == sdhip.SDH_ERR_INVALID
+    with pytest.raises(sdhip.SdhError) as e:
+        be.nchw_to_nlc(d, d, 2, 4, 6)  # in place
+    assert e.value.status == sdhip.SDH_ERR_INVALID
+    with pytest.raises(sdhip.SdhError) as e:
+        be.upsample_nearest2x(d, o, 2, 4, 6)  # y smaller than 4x the input
+    assert e.value.status == sdhip.SDH_ERR_INVALID
+
+
 # ---------------------------------------------------------------- vs the compiled reference itself
 def test_against_compiled_reference(be, ref, orc):
     """The same checks against oracle/_ref (the reference's tensor.cpp)."""

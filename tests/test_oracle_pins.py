@@ -12,8 +12,8 @@ oracle's own formulas:
   * an independent library routine (torch.nn.functional in float64) for
     group_norm / layer_norm / rms_norm / softmax / silu;
   * planted mistakes: each pin must FAIL when a plausible bug (dropped eps,
-    flipped sign, wrong channel index, exp(+g), missing max subtraction) is
-    planted in the oracle.
+    flipped sign, wrong channel index, exp(+g), missing max subtraction,
+    swapped patch axes, a missing transpose) is planted in the oracle.
 """
 import math
 
@@ -231,6 +231,37 @@ def test_torch_library_cross_check(orc):
     assert max_abs(orc.silu(z), F.silu(t(z)).numpy()) <= 1e-6
 
 
+# ---------------------------------------------------------------- layout ops
+# Each layout op is a permutation/duplication of its input. The pins state it
+# independently as a numpy reshape/transpose/repeat (library routines, not the
+# reference's loops), plus the round trips the reference relies on.
+def test_patchify_matches_reshape_transpose(orc):
+    for Cc, H, W, p in ((16, 6, 8, 2), (3, 9, 12, 3), (5, 4, 4, 4), (2, 5, 7, 1)):
+        x = _x(orc, (1, Cc, H, W), 70 + Cc + p)
+        want = x.reshape(Cc, H // p, p, W // p, p).transpose(1, 3, 2, 4, 0).reshape((H // p) * (W // p), p * p * Cc)
+        tok = orc.patchify(x, p)
+        assert np.array_equal(tok, want), (Cc, H, W, p)
+        assert np.array_equal(orc.unpatchify(tok, Cc, H, W, p), x), "unpatchify(patchify(x)) != x"
+
+
+def test_nchw_nlc_match_transpose(orc):
+    for N, Cc, H, W in ((2, 3, 4, 5), (1, 64, 16, 24), (3, 7, 1, 9)):
+        x = _x(orc, (N, Cc, H, W), 80 + Cc)
+        nlc = orc.nchw_to_nlc(x)
+        assert np.array_equal(nlc, x.reshape(N, Cc, H * W).transpose(0, 2, 1))
+        back = orc.nlc_to_nchw(nlc, H, W)
+        assert np.array_equal(back, x), "nlc_to_nchw(nchw_to_nlc(x)) != x"
+
+
+def test_upsample_and_concat_match_numpy(orc):
+    x = _x(orc, (2, 3, 4, 5), 90)
+    assert np.array_equal(orc.upsample_nearest2x(x), np.repeat(np.repeat(x, 2, axis=2), 2, axis=3))
+    b = _x(orc, (2, 2, 4, 5), 91)
+    assert np.array_equal(orc.concat_channels(x, b), np.concatenate([x, b], axis=1))
+    e = np.zeros((2, 0, 4, 5), np.float32)
+    assert np.array_equal(orc.concat_channels(e, b), b)
+
+
 # ---------------------------------------------------------------- planted mistakes
 PLANTS = {
     1: ("rope interleaved sign", test_rope_interleaved_closed_form),
@@ -238,6 +269,8 @@ PLANTS = {
     3: ("softmax without max subtraction", test_softmax_brute_force_and_invariants),
     4: ("group_norm wrong gamma channel", test_group_norm_brute_force),
     5: ("swiglu exp(+g)", test_swiglu_closed_form),
+    6: ("patchify with ph and pw swapped", test_patchify_matches_reshape_transpose),
+    7: ("nlc_to_nchw without the transpose", test_nchw_nlc_match_transpose),
 }
 
 

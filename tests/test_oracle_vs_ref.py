@@ -92,3 +92,19 @@ def test_ln_modulate_gate_bitexact(orc, ref, shift):
     b = ref.ln_modulate_gate(x, r, sc, sh, gt, 1e-6)
     _eq(a[0], b[0], "res")
     _eq(a[1], b[1], "y")
+
+
+@pytest.mark.parametrize("N,Cc,H,W", [(2, 3, 4, 5), (1, 64, 16, 24), (3, 5, 7, 1), (1, 16, 6, 8)])
+def test_layout_bitexact(orc, ref, N, Cc, H, W):
+    x = orc.randn((N, Cc, H, W), 61 + Cc)
+    x2 = orc.randn((N, Cc + 1, H, W), 62 + Cc)
+    _eq(orc.upsample_nearest2x(x), ref.upsample_nearest2x(x), "upsample_nearest2x")
+    _eq(orc.concat_channels(x, x2), ref.concat_channels(x, x2), "concat_channels")
+    nlc = orc.nchw_to_nlc(x)
+    _eq(nlc, ref.nchw_to_nlc(x), "nchw_to_nlc")
+    _eq(orc.nlc_to_nchw(nlc, H, W), ref.nlc_to_nchw(nlc, H, W), "nlc_to_nchw")
+    for p in (1, 2, 3):
+        if H % p == 0 and W % p == 0 and N == 1:
+            tok = orc.patchify(x, p)
+            _eq(tok, ref.patchify(x, p), f"patchify p={p}")
+            _eq(orc.unpatchify(tok, Cc, H, W, p), ref.unpatchify(tok, Cc, H, W, p), f"unpatchify p={p}")
