@@ -150,6 +150,53 @@ class RopeQK(Workload):
         return run, [hq, hk, hc, hs]
 
 
+class QKNormRope(Workload):
+    """Fused QK-norm + RoPE at the config-3 shape (zimage.cpp:117-120). With
+    unfused=True the same result through the op sequence the reference calls
+    (two rms_norm_heads_ and the two rope_), for comparison; both are rated
+    on the fused op's algorithmic bytes."""
+
+    def __init__(self, unfused=False):
+        self.unfused = unfused
+        self.name = "qknorm_rope_unfused" if unfused else "qknorm_rope"
+        self.kernel = "k_heads" if unfused else "k_qknorm_rope_il"
+        self.desc = ("QK-norm (eps 1e-5, gamma [128]) then 3-axis interleaved RoPE on q and k [4096,30*128] in place" +
+                     (": the unfused GPU sequence (2 x rms_norm_heads + rope_qk), rated on the fused bytes"
+                      if unfused else ", one launch"))
+        self.algo_bytes = 4 * T * D * 4 + 2 * T * 128 * 4 + 2 * 128 * 4
+        self.cs, self.sn = _tables_3axis(T, 64)
+        if unfused:
+            self.cpu = None  # the CPU sequence is the fused line's baseline
+
+    def make(self, be, i):
+        return dict(q=be.randn((T, D), 17000 + i), k=be.randn((T, D), 17500 + i), c=be.array(self.cs),
+                    s=be.array(self.sn), gq=be.randn((128,), 17900 + i, 1.0, 0.1),
+                    gk=be.randn((128,), 17950 + i, 1.0, 0.1))
+
+    def step(self, be, s):
+        if self.unfused:
+            be.rms_norm_heads(s["q"], T * 30, 128, s["gq"], 1e-5)
+            be.rms_norm_heads(s["k"], T * 30, 128, s["gk"], 1e-5)
+            be.rope_qk(s["q"], D, s["k"], D, 1, T, 128, s["c"], s["s"], True)
+        else:
+            be.qknorm_rope(s["q"], D, s["k"], D, 1, T, 128, s["gq"], s["gk"], 1e-5, s["c"], s["s"], True)
+
+    def cpu(self, R, orc):
+        q, k = orc.randn((1, T, D), 17), orc.randn((1, T, D), 18)
+        gq, gk = orc.randn((128,), 19, 1.0, 0.1), orc.randn((128,), 20, 1.0, 0.1)
+        hq, hk, hgq, hgk = R.new(q.shape, q), R.new(k.shape, k), R.new(gq.shape, gq), R.new(gk.shape, gk)
+        hc, hs = R.new(self.cs.shape, self.cs), R.new(self.sn.shape, self.sn)
+
+        def run():
+            R._chk(R.lib.ref_rms_norm_heads_(hq, 128, hgq, 1e-5))
+            R._chk(R.lib.ref_rms_norm_heads_(hk, 128, hgk, 1e-5))
+            R._chk(R.lib.ref_rope_(hq, 128, hc, hs, 1))
+            R._chk(R.lib.ref_rope_(hk, 128, hc, hs, 1))
+            return []
+
+        return run, [hq, hk, hgq, hgk, hc, hs]
+
+
 class GNSiLU(Workload):
     kernel = "k_gn_"
 
@@ -328,6 +375,8 @@ def all_workloads():
         GNSiLU("4d", (2, 1280, 8, 8), 1e-5, "4d (SD 1.5, reported only)"),
         LNModGate(),
         Softmax(),
+        QKNormRope(),
+        QKNormRope(unfused=True),
     ] + [Layout(n) for n in Layout.SPECS]
 
 
@@ -369,7 +418,7 @@ def measure_cpu(w, reps):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     from oracle import Oracle, Reference, have_reference
 
-    if not hasattr(w, "cpu"):
+    if getattr(w, "cpu", None) is None:
         return None
     orc = Oracle()
     threads = cpu_threads()
@@ -425,6 +474,7 @@ KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
     "k_unary<4>": "copy_calibration", "k_add_rms": "add_rms_norm", "k_swiglu": "swiglu",
     "k_rope_il_reg": "rope_qk", "k_ln_mod_gate": "ln_modulate_gate", "k_softmax_block": "softmax_rows",
     "k_upsample2x_vec": "upsample_nearest2x", "k_concat_vec": "concat_channels", "k_patchify": "patchify2d",
+    "k_qknorm_rope_il": "qknorm_rope",
 }
 
 

@@ -115,6 +115,14 @@ int sdh_rope(float* x, int64_t N, int64_t S, int64_t inner, int64_t dim, const f
  * equals rope_(q, ...) then rope_(k, ...) (zimage.cpp:119-120). */
 int sdh_rope_qk(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
                 const float* cos, const float* sin, int interleaved);
+/* FUSED: QK-norm then RoPE on q [N, S, inner_q] and k [N, S, inner_k] in one
+ * launch; equals rms_norm_heads_(q, dim, gamma_q, eps),
+ * rms_norm_heads_(k, dim, gamma_k, eps), rope_(q, ...), rope_(k, ...)
+ * (zimage.cpp:117-120, interleaved; qwen3.cpp:59-62, rotate_half).
+ * gamma_q / gamma_k [dim] may be NULL; q and k must not overlap. */
+int sdh_qknorm_rope(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
+                    const float* gamma_q, const float* gamma_k, float eps, const float* cos, const float* sin,
+                    int interleaved);
 
 /* ---- softmax ------------------------------------------------------------- */
 /* backend_cuda.h:56 softmax_rows(); tensor.h:236. In place on x [rows, cols]:

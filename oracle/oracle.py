@@ -82,6 +82,7 @@ class Oracle:
             "orc_add_channel_bias": (None, [_f32p, _f32p, _i64, _i64, _i64]),
             "orc_add_rms_norm": (None, [_f32p, _f32p, _f32p, _i64, _i64, N, _fl]),
             "orc_ln_modulate_gate": (None, [_f32p, _f32p, _f32p, N, _f32p, N, _i64, _i64, _fl]),
+            "orc_qknorm_rope": (None, [_f32p, _i64, _f32p, _i64, _i64, _i64, _i64, N, N, _fl, _f32p, _f32p, C.c_int]),
             "orc_upsample_nearest2x": (None, [_f32p, _f32p, _i64, _i64, _i64]),
             "orc_concat_channels": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64]),
             "orc_nchw_to_nlc": (None, [_f32p, _f32p, _i64, _i64, _i64]),
@@ -253,6 +254,15 @@ class Oracle:
         self.lib.orc_ln_modulate_gate(x, r, _f32(scale), None if shift is None else _f32(shift), _f32(gate), y,
                                       x.size // Cc, Cc, eps)
         return r, y
+
+    def qknorm_rope(self, q, k, dim, gamma_q, gamma_k, eps, cos_t, sin_t, interleaved):
+        """q [N, S, inner_q], k [N, S, inner_k] -> (q', k'): QK-norm then RoPE."""
+        q2, k2 = _f32(q).copy(), _f32(k).copy()
+        N, S = q2.shape[0], q2.shape[1]
+        self.lib.orc_qknorm_rope(q2, q2.shape[-1], k2, k2.shape[-1], N, S, dim,
+                                 None if gamma_q is None else _f32(gamma_q), None if gamma_k is None else _f32(gamma_k),
+                                 eps, _f32(cos_t), _f32(sin_t), 1 if interleaved else 0)
+        return q2, k2
 
     # -- layout (tensor.cpp:931-1099) --
     def upsample_nearest2x(self, x):

@@ -494,6 +494,15 @@ void orc_add_channel_bias(float* x, const float* b, int64_t N, int64_t C, int64_
     items(N * C, add_channel_bias_body, &c);
 }
 
+void orc_qknorm_rope(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
+                     const float* gamma_q, const float* gamma_k, float eps, const float* cos_t, const float* sin_t,
+                     int interleaved) {
+    orc_rms_norm_heads(q, N * S * inner_q / dim, dim, gamma_q, eps);
+    orc_rms_norm_heads(k, N * S * inner_k / dim, dim, gamma_k, eps);
+    orc_rope(q, N, S, inner_q, dim, cos_t, sin_t, interleaved);
+    orc_rope(k, N, S, inner_k, dim, cos_t, sin_t, interleaved);
+}
+
 /* ------------------------------------------------------------------------ */
 /* Layout (tensor.cpp:931-1099): copies, in the reference's loop order       */
 /* ------------------------------------------------------------------------ */

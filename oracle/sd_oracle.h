@@ -87,6 +87,12 @@ void orc_group_norm_silu(const float* x, float* y, int64_t N, int64_t C, int64_t
 void orc_ln_modulate_gate(const float* x, float* res, const float* scale, const float* shift, const float* gate,
                           float* y_out, int64_t rows, int64_t C, float eps);
 
+/* rms_norm_heads_(q), rms_norm_heads_(k), rope_(q), rope_(k): zimage.cpp:117-120,
+ * qwen3.cpp:59-62 (composition of the functions above). */
+void orc_qknorm_rope(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
+                     const float* gamma_q, const float* gamma_k, float eps, const float* cos_t, const float* sin_t,
+                     int interleaved);
+
 /* ---- layout (tensor.cpp:931-1099); y never overlaps the inputs ---- */
 /* tensor.cpp:982-1004: x [NC, H, W] -> y [NC, 2H, 2W]. */
 void orc_upsample_nearest2x(const float* x, float* y, int64_t NC, int64_t H, int64_t W);

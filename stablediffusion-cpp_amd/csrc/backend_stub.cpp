@@ -62,6 +62,8 @@ STUB(int sdh_add_rms_norm(float*, const float*, float*, int64_t, int64_t, const 
 STUB(int sdh_group_norm_silu(const float*, float*, int64_t, int64_t, int64_t, int, const float*, const float*, float))
 STUB(int sdh_ln_modulate_gate(const float*, float*, const float*, const float*, const float*, float*, int64_t,
                               int64_t, float))
+STUB(int sdh_qknorm_rope(float*, int64_t, float*, int64_t, int64_t, int64_t, int64_t, const float*, const float*,
+                         float, const float*, const float*, int))
 STUB(int sdh_upsample_nearest2x(const float*, float*, int64_t, int64_t, int64_t))
 STUB(int sdh_concat_channels(const float*, const float*, float*, int64_t, int64_t, int64_t, int64_t))
 STUB(int sdh_nchw_to_nlc(const float*, float*, int64_t, int64_t, int64_t))

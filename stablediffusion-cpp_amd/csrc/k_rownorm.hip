@@ -39,10 +39,7 @@ enum Mode { M_LN = 0, M_RMS = 1 };
 
 __device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
 
-// rstd as the reference forms it: (float)(1 / sqrt(stat / C + eps)) in double.
-__device__ __forceinline__ float rstd_of(float stat, int64_t C, float eps) {
-    return (float)(1.0 / sqrt((double)stat / (double)C + (double)eps));
-}
+using dev::rstd_of;
 
 // y = layer_norm / rms_norm of each row of x (tensor.cpp:628-679).
 template <int V, int MODE, bool HAS_G, bool HAS_B>

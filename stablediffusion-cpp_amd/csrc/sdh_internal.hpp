@@ -151,6 +151,12 @@ __device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp
 // x / (1 + exp(-x)) with the hardware reciprocal (v_rcp_f32, 1 ulp).
 __device__ __forceinline__ float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(1.0f + exp_fast(-x)); }
 
+// rstd as the reference forms it: (float)(1 / sqrt(stat / C + eps)) in double
+// (tensor.cpp:648, :674, :692).
+__device__ __forceinline__ float rstd_of(float stat, int64_t C, float eps) {
+    return (float)(1.0 / sqrt((double)stat / (double)C + (double)eps));
+}
+
 // Reference-order activations (tensor.cpp:745, :847, :859, :866, :830).
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 __device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }

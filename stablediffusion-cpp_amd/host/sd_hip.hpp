@@ -10,8 +10,8 @@
 // backend reports failures (check()/launched(), backend_cuda.cu:41-48, and the
 // stub's throw, backend_cuda_stub.cpp:14).
 //
-// GEMM, conv2d, attention and the layout copies stay with their existing
-// implementations; they are not part of this backend.
+// GEMM, conv2d and attention stay with their existing implementations; they
+// are not part of this backend.
 #pragma once
 
 #include <cstddef>
@@ -127,6 +127,12 @@ inline void softmax_rows_batched(float* x, int64_t rows, int64_t cols, float sca
 inline void rope_qk(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
                     const float* cos, const float* sin, bool interleaved) {
     detail::check(sdh_rope_qk(q, inner_q, k, inner_k, N, S, dim, cos, sin, interleaved ? 1 : 0), "hip::rope_qk");
+}
+inline void qknorm_rope(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
+                        const float* gamma_q, const float* gamma_k, float eps, const float* cos, const float* sin,
+                        bool interleaved) {
+    detail::check(sdh_qknorm_rope(q, inner_q, k, inner_k, N, S, dim, gamma_q, gamma_k, eps, cos, sin, interleaved ? 1 : 0),
+                  "hip::qknorm_rope");
 }
 inline void add_rms_norm(float* x, const float* r, float* y, int64_t rows, int64_t C, const float* gamma, float eps) {
     detail::check(sdh_add_rms_norm(x, r, y, rows, C, gamma, eps), "hip::add_rms_norm");

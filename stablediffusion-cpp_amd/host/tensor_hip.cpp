@@ -424,4 +424,18 @@ void rope_qk_(Tensor& q, Tensor& k, int64_t dim, const Tensor& cos, const Tensor
     sd::hip::rope_qk(q.dptr(), q.dim(-1), k.dptr(), k.dim(-1), N, S, dim, cos.dptr(), sin.dptr(), interleaved);
 }
 
+// zimage.cpp:117-120 / qwen3.cpp:59-62 in one launch
+void qknorm_rope_(Tensor& q, Tensor& k, int64_t dim, const Tensor* gamma_q, const Tensor* gamma_k, float eps,
+                  const Tensor& cos, const Tensor& sin, bool interleaved) {
+    need_hip(q, "qknorm_rope_");
+    same_device(q, k, "qknorm_rope_");
+    if (gamma_q) same_device(q, *gamma_q, "qknorm_rope_");
+    if (gamma_k) same_device(q, *gamma_k, "qknorm_rope_");
+    const int64_t S = q.dim(-2), N = q.numel() / (S * q.dim(-1));
+    if (k.dim(-2) != S || k.numel() / (S * k.dim(-1)) != N) throw std::runtime_error("qknorm_rope_: q/k token mismatch");
+    if (cos.dim(0) < S || cos.dim(1) != dim) throw std::runtime_error("rope_: table shape mismatch");
+    sd::hip::qknorm_rope(q.dptr(), q.dim(-1), k.dptr(), k.dim(-1), N, S, dim, opt(gamma_q), opt(gamma_k), eps,
+                         cos.dptr(), sin.dptr(), interleaved);
+}
+
 }  // namespace sdh

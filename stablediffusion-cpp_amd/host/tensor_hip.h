@@ -112,5 +112,9 @@ void ln_modulate_gate_(const Tensor& x, Tensor& res, const Tensor& scale, const 
                        float eps, Tensor* y_out = nullptr);
 // rope_(q, ...) then rope_(k, ...) in one launch (zimage.cpp:119-120)
 void rope_qk_(Tensor& q, Tensor& k, int64_t dim, const Tensor& cos, const Tensor& sin, bool interleaved);
+// rms_norm_heads_(q, dim, gamma_q, eps); rms_norm_heads_(k, dim, gamma_k, eps);
+// rope_(q, ...); rope_(k, ...) in one launch (zimage.cpp:117-120)
+void qknorm_rope_(Tensor& q, Tensor& k, int64_t dim, const Tensor* gamma_q, const Tensor* gamma_k, float eps,
+                  const Tensor& cos, const Tensor& sin, bool interleaved);
 
 }  // namespace sdh

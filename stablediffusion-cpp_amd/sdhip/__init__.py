@@ -63,6 +63,7 @@ SIGNATURES = {
     "sdh_rms_norm_heads": [_vp, _i64, _i64, _vp, _fl],
     "sdh_rope": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _int],
     "sdh_rope_qk": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _int],
+    "sdh_qknorm_rope": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _fl, _vp, _vp, C.c_int],
     "sdh_softmax_rows": [_vp, _i64, _i64, _fl, _int],
     "sdh_softmax_rows_batched": [_vp, _i64, _i64, _fl, _int, _i64],
     "sdh_swiglu": [_vp, _vp, _vp, _i64],
@@ -252,6 +253,10 @@ class Backend:
     def rope_qk(self, q, inner_q, k, inner_k, N, S, dim, cos_t, sin_t, interleaved):
         self.call("sdh_rope_qk", _p(q), inner_q, _p(k), inner_k, N, S, dim, _p(cos_t), _p(sin_t),
                   int(bool(interleaved)))
+
+    def qknorm_rope(self, q, inner_q, k, inner_k, N, S, dim, gamma_q, gamma_k, eps, cos, sin, interleaved):
+        self.call("sdh_qknorm_rope", _p(q), inner_q, _p(k), inner_k, N, S, dim, _p(gamma_q), _p(gamma_k), eps, _p(cos),
+                  _p(sin), 1 if interleaved else 0)
 
     def softmax_rows(self, x, rows, cols, scale, causal=False, period=None):
         if period is None:

@@ -257,6 +257,15 @@ static void test_hip() {
         sdh::rope_qk_(qg, kg, dim, cs.to(G), sn.to(G), true);
         hip_check_op("rope_qk_ q (Z-Image tables)", q, qg, 1e-5);
         hip_check_op("rope_qk_ k (Z-Image tables)", k, kg, 1e-5);
+        // QK-norm + RoPE fused (zimage.cpp:117-120) vs the oracle's op sequence
+        Tensor q2 = randn_t({1, S, inner}), k2 = randn_t({1, S, inner});
+        Tensor gq = randn_t({dim}, 1.f, 0.1f), gk = randn_t({dim}, 1.f, 0.1f);
+        Tensor q2g = q2.to(G), k2g = k2.to(G), gqg = gq.to(G), gkg = gk.to(G);
+        orc_qknorm_rope(q2.data.data(), inner, k2.data.data(), inner, 1, S, dim, gq.data.data(), gk.data.data(), 1e-5f,
+                        cs.data.data(), sn.data.data(), 1);
+        sdh::qknorm_rope_(q2g, k2g, dim, &gqg, &gkg, 1e-5f, cs.to(G), sn.to(G), true);
+        check("hip qknorm_rope_ q (rel)", rel_diff(q2, q2g), 1e-4);
+        check("hip qknorm_rope_ k (rel)", rel_diff(k2, k2g), 1e-4);
     }
     // error behaviour: the reference's shape/device checks throw
     {

@@ -350,6 +350,47 @@ def test_rope_qk_gqa_half(be, orc):
     assert_elementwise(dk.download(), orc.rope(k, dim, cs, sn, False), "rope_qk half k")
 
 
+# ---------------------------------------------------------------- fused QK-norm + RoPE
+# (interleaved, N, S, q heads, k heads, dim, gamma): the Z-Image config shape;
+# Qwen3-style GQA rotate_half; no gamma; dims 64 and 32; 1, 2 and 4 float4
+# steps; and shapes that take the op-by-op path (dim 24; rows wider than 8
+# float4 per thread).
+QKN = [
+    (True, 1, T, 30, 30, 128, True), (False, 2, 37, 8, 2, 128, True), (True, 2, 9, 40, 40, 64, False),
+    (False, 1, 11, 100, 100, 32, True), (True, 1, 5, 6, 2, 128, True), (True, 1, 7, 5, 5, 24, True),
+    (True, 1, 3, 70, 70, 128, True), (False, 1, 3, 40, 40, 128, False), (True, 1, 4, 12, 12, 128, True),
+    (True, 1, 3, 60, 60, 128, False),
+]
+
+
+@pytest.mark.parametrize("inter,N,S,hq,hk,dim,gam", QKN)
+def test_qknorm_rope(be, orc, inter, N, S, hq, hk, dim, gam):
+    q = orc.randn((N, S, hq * dim), _seed("qkn_q", N, S, hq, dim), 0.5, 2.0)
+    k = orc.randn((N, S, hk * dim), _seed("qkn_k", N, S, hk, dim), 0.5, 2.0)
+    gq = orc.randn((dim,), _seed("qkn_gq", dim), 1.0, 0.1) if gam else None
+    gk = orc.randn((dim,), _seed("qkn_gk", dim), 1.0, 0.1) if gam else None
+    if inter and dim == 128 and S == T:
+        cs, sn = _zimage_tables(orc, T, 64)
+    else:
+        ang = orc.randn((S, dim), _seed("qkn_t", S, dim), 0.0, 1.0)
+        cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    dq, dk, dc, ds = be.array(q), be.array(k), be.array(cs), be.array(sn)
+    dgq = be.array(gq) if gam else None
+    dgk = be.array(gk) if gam else None
+    be.qknorm_rope(dq, hq * dim, dk, hk * dim, N, S, dim, dgq, dgk, 1e-5, dc, ds, inter)
+    wq, wk = orc.qknorm_rope(q, k, dim, gq, gk, 1e-5, cs, sn, inter)
+    got_q, got_k = dq.download(), dk.download()
+    assert_reduction(got_q, wq, f"qknorm_rope q inter={inter} dim={dim}")
+    assert_reduction(got_k, wk, f"qknorm_rope k inter={inter} dim={dim}")
+    # the same ops unfused on the GPU
+    uq, uk = be.array(q), be.array(k)
+    be.rms_norm_heads(uq, N * S * hq, dim, dgq, 1e-5)
+    be.rms_norm_heads(uk, N * S * hk, dim, dgk, 1e-5)
+    be.rope_qk(uq, hq * dim, uk, hk * dim, N, S, dim, dc, ds, inter)
+    print(f"fused vs unfused GPU: q {np.max(np.abs(got_q - uq.download())):.3e}, "
+          f"k {np.max(np.abs(got_k - uk.download())):.3e}")
+
+
 # ---------------------------------------------------------------- layout (bit-exact copies)
 def _exact(got, want, what):
     assert got.shape == want.shape, what

@@ -108,3 +108,21 @@ def test_layout_bitexact(orc, ref, N, Cc, H, W):
             tok = orc.patchify(x, p)
             _eq(tok, ref.patchify(x, p), f"patchify p={p}")
             _eq(orc.unpatchify(tok, Cc, H, W, p), ref.unpatchify(tok, Cc, H, W, p), f"unpatchify p={p}")
+
+
+@pytest.mark.parametrize("interleaved", [True, False])
+def test_qknorm_rope_bitexact(orc, ref, interleaved):
+    """The fused QK-norm + RoPE oracle equals the reference's op sequence
+    (zimage.cpp:117-120, qwen3.cpp:59-62) run through its own tensor.cpp."""
+    S, dim = 16, 64
+    q = orc.randn((2, S, 4 * dim), 71, 0.5, 2.0)
+    k = orc.randn((2, S, 2 * dim), 72, 0.5, 2.0)
+    gq = orc.randn((dim,), 73, 1.0, 0.1)
+    gk = orc.randn((dim,), 74, 1.0, 0.1)
+    ang = orc.randn((S, dim), 75, 0.0, 1.0)
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    q2, k2 = orc.qknorm_rope(q, k, dim, gq, gk, 1e-5, cs, sn, interleaved)
+    rq = ref.rope(ref.rms_norm_heads(q, dim, gq, 1e-5).reshape(q.shape), dim, cs, sn, interleaved)
+    rk = ref.rope(ref.rms_norm_heads(k, dim, gk, 1e-5).reshape(k.shape), dim, cs, sn, interleaved)
+    _eq(q2, rq, "qknorm_rope q")
+    _eq(k2, rk, "qknorm_rope k")
