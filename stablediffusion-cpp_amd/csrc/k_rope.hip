@@ -270,9 +270,9 @@ void run_rope(const char* op, float* q, int64_t inner_q, float* k, int64_t inner
 // L lanes holds one head at every step (L divides 256): group_sum<L> gives the
 // head's sum of squares, and a lane's position in the head -- hence its gamma
 // and table entries -- is the same at every step. Per element it applies
-// k_heads' operations (o = x * rstd, then * gamma) and then k_rope_il_reg's;
-// where the compiler contracts them differently the results differ from the
-// unfused kernels by an ulp or two (measured <= 7.2e-7 on O(1) outputs).
+// k_heads' operations (o = x * rstd, then * gamma, with the fp32 rstd_fast)
+// and then k_rope_il_reg's; where the compiler contracts them differently the
+// results differ from the unfused kernels by an ulp or two.
 // rotate_half: a lane holds the pair (k, k + dim/8) of float4, L = dim / 8
 // lanes per head. All lanes join the reductions (rows outside the tensor are
 // zeros); only the loads and stores are guarded.
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(kThreads) void k_qknorm_rope_il(QKArgs a, int64_t S
 #pragma unroll
     for (int j = 0; j < RV; ++j) {
         const float q = dev::group_sum<L>(dev::hsum(v[j] * v[j]));
-        const float rstd = dev::rstd_of(q, dim, eps);
+        const float rstd = dev::rstd_fast(q, 1.0f / (4 * L), eps);  // dim = 4 L
         f4 o = v[j] * rstd;
         if (gp) o = o * g;
         f4 r;
@@ -352,7 +352,7 @@ __global__ __launch_bounds__(kThreads) void k_qknorm_rope_half(QKArgs a, int64_t
 #pragma unroll
     for (int j = 0; j < RV; ++j) {
         const float q = dev::group_sum<L>(dev::hsum(lo[j] * lo[j]) + dev::hsum(hi[j] * hi[j]));
-        const float rstd = dev::rstd_of(q, dim, eps);
+        const float rstd = dev::rstd_fast(q, 1.0f / (8 * L), eps);  // dim = 8 L
         f4 a0 = lo[j] * rstd, b0 = hi[j] * rstd;
         if (gp) {
             a0 = a0 * glo;

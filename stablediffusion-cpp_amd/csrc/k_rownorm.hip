@@ -254,7 +254,7 @@ __global__ __launch_bounds__(kThreads) void k_heads(float* __restrict__ x, int64
     f4* p = (f4*)(x + grp * dim) + sub;
     const f4 v = ok ? *p : zero4();
     const float q = dev::group_sum<L>(dev::hsum(v * v));  // all 64 lanes take part
-    const float rstd = rstd_of(q, dim, eps);
+    const float rstd = dev::rstd_fast(q, 1.0f / (4 * L), eps);  // dim = 4 L
     f4 o = v * rstd;
     if constexpr (HAS_G) o = o * ((const f4*)gamma)[sub];
     if (ok) dev::st_stream(p, o);

@@ -156,6 +156,14 @@ __device__ __forceinline__ float silu_fast(float x) { return x * __builtin_amdgc
 __device__ __forceinline__ float rstd_of(float stat, int64_t C, float eps) {
     return (float)(1.0 / sqrt((double)stat / (double)C + (double)eps));
 }
+// rstd for per-head statistics (one per few float4 per lane, as in QK-norm):
+// stat * (1/C) + eps in fp32, then the hardware reciprocal square root
+// (v_rsq_f32, 1 ulp). A few ulp from rstd_of's double form, far inside the
+// 1e-4 bound of the norms; the double divide and square root per head
+// measured 6 of 46 us in the fused QK-norm + RoPE kernel on MI355X.
+__device__ __forceinline__ float rstd_fast(float stat, float inv_c, float eps) {
+    return __builtin_amdgcn_rsqf(stat * inv_c + eps);
+}
 
 // Reference-order activations (tensor.cpp:745, :847, :859, :866, :830).
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
