@@ -20,9 +20,9 @@
 //       finalize (k_gn_finalize): one wave per segment merges the
 //         segment's chunk pairs in double in a fixed order (M2 = sum M2_i +
 //         n_i (mean_i - mean)^2, the exact pairwise identity) into
-//         (mean, rstd). A separate tiny launch measured faster than merging
-//         inside every pass-B workgroup, which puts a dependent L2 round trip
-//         and two reductions in front of each workgroup's stores.
+//         (mean, rstd). Segments of at most 64 chunks skip this launch: each
+//         pass-B wave merges the pairs itself, loading them before its x
+//         loads so the merge overlaps them (4a: 16.6 -> 14.7 us).
 //       pass B (k_gn_apply): one workgroup per chunk, with the same
 //         workgroup -> chunk mapping as pass A, so each chunk is re-read on
 //         the XCD whose L2 read it in pass A (tensors up to the 32 MB of
@@ -188,37 +188,61 @@ __global__ __launch_bounds__(64) void k_gn_finalize(const float2* __restrict__ p
 // segments are < 2^31 floats on this path). Index math stays 32-bit: a
 // 64-bit division here expands into a software routine that doubled the
 // kernel's VGPR count and cost a third of its bandwidth.
-template <bool SILU, bool UNIFORM>
+// MERGE (segments of at most 64 chunks): no finalize launch; every wave
+// merges its segment's chunk pairs itself with k_gn_finalize's arithmetic
+// (one pair per lane) and takes lane 0's result, the value the finalize
+// kernel would store. The pair loads are issued before the x loads: loads
+// complete in order, so the merge runs while the x loads are in flight
+// instead of after them.
+template <bool SILU, bool UNIFORM, bool MERGE>
 __global__ __launch_bounds__(kThreads) void k_gn_apply(const float* __restrict__ x, float* __restrict__ y, int64_t L,
                                                       int HW, int chunks_per_ch, int cg, int groups, int seg0,
                                                       const float2* __restrict__ stats,
+                                                      const float2* __restrict__ part, int nchunks, float eps,
                                                       const float* __restrict__ gamma,
                                                       const float* __restrict__ beta) {
     const int seg = blockIdx.y, chunk = blockIdx.x;
     const int off = chunk * (int)kChunk;
     const f4* p = (const f4*)(x + (int64_t)seg * L + off);
     f4* q = (f4*)(y + (int64_t)seg * L + off);
-    const float2 st = stats[seg];
-    const float meanf = st.x, rstd = st.y;
+    const int lane = threadIdx.x & 63;
+    float2 st = make_float2(0.f, 0.f);
+    if constexpr (MERGE) st = lane < nchunks ? part[(int64_t)seg * nchunks + lane] : make_float2(0.f, 0.f);
+    else st = stats[seg];
+    const int cnt = UNIFORM ? (int)kChunk : (int)(L - off < kChunk ? L - off : kChunk);
+    const int n4 = cnt >> 2;
+    f4 v[kChunkV];
+#pragma unroll
+    for (int j = 0; j < kChunkV; ++j) {
+        const int idx = threadIdx.x + kThreads * j;
+        if (UNIFORM || idx < n4) v[j] = dev::ld_stream(p + idx);
+    }
+    float meanf, rstd;
+    if constexpr (MERGE) {
+        const double tot = lane < nchunks ? (double)st.x : 0.0;
+        const double mean = wave_dsum(tot) / (double)L;
+        double m2t = 0.0;
+        if (lane < nchunks) {
+            const int64_t o = (int64_t)lane * kChunk;
+            const double ni = (double)(L - o < kChunk ? L - o : kChunk);
+            const double dm = (double)st.x / ni - mean;
+            m2t = (double)st.y + ni * dm * dm;
+        }
+        const double m2 = wave_dsum(m2t);
+        meanf = dev::readlane((float)mean, 0);
+        rstd = dev::readlane((float)(1.0 / sqrt(m2 / (double)L + (double)eps)), 0);
+    } else {
+        meanf = st.x;
+        rstd = st.y;
+    }
     const int gc = ((seg0 + seg) % groups) * cg;
     if constexpr (UNIFORM) {
-        f4 v[kChunkV];
-#pragma unroll
-        for (int j = 0; j < kChunkV; ++j) v[j] = dev::ld_stream(p + threadIdx.x + kThreads * j);
         const int ch = gc + chunk / chunks_per_ch;
         const float a = rstd * gamma[ch];
         const float b = beta[ch] - meanf * a;
 #pragma unroll
         for (int j = 0; j < kChunkV; ++j) dev::st_stream(q + threadIdx.x + kThreads * j, apply4<SILU>(v[j], a, b));
     } else {
-        const int cnt = (int)(L - off < kChunk ? L - off : kChunk);
-        const int n4 = cnt >> 2;
-        f4 v[kChunkV];
-#pragma unroll
-        for (int j = 0; j < kChunkV; ++j) {
-            const int idx = threadIdx.x + kThreads * j;
-            if (idx < n4) v[j] = dev::ld_stream(p + idx);
-        }
 #pragma unroll
         for (int j = 0; j < kChunkV; ++j) {
             const int idx = threadIdx.x + kThreads * j;
@@ -349,13 +373,22 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
             const dim3 grid((unsigned)nchunks, (unsigned)k);
             k_gn_partial<<<grid, kThreads, 0, stream()>>>(xb, L, nchunks, part);
             launched(op);
-            k_gn_finalize<<<(unsigned)k, 64, 0, stream()>>>(part, L, nchunks, stats, eps);
-            launched(op);
+            const bool merge = nchunks <= 64;  // one chunk pair per lane: merged inside pass B
+            if (!merge) {
+                k_gn_finalize<<<(unsigned)k, 64, 0, stream()>>>(part, L, nchunks, stats, eps);
+                launched(op);
+            }
             const int seg0 = (int)(s0 % groups);
             auto apply = [&](auto sc, auto uc) {
                 constexpr bool S = decltype(sc)::value, U = decltype(uc)::value;
-                k_gn_apply<S, U><<<grid, kThreads, 0, stream()>>>(xb, yb, L, (int)HW, cpc, (int)cg, groups, seg0,
-                                                                  stats, gamma, beta);
+                if (merge)
+                    k_gn_apply<S, U, true><<<grid, kThreads, 0, stream()>>>(xb, yb, L, (int)HW, cpc, (int)cg, groups,
+                                                                            seg0, stats, part, (int)nchunks, eps,
+                                                                            gamma, beta);
+                else
+                    k_gn_apply<S, U, false><<<grid, kThreads, 0, stream()>>>(xb, yb, L, (int)HW, cpc, (int)cg, groups,
+                                                                             seg0, stats, part, (int)nchunks, eps,
+                                                                             gamma, beta);
             };
             using T_ = std::true_type;
             using F_ = std::false_type;

@@ -180,6 +180,7 @@ GN_SHAPES = [
     ((2, 320, 64, 64), 32, 1e-5),       # config 4c (SD 1.5)
     ((2, 1280, 8, 8), 32, 1e-5),        # config 4d (SD 1.5)
     ((1, 96, 33, 17), 32, 1e-6),        # odd plane: generic kernel
+    ((1, 16, 300, 300), 2, 1e-6),       # > 64 chunks per segment, plane not a whole number of chunks
     ((3, 8, 4, 4), 4, 1e-6),
 ]
 
