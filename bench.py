@@ -42,6 +42,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "stablediffusion-cpp_amd"))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFS = 2500.0  # dense bf16 MFMA peak of the MI355X (no sparsity)
 METRIC = "achieved HBM GB/s (% of peak) per op at Z-Image 1024² shapes; speedup vs CPU"
 T, D, F = 4096, 3840, 10240
 MIN_ROTATION_BYTES = 512_000_000  # 2x the 256 MB Infinity Cache
@@ -347,6 +348,71 @@ class Layout(Workload):
         return (lambda: [R._ptr(fn())]), hs
 
 
+def _bf16_weights(shape, seed, std):
+    """Synthetic bf16 weights (uint16 bit patterns): seeded normals rounded to
+    nearest even."""
+    w = (np.random.default_rng(seed).standard_normal(shape, dtype=np.float32) * np.float32(std)).view(np.uint32)
+    return ((w + np.uint32(0x7FFF) + ((w >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+
+
+class Linear(Workload):
+    """The linear layer with bf16 weights on the MFMA units (backend_cuda.h:42)
+    at the Z-Image DiT shapes, 4096 image tokens: an attention projection
+    [4096,3840] x [3840,3840]^T + bias, and the FFN front half
+    swiglu(x w1^T, x w3^T) with w1, w3 [10240,3840] -- fused, and unfused as the
+    reference runs it (two GEMMs, then swiglu). Rated in TFLOP/s against the
+    dense bf16 MFMA peak."""
+
+    def __init__(self, kind):
+        self.name = kind
+        self.kernel = "k_gemm_bf16"
+        if kind == "linear_bf16":
+            self.M, self.N, self.K = T, D, D
+            self.flops = 2 * self.M * self.N * self.K
+            self.algo_bytes = self.M * self.K * 4 + self.N * self.K * 2 + self.M * self.N * 4 + self.N * 4
+            self.desc = "linear, bf16 weights: y = x W^T + b, x [4096,3840] fp32, W [3840,3840] bf16 (Z-Image to_q/k/v/out)"
+        else:
+            self.M, self.N, self.K = T, F, D
+            self.flops = 2 * 2 * self.M * self.N * self.K
+            self.algo_bytes = self.M * self.K * 4 + 2 * self.N * self.K * 2 + self.M * self.N * 4
+            self.desc = ("swiglu(x w1^T, x w3^T), x [4096,3840] fp32, w1, w3 [10240,3840] bf16 (Z-Image FFN, zimage.cpp:130)" +
+                         (": the reference's sequence (two GEMMs, then swiglu)" if kind.endswith("unfused") else ", one GEMM"))
+        if kind != "linear_bf16":
+            self.cpu = None  # tens of seconds per step on the host; the projection line carries the CPU baseline
+
+    def make(self, be, i):
+        d = dict(x=be.randn((self.M, self.K), 18000 + i))
+        if self.name == "linear_bf16":
+            d["w"] = be.array(_bf16_weights((self.N, self.K), 18100 + i, 0.02))
+            d["b"] = be.randn((self.N,), 18200 + i, 0.0, 0.1)
+        else:
+            d["w1"] = be.array(_bf16_weights((self.N, self.K), 18300 + i, 0.02))
+            d["w3"] = be.array(_bf16_weights((self.N, self.K), 18400 + i, 0.02))
+            if self.name.endswith("unfused"):
+                d["g"], d["u"] = be.empty((self.M, self.N)), be.empty((self.M, self.N))
+        d["y"] = be.empty((self.M, self.N))
+        return d
+
+    def step(self, be, s):
+        M, N, K = self.M, self.N, self.K
+        if self.name == "linear_bf16":
+            be.gemm_nt_bf16(M, N, K, s["x"], K, s["w"], K, s["y"], N, s["b"])
+        elif self.name == "linear_swiglu":
+            be.linear_swiglu(s["x"], s["w1"], s["w3"], s["y"], M, K, N)
+        else:
+            be.gemm_nt_bf16(M, N, K, s["x"], K, s["w1"], K, s["g"], N)
+            be.gemm_nt_bf16(M, N, K, s["x"], K, s["w3"], K, s["u"], N)
+            be.swiglu(s["g"], s["u"], s["y"], M * N)
+
+    def cpu(self, R, orc):
+        x = orc.randn((self.M, self.K), 18)
+        W = orc.randn((self.N, self.K), 19, 0.0, 0.02)
+        b = orc.randn((self.N,), 20, 0.0, 0.1)
+        hx, hw, hb = R.new(x.shape, x), R.new(W.shape, W), R.new(b.shape, b)
+        R._chk(R.lib.ref_tensor_to_bf16(hw))
+        return (lambda: [R._ptr(R.lib.ref_linear(hx, hw, hb))]), [hx, hw, hb]
+
+
 class CopyCalibration(Workload):
     """Not a BASELINE config: an in-place x *= 1 stream over [4096,10240]
     (one read + one write of 168 MB), the plain-copy reference for what HBM
@@ -377,7 +443,7 @@ def all_workloads():
         Softmax(),
         QKNormRope(),
         QKNormRope(unfused=True),
-    ] + [Layout(n) for n in Layout.SPECS]
+    ] + [Layout(n) for n in Layout.SPECS] + [Linear(k) for k in ("linear_bf16", "linear_swiglu", "linear_swiglu_unfused")]
 
 
 # ------------------------------------------------------------------ GPU timing
@@ -619,15 +685,21 @@ def main():
         entry = dict(op=w.name, desc=w.desc, algo_bytes=w.algo_bytes, us_per_op=round(r["event_ms"] * 1e3, 2),
                      GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1), rotation_sets=r["nsets"],
                      rotation_MB=round(r["footprint"] / 2**20), traffic_bytes=read_traffic(w.name))
+        flops = getattr(w, "flops", None)
+        if flops:
+            tfs = flops / (r["event_ms"] * 1e-3) / 1e12
+            entry.update(flops=flops, TFLOPs=round(tfs, 1), pct_mfma_peak=round(100 * tfs / MFMA_BF16_PEAK_TFS, 1))
         if args.cpu_all and not args.no_cpu:
-            c = measure_cpu(w, 3 if w.algo_bytes > (1 << 30) else args.cpu_reps)
+            heavy = w.algo_bytes > (1 << 30) or (flops or 0) > 1e10
+            c = measure_cpu(w, 1 if (flops or 0) > 1e10 else 3 if heavy else args.cpu_reps)
             if c:
                 entry.update(cpu_ms=round(c["ms"], 3), cpu_threads=c["threads"],
                              speedup_vs_cpu=round(c["ms"] / (r["event_ms"]), 1))
         ops.append(entry)
-        print(f"# {w.name:22s} {entry['us_per_op']:10.2f} us  {entry['GBps']:8.1f} GB/s  "
-              f"{entry['pct_hbm_peak']:5.1f}% of 8 TB/s" + (f"  cpu {entry['cpu_ms']:.2f} ms" if 'cpu_ms' in entry else ""),
-              file=sys.stderr, flush=True)
+        rate = (f"{entry['TFLOPs']:8.1f} TFLOP/s {entry['pct_mfma_peak']:5.1f}% of 2.5 PF bf16" if flops else
+                f"{entry['GBps']:8.1f} GB/s  {entry['pct_hbm_peak']:5.1f}% of 8 TB/s")
+        print(f"# {w.name:22s} {entry['us_per_op']:10.2f} us  {rate}" +
+              (f"  cpu {entry['cpu_ms']:.2f} ms" if 'cpu_ms' in entry else ""), file=sys.stderr, flush=True)
         if w is head:
             head_res = r
 

@@ -88,6 +88,19 @@ int sdh_unregister_external(void* p);
  * handed out to live blocks). */
 int sdh_memory_stats(size_t* reserved, size_t* in_use);
 
+/* ---- GEMM (MFMA) ------------------------------------------------------- */
+/* backend_cuda.h:41-43 gemm_nt_bf16(): C[M,N] = A[M,K] * B[N,K]^T (+ C when
+ * accumulate) (+ bias[N]); row-major with leading dimensions in elements; A
+ * fp32 (rounded to bf16 on the device, as the reference's tensor-core path),
+ * B bf16, fp32 accumulation. bias may be NULL. */
+int sdh_gemm_nt_bf16(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const uint16_t* B, int64_t ldb,
+                     float* C, int64_t ldc, const float* bias, int accumulate);
+/* FUSED: y [rows, hidden] = swiglu(x w1^T, x w3^T) with x [rows, in] fp32 and
+ * w1, w3 [hidden, in] bf16 (no biases); equals swiglu(linear(x, w1),
+ * linear(x, w3)) (zimage.cpp:130) without writing the two products. */
+int sdh_linear_swiglu(const float* x, const uint16_t* w1, const uint16_t* w3, float* y, int64_t rows, int64_t in,
+                      int64_t hidden);
+
 /* ---- norms -------------------------------------------------------------- */
 /* backend_cuda.h:48 group_norm(); tensor.h:166. x, y [N, C, HW]; gamma, beta
  * [C]; C % groups == 0. y may equal x. */

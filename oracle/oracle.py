@@ -45,6 +45,21 @@ class _NullableF32:
         return obj.ctypes.data_as(C.c_void_p)
 
 
+def f32_to_bf16(a) -> np.ndarray:
+    """bf16 bit patterns of float32 values: nearest even, inf and NaN keep
+    their top 16 bits (tensor.cpp:114-121, and the device pack kernel
+    backend_cuda.cu:183-188)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32)
+    r = ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+    special = (u & np.uint32(0x7F800000)) == np.uint32(0x7F800000)
+    r[special] = (u[special] >> np.uint32(16)).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    return (np.asarray(h, np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
 class Oracle:
     """numpy-level wrapper of liboracle.so (the C restatement)."""
 
@@ -104,6 +119,7 @@ class Oracle:
 
     def plant(self, which: int):
         self.lib.orc_plant_mistake(which)
+        self._plant_py = which  # plants of the numpy-level functions
 
     # -- generator --
     def randn(self, shape, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
@@ -264,6 +280,38 @@ class Oracle:
                                  eps, _f32(cos_t), _f32(sin_t), 1 if interleaved else 0)
         return q2, k2
 
+    # -- linear with bf16 weights (the reference's device path) --
+    # backend_cuda.cu:466-479: A is rounded to bf16, products of bf16 pairs are
+    # exact, the device sums them in fp32. Here they are summed exactly
+    # (float64 products of bf16 values are exact, and the sums of K <= 2^20
+    # terms are far inside float64), so a GPU result differs from this only
+    # by its fp32 accumulation. Returns (C, S) with S = sum_k |a_k b_k| per
+    # element, the scale of that accumulation error.
+    def gemm_nt_bf16(self, A, B16, bias=None, C=None, accumulate=False):
+        a = bf16_to_f32(f32_to_bf16(A)).astype(np.float64)
+        if getattr(self, "_plant_py", 0) == 8:  # planted: A not rounded to bf16
+            a = np.asarray(A, np.float64)
+        b = bf16_to_f32(B16).astype(np.float64)
+        acc = a @ b.T
+        if accumulate:
+            acc = np.asarray(C, np.float64) + acc
+        if bias is not None:
+            bb = np.asarray(bias, np.float64)
+            if getattr(self, "_plant_py", 0) == 9:  # planted: bias indexed by row
+                acc = acc + bb[: acc.shape[0], None]
+            else:
+                acc = acc + bb[None, :]
+        return acc.astype(np.float32), np.abs(a) @ np.abs(b).T
+
+    def linear_swiglu(self, x, w1_16, w3_16):
+        """y = swiglu(x w1^T, x w3^T) with exact products, plus the exact g,
+        u and their accumulation scales (for the test's error bound)."""
+        g, sg = self.gemm_nt_bf16(x, w1_16)
+        u, su = self.gemm_nt_bf16(x, w3_16)
+        g64, u64 = g.astype(np.float64), u.astype(np.float64)
+        y = (g64 / (1.0 + np.exp(-g64)) * u64).astype(np.float32)
+        return y, g, u, sg, su
+
     # -- layout (tensor.cpp:931-1099) --
     def upsample_nearest2x(self, x):
         x = _f32(x)
@@ -344,6 +392,9 @@ class Reference:
             "ref_mul_rows_": (C.c_int, [_vp, _vp]),
             "ref_add_rows_scaled_": (C.c_int, [_vp, _vp, _vp]),
             "ref_add_channel_bias_": (C.c_int, [_vp, _vp]),
+            "ref_tensor_to_bf16": (C.c_int, [_vp]),
+            "ref_tensor_data16": (C.POINTER(C.c_uint16), [_vp]),
+            "ref_linear": (_vp, [_vp, _vp, _vp]),
             "ref_patchify2d": (_vp, [_vp, C.c_int]),
             "ref_unpatchify2d": (_vp, [_vp, _i64, _i64, _i64, C.c_int]),
             "ref_slice_rows": (_vp, [_vp, _i64, _i64]),
@@ -513,6 +564,30 @@ class Reference:
         self._chk(self.lib.ref_add_channel_bias_(hx, hb))
         self.free(hb)
         return self.take(hx, x.shape)
+
+    # -- bf16 / linear --
+    def to_bf16(self, a):
+        """The reference's own Tensor::to_bf16 rounding of a float32 array."""
+        a = _f32(a)
+        h = self.new(a.shape, a)
+        try:
+            self._chk(self.lib.ref_tensor_to_bf16(h))
+            return np.ctypeslib.as_array(self.lib.ref_tensor_data16(h), shape=(a.size,)).copy().reshape(a.shape)
+        finally:
+            self.free(h)
+
+    def linear(self, x, W, b=None):
+        """The reference's CPU linear with W converted to BF16 (tensor.cpp:496-497):
+        x stays fp32 there, W is rounded to bf16, products summed in fp32."""
+        x, W = _f32(x), _f32(W)
+        hx, hw = self.new(x.shape, x), self.new(W.shape, W)
+        hb = self.new(b.shape, b) if b is not None else None
+        try:
+            self._chk(self.lib.ref_tensor_to_bf16(hw))
+            h = self._ptr(self.lib.ref_linear(hx, hw, hb))
+        finally:
+            self.free(hx, hw, hb)
+        return self.take(h, x.shape[:-1] + (W.shape[0],))
 
     # -- layout --
     def _new_op(self, fn, inputs, out_shape, *args):

@@ -97,6 +97,11 @@ int ref_mul_rows_(void* x, void* v) { return guard([&] { sd::mul_rows_(*T(x), *T
 int ref_add_rows_scaled_(void* x, void* y, void* g) { return guard([&] { sd::add_rows_scaled_(*T(x), *T(y), *T(g)); }); }
 int ref_add_channel_bias_(void* x, void* b) { return guard([&] { sd::add_channel_bias_(*T(x), *T(b)); }); }
 
+// ---- bf16 weights and linear ----
+int ref_tensor_to_bf16(void* h) { return guard([&] { T(h)->to_bf16(); }); }
+const uint16_t* ref_tensor_data16(void* h) { return T(h)->ptr16(); }
+void* ref_linear(void* x, void* W, void* b) { return guard_ptr([&] { return wrap(sd::linear(*T(x), *T(W), opt(b))); }); }
+
 // ---- layout ops (new tensors) ----
 void* ref_patchify2d(void* x, int p) { return guard_ptr([&] { return wrap(sd::patchify2d(*T(x), p)); }); }
 void* ref_unpatchify2d(void* t, int64_t C, int64_t H, int64_t W, int p) {

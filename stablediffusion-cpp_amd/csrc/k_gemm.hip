@@ -1,0 +1,267 @@
+// k_gemm.hip - the linear layer's GEMM on the MFMA units, with fused
+// epilogues: C[M,N] = A[M,K] * B[N,K]^T (+ C) (+ bias[N]) with fp32 A and bf16
+// weights B (backend_cuda.h:38-43, gemm_nt_bf16), and the Z-Image FFN front
+// half y = swiglu(A W1^T, A W3^T) (zimage.cpp:130) in one GEMM.
+//
+// Numerics are the reference GPU path's (backend_cuda.cu:236-238, :466-479):
+// A is rounded to bf16 (nearest even; inf/NaN truncated) once per call into
+// library scratch, products of bf16 pairs are exact in fp32, and they are
+// accumulated in fp32 by the MFMA units. Only the accumulation order differs
+// from cuBLAS.
+//
+// Kernel: 128 x 128 output tile per 256-thread workgroup, K in steps of 64.
+// Each wave owns a 64 x 64 sub-tile as 2 x 2 tiles of
+// v_mfma_f32_32x32x16_bf16 (lane l: A row l%32, B row l%32, k (l/32)*8..+7;
+// result column l%32, rows (i/4)*8 + (l/32)*4 + i%4). The A and B tiles are
+// staged in LDS, double-buffered, with 72-element (144 B) rows so that the
+// 128-bit fragment reads of eight consecutive rows fall in distinct banks; the
+// next K step's global loads are in registers while the current step
+// multiplies, and one barrier per step separates the two buffers.
+// For the SwiGLU epilogue the B tile holds 64 rows of W1 and the same 64 rows
+// of W3, and each wave's two column sub-tiles are a W1 and a W3 sub-tile of
+// the same output columns, so g and u of an output element sit in one lane.
+#include <algorithm>
+
+#include "sdh_internal.hpp"
+
+namespace sdh {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));  // 8 bf16
+typedef unsigned short u16;
+using dev::f4;
+
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kRow = kBK + 8;  // LDS row length in bf16 (144 B)
+constexpr int kGT = 256;
+
+enum Epi { E_LINEAR = 0, E_SWIGLU = 1 };
+
+// Nearest-even float -> bf16 bits; inf and NaN keep their top 16 bits.
+__device__ __forceinline__ unsigned bf16_bits(float f) {
+    const unsigned b = __float_as_uint(f);
+    if ((b & 0x7F800000u) == 0x7F800000u) return b >> 16;
+    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+
+// A fp32 [M, lda] -> P bf16 [M, K] (dense rows). One thread per 8 elements;
+// grid.y walks rows (K % 8 == 0, lda % 4 == 0, A 16-byte aligned).
+__global__ __launch_bounds__(kGT) void k_pack_bf16(const float* __restrict__ A, int64_t lda, u32x4* __restrict__ P,
+                                                  int64_t M, int K) {
+    const int kg = K >> 3;
+    const int g = blockIdx.x * kGT + threadIdx.x;
+    if (g >= kg) return;
+    for (int64_t m = blockIdx.y; m < M; m += gridDim.y) {
+        const f4* p = (const f4*)(A + m * lda) + 2 * g;
+        const f4 a = dev::ld_stream(p), b = dev::ld_stream(p + 1);
+        u32x4 o;
+        o.x = bf16_bits(a.x) | (bf16_bits(a.y) << 16);
+        o.y = bf16_bits(a.z) | (bf16_bits(a.w) << 16);
+        o.z = bf16_bits(b.x) | (bf16_bits(b.y) << 16);
+        o.w = bf16_bits(b.z) | (bf16_bits(b.w) << 16);
+        P[m * kg + g] = o;  // re-read by the GEMM right after: ordinary store
+    }
+}
+
+// P bf16 [M, K] dense; B0 (and B1 for SwiGLU) bf16 [N, ldb]. EPI E_LINEAR:
+// the block covers output columns n0 .. n0+127 of B0. E_SWIGLU: n0 .. n0+63,
+// B tile rows 0..63 from B0 (W1), 64..127 from B1 (W3).
+template <int EPI>
+__global__ __launch_bounds__(kGT, 2) void k_gemm_bf16(const u16* __restrict__ P, const u16* __restrict__ B0,
+                                                     const u16* __restrict__ B1, int64_t ldb, float* __restrict__ C,
+                                                     int64_t ldc, const float* __restrict__ bias, int M, int N, int K,
+                                                     int accumulate) {
+    __shared__ __attribute__((aligned(16))) u16 sA[2][kBM * kRow];
+    __shared__ __attribute__((aligned(16))) u16 sB[2][kBN * kRow];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int wm = w >> 1, wn = w & 1;
+    const int m0 = blockIdx.y * kBM;
+    const int n0 = blockIdx.x * (EPI == E_SWIGLU ? kBN / 2 : kBN);
+    const int c8 = (t & 7) * 8, r0 = t >> 3;  // global/LDS staging: 16 B chunk c8 of rows r0 + 32 j
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    u32x4 ra[4], rb[4];
+
+    auto gload = [&](int k0) {
+        const int kk = k0 + c8;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = r0 + 32 * j;
+            const int am = m0 + r;
+            ra[j] = (am < M && kk < K) ? *(const u32x4*)(P + (int64_t)am * K + kk) : zero;
+            const u16* bp = B0;
+            int bn = n0 + r;
+            if constexpr (EPI == E_SWIGLU) {
+                bp = r < 64 ? B0 : B1;
+                bn = n0 + (r & 63);
+            }
+            rb[j] = (bn < N && kk < K) ? *(const u32x4*)(bp + (int64_t)bn * ldb + kk) : zero;
+        }
+    };
+    auto swrite = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            *(u32x4*)(&sA[buf][(r0 + 32 * j) * kRow + c8]) = ra[j];
+            *(u32x4*)(&sB[buf][(r0 + 32 * j) * kRow + c8]) = rb[j];
+        }
+    };
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.f;
+
+    // B rows of this wave's two column sub-tiles
+    const int nb0 = EPI == E_SWIGLU ? wn * 32 : wn * 64;
+    const int nb1 = EPI == E_SWIGLU ? 64 + wn * 32 : wn * 64 + 32;
+    const int fr = lane & 31, fk = (lane >> 5) * 8;
+
+    const int nk = (K + kBK - 1) / kBK;
+    gload(0);
+    swrite(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload((kt + 1) * kBK);
+#pragma unroll
+        for (int ks = 0; ks < kBK / 16; ++ks) {
+            const int col = ks * 16 + fk;
+            bf16x8 af[2], bfr[2];
+#pragma unroll
+            for (int ms = 0; ms < 2; ++ms) af[ms] = *(const bf16x8*)(&sA[buf][(wm * 64 + ms * 32 + fr) * kRow + col]);
+            bfr[0] = *(const bf16x8*)(&sB[buf][(nb0 + fr) * kRow + col]);
+            bfr[1] = *(const bf16x8*)(&sB[buf][(nb1 + fr) * kRow + col]);
+#pragma unroll
+            for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+                for (int ns = 0; ns < 2; ++ns)
+                    acc[ms][ns] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ms], bfr[ns], acc[ms][ns], 0, 0, 0);
+        }
+        if (kt + 1 < nk) swrite(buf ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue
+#pragma unroll
+    for (int ms = 0; ms < 2; ++ms) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int m = m0 + wm * 64 + ms * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+            if (m >= M) continue;
+            if constexpr (EPI == E_SWIGLU) {
+                const int n = n0 + wn * 32 + fr;
+                if (n < N) {
+                    const float g = acc[ms][0][i], u = acc[ms][1][i];
+                    C[(int64_t)m * ldc + n] = g / (1.0f + expf(-g)) * u;  // tensor.cpp:745 order
+                }
+            } else {
+#pragma unroll
+                for (int ns = 0; ns < 2; ++ns) {
+                    const int n = n0 + wn * 64 + ns * 32 + fr;
+                    if (n < N) {
+                        float v = acc[ms][ns][i];
+                        float* cp = C + (int64_t)m * ldc + n;
+                        if (accumulate) v = *cp + v;
+                        if (bias) v += bias[n];
+                        *cp = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Any alignment and K: one thread per output element, bf16-rounded A times
+// bf16 B accumulated in fp32 in k order.
+template <int EPI>
+__global__ __launch_bounds__(kGT) void k_gemm_scalar(const float* __restrict__ A, int64_t lda,
+                                                    const u16* __restrict__ B0, const u16* __restrict__ B1,
+                                                    int64_t ldb, float* __restrict__ C, int64_t ldc,
+                                                    const float* __restrict__ bias, int64_t M, int64_t N, int64_t K,
+                                                    int accumulate) {
+    for (int64_t idx = (int64_t)blockIdx.x * kGT + threadIdx.x; idx < M * N; idx += (int64_t)gridDim.x * kGT) {
+        const int64_t m = idx / N, n = idx - m * N;
+        const float* a = A + m * lda;
+        const u16* b0 = B0 + n * ldb;
+        float s0 = 0.f, s1 = 0.f;
+        for (int64_t k = 0; k < K; ++k) {
+            const float av = __uint_as_float(bf16_bits(a[k]) << 16);
+            s0 += av * __uint_as_float((unsigned)b0[k] << 16);
+            if constexpr (EPI == E_SWIGLU) s1 += av * __uint_as_float((unsigned)B1[n * ldb + k] << 16);
+        }
+        float* cp = C + m * ldc + n;
+        if constexpr (EPI == E_SWIGLU) {
+            *cp = s0 / (1.0f + expf(-s0)) * s1;
+        } else {
+            float v = s0;
+            if (accumulate) v = *cp + v;
+            if (bias) v += bias[n];
+            *cp = v;
+        }
+    }
+}
+
+bool aligned(const void* p, unsigned a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+template <int EPI>
+void run_gemm(const char* op, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const u16* B0,
+              const u16* B1, int64_t ldb, float* C, int64_t ldc, const float* bias, bool accumulate) {
+    need(M >= 0 && N >= 0 && K >= 0, op, "negative size");
+    need(lda >= K && ldb >= K && ldc >= N, op, "leading dimension smaller than the row");
+    if (M == 0 || N == 0) return;
+    ensure_init();
+    if (K > 0) {
+        check_range(A, (size_t)((M - 1) * lda + K) * 4, op, "A");
+        check_range(B0, (size_t)((N - 1) * ldb + K) * 2, op, EPI == E_SWIGLU ? "w1" : "B");
+        if (EPI == E_SWIGLU) check_range(B1, (size_t)((N - 1) * ldb + K) * 2, op, "w3");
+    }
+    check_range(C, (size_t)((M - 1) * ldc + N) * 4, op, EPI == E_SWIGLU ? "y" : "C");
+    if (bias) check_range(bias, (size_t)N * 4, op, "bias");
+    const bool fast = K > 0 && K % 8 == 0 && lda % 4 == 0 && ldb % 8 == 0 && aligned(A, 16) && aligned(B0, 16) &&
+                      (EPI != E_SWIGLU || aligned(B1, 16)) && M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31);
+    if (fast) {
+        u16* P = (u16*)scratch((size_t)(M * K) * 2);
+        const int kg = (int)(K / 8);
+        const unsigned gy = (unsigned)std::min<int64_t>(M, 65535);
+        k_pack_bf16<<<dim3(blocks_for(kg, kGT), gy), kGT, 0, stream()>>>(A, lda, (u32x4*)P, M, (int)K);
+        launched(op);
+        const int bn = EPI == E_SWIGLU ? kBN / 2 : kBN;
+        const int64_t gx = (N + bn - 1) / bn, gym = (M + kBM - 1) / kBM;
+        need(gym <= 65535, op, "too many rows for one launch");
+        k_gemm_bf16<EPI><<<dim3((unsigned)gx, (unsigned)gym), kGT, 0, stream()>>>(
+            P, B0, B1, ldb, C, ldc, bias, (int)M, (int)N, (int)K, accumulate ? 1 : 0);
+    } else {
+        const int64_t want = (M * N + kGT - 1) / kGT;
+        const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(want, (int64_t)num_cus() * 16));
+        k_gemm_scalar<EPI><<<grid, kGT, 0, stream()>>>(A, lda, B0, B1, ldb, C, ldc, bias, M, N, K, accumulate ? 1 : 0);
+    }
+    launched(op);
+}
+
+}  // namespace
+}  // namespace sdh
+
+using namespace sdh;
+
+extern "C" {
+
+int sdh_gemm_nt_bf16(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const uint16_t* B, int64_t ldb,
+                     float* C, int64_t ldc, const float* bias, int accumulate) {
+    return guarded([&] {
+        run_gemm<E_LINEAR>("sdh_gemm_nt_bf16", M, N, K, A, lda, B, nullptr, ldb, C, ldc, bias, accumulate != 0);
+    });
+}
+
+int sdh_linear_swiglu(const float* x, const uint16_t* w1, const uint16_t* w3, float* y, int64_t rows, int64_t in,
+                      int64_t hidden) {
+    return guarded([&] {
+        need(w1 != nullptr && w3 != nullptr, "sdh_linear_swiglu", "w1 and w3 are required");
+        run_gemm<E_SWIGLU>("sdh_linear_swiglu", rows, hidden, in, x, in, w1, w3, in, y, hidden, nullptr, false);
+    });
+}
+
+}  // extern "C"

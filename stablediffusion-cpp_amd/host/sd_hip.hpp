@@ -10,8 +10,8 @@
 // backend reports failures (check()/launched(), backend_cuda.cu:41-48, and the
 // stub's throw, backend_cuda_stub.cpp:14).
 //
-// GEMM, conv2d and attention stay with their existing implementations; they
-// are not part of this backend.
+// conv2d and attention stay with their existing implementations; they are
+// not part of this backend (GEMM is, for BF16 weights: gemm_nt_bf16).
 #pragma once
 
 #include <cstddef>
@@ -49,6 +49,12 @@ inline void download(void* dst, const void* src, size_t bytes) {
 inline void copy(void* dst, const void* src, size_t bytes) { detail::check(sdh_copy(dst, src, bytes), "hip::copy"); }
 inline void zero(void* dst, size_t bytes) { detail::check(sdh_zero(dst, bytes), "hip::zero"); }
 inline void synchronize() { detail::check(sdh_synchronize(), "hip::synchronize"); }
+
+// backend_cuda.h:41-43
+inline void gemm_nt_bf16(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const uint16_t* B, int64_t ldb,
+                         float* C, int64_t ldc, const float* bias, bool accumulate) {
+    detail::check(sdh_gemm_nt_bf16(M, N, K, A, lda, B, ldb, C, ldc, bias, accumulate ? 1 : 0), "hip::gemm_nt_bf16");
+}
 
 // backend_cuda.h:48-52
 inline void group_norm(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups, const float* gamma,
@@ -133,6 +139,10 @@ inline void qknorm_rope(float* q, int64_t inner_q, float* k, int64_t inner_k, in
                         bool interleaved) {
     detail::check(sdh_qknorm_rope(q, inner_q, k, inner_k, N, S, dim, gamma_q, gamma_k, eps, cos, sin, interleaved ? 1 : 0),
                   "hip::qknorm_rope");
+}
+inline void linear_swiglu(const float* x, const uint16_t* w1, const uint16_t* w3, float* y, int64_t rows, int64_t in,
+                          int64_t hidden) {
+    detail::check(sdh_linear_swiglu(x, w1, w3, y, rows, in, hidden), "hip::linear_swiglu");
 }
 inline void add_rms_norm(float* x, const float* r, float* y, int64_t rows, int64_t C, const float* gamma, float eps) {
     detail::check(sdh_add_rms_norm(x, r, y, rows, C, gamma, eps), "hip::add_rms_norm");

@@ -4,6 +4,7 @@
 #include "tensor_hip.h"
 
 #include <algorithm>
+#include <cstring>
 #include <sstream>
 #include <stdexcept>
 
@@ -79,15 +80,36 @@ Tensor Tensor::to(Device d) const {
     Tensor t;
     t.shape = shape;
     t.device = d;
-    const size_t bytes = (size_t)numel() * sizeof(float);
+    t.dtype = dtype;
+    const size_t bytes = (size_t)numel() * (is_bf16() ? sizeof(uint16_t) : sizeof(float));
     if (d == Device::HIP) {
         t.dev = std::make_shared<DeviceBuffer>(bytes);
-        if (bytes) sd::hip::upload(t.dev->p, data.data(), bytes);
+        if (bytes) sd::hip::upload(t.dev->p, is_bf16() ? (const void*)data16.data() : (const void*)data.data(), bytes);
+    } else if (is_bf16()) {
+        t.data16.resize((size_t)numel());
+        if (bytes) sd::hip::download(t.data16.data(), dev->p, bytes);
     } else {
         t.data.resize((size_t)numel());
         if (bytes) sd::hip::download(t.data.data(), dev->p, bytes);
     }
     return t;
+}
+
+const uint16_t* Tensor::dptr16() const { return is_hip() && dev ? (const uint16_t*)dev->p : nullptr; }
+
+// tensor.cpp:114-121 rounding (nearest even; inf and NaN keep their top bits)
+void Tensor::to_bf16() {
+    if (is_bf16()) return;
+    if (is_hip()) throw std::runtime_error("to_bf16: device tensor " + shape_str());
+    data16.resize(data.size());
+    for (size_t i = 0; i < data.size(); ++i) {
+        uint32_t b;
+        std::memcpy(&b, &data[i], 4);
+        data16[i] = (b & 0x7F800000u) == 0x7F800000u ? (uint16_t)(b >> 16) : (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+    }
+    data.clear();
+    data.shrink_to_fit();
+    dtype = DType::BF16;
 }
 
 Tensor& Tensor::reshape(std::vector<int64_t> s) {
@@ -367,6 +389,39 @@ Tensor repeat_batch(const Tensor& x, int64_t times) {
     Tensor y = Tensor::empty(s, Device::HIP);
     for (int64_t t = 0; t < times; ++t)
         if (x.numel()) sd::hip::copy(y.dptr() + t * x.numel(), x.dptr(), x.numel() * sizeof(float));
+    return y;
+}
+
+// ---- linear ------------------------------------------------------------------
+
+// tensor.cpp:481-494, device branch with BF16 weights
+Tensor linear(const Tensor& x, const Tensor& W, const Tensor* b) {
+    const int64_t in = x.dim(-1), out = W.dim(0);
+    if (W.dim(1) != in) throw std::runtime_error("linear: input dim " + x.shape_str() + " vs weight " + W.shape_str());
+    const int64_t rows = x.numel() / in;
+    std::vector<int64_t> oshape = x.shape;
+    oshape.back() = out;
+    same_device(x, W, "linear");
+    need_hip(x, "linear");
+    if (!W.is_bf16()) throw std::runtime_error("linear: F32 weights; backend_hip takes BF16 weights (the tensor-core path)");
+    if (b) same_device(x, *b, "linear");
+    Tensor y = Tensor::empty(oshape, Device::HIP);
+    sd::hip::gemm_nt_bf16(rows, out, in, x.dptr(), in, W.dptr16(), in, y.dptr(), out, opt(b), false);
+    return y;
+}
+
+Tensor linear_swiglu(const Tensor& x, const Tensor& w1, const Tensor& w3) {
+    const int64_t in = x.dim(-1), hidden = w1.dim(0);
+    if (w1.dim(1) != in || w3.dim(0) != hidden || w3.dim(1) != in)
+        throw std::runtime_error("linear_swiglu: " + x.shape_str() + " vs " + w1.shape_str() + " / " + w3.shape_str());
+    same_device(x, w1, "linear_swiglu");
+    same_device(x, w3, "linear_swiglu");
+    need_hip(x, "linear_swiglu");
+    if (!w1.is_bf16() || !w3.is_bf16()) throw std::runtime_error("linear_swiglu: weights must be BF16");
+    std::vector<int64_t> oshape = x.shape;
+    oshape.back() = hidden;
+    Tensor y = Tensor::empty(oshape, Device::HIP);
+    sd::hip::linear_swiglu(x.dptr(), w1.dptr16(), w3.dptr16(), y.dptr(), x.numel() / in, in, hidden);
     return y;
 }
 

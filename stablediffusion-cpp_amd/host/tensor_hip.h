@@ -27,9 +27,15 @@ Device parse_device(const std::string& s);  // "cpu", "hip", or "auto" (hip if a
 
 struct DeviceBuffer;  // one backend_hip arena block
 
+// tensor.h:45. Activations are F32; weights may be BF16 (the top 16 bits of a
+// float32), accepted by linear.
+enum class DType { F32, BF16 };
+
 struct Tensor {
     std::vector<int64_t> shape;
-    std::vector<float> data;            // host storage when device == CPU
+    std::vector<float> data;            // F32 host storage when device == CPU
+    std::vector<uint16_t> data16;       // BF16 host storage when device == CPU
+    DType dtype = DType::F32;
     Device device = Device::CPU;
     std::shared_ptr<DeviceBuffer> dev;  // device storage when device == HIP
 
@@ -45,6 +51,10 @@ struct Tensor {
     static int64_t numel_of(const std::vector<int64_t>& s);
     int64_t numel() const { return numel_of(shape); }
     bool is_hip() const { return device == Device::HIP; }
+    bool is_bf16() const { return dtype == DType::BF16; }
+    const uint16_t* dptr16() const;  // BF16 device storage
+    // F32 host storage -> BF16, rounding to nearest even (tensor.h:86-87).
+    void to_bf16();
     Tensor to(Device d) const;  // tensor.cpp:72-93
     float* dptr();
     const float* dptr() const;
@@ -93,6 +103,13 @@ Tensor nchw_to_nlc(const Tensor& x);
 Tensor nlc_to_nchw(const Tensor& x, int64_t H, int64_t W);
 Tensor slice_batch(const Tensor& x, int64_t b);
 Tensor repeat_batch(const Tensor& x, int64_t times);
+
+// ---- linear (tensor.h:146): y = x W^T (+ b) with BF16 weights W [out, in] ----
+// The reference's device branch (tensor.cpp:489-494): x is rounded to bf16,
+// products accumulate in fp32. F32 weights are outside this backend.
+Tensor linear(const Tensor& x, const Tensor& W, const Tensor* b);
+// swiglu(linear(x, w1), linear(x, w3)) in one GEMM (zimage.cpp:130)
+Tensor linear_swiglu(const Tensor& x, const Tensor& w1, const Tensor& w3);
 
 // ---- softmax (tensor.h:236) ----
 // Same parameters as the reference; x is a DEVICE pointer here (rows x cols

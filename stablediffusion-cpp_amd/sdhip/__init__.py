@@ -79,6 +79,8 @@ SIGNATURES = {
     "sdh_add_rows_scaled": [_vp, _vp, _vp, _i64, _i64],
     "sdh_add_channel_bias": [_vp, _vp, _i64, _i64, _i64],
     "sdh_add_rows": [_vp, _vp, _i64, _i64],
+    "sdh_gemm_nt_bf16": [_i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, C.c_int],
+    "sdh_linear_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _i64],
     "sdh_upsample_nearest2x": [_vp, _vp, _i64, _i64, _i64],
     "sdh_concat_channels": [_vp, _vp, _vp, _i64, _i64, _i64, _i64],
     "sdh_nchw_to_nlc": [_vp, _vp, _i64, _i64, _i64],
@@ -124,27 +126,32 @@ def _p(x) -> Optional[int]:
 
 
 class DArray:
-    """A float32 array in the backend's device arena."""
+    """An array in the backend's device arena: float32 (activations) or
+    uint16 (bf16 bit patterns, for weights)."""
 
-    def __init__(self, backend: "Backend", shape: Sequence[int], ptr: Optional[int] = None, owned: bool = True):
+    def __init__(self, backend: "Backend", shape: Sequence[int], ptr: Optional[int] = None, owned: bool = True,
+                 dtype=np.float32):
         self.be = backend
         self.shape = tuple(int(s) for s in shape)
         self.size = int(np.prod(self.shape)) if self.shape else 1
-        self.nbytes = self.size * 4
+        self.dtype = np.dtype(dtype)
+        if self.dtype not in (np.dtype(np.float32), np.dtype(np.uint16)):
+            raise TypeError("DArray holds float32 or uint16 (bf16) data")
+        self.nbytes = self.size * self.dtype.itemsize
         self.owned = owned
         if ptr is None:
             ptr = backend.malloc(self.nbytes)
         self.ptr = ptr
 
     def upload(self, a: np.ndarray) -> "DArray":
-        a = np.ascontiguousarray(a, dtype=np.float32)
+        a = np.ascontiguousarray(a, dtype=self.dtype)
         if a.size != self.size:
             raise ValueError(f"upload size {a.size} != {self.size}")
         self.be.upload(self.ptr, a)
         return self
 
     def download(self) -> np.ndarray:
-        out = np.empty(self.shape, np.float32)
+        out = np.empty(self.shape, self.dtype)
         self.be.download(out, self.ptr)
         return out
 
@@ -217,8 +224,10 @@ class Backend:
         return DArray(self, shape)
 
     def array(self, a: np.ndarray) -> DArray:
-        a = np.ascontiguousarray(a, dtype=np.float32)
-        return DArray(self, a.shape).upload(a)
+        """float32 arrays stay float32; uint16 arrays are bf16 bit patterns."""
+        dt = np.uint16 if np.asarray(a).dtype == np.uint16 else np.float32
+        a = np.ascontiguousarray(a, dtype=dt)
+        return DArray(self, a.shape, dtype=dt).upload(a)
 
     def randn(self, shape, seed: int, mean: float = 0.0, std: float = 1.0) -> DArray:
         d = DArray(self, shape)
@@ -302,6 +311,13 @@ class Backend:
 
     def add_channel_bias(self, x, b, N, Cc, HW):
         self.call("sdh_add_channel_bias", _p(x), _p(b), N, Cc, HW)
+
+    # GEMM (bf16 weights held in DArray buffers of uint16)
+    def gemm_nt_bf16(self, M, N, K, A, lda, B, ldb, Cm, ldc, bias=None, accumulate=False):
+        self.call("sdh_gemm_nt_bf16", M, N, K, _p(A), lda, _p(B), ldb, _p(Cm), ldc, _p(bias), 1 if accumulate else 0)
+
+    def linear_swiglu(self, x, w1, w3, y, rows, inn, hidden):
+        self.call("sdh_linear_swiglu", _p(x), _p(w1), _p(w3), _p(y), rows, inn, hidden)
 
     # layout (tensor.cpp:931-1099)
     def upsample_nearest2x(self, x, y, NC, H, W):

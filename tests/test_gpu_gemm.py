@@ -1,0 +1,129 @@
+"""GPU parity of the bf16-weight linear layer (sdh_gemm_nt_bf16) and the fused
+FFN front half (sdh_linear_swiglu), through the C ABI.
+
+The oracle sums the exact bf16 products in float64 (oracle/oracle.py); the GPU
+sums them in fp32 on the MFMA units, so every element must lie within the
+rigorous fp32 accumulation bound n u sum|terms| (tolerances.assert_gemm).
+Shapes: tile edges in M and N, a partial last K step, accumulate and bias, the
+scalar path (K not a multiple of 8), and the Z-Image DiT shapes (attention
+projection [4096 x 3840] x [3840 x 3840]; FFN [4096 x 3840] x [10240 x 3840]
+twice) checked on a sample of rows. Also the reference's own GPU-vs-CPU check
+of linear (test_ops.cpp:377-379: 3e-2 against the CPU path, which keeps x in
+fp32).
+"""
+import numpy as np
+import pytest
+
+from oracle import f32_to_bf16
+from tolerances import U32, assert_gemm
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(orc, M, N, K, seed):
+    a = orc.randn((M, K), seed, 0.0, 1.0)
+    w = f32_to_bf16(orc.randn((N, K), seed + 1, 0.0, 0.05))
+    return a, w
+
+
+@pytest.mark.parametrize("M,N,K,with_bias,acc", [
+    (5, 7, 16, False, False), (129, 130, 72, True, False), (256, 384, 512, True, True),
+    (300, 200, 96, False, True), (7, 9, 12, True, False), (64, 128, 8, True, False),
+])
+def test_gemm_nt_bf16(be, orc, M, N, K, with_bias, acc):
+    a, w = _inputs(orc, M, N, K, 100 + M + N + K)
+    b = orc.randn((N,), 7, 0.0, 0.5) if with_bias else None
+    c0 = orc.randn((M, N), 8, 0.0, 1.0) if acc else None
+    dC = be.array(c0) if acc else be.empty((M, N))
+    be.gemm_nt_bf16(M, N, K, be.array(a), K, be.array(w), K, dC, N, be.array(b) if with_bias else None, acc)
+    want, S = orc.gemm_nt_bf16(a, w, b, c0, acc)
+    S = S + (np.abs(b)[None, :] if with_bias else 0) + (np.abs(c0) if acc else 0)
+    assert_gemm(dC.download(), want, S, K + 2, f"gemm {M}x{N}x{K}")
+
+
+def test_gemm_strided_operands(be, orc):
+    """Leading dimensions larger than the rows (sub-matrices of wider buffers)."""
+    M, N, K, lda, ldb, ldc = 70, 100, 64, 96, 80, 130
+    A = orc.randn((M, lda), 31)
+    W = f32_to_bf16(orc.randn((N, ldb), 32, 0.0, 0.05))
+    dC = be.array(np.zeros((M, ldc), np.float32))
+    be.gemm_nt_bf16(M, N, K, be.array(A), lda, be.array(W), ldb, dC, ldc)
+    want, S = orc.gemm_nt_bf16(A[:, :K], W[:, :K])
+    got = dC.download()
+    assert_gemm(got[:, :N], want, S, K + 1, "strided gemm")
+    assert np.all(got[:, N:] == 0), "columns beyond N were written"
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 3840, 3840)])
+def test_gemm_zimage_projection(be, orc, M, N, K):
+    a, w = _inputs(orc, M, N, K, 200)
+    b = orc.randn((N,), 9, 0.0, 0.5)
+    dC = be.empty((M, N))
+    be.gemm_nt_bf16(M, N, K, be.array(a), K, be.array(w), K, dC, N, be.array(b))
+    rows = np.arange(0, M, 61)
+    got = dC.download()[rows]
+    want, S = orc.gemm_nt_bf16(a[rows], w, b)
+    assert_gemm(got, want, S + np.abs(b)[None, :], K + 2, "Z-Image projection (sampled rows)")
+
+
+def _swiglu_bound(g, u, sg, su, K):
+    """Error bound of y = silu(g) u when g, u carry fp32 accumulation errors:
+    |dy| <= |silu'(g)| eg |u| + |silu(g)| eu + 8 ulp(y), |silu'| <= 1.1."""
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    eg, eu = K * U32 * sg, K * U32 * su
+    silu = g64 / (1.0 + np.exp(-g64))
+    y = silu * u64
+    return 1.1 * eg * (np.abs(u64) + eu) + np.abs(silu) * eu + 8 * np.spacing(np.abs(y).astype(np.float32)), y
+
+
+@pytest.mark.parametrize("M,H,K", [(300, 520, 256), (64, 80, 72), (5, 3, 24), (17, 33, 12)])
+def test_linear_swiglu(be, orc, M, H, K):
+    x = orc.randn((M, K), 300 + M, 0.0, 1.0)
+    w1 = f32_to_bf16(orc.randn((H, K), 301 + H, 0.0, 0.1))
+    w3 = f32_to_bf16(orc.randn((H, K), 302 + H, 0.0, 0.1))
+    dy = be.empty((M, H))
+    be.linear_swiglu(be.array(x), be.array(w1), be.array(w3), dy, M, K, H)
+    y, g, u, sg, su = orc.linear_swiglu(x, w1, w3)
+    bound, y64 = _swiglu_bound(g, u, sg, su, K + 1)
+    err = np.abs(dy.download().astype(np.float64) - y64)
+    assert np.all(err <= bound + 1e-30), f"linear_swiglu {M}x{H}x{K}: {float(np.max(err / (bound + 1e-30))):.2f} x bound"
+
+
+def test_linear_swiglu_zimage_ffn(be, orc):
+    M, H, K = 4096, 10240, 3840
+    x = orc.randn((M, K), 400, 0.0, 1.0)
+    w1 = f32_to_bf16(orc.randn((H, K), 401, 0.0, 0.02))
+    w3 = f32_to_bf16(orc.randn((H, K), 402, 0.0, 0.02))
+    dy = be.empty((M, H))
+    be.linear_swiglu(be.array(x), be.array(w1), be.array(w3), dy, M, K, H)
+    rows = np.arange(0, M, 97)
+    y, g, u, sg, su = orc.linear_swiglu(x[rows], w1, w3)
+    bound, y64 = _swiglu_bound(g, u, sg, su, K + 1)
+    err = np.abs(dy.download()[rows].astype(np.float64) - y64)
+    assert np.all(err <= bound + 1e-30), f"Z-Image FFN: {float(np.max(err / (bound + 1e-30))):.2f} x bound"
+
+
+def test_linear_matches_reference_test_ops(be, orc, ref):
+    """test_ops.cpp:377-379: linear with bf16 weights and bias on the device vs
+    the reference's CPU path (x kept in fp32 there), max-abs 3e-2."""
+    x = orc.randn((2, 5, 24), 500)
+    W = orc.randn((16, 24), 501)
+    b = orc.randn((16,), 502)
+    cpu = ref.linear(x, W, b)
+    dC = be.empty((10, 16))
+    be.gemm_nt_bf16(10, 16, 24, be.array(x), 24, be.array(f32_to_bf16(W)), 24, dC, 16, be.array(b))
+    assert float(np.max(np.abs(dC.download().reshape(2, 5, 16) - cpu))) <= 3e-2
+
+
+def test_gemm_invalid_arguments(be):
+    import sdhip
+
+    a = be.empty((4, 8))
+    w = be.array(np.zeros((4, 8), np.uint16))
+    c = be.empty((4, 4))
+    with pytest.raises(sdhip.SdhError) as e:
+        be.gemm_nt_bf16(4, 4, 8, a, 4, w, 8, c, 4)  # lda < K
+    assert e.value.status == sdhip.SDH_ERR_INVALID
+    with pytest.raises(sdhip.SdhError) as e:
+        be.gemm_nt_bf16(5, 4, 8, a, 8, w, 8, c, 4)  # A has 4 rows, not 5
+    assert e.value.status == sdhip.SDH_ERR_INVALID

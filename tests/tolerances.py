@@ -59,3 +59,27 @@ def assert_softmax(got, want, what=""):
     e = rel_softmax(got, want)
     assert e <= SOFTMAX_REL, f"{what}: rel {e:.3e} > {SOFTMAX_REL}"
     return e
+
+
+# ---------------------------------------------------------------- GEMM
+# A bf16-weight GEMM accumulates exact bf16 products in fp32, in an order the
+# hardware (MFMA) or the reference's micro-kernel chooses. Against the exact
+# sum of the same products the classic recursive-summation bound applies
+# whatever the order: |error| <= n u sum_k |a_k b_k| (u = 2^-24, n the number
+# of terms, bias and accumulated C counted as terms). It is rigorous, yet
+# tight enough that an indexing mistake (a dropped K tile, a transposed
+# operand, a missing bf16 rounding of A) exceeds it by orders of magnitude.
+U32 = 2.0 ** -24
+
+
+def fp32_sum_bound(S, n):
+    return n * U32 * np.asarray(S, np.float64)
+
+
+def assert_gemm(got, want, S, n, what=""):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    bound = fp32_sum_bound(S, n) + 1e-30
+    ratio = float(np.max(np.abs(got - want) / bound)) if got.size else 0.0
+    assert ratio <= 1.0, f"{what}: error {ratio:.3f} x the fp32 accumulation bound"
+    return ratio
