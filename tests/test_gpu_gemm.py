@@ -5,7 +5,8 @@ The oracle sums the exact bf16 products in float64 (oracle/oracle.py); the GPU
 sums them in fp32 on the MFMA units, so every element must lie within the
 rigorous fp32 accumulation bound n u sum|terms| (tolerances.assert_gemm).
 Shapes: tile edges in M and N, a partial last K step, accumulate and bias, the
-scalar path (K not a multiple of 8), and the Z-Image DiT shapes (attention
+three kernels (K % 64 == 0: direct-to-LDS; K % 8 == 0: register staging;
+otherwise scalar), and the Z-Image DiT shapes (attention
 projection [4096 x 3840] x [3840 x 3840]; FFN [4096 x 3840] x [10240 x 3840]
 twice) checked on a sample of rows. Also the reference's own GPU-vs-CPU check
 of linear (test_ops.cpp:377-379: 3e-2 against the CPU path, which keeps x in
@@ -29,6 +30,7 @@ def _inputs(orc, M, N, K, seed):
 @pytest.mark.parametrize("M,N,K,with_bias,acc", [
     (5, 7, 16, False, False), (129, 130, 72, True, False), (256, 384, 512, True, True),
     (300, 200, 96, False, True), (7, 9, 12, True, False), (64, 128, 8, True, False),
+    (300, 200, 128, True, True), (1, 1, 64, True, False), (257, 129, 192, False, False),
 ])
 def test_gemm_nt_bf16(be, orc, M, N, K, with_bias, acc):
     a, w = _inputs(orc, M, N, K, 100 + M + N + K)
