@@ -413,6 +413,38 @@ class Linear(Workload):
         return (lambda: [R._ptr(R.lib.ref_linear(hx, hw, hb))]), [hx, hw, hb]
 
 
+class Attention(Workload):
+    """Multi-head attention fused on the MFMA units (backend_cuda.h:57-59;
+    tensor.cpp:776-810) at the Z-Image DiT layer: q, k, v [1,4096,30*128]
+    fp32, no mask (zimage.cpp:121). Rated in TFLOP/s by the reference's own
+    formula 4 S^2 d H (test_ops.cpp:352); the MFMA units execute three bf16
+    products per fp32 product (split operands), which pct_mfma_peak counts.
+    The CPU baseline times the reference's attention on one of the 30 heads
+    and scales it by 30 (heads are independent, tensor.cpp:793-808)."""
+
+    name, kernel = "attention", "k_attn_fwd"
+    S, H, d = T, 30, 128
+    flops = 4 * T * T * 128 * 30
+    mfma_mult = 3
+    algo_bytes = 4 * T * 30 * 128 * 4
+    cpu_scale = 30
+    desc = "attention, q k v [1,4096,30x128] fp32, softmax(q k^T / sqrt(128)) v per head (Z-Image DiT layer)"
+
+    def make(self, be, i):
+        shp = (1, self.S, self.H * self.d)
+        return dict(q=be.randn(shp, 19000 + i), k=be.randn(shp, 19100 + i), v=be.randn(shp, 19200 + i),
+                    o=be.empty(shp))
+
+    def step(self, be, s):
+        be.attention(s["q"], s["k"], s["v"], s["o"], 1, self.S, self.S, self.H, self.H, self.d, False)
+
+    def cpu(self, R, orc):
+        shp = (1, self.S, self.d)  # one head
+        q, k, v = orc.randn(shp, 21), orc.randn(shp, 22), orc.randn(shp, 23)
+        hq, hk, hv = R.new(shp, q), R.new(shp, k), R.new(shp, v)
+        return (lambda: [R._ptr(R.lib.ref_attention(hq, hk, hv, 1, 0, 1))]), [hq, hk, hv]
+
+
 class CopyCalibration(Workload):
     """Not a BASELINE config: an in-place x *= 1 stream over [4096,10240]
     (one read + one write of 168 MB), the plain-copy reference for what HBM
@@ -443,7 +475,8 @@ def all_workloads():
         Softmax(),
         QKNormRope(),
         QKNormRope(unfused=True),
-    ] + [Layout(n) for n in Layout.SPECS] + [Linear(k) for k in ("linear_bf16", "linear_swiglu", "linear_swiglu_unfused")]
+    ] + [Layout(n) for n in Layout.SPECS] + [Linear(k) for k in ("linear_bf16", "linear_swiglu", "linear_swiglu_unfused")] + [
+        Attention()]
 
 
 # ------------------------------------------------------------------ GPU timing
@@ -503,7 +536,9 @@ def measure_cpu(w, reps):
         if i:
             times.append(dt)
     R.free(*handles)
-    return dict(ms=statistics.median(times) * 1e3, reps=reps, threads=threads, kind="reference")
+    # a workload may time a fixed fraction of its step (independent heads) and scale it
+    return dict(ms=statistics.median(times) * 1e3 * getattr(w, "cpu_scale", 1), reps=reps, threads=threads,
+                kind="reference")
 
 
 def measure_cpu_port(w, orc, reps, threads):
@@ -540,7 +575,7 @@ KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
     "k_unary<4>": "copy_calibration", "k_add_rms": "add_rms_norm", "k_swiglu": "swiglu",
     "k_rope_il_reg": "rope_qk", "k_ln_mod_gate": "ln_modulate_gate", "k_softmax_block": "softmax_rows",
     "k_upsample2x_vec": "upsample_nearest2x", "k_concat_vec": "concat_channels", "k_patchify": "patchify2d",
-    "k_qknorm_rope_il": "qknorm_rope",
+    "k_qknorm_rope_il": "qknorm_rope", "k_attn_fwd": "attention",
 }
 
 
@@ -688,7 +723,9 @@ def main():
         flops = getattr(w, "flops", None)
         if flops:
             tfs = flops / (r["event_ms"] * 1e-3) / 1e12
-            entry.update(flops=flops, TFLOPs=round(tfs, 1), pct_mfma_peak=round(100 * tfs / MFMA_BF16_PEAK_TFS, 1))
+            mult = getattr(w, "mfma_mult", 1)  # bf16 MFMA products per counted product
+            entry.update(flops=flops, TFLOPs=round(tfs, 1),
+                         pct_mfma_peak=round(100 * tfs * mult / MFMA_BF16_PEAK_TFS, 1))
         if args.cpu_all and not args.no_cpu:
             heavy = w.algo_bytes > (1 << 30) or (flops or 0) > 1e10
             c = measure_cpu(w, 1 if (flops or 0) > 1e10 else 3 if heavy else args.cpu_reps)

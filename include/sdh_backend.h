@@ -147,6 +147,16 @@ int sdh_softmax_rows(float* x, int64_t rows, int64_t cols, float scale, int caus
  * at backend_cuda.cu:578). */
 int sdh_softmax_rows_batched(float* x, int64_t rows, int64_t cols, float scale, int causal, int64_t period);
 
+/* ---- attention ------------------------------------------------------------ */
+/* backend_cuda.h:57-59 attention(); tensor.h:205-212 (tensor.cpp:776-810).
+ * q [N, Sq, heads*d], k and v [N, Skv, kv_heads*d], out [N, Sq, heads*d]:
+ * out = softmax(q k^T / sqrt(d)) v per head, query head h reading key/value
+ * head h / (heads / kv_heads); causal keeps keys 0..i for query i.
+ * kv_heads <= 0 means kv_heads = heads. out must not overlap the inputs.
+ * Fused on the MFMA units (no score matrix in memory) for d <= 128. */
+int sdh_attention(const float* q, const float* k, const float* v, float* out, int64_t N, int64_t Sq, int64_t Skv,
+                  int heads, int kv_heads, int64_t d, int causal);
+
 /* ---- activations ----------------------------------------------------------- */
 /* backend_cuda.h:61 swiglu(); tensor.h:191. y = gate / (1 + exp(-gate)) * up. */
 int sdh_swiglu(const float* gate, const float* up, float* y, int64_t n);

@@ -312,6 +312,42 @@ class Oracle:
         y = (g64 / (1.0 + np.exp(-g64)) * u64).astype(np.float32)
         return y, g, u, sg, su
 
+    # -- attention (tensor.cpp:776-810) --
+    def attention(self, q, k, v, heads, causal=False, kv_heads=0, rows=None):
+        """float64 restatement of the reference's attention, as its own test
+        restates it in double (test_ops.cpp:84-114): per head h, key/value
+        head g = h / (heads / kv_heads) (tensor.cpp:795-797), scores
+        q_h k_g^T scaled by the fp32 1/sqrt(d) (tensor.cpp:784), causal rows
+        keep keys j <= i (softmax_rows_, tensor.cpp:756), softmax, then P v_g.
+        q [N, Sq, heads*d], k and v [N, Skv, kv_heads*d]. `rows` restricts
+        the result to those query rows (returned [N, len(rows), heads*d])."""
+        plant = getattr(self, "_plant_py", 0)
+        if kv_heads <= 0:
+            kv_heads = heads
+        q, k, v = (np.asarray(a, np.float32) for a in (q, k, v))
+        N, Sq, inner = q.shape
+        Skv = k.shape[1]
+        d = inner // heads
+        group = heads // kv_heads
+        rows = np.arange(Sq) if rows is None else np.asarray(rows)
+        scale = np.float64(np.float32(1.0) / np.sqrt(np.float32(d)))
+        if plant == 10:  # planted: no 1/sqrt(d)
+            scale = np.float64(1.0)
+        qh = q[:, rows].reshape(N, len(rows), heads, d).transpose(0, 2, 1, 3).astype(np.float64)
+        kh = k.reshape(N, Skv, kv_heads, d).transpose(0, 2, 1, 3).astype(np.float64)
+        vh = v.reshape(N, Skv, kv_heads, d).transpose(0, 2, 1, 3).astype(np.float64)
+        g = np.arange(heads) % kv_heads if plant == 12 else np.arange(heads) // group  # planted 12: heads interleaved
+        kh, vh = kh[:, g], vh[:, g]
+        s = np.matmul(qh, kh.transpose(0, 1, 3, 2)) * scale
+        if causal:
+            lim = rows[:, None] + (1 if plant == 11 else 0)  # planted 11: one key past the diagonal
+            s = np.where(np.arange(Skv)[None, :] > lim, -np.inf, s)
+        s = s - s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(axis=-1, keepdims=True)
+        o = np.matmul(p, vh)
+        return o.transpose(0, 2, 1, 3).reshape(N, len(rows), inner).astype(np.float32)
+
     # -- layout (tensor.cpp:931-1099) --
     def upsample_nearest2x(self, x):
         x = _f32(x)
@@ -395,6 +431,7 @@ class Reference:
             "ref_tensor_to_bf16": (C.c_int, [_vp]),
             "ref_tensor_data16": (C.POINTER(C.c_uint16), [_vp]),
             "ref_linear": (_vp, [_vp, _vp, _vp]),
+            "ref_attention": (_vp, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
             "ref_patchify2d": (_vp, [_vp, C.c_int]),
             "ref_unpatchify2d": (_vp, [_vp, _i64, _i64, _i64, C.c_int]),
             "ref_slice_rows": (_vp, [_vp, _i64, _i64]),
@@ -588,6 +625,17 @@ class Reference:
         finally:
             self.free(hx, hw, hb)
         return self.take(h, x.shape[:-1] + (W.shape[0],))
+
+    def attention(self, q, k, v, heads, causal=False, kv_heads=0):
+        """The reference's CPU attention (tensor.cpp:776-810): fp32 gemm_nt
+        scores, softmax_rows_ with scale 1/sqrt(d), fp32 gemm_nt with v^T."""
+        q, k, v = _f32(q), _f32(k), _f32(v)
+        hq, hk, hv = self.new(q.shape, q), self.new(k.shape, k), self.new(v.shape, v)
+        try:
+            h = self._ptr(self.lib.ref_attention(hq, hk, hv, heads, int(bool(causal)), kv_heads))
+        finally:
+            self.free(hq, hk, hv)
+        return self.take(h, q.shape)
 
     # -- layout --
     def _new_op(self, fn, inputs, out_shape, *args):

@@ -102,6 +102,11 @@ int ref_tensor_to_bf16(void* h) { return guard([&] { T(h)->to_bf16(); }); }
 const uint16_t* ref_tensor_data16(void* h) { return T(h)->ptr16(); }
 void* ref_linear(void* x, void* W, void* b) { return guard_ptr([&] { return wrap(sd::linear(*T(x), *T(W), opt(b))); }); }
 
+// ---- attention (new tensor) ----
+void* ref_attention(void* q, void* k, void* v, int heads, int causal, int kv_heads) {
+    return guard_ptr([&] { return wrap(sd::attention(*T(q), *T(k), *T(v), heads, causal != 0, kv_heads)); });
+}
+
 // ---- layout ops (new tensors) ----
 void* ref_patchify2d(void* x, int p) { return guard_ptr([&] { return wrap(sd::patchify2d(*T(x), p)); }); }
 void* ref_unpatchify2d(void* t, int64_t C, int64_t H, int64_t W, int p) {

@@ -1,0 +1,530 @@
+// k_attention.hip - multi-head scaled dot-product attention, fused (flash
+// style) on the MFMA units: out = softmax(q k^T / sqrt(d)) v per head, with
+// grouped-query heads and the causal mask (backend_cuda.h:57-59; tensor.cpp:
+// 776-810; the reference's GPU path backend_cuda.cu:550-586 materialises the
+// [Sq, Skv] scores and runs them through softmax_rows, tensor.cpp:752-769).
+//
+// Numerics: the reference computes scores, softmax and the weighted sum in
+// fp32. Here the operands are put in block floating point and split into two
+// fp16 halves: a block (one query row of q; one 64-key tile of k, of v) is
+// scaled by a power of two 2^-e that brings its largest magnitude into
+// [2^13, 2^14), and each scaled value x becomes hi = rne16(x), lo =
+// rne16(x - hi) (|x - hi - lo| <= 2^-22 |x| for normal lo). A product is
+// formed as hi_a hi_b + hi_a lo_b + lo_a hi_b on the fp16 MFMA units with
+// fp32 accumulation: about 2^-21 relative per product, three dense-fp16
+// MFMAs per product (fp32 MFMA has 1/16 of the fp16 rate). The exponents
+// are exact and fold into per-lane constants: the score scale becomes
+// c = log2(e) / sqrt(d) * 2^(e_q + e_k) per query and tile; softmax weights
+// are formed as 2^(s c - m + 14 + e_v - E) (E = the largest e_v of the head,
+// so they stay below 2^14) against values scaled by 2^-e_v, which keeps every
+// tile's P V on the common scale 2^(14 - E); the sum of the weights is
+// carried as 2^14 sum(p), and the output is divided by it (and scaled by 2^E)
+// once at the end. The softmax is the online form (running row max m and
+// sum); masked scores (kv > q when causal, kv past the keys) contribute
+// exactly zero.
+//
+// Layout. A pack kernel splits k and v of each key/value head into 64-key
+// tiles of library scratch, each one contiguous block:
+//   [K hi: 64 keys x DP][K lo][V^T hi: DP x 64 keys][V^T lo]   (fp16)
+// plus the tile's two exponents (e_k, e_v) in a side array,
+// with the head dimension zero-padded to DP (64 or 128) and keys past Skv
+// zero. Rows sit in the order the MFMA fragment reads want them in LDS (16-B
+// chunk c of row r at c ^ swz(r)), so the attention kernel copies a tile from
+// global memory to LDS as one contiguous block (global_load_lds_dwordx4).
+// The kernel computes S^T = K Q^T (v_mfma_f32_32x32x16_f16: K tile as the A
+// operand, rows = keys; Q in registers as the B operand, columns = queries),
+// so lane l holds scores of query l%32 only: the softmax statistics are
+// per-lane values (one cross-lane max per tile, lanes l and l^32), and
+// O^T = V^T P^T takes P straight from the score registers as its B operand.
+// The accumulator gives lane l the keys 8(i/4) + 4(l/32) + i%4 of a 32-key
+// block (i = 0..15); the pack kernel stores V^T with the keys of every
+// 16-key group in the matching order (positions 8h + 4a + b hold key
+// 8a + 4h + b), so the A operand of O^T is again one 16-B LDS read per lane.
+// Workgroup: 8 waves x 32 queries of one head; K/V tiles double-buffered in
+// LDS (one barrier per tile); the softmax rescale of O is skipped when no
+// row max of the wave changed (exactly alpha = 1).
+// Head dimensions above 128 take a plain fp32 kernel (one wave per query).
+#include <algorithm>
+#include <cmath>
+
+#include "sdh_internal.hpp"
+
+namespace sdh {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned short u16;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+using dev::f4;
+
+constexpr int kKT = 64;                     // keys per tile
+constexpr int kWaves = 8, kThreads = 64 * kWaves;
+constexpr int kBM = 32 * kWaves;            // queries per workgroup
+constexpr float kLog2e = 1.44269504088896341f;
+constexpr float kNoMax = -1e30f;            // running max before any key: finite, so 2^(m - m') never sees inf - inf
+
+// 16-B chunk c of row r of a K tile (rows of DP fp16) sits at c ^ swz_k(r):
+// for 256-B rows (DP = 128) 16 consecutive rows map one logical chunk to 16
+// distinct chunks of LDS; for 128-B rows (DP = 64, and the 64-key rows of the
+// V^T tile) the same holds per pair of rows.
+template <int DP>
+__device__ __host__ __forceinline__ int swz_k(int r) {
+    return DP == 128 ? (r & 15) : ((r >> 1) & 7);
+}
+__device__ __host__ __forceinline__ int swz_v(int r) { return (r >> 1) & 7; }
+// Key stored at position p of a V^T row (an involution on 0..63: bits 2 and 3 swap).
+__device__ __host__ __forceinline__ int key_at(int p) { return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1); }
+
+__device__ __forceinline__ void split(float x, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+// Exponent e of a block whose largest magnitude is amax: amax 2^-e lies in
+// [2^13, 2^14). Zero, subnormal, inf and NaN maxima give 0 (no scaling).
+__device__ __forceinline__ int block_exp(float amax) {
+    const int f = (int)((__float_as_uint(amax) >> 23) & 0xFFu);
+    if (f == 0 || f == 255) return 0;
+    return min(max(f - 140, -126), 126);
+}
+// 2^e for e in [-126, 127]
+__device__ __forceinline__ float pow2(int e) { return __uint_as_float((unsigned)(127 + e) << 23); }
+
+// ---------------------------------------------------------------------------
+// Pack: k, v [N, Skv, kv_heads * d] (fp32) -> tiles as described above, and
+// the exponents (e_k, e_v) of every tile. One workgroup per (tile, kv head,
+// batch); 256 threads.
+// ---------------------------------------------------------------------------
+template <int DP>
+__global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, const float* __restrict__ V,
+                                                   u16* __restrict__ tiles, int2* __restrict__ exps, int Skv,
+                                                   int kv_inner, int d, int ntiles, int kv_heads) {
+    constexpr int CPR = DP / 8;              // 16-B chunks per K row
+    constexpr int KCH = kKT * CPR / 256;     // K chunks per thread
+    __shared__ float sv[kKT][DP + 1];
+    __shared__ float red[2][4];
+    const int t = blockIdx.x, kh = blockIdx.y, nb = blockIdx.z;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t row0 = (int64_t)nb * Skv + (int64_t)t * kKT;
+    const int64_t col0 = (int64_t)kh * d;
+    const int64_t tile = ((int64_t)nb * kv_heads + kh) * ntiles + t;
+    u16* out = tiles + tile * 4 * (kKT * DP);
+    const int nrows = min(kKT, Skv - t * kKT);
+    // K chunks into registers: slot i holds logical chunk (i % CPR) ^ swz of row i / CPR
+    float kx[KCH][8];
+    float kmax = 0.f, vmax = 0.f;
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+        const int i = threadIdx.x + j * 256, r = i / CPR, c = (i % CPR) ^ swz_k<DP>(r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int col = c * 8 + e;
+            const float x = (r < nrows && col < d) ? K[(row0 + r) * kv_inner + col0 + col] : 0.f;
+            kx[j][e] = x;
+            kmax = fmaxf(kmax, fabsf(x));
+        }
+    }
+    // V tile into LDS (zero beyond the keys and the head dimension)
+    for (int i = threadIdx.x; i < kKT * DP; i += 256) {
+        const int r = i / DP, c = i % DP;
+        const float x = (r < nrows && c < d) ? V[(row0 + r) * kv_inner + col0 + c] : 0.f;
+        sv[r][c] = x;
+        vmax = fmaxf(vmax, fabsf(x));
+    }
+    kmax = dev::wave_max(kmax);
+    vmax = dev::wave_max(vmax);
+    if (lane == 0) {
+        red[0][w] = kmax;
+        red[1][w] = vmax;
+    }
+    __syncthreads();
+    kmax = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    vmax = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+    const int ek = block_exp(kmax), ev = block_exp(vmax);
+    if (threadIdx.x == 0) exps[tile] = make_int2(ek, ev);
+    const float sk = pow2(-ek), svs = pow2(-ev);
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+        const int i = threadIdx.x + j * 256, r = i / CPR, p = i % CPR;
+        h8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            _Float16 a, b;
+            split(kx[j][e] * sk, a, b);
+            hi[e] = a;
+            lo[e] = b;
+        }
+        *(h8*)(out + r * DP + p * 8) = hi;
+        *(h8*)(out + kKT * DP + r * DP + p * 8) = lo;
+    }
+    // V^T: row = head-dim index, 8 chunks of 8 key positions
+    u16* vt = out + 2 * kKT * DP;
+    for (int i = threadIdx.x; i < DP * 8; i += 256) {
+        const int r = i / 8, p = i % 8, c = p ^ swz_v(r);
+        h8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            _Float16 a, b;
+            split(sv[key_at(c * 8 + e)][r] * svs, a, b);
+            hi[e] = a;
+            lo[e] = b;
+        }
+        *(h8*)(vt + r * kKT + p * 8) = hi;
+        *(h8*)(vt + DP * kKT + r * kKT + p * 8) = lo;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fused attention, head dimension padded to DP (64 or 128).
+// grid (ceil(Sq / 256), heads, N); 512 threads.
+// ---------------------------------------------------------------------------
+template <int DP, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restrict__ Q, const u16* __restrict__ tiles,
+                                                          const int2* __restrict__ exps, float* __restrict__ O, int Sq,
+                                                          int Skv, int inner, int d, int group, int kv_heads,
+                                                          int ntiles, float c2, int qvec) {
+    constexpr int DS = DP / 16;            // 16-wide head-dim steps of S^T = K Q^T
+    constexpr int DT = DP / 32;            // 32-row head-dim tiles of O^T
+    constexpr int TILE = 4 * kKT * DP;     // fp16 values per packed tile
+    constexpr int NLD = TILE * 2 / 16 / kThreads;  // 16-B loads per thread per tile
+    __shared__ __attribute__((aligned(1024))) u16 sbuf[2][TILE];
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int fr = lane & 31, fh = lane >> 5;
+    const int h = blockIdx.y, nb = blockIdx.z, kh = h / group;
+    const int q0 = blockIdx.x * kBM, qw0 = q0 + w * 32;
+    const int qlane = qw0 + fr;
+    const int qend = min(q0 + kBM, Sq);
+    const int T = CAUSAL ? min(ntiles, (qend - 1) / kKT + 1) : ntiles;
+    const u16* src = tiles + ((int64_t)nb * kv_heads + kh) * ntiles * TILE;
+    const int2* ex = exps + ((int64_t)nb * kv_heads + kh) * ntiles;
+    auto issue = [&](int t, u16* dst) {
+        const u16* g = src + (int64_t)t * TILE;
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            const int chunk = (j * kWaves + w) * 64;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(g + (chunk + lane) * 8),
+                                             (__attribute__((address_space(3))) void*)(dst + chunk * 8), 16, 0, 0);
+        }
+    };
+    issue(0, sbuf[0]);
+
+    // Q fragments (B operand of S^T): query qlane, head dims ds*16 + fh*8 .. +7,
+    // scaled by 2^-eq for the query's largest magnitude (lanes l and l^32 hold its two halves)
+    h8 qh[DS], ql[DS];
+    int eq;
+    {
+        const float* qp = Q + ((int64_t)nb * Sq + min(qlane, Sq - 1)) * inner + (int64_t)h * d;
+        float x[DS][8];
+        float qmax = 0.f;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            const int c0 = ds * 16 + fh * 8;
+            if (qvec) {
+                const f4 a = *(const f4*)(qp + c0), b = *(const f4*)(qp + c0 + 4);
+                x[ds][0] = a.x; x[ds][1] = a.y; x[ds][2] = a.z; x[ds][3] = a.w;
+                x[ds][4] = b.x; x[ds][5] = b.y; x[ds][6] = b.z; x[ds][7] = b.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[ds][e] = c0 + e < d ? qp[c0 + e] : 0.f;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qmax = fmaxf(qmax, fabsf(x[ds][e]));
+        }
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+        eq = block_exp(qmax);
+        const float sc = pow2(-eq);
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                _Float16 hi, lo;
+                split(x[ds][e] * sc, hi, lo);
+                qh[ds][e] = hi;
+                ql[ds][e] = lo;
+            }
+    }
+    // E: the largest value exponent among the tiles this workgroup reads
+    int E;
+    {
+        float em = -1e30f;
+        for (int t = lane; t < T; t += 64) em = fmaxf(em, (float)ex[t].y);
+        E = (int)dev::wave_max(em);
+    }
+
+    f32x16 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+    float m = kNoMax, lsum = 0.f;
+
+    for (int t = 0; t < T; ++t) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (t + 1 < T) issue(t + 1, sbuf[(t + 1) & 1]);
+        const int k0 = t * kKT;
+        // a wave with no real query, or (causal) whose queries all precede the tile, skips it
+        if (qw0 >= Sq || (CAUSAL && qw0 + 31 < k0)) continue;
+        const int2 et = ex[t];
+        const u16* Kh = sbuf[t & 1];
+        const u16* Kl = Kh + kKT * DP;
+        const u16* Vh = Kh + 2 * kKT * DP;
+        const u16* Vl = Kh + 3 * kKT * DP;
+
+        f32x16 s[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[j][i] = 0.f;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int r = j * 32 + fr;
+                const int off = r * DP + (((ds * 2 + fh) ^ swz_k<DP>(r)) << 3);
+                const h8 kh8 = *(const h8*)(Kh + off);
+                const h8 kl8 = *(const h8*)(Kl + off);
+                s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh8, qh[ds], s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh8, ql[ds], s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl8, qh[ds], s[j], 0, 0, 0);
+            }
+        }
+        // mask: keys past Skv, and (causal) keys after the query
+        if (k0 + kKT > Skv || (CAUSAL && k0 + kKT - 1 > qw0)) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int kv = k0 + j * 32 + (i >> 2) * 8 + fh * 4 + (i & 3);
+                    if (kv >= Skv || (CAUSAL && kv > qlane)) s[j][i] = -INFINITY;
+                }
+        }
+        // log2(e)/sqrt(d) on the unscaled scores; kept normal so that a masked -inf stays -inf
+        const float ct = fmaxf(ldexpf(c2, eq + et.x), 1.17549435e-38f);
+        float mx = s[0][0];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[j][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(m, mx * ct);
+        const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+        m = mnew;
+        // weights 2^(s ct - m) times 2^(14 + e_v - E), <= 2^14
+        const float shift = (float)(14 + et.y - E) - mnew;
+        float rs = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(s[j][i], ct, shift));
+                s[j][i] = p;
+                rs += p;
+            }
+        lsum = lsum * alpha + ldexpf(rs, E - et.y);  // 2^14 sum(p)
+        if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+        }
+        // O^T += V^T P^T over four 16-key steps
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            h8 ph, pl;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                _Float16 hi, lo;
+                split(s[ks >> 1][(ks & 1) * 8 + e], hi, lo);
+                ph[e] = hi;
+                pl[e] = lo;
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int r = dt * 32 + fr;
+                const int off = r * kKT + (((ks * 2 + fh) ^ swz_v(r)) << 3);
+                const h8 vh8 = *(const h8*)(Vh + off);
+                const h8 vl8 = *(const h8*)(Vl + off);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh8, ph, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh8, pl, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl8, ph, o[dt], 0, 0, 0);
+            }
+        }
+    }
+    if (qlane >= Sq) return;
+    lsum += __shfl_xor(lsum, 32, 64);
+    // the reference scales P by 1/sum (tensor.cpp:761-764); O^T carries 2^(14-E) sum(p v), lsum 2^14 sum(p)
+    const float inv = ldexpf(1.0f / lsum, E);
+    float* op = O + ((int64_t)nb * Sq + qlane) * inner + (int64_t)h * d;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int c0 = dt * 32 + g * 8 + fh * 4;
+            const f4 v = {o[dt][g * 4] * inv, o[dt][g * 4 + 1] * inv, o[dt][g * 4 + 2] * inv, o[dt][g * 4 + 3] * inv};
+            if (qvec) {
+                *(f4*)(op + c0) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (c0 + e < d) op[c0 + e] = v[e];
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
+// Any head dimension: fp32 online softmax, one wave per (query, head, batch).
+// Lanes take 64 keys at a time for the scores, then 64 head-dim columns at a
+// time for the weighted sum. The query row and the scores pass through LDS.
+// ---------------------------------------------------------------------------
+constexpr int kGenWaves = 4, kGenMaxD = 1024;
+
+template <bool CAUSAL>
+__global__ __launch_bounds__(64 * kGenWaves) void k_attn_generic(const float* __restrict__ Q, const float* __restrict__ K,
+                                                                 const float* __restrict__ V, float* __restrict__ O,
+                                                                 int Sq, int Skv, int inner, int kv_inner, int d,
+                                                                 int group, float c2) {
+    __shared__ float sq[kGenWaves][kGenMaxD];
+    __shared__ float sp[kGenWaves][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int q = blockIdx.x * kGenWaves + w, h = blockIdx.y, nb = blockIdx.z;
+    if (q >= Sq) return;  // whole wave; no block-level barrier below
+    const float* qp = Q + ((int64_t)nb * Sq + q) * inner + (int64_t)h * d;
+    const float* kb = K + (int64_t)nb * Skv * kv_inner + (int64_t)(h / group) * d;
+    const float* vb = V + (int64_t)nb * Skv * kv_inner + (int64_t)(h / group) * d;
+    for (int c = lane; c < d; c += 64) sq[w][c] = qp[c];
+    __builtin_amdgcn_wave_barrier();
+    constexpr int kAcc = kGenMaxD / 64;
+    float acc[kAcc];
+#pragma unroll
+    for (int i = 0; i < kAcc; ++i) acc[i] = 0.f;
+    float m = kNoMax, lsum = 0.f;
+    const int kend = CAUSAL ? min(Skv, q + 1) : Skv;
+    for (int k0 = 0; k0 < kend; k0 += 64) {
+        const int kv = k0 + lane;
+        float s = -INFINITY;
+        if (kv < kend) {
+            const float* kp = kb + (int64_t)kv * kv_inner;
+            float a = 0.f;
+            for (int c = 0; c < d; ++c) a = fmaf(sq[w][c], kp[c], a);
+            s = a;
+        }
+        const float mnew = fmaxf(m, dev::wave_max(s) * c2);
+        const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+        m = mnew;
+        const float p = __builtin_amdgcn_exp2f(fmaf(s, c2, -mnew));
+        lsum = lsum * alpha + dev::wave_sum(p);
+        __builtin_amdgcn_wave_barrier();
+        sp[w][lane] = p;
+        __builtin_amdgcn_wave_barrier();
+        const int nk = min(64, kend - k0);
+#pragma unroll
+        for (int i = 0; i < kAcc; ++i) {
+            const int c = i * 64 + lane;
+            if (i * 64 >= d) break;
+            float a = acc[i] * alpha;
+            if (c < d)
+                for (int j = 0; j < nk; ++j) a = fmaf(sp[w][j], vb[(int64_t)(k0 + j) * kv_inner + c], a);
+            acc[i] = a;
+        }
+    }
+    const float inv = 1.0f / lsum;
+    float* op = O + ((int64_t)nb * Sq + q) * inner + (int64_t)h * d;
+#pragma unroll
+    for (int i = 0; i < kAcc; ++i) {
+        const int c = i * 64 + lane;
+        if (i * 64 >= d) break;
+        if (c < d) op[c] = acc[i] * inv;
+    }
+}
+
+bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return x < y + nb && y < x + na;
+}
+
+template <int DP>
+void run_mfma(const float* q, const float* k, const float* v, float* out, int64_t N, int64_t Sq, int64_t Skv,
+              int heads, int kv_heads, int64_t d, bool causal, float c2) {
+    const int64_t ntiles = (Skv + kKT - 1) / kKT;
+    const int64_t ntot = N * kv_heads * ntiles;
+    const size_t tile_bytes = (size_t)4 * kKT * DP * 2;
+    char* base = (char*)scratch((size_t)ntot * (tile_bytes + sizeof(int2)));
+    u16* tiles = (u16*)base;
+    int2* exps = (int2*)(base + (size_t)ntot * tile_bytes);
+    const int64_t inner = heads * d, kv_inner = (int64_t)kv_heads * d;
+    k_attn_pack<DP><<<dim3((unsigned)ntiles, (unsigned)kv_heads, (unsigned)N), 256, 0, stream()>>>(
+        k, v, tiles, exps, (int)Skv, (int)kv_inner, (int)d, (int)ntiles, kv_heads);
+    launched("sdh_attention");
+    const int qvec = d == DP && inner % 4 == 0 && aligned16(q) && aligned16(out);
+    const dim3 grid((unsigned)((Sq + kBM - 1) / kBM), (unsigned)heads, (unsigned)N);
+    if (causal)
+        k_attn_fwd<DP, true><<<grid, kThreads, 0, stream()>>>(q, tiles, exps, out, (int)Sq, (int)Skv, (int)inner,
+                                                               (int)d, heads / kv_heads, kv_heads, (int)ntiles, c2,
+                                                               qvec);
+    else
+        k_attn_fwd<DP, false><<<grid, kThreads, 0, stream()>>>(q, tiles, exps, out, (int)Sq, (int)Skv, (int)inner,
+                                                                (int)d, heads / kv_heads, kv_heads, (int)ntiles, c2,
+                                                                qvec);
+    launched("sdh_attention");
+}
+
+void run_attention(const float* q, const float* k, const float* v, float* out, int64_t N, int64_t Sq, int64_t Skv,
+                   int heads, int kv_heads, int64_t d, bool causal) {
+    const char* op = "sdh_attention";
+    if (kv_heads <= 0) kv_heads = heads;  // tensor.cpp:777
+    need(N >= 0 && Sq >= 0 && Skv >= 0, op, "negative size");
+    need(heads > 0 && d > 0, op, "heads and d must be positive");
+    need(heads % kv_heads == 0, op, "heads mismatch");  // tensor.cpp:779
+    need(d <= kGenMaxD, op, "head dimension above 1024");
+    const int64_t inner = heads * d, kv_inner = (int64_t)kv_heads * d;
+    need(N <= 65535 && heads <= 65535 && kv_heads <= 65535, op, "too many batches or heads for one launch");
+    need(N * Sq * inner < (1LL << 31) && N * Skv * kv_inner < (1LL << 31), op, "tensor too large (2^31 elements)");
+    if (N == 0 || Sq == 0) return;
+    ensure_init();
+    const size_t qb = (size_t)(N * Sq * inner) * 4, kb = (size_t)(N * Skv * kv_inner) * 4;
+    check_range(q, qb, op, "q");
+    check_range(out, qb, op, "out");
+    if (Skv > 0) {
+        check_range(k, kb, op, "k");
+        check_range(v, kb, op, "v");
+    }
+    need(!overlaps(out, qb, q, qb) && !(Skv > 0 && (overlaps(out, qb, k, kb) || overlaps(out, qb, v, kb))), op,
+         "out overlaps an input");
+    if (Skv == 0) {  // empty key set: every weighted sum is empty (the reference's gemm leaves 0)
+        zero_device(out, qb);
+        return;
+    }
+    const float scale = 1.0f / std::sqrt((float)d);  // tensor.cpp:784
+    const float c2 = scale * kLog2e;
+    if (d <= 64) {
+        run_mfma<64>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2);
+    } else if (d <= 128) {
+        run_mfma<128>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2);
+    } else {
+        const dim3 grid((unsigned)((Sq + kGenWaves - 1) / kGenWaves), (unsigned)heads, (unsigned)N);
+        if (causal)
+            k_attn_generic<true><<<grid, 64 * kGenWaves, 0, stream()>>>(q, k, v, out, (int)Sq, (int)Skv, (int)inner,
+                                                                         (int)kv_inner, (int)d, heads / kv_heads, c2);
+        else
+            k_attn_generic<false><<<grid, 64 * kGenWaves, 0, stream()>>>(q, k, v, out, (int)Sq, (int)Skv, (int)inner,
+                                                                          (int)kv_inner, (int)d, heads / kv_heads, c2);
+        launched(op);
+    }
+}
+
+}  // namespace
+}  // namespace sdh
+
+using namespace sdh;
+
+extern "C" {
+
+int sdh_attention(const float* q, const float* k, const float* v, float* out, int64_t N, int64_t Sq, int64_t Skv,
+                  int heads, int kv_heads, int64_t d, int causal) {
+    return guarded([&] { run_attention(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal != 0); });
+}
+
+}  // extern "C"

@@ -81,6 +81,7 @@ SIGNATURES = {
     "sdh_add_rows": [_vp, _vp, _i64, _i64],
     "sdh_gemm_nt_bf16": [_i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, C.c_int],
     "sdh_linear_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _i64],
+    "sdh_attention": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
     "sdh_upsample_nearest2x": [_vp, _vp, _i64, _i64, _i64],
     "sdh_concat_channels": [_vp, _vp, _vp, _i64, _i64, _i64, _i64],
     "sdh_nchw_to_nlc": [_vp, _vp, _i64, _i64, _i64],
@@ -272,6 +273,10 @@ class Backend:
             self.call("sdh_softmax_rows", _p(x), rows, cols, scale, int(bool(causal)))
         else:
             self.call("sdh_softmax_rows_batched", _p(x), rows, cols, scale, int(bool(causal)), period)
+
+    def attention(self, q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal=False):
+        """out [N, Sq, heads*d] = softmax(q k^T / sqrt(d)) v per head (tensor.cpp:776-810)."""
+        self.call("sdh_attention", _p(q), _p(k), _p(v), _p(out), N, Sq, Skv, heads, kv_heads, d, int(bool(causal)))
 
     def swiglu(self, g, u, y, n):
         self.call("sdh_swiglu", _p(g), _p(u), _p(y), n)

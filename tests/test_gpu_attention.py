@@ -1,0 +1,131 @@
+"""GPU parity of the fused attention (sdh_attention), through the C ABI.
+
+Bar: max-abs 1e-4 against the float64 oracle, the reference's own bar for
+attention (test_ops.cpp:113 against its double restatement, :442-451 GPU vs
+CPU), on unit-variance inputs. Shapes: the reference's GPU checks
+(test_ops.cpp:440-451: MHA, causal, grouped heads, 100 tokens, 8/2 causal
+batch 2), head dimensions on both sides of the two packed widths (64, 128)
+and above them (the fp32 kernel), Skv != Sq (cross-attention), a single
+query or key, key counts off the 64-key tile, the Qwen3 text encoder
+(16/8 heads, d 128, causal) and the Z-Image DiT layer ([1, 4096, 30 x 128],
+checked on sampled query rows). At the full shape, constant values must come
+back as that constant to relative 1e-5 on every row (weights sum to one).
+Inputs far from unit scale are held to the reference's own fp32 error.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _qkv(orc, N, Sq, Skv, heads, kvh, d, seed, std=1.0):
+    q = orc.randn((N, Sq, heads * d), seed, 0.0, std)
+    k = orc.randn((N, Skv, kvh * d), seed + 1, 0.0, std)
+    v = orc.randn((N, Skv, kvh * d), seed + 2)
+    return q, k, v
+
+
+def _run(be, q, k, v, heads, kvh, causal):
+    N, Sq, inner = q.shape
+    Skv = k.shape[1]
+    d = inner // heads
+    out = be.empty((N, Sq, inner))
+    be.attention(be.array(q), be.array(k), be.array(v), out, N, Sq, Skv, heads, kvh, d, causal)
+    return out.download()
+
+
+SHAPES = [  # N, Sq, Skv, heads, kv_heads, d, causal
+    (2, 9, 9, 3, 3, 8, False), (2, 9, 9, 3, 3, 8, True), (2, 9, 9, 3, 1, 8, False),
+    (1, 100, 100, 2, 2, 32, False), (2, 37, 37, 8, 2, 16, True),
+    (1, 300, 77, 8, 8, 40, False), (2, 257, 257, 5, 5, 64, True), (1, 130, 70, 4, 2, 80, False),
+    (1, 513, 513, 2, 1, 128, True), (1, 64, 64, 1, 1, 128, False), (1, 1, 1, 1, 1, 64, False),
+    (1, 1, 300, 2, 2, 128, False), (3, 65, 129, 6, 3, 100, True), (1, 260, 200, 2, 2, 72, True),
+    (1, 70, 90, 2, 2, 160, False), (1, 33, 33, 2, 1, 200, True),
+]
+
+
+@pytest.mark.parametrize("N,Sq,Skv,heads,kvh,d,causal", SHAPES)
+def test_attention_parity(be, orc, N, Sq, Skv, heads, kvh, d, causal):
+    q, k, v = _qkv(orc, N, Sq, Skv, heads, kvh, d, 2000 + Sq + Skv + d)
+    got = _run(be, q, k, v, heads, kvh, causal)
+    want = orc.attention(q, k, v, heads, causal, kvh)
+    err = float(np.max(np.abs(got - want)))
+    assert err <= TOL, f"attention {N}x{Sq}x{Skv} h{heads}/{kvh} d{d} causal={causal}: max-abs {err:.3g}"
+
+
+@pytest.mark.parametrize("std_qk,std_v", [(3.0, 1.0), (10.0, 1.0), (30.0, 100.0), (1e-3, 1e-3), (1e-20, 1e15)])
+def test_attention_input_range(be, orc, ref, std_qk, std_v):
+    """Inputs far from unit scale: scores with a spread of 9, 100 and 900
+    (weights near one-hot, where score errors are amplified), near-zero
+    scores, and values of 1e15 (beyond fp16). Bar: within 4x the reference
+    CPU path's own fp32 error against the float64 oracle, plus 1e-6 of the
+    value scale. (The split-fp16 products carry about 2^-21 relative error
+    against 2^-24 for an fp32 product; at score spreads of 100 and more the
+    measured ratio is 2.4-2.8x, and below unit scale the GPU is closer to the
+    oracle than the reference.)"""
+    q, k, _ = _qkv(orc, 1, 160, 200, 4, 4, 128, 3100, std=std_qk)
+    v = orc.randn((1, 200, 512), 3103, 0.0, std_v)
+    got = _run(be, q, k, v, 4, 4, False)
+    want = orc.attention(q, k, v, 4, False).astype(np.float64)
+    err = float(np.max(np.abs(got - want)))
+    err_ref = float(np.max(np.abs(ref.attention(q, k, v, 4, False) - want)))
+    print(f"std_qk={std_qk} std_v={std_v}: gpu {err:.3g}, reference cpu {err_ref:.3g} (value scale {std_v})")
+    assert err <= 4 * err_ref + 1e-6 * std_v
+
+
+def test_attention_matches_reference_gpu_checks(be, orc, ref):
+    """test_ops.cpp:440-451 against the reference's own CPU attention."""
+    for (N, Sq, Skv, heads, kvh, d, causal) in SHAPES[:5]:
+        q, k, v = _qkv(orc, N, Sq, Skv, heads, kvh, d, 4000 + Sq)
+        got = _run(be, q, k, v, heads, kvh, causal)
+        assert float(np.max(np.abs(got - ref.attention(q, k, v, heads, causal, kvh)))) <= TOL
+
+
+def test_attention_qwen3_text_encoder(be, orc):
+    q, k, v = _qkv(orc, 1, 512, 512, 16, 8, 128, 5000)
+    got = _run(be, q, k, v, 16, 8, True)
+    rows = np.arange(0, 512, 7)
+    want = orc.attention(q, k, v, 16, True, 8, rows=rows)
+    assert float(np.max(np.abs(got[:, rows] - want))) <= TOL
+
+
+def test_attention_zimage_layer(be, orc):
+    N, S, heads, d = 1, 4096, 30, 128
+    q, k, v = _qkv(orc, N, S, S, heads, heads, d, 6000)
+    got = _run(be, q, k, v, heads, heads, False)
+    rows = np.concatenate([np.arange(0, S, 97), [S - 1]])
+    want = orc.attention(q, k, v, heads, False, rows=rows)
+    assert float(np.max(np.abs(got[:, rows] - want))) <= TOL
+    # the weights of every row sum to one: constant values come back unchanged,
+    # up to fp32 sums of 4096 weights taken in two orders (relative 1e-5)
+    ones = np.full_like(v, 0.5)
+    got1 = _run(be, q, k, ones, heads, heads, False)
+    assert float(np.max(np.abs(got1 - 0.5))) <= 5e-6
+
+
+def test_attention_empty_keys_and_queries(be, orc):
+    q, k, v = _qkv(orc, 1, 5, 0, 2, 2, 8, 7000)
+    out = be.array(np.full((1, 5, 16), 3.0, np.float32))
+    be.attention(be.array(q), be.array(np.zeros((1, 1, 16), np.float32)), be.array(np.zeros((1, 1, 16), np.float32)),
+                 out, 1, 5, 0, 2, 2, 8, False)
+    assert np.all(out.download() == 0.0)  # empty weighted sums
+    be.attention(be.array(q), be.array(k), be.array(v), be.empty((1, 1, 16)), 1, 0, 0, 2, 2, 8, False)  # no queries
+
+
+def test_attention_invalid_arguments(be):
+    import sdhip
+
+    q = be.empty((1, 4, 12))
+    k = be.empty((1, 4, 12))
+    out = be.empty((1, 4, 12))
+    with pytest.raises(sdhip.SdhError) as e:
+        be.attention(q, k, k, out, 1, 4, 4, 3, 2, 4, False)  # 3 heads over 2 key/value heads
+    assert e.value.status == sdhip.SDH_ERR_INVALID
+    with pytest.raises(sdhip.SdhError) as e:
+        be.attention(q, k, k, q, 1, 4, 4, 3, 3, 4, False)  # out is q
+    assert e.value.status == sdhip.SDH_ERR_INVALID
+    with pytest.raises(sdhip.SdhError) as e:
+        be.attention(q, k, k, out, 1, 8, 4, 3, 3, 4, False)  # q holds 4 rows, not 8
+    assert e.value.status == sdhip.SDH_ERR_INVALID
