@@ -40,9 +40,10 @@
 // block (i = 0..15); the pack kernel stores V^T with the keys of every
 // 16-key group in the matching order (positions 8h + 4a + b hold key
 // 8a + 4h + b), so the A operand of O^T is again one 16-B LDS read per lane.
-// Workgroup: 8 waves x 32 queries of one head; K/V tiles double-buffered in
-// LDS (one barrier per tile); the softmax rescale of O is skipped when no
-// row max of the wave changed (exactly alpha = 1).
+// Workgroup: 8 waves x 32 queries of one head, in two groups that run half
+// a tile apart (see k_attn_fwd); K and V tiles double-buffered in LDS; the
+// softmax rescale of O is skipped when no row max of the wave changed
+// (exactly alpha = 1).
 // Head dimensions above 128 take a plain fp32 kernel (one wave per query).
 #include <algorithm>
 #include <cmath>
@@ -94,15 +95,16 @@ __device__ __forceinline__ float pow2(int e) { return __uint_as_float((unsigned)
 // ---------------------------------------------------------------------------
 // Pack: k, v [N, Skv, kv_heads * d] (fp32) -> tiles as described above, and
 // the exponents (e_k, e_v) of every tile. One workgroup per (tile, kv head,
-// batch); 256 threads.
+// batch); 256 threads. VEC: d == DP and 16-B aligned rows (float4 loads).
 // ---------------------------------------------------------------------------
-template <int DP>
+template <int DP, bool VEC>
 __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, const float* __restrict__ V,
                                                    u16* __restrict__ tiles, int2* __restrict__ exps, int Skv,
                                                    int kv_inner, int d, int ntiles, int kv_heads) {
     constexpr int CPR = DP / 8;              // 16-B chunks per K row
     constexpr int KCH = kKT * CPR / 256;     // K chunks per thread
-    __shared__ float sv[kKT][DP + 1];
+    constexpr int VCH = kKT * DP / 4 / 256;  // V float4 per thread
+    __shared__ float sv[kKT][DP + 4];
     __shared__ float red[2][4];
     const int t = blockIdx.x, kh = blockIdx.y, nb = blockIdx.z;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -117,20 +119,39 @@ __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, 
 #pragma unroll
     for (int j = 0; j < KCH; ++j) {
         const int i = threadIdx.x + j * 256, r = i / CPR, c = (i % CPR) ^ swz_k<DP>(r);
+        if constexpr (VEC) {
+            f4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+            if (r < nrows) {
+                const f4* p = (const f4*)(K + (row0 + r) * kv_inner + col0 + c * 8);
+                a = p[0];
+                b = p[1];
+            }
+            kx[j][0] = a.x; kx[j][1] = a.y; kx[j][2] = a.z; kx[j][3] = a.w;
+            kx[j][4] = b.x; kx[j][5] = b.y; kx[j][6] = b.z; kx[j][7] = b.w;
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int col = c * 8 + e;
-            const float x = (r < nrows && col < d) ? K[(row0 + r) * kv_inner + col0 + col] : 0.f;
-            kx[j][e] = x;
-            kmax = fmaxf(kmax, fabsf(x));
+            for (int e = 0; e < 8; ++e) {
+                const int col = c * 8 + e;
+                kx[j][e] = (r < nrows && col < d) ? K[(row0 + r) * kv_inner + col0 + col] : 0.f;
+            }
         }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kmax = fmaxf(kmax, fabsf(kx[j][e]));
     }
     // V tile into LDS (zero beyond the keys and the head dimension)
-    for (int i = threadIdx.x; i < kKT * DP; i += 256) {
-        const int r = i / DP, c = i % DP;
-        const float x = (r < nrows && c < d) ? V[(row0 + r) * kv_inner + col0 + c] : 0.f;
-        sv[r][c] = x;
-        vmax = fmaxf(vmax, fabsf(x));
+#pragma unroll
+    for (int j = 0; j < VCH; ++j) {
+        const int i = threadIdx.x + j * 256, r = i / (DP / 4), c = (i % (DP / 4)) * 4;
+        f4 x = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (VEC) {
+            if (r < nrows) x = *(const f4*)(V + (row0 + r) * kv_inner + col0 + c);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (r < nrows && c + e < d) x[e] = V[(row0 + r) * kv_inner + col0 + c + e];
+        }
+        *(f4*)&sv[r][c] = x;
+        vmax = fmaxf(vmax, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
     }
     kmax = dev::wave_max(kmax);
     vmax = dev::wave_max(vmax);
@@ -177,20 +198,31 @@ __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, 
 
 // ---------------------------------------------------------------------------
 // Fused attention, head dimension padded to DP (64 or 128).
-// grid (ceil(Sq / 256), heads, N); 512 threads.
+// grid (ceil(Sq / 256), heads, N); 512 threads = 8 waves of 32 queries.
+// Waves 0-3 (X) and 4-7 (Y) run half a tile apart (waves w and w + 4 share a
+// SIMD): per iteration t, between two barriers,
+//   segment 1:  X: S^T(t) = K(t) Q^T          Y: softmax(t-1), O += V(t-1) P
+//   segment 2:  X: softmax(t), O += V(t) P    Y: S^T(t)
+// so one wave's MFMAs run while the other wave of its SIMD is in its softmax
+// (a single barrier per tile keeps both in the same phase: 760 -> 722 us on
+// the Z-Image layer). K and V have separate double buffers: K(t+1) is loaded
+// after barrier 1 of t (K(t-1)'s last reader, Y's S^T(t-1), is done), V(t+1)
+// after barrier 2 of t (V(t-1)'s last reader, Y's O(t-1), is done).
 // ---------------------------------------------------------------------------
 template <int DP, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restrict__ Q, const u16* __restrict__ tiles,
                                                           const int2* __restrict__ exps, float* __restrict__ O, int Sq,
                                                           int Skv, int inner, int d, int group, int kv_heads,
                                                           int ntiles, float c2, int qvec) {
-    constexpr int DS = DP / 16;            // 16-wide head-dim steps of S^T = K Q^T
-    constexpr int DT = DP / 32;            // 32-row head-dim tiles of O^T
-    constexpr int TILE = 4 * kKT * DP;     // fp16 values per packed tile
-    constexpr int NLD = TILE * 2 / 16 / kThreads;  // 16-B loads per thread per tile
-    __shared__ __attribute__((aligned(1024))) u16 sbuf[2][TILE];
+    constexpr int DS = DP / 16;                    // 16-wide head-dim steps of S^T = K Q^T
+    constexpr int DT = DP / 32;                    // 32-row head-dim tiles of O^T
+    constexpr int TILE = 4 * kKT * DP, HALF = TILE / 2;  // fp16 values per packed tile, per K or V part
+    constexpr int NLD = HALF * 2 / 16 / kThreads;  // 16-B loads per thread per part
+    __shared__ __attribute__((aligned(1024))) u16 kbuf[2][HALF];
+    __shared__ __attribute__((aligned(1024))) u16 vbuf[2][HALF];
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const bool isY = w >= kWaves / 2;
     const int fr = lane & 31, fh = lane >> 5;
     const int h = blockIdx.y, nb = blockIdx.z, kh = h / group;
     const int q0 = blockIdx.x * kBM, qw0 = q0 + w * 32;
@@ -199,8 +231,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
     const int T = CAUSAL ? min(ntiles, (qend - 1) / kKT + 1) : ntiles;
     const u16* src = tiles + ((int64_t)nb * kv_heads + kh) * ntiles * TILE;
     const int2* ex = exps + ((int64_t)nb * kv_heads + kh) * ntiles;
-    auto issue = [&](int t, u16* dst) {
-        const u16* g = src + (int64_t)t * TILE;
+    auto issue = [&](int t, int part, u16* dst) {
+        const u16* g = src + (int64_t)t * TILE + part * HALF;
 #pragma unroll
         for (int j = 0; j < NLD; ++j) {
             const int chunk = (j * kWaves + w) * 64;
@@ -208,7 +240,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
                                              (__attribute__((address_space(3))) void*)(dst + chunk * 8), 16, 0, 0);
         }
     };
-    issue(0, sbuf[0]);
+    issue(0, 0, kbuf[0]);
+    issue(0, 1, vbuf[0]);
 
     // Q fragments (B operand of S^T): query qlane, head dims ds*16 + fh*8 .. +7,
     // scaled by 2^-eq for the query's largest magnitude (lanes l and l^32 hold its two halves)
@@ -259,21 +292,10 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
     float m = kNoMax, lsum = 0.f;
+    f32x16 s[2];  // S^T of the tile in flight (kept across a barrier by Y)
 
-    for (int t = 0; t < T; ++t) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (t + 1 < T) issue(t + 1, sbuf[(t + 1) & 1]);
-        const int k0 = t * kKT;
-        // a wave with no real query, or (causal) whose queries all precede the tile, skips it
-        if (qw0 >= Sq || (CAUSAL && qw0 + 31 < k0)) continue;
-        const int2 et = ex[t];
-        const u16* Kh = sbuf[t & 1];
+    auto scores = [&](const u16* Kh) {
         const u16* Kl = Kh + kKT * DP;
-        const u16* Vh = Kh + 2 * kKT * DP;
-        const u16* Vl = Kh + 3 * kKT * DP;
-
-        f32x16 s[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -291,6 +313,11 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
                 s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl8, qh[ds], s[j], 0, 0, 0);
             }
         }
+    };
+    auto softmax_pv = [&](int t, const u16* Vh) {
+        const u16* Vl = Vh + DP * kKT;
+        const int k0 = t * kKT;
+        const int2 et = ex[t];
         // mask: keys past Skv, and (causal) keys after the query
         if (k0 + kKT > Skv || (CAUSAL && k0 + kKT - 1 > qw0)) {
 #pragma unroll
@@ -351,6 +378,30 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh8, pl, o[dt], 0, 0, 0);
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl8, ph, o[dt], 0, 0, 0);
             }
+        }
+    };
+    // a wave with no real query, or (causal) whose queries all precede tile t, skips it
+    const bool active = qw0 < Sq;
+    auto wants = [&](int t) { return active && !(CAUSAL && qw0 + 31 < t * kKT); };
+
+    for (int t = 0; t <= T; ++t) {
+        // barrier 1: K(t) has landed; no wave reads K(t-1) any more
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (t + 1 < T) issue(t + 1, 0, kbuf[(t + 1) & 1]);
+        if (!isY) {
+            if (t < T && wants(t)) scores(kbuf[t & 1]);
+        } else {
+            if (t >= 1 && wants(t - 1)) softmax_pv(t - 1, vbuf[(t - 1) & 1]);
+        }
+        // barrier 2: V(t) has landed; no wave reads V(t-1) any more
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (t + 1 < T) issue(t + 1, 1, vbuf[(t + 1) & 1]);
+        if (!isY) {
+            if (t < T && wants(t)) softmax_pv(t, vbuf[t & 1]);
+        } else {
+            if (t < T && wants(t)) scores(kbuf[t & 1]);
         }
     }
     if (qlane >= Sq) return;
@@ -455,8 +506,13 @@ void run_mfma(const float* q, const float* k, const float* v, float* out, int64_
     u16* tiles = (u16*)base;
     int2* exps = (int2*)(base + (size_t)ntot * tile_bytes);
     const int64_t inner = heads * d, kv_inner = (int64_t)kv_heads * d;
-    k_attn_pack<DP><<<dim3((unsigned)ntiles, (unsigned)kv_heads, (unsigned)N), 256, 0, stream()>>>(
-        k, v, tiles, exps, (int)Skv, (int)kv_inner, (int)d, (int)ntiles, kv_heads);
+    const dim3 pgrid((unsigned)ntiles, (unsigned)kv_heads, (unsigned)N);
+    if (d == DP && kv_inner % 4 == 0 && aligned16(k) && aligned16(v))
+        k_attn_pack<DP, true><<<pgrid, 256, 0, stream()>>>(k, v, tiles, exps, (int)Skv, (int)kv_inner, (int)d,
+                                                           (int)ntiles, kv_heads);
+    else
+        k_attn_pack<DP, false><<<pgrid, 256, 0, stream()>>>(k, v, tiles, exps, (int)Skv, (int)kv_inner, (int)d,
+                                                            (int)ntiles, kv_heads);
     launched("sdh_attention");
     const int qvec = d == DP && inner % 4 == 0 && aligned16(q) && aligned16(out);
     const dim3 grid((unsigned)((Sq + kBM - 1) / kBM), (unsigned)heads, (unsigned)N);
