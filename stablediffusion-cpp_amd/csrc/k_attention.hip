@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, 
 
 // ---------------------------------------------------------------------------
 // Fused attention, head dimension padded to DP (64 or 128).
-// grid (ceil(Sq / 256), heads, N); 512 threads = 8 waves of 32 queries.
+// 1-D grid of ceil(Sq / 256) * heads * N workgroups; 512 threads = 8 waves of 32 queries.
 // Waves 0-3 (X) and 4-7 (Y) run half a tile apart (waves w and w + 4 share a
 // SIMD): per iteration t, between two barriers,
 //   segment 1:  X: S^T(t) = K(t) Q^T          Y: softmax(t-1), O += V(t-1) P
@@ -213,7 +213,7 @@ template <int DP, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restrict__ Q, const u16* __restrict__ tiles,
                                                           const int2* __restrict__ exps, float* __restrict__ O, int Sq,
                                                           int Skv, int inner, int d, int group, int kv_heads,
-                                                          int ntiles, float c2, int qvec) {
+                                                          int ntiles, float c2, int qvec, int nqb, int heads) {
     constexpr int DS = DP / 16;                    // 16-wide head-dim steps of S^T = K Q^T
     constexpr int DT = DP / 32;                    // 32-row head-dim tiles of O^T
     constexpr int TILE = 4 * kKT * DP, HALF = TILE / 2;  // fp16 values per packed tile, per K or V part
@@ -224,8 +224,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const bool isY = w >= kWaves / 2;
     const int fr = lane & 31, fh = lane >> 5;
-    const int h = blockIdx.y, nb = blockIdx.z, kh = h / group;
-    const int q0 = blockIdx.x * kBM, qw0 = q0 + w * 32;
+    // Workgroups are dealt to the 8 XCDs round robin (id % 8). Logical blocks
+    // (query block fastest, then head, then batch) are renumbered so that each
+    // XCD runs one contiguous range of them: the query blocks of a head share
+    // one L2, which then fetches each K/V tile once instead of once per XCD.
+    const int nblk = gridDim.x, xcd = blockIdx.x & 7, per = nblk >> 3, rem = nblk & 7;
+    const int lb = xcd * per + min(xcd, rem) + (blockIdx.x >> 3);
+    const int qb = lb % nqb, h = (lb / nqb) % heads, nb = lb / (nqb * heads), kh = h / group;
+    const int q0 = qb * kBM, qw0 = q0 + w * 32;
     const int qlane = qw0 + fr;
     const int qend = min(q0 + kBM, Sq);
     const int T = CAUSAL ? min(ntiles, (qend - 1) / kKT + 1) : ntiles;
@@ -515,15 +521,16 @@ void run_mfma(const float* q, const float* k, const float* v, float* out, int64_
                                                             (int)ntiles, kv_heads);
     launched("sdh_attention");
     const int qvec = d == DP && inner % 4 == 0 && aligned16(q) && aligned16(out);
-    const dim3 grid((unsigned)((Sq + kBM - 1) / kBM), (unsigned)heads, (unsigned)N);
+    const int64_t nqb = (Sq + kBM - 1) / kBM, nblk = nqb * heads * N;
+    need(nblk < (1LL << 31), "sdh_attention", "too many query blocks for one launch");
     if (causal)
-        k_attn_fwd<DP, true><<<grid, kThreads, 0, stream()>>>(q, tiles, exps, out, (int)Sq, (int)Skv, (int)inner,
-                                                               (int)d, heads / kv_heads, kv_heads, (int)ntiles, c2,
-                                                               qvec);
+        k_attn_fwd<DP, true><<<(unsigned)nblk, kThreads, 0, stream()>>>(
+            q, tiles, exps, out, (int)Sq, (int)Skv, (int)inner, (int)d, heads / kv_heads, kv_heads, (int)ntiles, c2,
+            qvec, (int)nqb, heads);
     else
-        k_attn_fwd<DP, false><<<grid, kThreads, 0, stream()>>>(q, tiles, exps, out, (int)Sq, (int)Skv, (int)inner,
-                                                                (int)d, heads / kv_heads, kv_heads, (int)ntiles, c2,
-                                                                qvec);
+        k_attn_fwd<DP, false><<<(unsigned)nblk, kThreads, 0, stream()>>>(
+            q, tiles, exps, out, (int)Sq, (int)Skv, (int)inner, (int)d, heads / kv_heads, kv_heads, (int)ntiles, c2,
+            qvec, (int)nqb, heads);
     launched("sdh_attention");
 }
 
