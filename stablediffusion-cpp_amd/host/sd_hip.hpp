@@ -79,6 +79,11 @@ inline void rope(float* x, int64_t N, int64_t S, int64_t inner, int64_t dim, con
 inline void softmax_rows(float* x, int64_t rows, int64_t cols, float scale, bool causal) {
     detail::check(sdh_softmax_rows(x, rows, cols, scale, causal ? 1 : 0), "hip::softmax_rows");
 }
+// backend_cuda.h:57-59: q [N, Sq, heads*d]; k, v [N, Skv, kv_heads*d]; out [N, Sq, heads*d]
+inline void attention(const float* q, const float* k, const float* v, float* out, int64_t N, int64_t Sq, int64_t Skv,
+                      int heads, int kv_heads, int64_t d, bool causal) {
+    detail::check(sdh_attention(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal ? 1 : 0), "hip::attention");
+}
 // backend_cuda.h:60-61
 inline void geglu(const float* x, float* y, int64_t rows, int64_t D) {
     detail::check(sdh_geglu(x, y, rows, D), "hip::geglu");

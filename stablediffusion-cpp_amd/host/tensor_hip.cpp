@@ -425,6 +425,22 @@ Tensor linear_swiglu(const Tensor& x, const Tensor& w1, const Tensor& w3) {
     return y;
 }
 
+// tensor.cpp:776-790: the reference's shape checks and messages, device branch
+Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal, int kv_heads) {
+    if (kv_heads <= 0) kv_heads = heads;
+    const int64_t N = q.dim(0), Sq = q.dim(1), inner = q.dim(2), Skv = k.dim(1), kv_inner = k.dim(2);
+    if (inner % heads != 0 || heads % kv_heads != 0) throw std::runtime_error("attention: heads mismatch");
+    const int64_t d = inner / heads;
+    if (k.dim(0) != N || v.dim(0) != N || v.dim(1) != Skv || kv_inner != kv_heads * d || v.dim(2) != kv_inner)
+        throw std::runtime_error("attention: shape mismatch q" + q.shape_str() + " k" + k.shape_str());
+    same_device(q, k, "attention");
+    same_device(q, v, "attention");
+    need_hip(q, "attention");
+    Tensor out = Tensor::empty({N, Sq, inner}, Device::HIP);
+    sd::hip::attention(q.dptr(), k.dptr(), v.dptr(), out.dptr(), N, Sq, Skv, heads, kv_heads, d, causal);
+    return out;
+}
+
 // tensor.cpp:752 (device pointer)
 void softmax_rows_(float* x, int64_t rows, int64_t cols, float scale, bool causal) {
     sd::hip::softmax_rows(x, rows, cols, scale, causal);

@@ -111,6 +111,11 @@ Tensor linear(const Tensor& x, const Tensor& W, const Tensor* b);
 // swiglu(linear(x, w1), linear(x, w3)) in one GEMM (zimage.cpp:130)
 Tensor linear_swiglu(const Tensor& x, const Tensor& w1, const Tensor& w3);
 
+// ---- attention (tensor.h:205-212) ----
+// q [N, Sq, heads*d], k and v [N, Skv, kv_heads*d] -> [N, Sq, heads*d];
+// query head h reads key/value head h / (heads / kv_heads); kv_heads 0 = heads.
+Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal = false, int kv_heads = 0);
+
 // ---- softmax (tensor.h:236) ----
 // Same parameters as the reference; x is a DEVICE pointer here (rows x cols
 // floats inside a backend_hip block).

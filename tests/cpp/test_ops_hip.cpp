@@ -69,8 +69,66 @@ static bool throws(const std::function<void()>& f) {
     return false;
 }
 
+// test_ops.cpp:84-114: attention restated per head in double, softmax(q k^T / sqrt(d)) v
+static Tensor attention_double(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal,
+                               int kv_heads) {
+    if (kv_heads <= 0) kv_heads = heads;
+    const int64_t N = q.dim(0), Sq = q.dim(1), inner = q.dim(2), Skv = k.dim(1), d = inner / heads;
+    const int64_t kv_inner = kv_heads * d, group = heads / kv_heads;
+    const double scale = 1.0 / std::sqrt((double)(float)d);
+    Tensor o({N, Sq, inner});
+    std::vector<double> sc((size_t)Skv);
+    for (int64_t n = 0; n < N; ++n)
+        for (int h = 0; h < heads; ++h) {
+            const float* qb = q.data.data() + n * Sq * inner + h * d;
+            const float* kb = k.data.data() + n * Skv * kv_inner + (h / group) * d;
+            const float* vb = v.data.data() + n * Skv * kv_inner + (h / group) * d;
+            for (int64_t i = 0; i < Sq; ++i) {
+                double m = -1e300;
+                for (int64_t j = 0; j < Skv; ++j) {
+                    double s = 0;
+                    for (int64_t t = 0; t < d; ++t) s += (double)qb[i * inner + t] * kb[j * kv_inner + t];
+                    sc[j] = (causal && j > i) ? -1e300 : s * scale;
+                    m = std::max(m, sc[j]);
+                }
+                double sum = 0;
+                for (int64_t j = 0; j < Skv; ++j) {
+                    sc[j] = (causal && j > i) ? 0.0 : std::exp(sc[j] - m);
+                    sum += sc[j];
+                }
+                for (int64_t t = 0; t < d; ++t) {
+                    double acc = 0;
+                    for (int64_t j = 0; j < Skv; ++j) acc += sc[j] / sum * vb[j * kv_inner + t];
+                    o.data[(n * Sq + i) * inner + h * d + t] = (float)acc;
+                }
+            }
+        }
+    return o;
+}
+
 static void test_hip() {
     const Device G = Device::HIP;
+    // attention: MHA, causal, GQA, 100 tokens, 8/2 causal batch 2 (test_ops.cpp:439-451), 1e-4
+    {
+        Tensor q = randn_t({2, 9, 24}), k = randn_t({2, 9, 24}), v = randn_t({2, 9, 24});
+        hip_check_op("attention h3", attention_double(q, k, v, 3, false, 0),
+                     sdh::attention(q.to(G), k.to(G), v.to(G), 3), 1e-4);
+        hip_check_op("attention h3 causal", attention_double(q, k, v, 3, true, 0),
+                     sdh::attention(q.to(G), k.to(G), v.to(G), 3, true), 1e-4);
+        Tensor kk = randn_t({2, 9, 8}), vv = randn_t({2, 9, 8});
+        hip_check_op("attention gqa", attention_double(q, kk, vv, 3, false, 1),
+                     sdh::attention(q.to(G), kk.to(G), vv.to(G), 3, false, 1), 1e-4);
+        Tensor qb = randn_t({1, 100, 64}), kb = randn_t({1, 100, 64}), vb = randn_t({1, 100, 64});
+        hip_check_op("attention 100 tokens", attention_double(qb, kb, vb, 2, false, 0),
+                     sdh::attention(qb.to(G), kb.to(G), vb.to(G), 2), 1e-4);
+        Tensor q8 = randn_t({2, 37, 8 * 16}), k2 = randn_t({2, 37, 2 * 16}), v2 = randn_t({2, 37, 2 * 16});
+        hip_check_op("attention gqa 8/2 causal", attention_double(q8, k2, v2, 8, true, 2),
+                     sdh::attention(q8.to(G), k2.to(G), v2.to(G), 8, true, 2), 1e-4);
+        int bad = 0;
+        bad += !throws([&] { sdh::attention(q.to(G), kk.to(G), vv.to(G), 3, false, 2); });  // tensor.cpp:779
+        bad += !throws([&] { sdh::attention(q.to(G), qb.to(G), qb.to(G), 3); });            // tensor.cpp:781-782
+        check("attention shape errors throw", (double)bad, 0.0);
+    }
     // round trip (test_ops.cpp:365-368)
     {
         Tensor x = randn_t({3, 70});
