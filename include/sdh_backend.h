@@ -88,6 +88,16 @@ int sdh_unregister_external(void* p);
  * handed out to live blocks). */
 int sdh_memory_stats(size_t* reserved, size_t* in_use);
 
+/* ---- GEMM with fp32 weights --------------------------------------------- */
+/* backend_cuda.h:38-40 gemm_nt_f32(): C[M,N] = A[M,K] * B[N,K]^T (+ C when
+ * accumulate) (+ bias[N]), all fp32, row-major with leading dimensions in
+ * elements; bias may be NULL. The linear layers whose weights stay fp32. */
+int sdh_gemm_nt_f32(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B, int64_t ldb,
+                    float* C, int64_t ldc, const float* bias, int accumulate);
+/* Tensor::to_bf16 (tensor.cpp:131-137) on device memory: y[i] = bf16 bits of
+ * x[i] (nearest even; inf and NaN keep their top 16 bits). */
+int sdh_to_bf16(const float* x, uint16_t* y, int64_t n);
+
 /* ---- GEMM (MFMA) ------------------------------------------------------- */
 /* backend_cuda.h:41-43 gemm_nt_bf16(): C[M,N] = A[M,K] * B[N,K]^T (+ C when
  * accumulate) (+ bias[N]); row-major with leading dimensions in elements; A

@@ -303,6 +303,20 @@ class Oracle:
                 acc = acc + bb[None, :]
         return acc.astype(np.float32), np.abs(a) @ np.abs(b).T
 
+    def gemm_nt_f32(self, A, B, bias=None, C=None, accumulate=False):
+        """C = A B^T (+ C) (+ bias) with fp32 operands, summed exactly
+        (float64): the reference's fp32 linear (tensor.cpp:354-406,
+        backend_cuda.cu:453-464) differs from this only by its fp32 sums.
+        Returns (C, S), S = sum_k |a_k b_k| per element."""
+        a = np.asarray(A, np.float32).astype(np.float64)
+        b = np.asarray(B, np.float32).astype(np.float64)
+        acc = a @ b.T
+        if accumulate:
+            acc = np.asarray(C, np.float64) + acc
+        if bias is not None:
+            acc = acc + np.asarray(bias, np.float64)[None, :]
+        return acc.astype(np.float32), np.abs(a) @ np.abs(b).T
+
     def linear_swiglu(self, x, w1_16, w3_16):
         """y = swiglu(x w1^T, x w3^T) with exact products, plus the exact g,
         u and their accumulation scales (for the test's error bound)."""
@@ -613,14 +627,16 @@ class Reference:
         finally:
             self.free(h)
 
-    def linear(self, x, W, b=None):
-        """The reference's CPU linear with W converted to BF16 (tensor.cpp:496-497):
-        x stays fp32 there, W is rounded to bf16, products summed in fp32."""
+    def linear(self, x, W, b=None, bf16=True):
+        """The reference's CPU linear. bf16: W converted to BF16 first
+        (tensor.cpp:496-497: x stays fp32, W is rounded to bf16, products
+        summed in fp32); otherwise the fp32 path (tensor.cpp:498, :354-406)."""
         x, W = _f32(x), _f32(W)
         hx, hw = self.new(x.shape, x), self.new(W.shape, W)
         hb = self.new(b.shape, b) if b is not None else None
         try:
-            self._chk(self.lib.ref_tensor_to_bf16(hw))
+            if bf16:
+                self._chk(self.lib.ref_tensor_to_bf16(hw))
             h = self._ptr(self.lib.ref_linear(hx, hw, hb))
         finally:
             self.free(hx, hw, hb)

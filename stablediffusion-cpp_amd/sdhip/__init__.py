@@ -81,6 +81,8 @@ SIGNATURES = {
     "sdh_add_rows": [_vp, _vp, _i64, _i64],
     "sdh_gemm_nt_bf16": [_i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, C.c_int],
     "sdh_linear_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _i64],
+    "sdh_gemm_nt_f32": [_i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, C.c_int],
+    "sdh_to_bf16": [_vp, _vp, _i64],
     "sdh_attention": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
     "sdh_upsample_nearest2x": [_vp, _vp, _i64, _i64, _i64],
     "sdh_concat_channels": [_vp, _vp, _vp, _i64, _i64, _i64, _i64],
@@ -320,6 +322,12 @@ class Backend:
     # GEMM (bf16 weights held in DArray buffers of uint16)
     def gemm_nt_bf16(self, M, N, K, A, lda, B, ldb, Cm, ldc, bias=None, accumulate=False):
         self.call("sdh_gemm_nt_bf16", M, N, K, _p(A), lda, _p(B), ldb, _p(Cm), ldc, _p(bias), 1 if accumulate else 0)
+
+    def gemm_nt_f32(self, M, N, K, A, lda, B, ldb, C, ldc, bias=None, accumulate=False):
+        self.call("sdh_gemm_nt_f32", M, N, K, _p(A), lda, _p(B), ldb, _p(C), ldc, _p(bias), int(bool(accumulate)))
+
+    def to_bf16(self, x, y, n):
+        self.call("sdh_to_bf16", _p(x), _p(y), n)
 
     def linear_swiglu(self, x, w1, w3, y, rows, inn, hidden):
         self.call("sdh_linear_swiglu", _p(x), _p(w1), _p(w3), _p(y), rows, inn, hidden)

@@ -129,3 +129,45 @@ def test_gemm_invalid_arguments(be):
     with pytest.raises(sdhip.SdhError) as e:
         be.gemm_nt_bf16(5, 4, 8, a, 8, w, 8, c, 4)  # A has 4 rows, not 5
     assert e.value.status == sdhip.SDH_ERR_INVALID
+
+
+@pytest.mark.parametrize("M,N,K,lda,with_bias,acc", [
+    (5, 7, 16, 16, False, False), (70, 130, 64, 64, True, False), (4096, 64, 3840, 3840, True, False),
+    (129, 3840, 64, 64, True, True), (9, 33, 13, 13, True, False), (65, 64, 100, 104, False, True),
+    (1, 1024, 256, 256, True, False),
+])
+def test_gemm_nt_f32(be, orc, M, N, K, lda, with_bias, acc):
+    """The fp32-weight linear (sdh_gemm_nt_f32) against the exact sum, within
+    the fp32 accumulation bound; the Z-Image final projection [4096,3840] x
+    [64,3840]^T and patch embedding [*, 64] x [3840, 64]^T shapes; K not a
+    multiple of 4 (scalar loads), padded rows, accumulate and bias."""
+    A = orc.randn((M, lda), 600 + M + K)
+    W = orc.randn((N, K), 601 + N, 0.0, 0.05)
+    b = orc.randn((N,), 602, 0.0, 0.5) if with_bias else None
+    c0 = orc.randn((M, N), 603) if acc else None
+    dC = be.array(c0) if acc else be.empty((M, N))
+    be.gemm_nt_f32(M, N, K, be.array(A), lda, be.array(W), K, dC, N, be.array(b) if with_bias else None, acc)
+    want, S = orc.gemm_nt_f32(A[:, :K], W, b, c0, acc)
+    S = S + (np.abs(b)[None, :] if with_bias else 0) + (np.abs(c0) if acc else 0)
+    assert_gemm(dC.download(), want, S, K + 2, f"gemm_f32 {M}x{N}x{K}")
+
+
+def test_gemm_f32_matches_reference_linear(be, orc, ref):
+    """test_ops.cpp:370-375: linear with fp32 weights and bias, x [2,37,300],
+    W [130,300], against the reference's CPU path, max-abs 1e-3."""
+    x = orc.randn((2, 37, 300), 610)
+    W = orc.randn((130, 300), 611)
+    b = orc.randn((130,), 612)
+    cpu = ref.linear(x, W, b, bf16=False)
+    dC = be.empty((74, 130))
+    be.gemm_nt_f32(74, 130, 300, be.array(x), 300, be.array(W), 300, dC, 130, be.array(b))
+    assert float(np.max(np.abs(dC.download().reshape(2, 37, 130) - cpu))) <= 1e-3
+
+
+def test_to_bf16_device(be, orc):
+    x = np.concatenate([orc.randn((5000,), 620, 0.0, 3.0), orc.randn((300,), 621, 0.0, 1e-30),
+                        np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, 3.3895314e38, np.finfo(np.float32).max],
+                                 np.float32)])
+    y = be.array(np.zeros(x.size, np.uint16))
+    be.to_bf16(be.array(x), y, x.size)
+    assert np.array_equal(y.download(), f32_to_bf16(x))

@@ -12,6 +12,8 @@ an exact (float64) sum. It is pinned by:
     sums within the fp32 accumulation bound; with and without bias;
   * planted mistakes: A not rounded to bf16, bias broadcast along the wrong
     axis.
+The fp32-weight linear (Oracle.gemm_nt_f32) is pinned the same way against the
+reference's fp32 CPU path (tensor.cpp:354-406, :498).
 """
 import numpy as np
 import pytest
@@ -105,3 +107,16 @@ def test_gemm_pins_catch_planted_mistakes(orc, ref, which, pin):
             pin(orc, ref)
     finally:
         orc.plant(0)
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 7, 16), (70, 130, 64), (9, 64, 200), (1, 256, 33)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_gemm_f32_oracle_vs_reference_linear(orc, ref, M, N, K, with_bias):
+    a = orc.randn((M, K), 41 + K)
+    w = orc.randn((N, K), 42 + N, 0.0, 0.05)
+    b = orc.randn((N,), 43, 0.0, 0.1) if with_bias else None
+    want, S = orc.gemm_nt_f32(a, w, b)
+    got = ref.linear(a, w, b, bf16=False)
+    assert np.all(np.abs(got - want) <= fp32_sum_bound(S + (np.abs(b)[None, :] if with_bias else 0), K + 1) + 1e-30)
+    # and the bf16 path differs from it: the pin tells the two apart
+    assert float(np.max(np.abs(ref.linear(a, w, b) - want))) > 1e-4
