@@ -362,6 +362,145 @@ class Oracle:
         o = np.matmul(p, vh)
         return o.transpose(0, 2, 1, 3).reshape(N, len(rows), inner).astype(np.float32)
 
+    # -- the Z-Image transformer (zimage.cpp:71-228) --
+    def zimage_forward(self, weights, x, t, cap, heads, bf16_names=(), act_bf16=False, patch=2, eps=1e-5,
+                       theta=256.0, t_scale=1000.0, axes=(32, 48, 48)):
+        """float64 restatement of ZImageTransformer::forward. `weights` maps
+        checkpoint names to float32 arrays (the values the loader produces);
+        `bf16_names` are the weights held in BF16. With act_bf16 the input of
+        every linear with a BF16 weight is rounded to bf16 first, as the
+        device path does (backend_cuda.cu:466-479); without it the inputs stay
+        exact, as the reference's CPU path keeps them fp32 (tensor.cpp:496-497).
+        x [1, C, H, W], cap [1, L, cap_dim] -> [1, C, H, W]."""
+        plant = getattr(self, "_plant_py", 0)
+        f64 = np.float64
+        Wd = {k: np.asarray(v, np.float32).astype(f64) for k, v in weights.items()}
+        bf = set(bf16_names)
+
+        def lin(name, h):  # modules.h:23-30, tensor.cpp:481-500
+            if act_bf16 and name + ".weight" in bf:
+                h = bf16_to_f32(f32_to_bf16(h.astype(np.float32))).astype(f64)
+            y = h @ Wd[name + ".weight"].T
+            b = Wd.get(name + ".bias")
+            return y if b is None else y + b
+
+        def rms(h, g, e):  # tensor.cpp:660-679
+            return h / np.sqrt((h * h).mean(-1, keepdims=True) + e) * (Wd[g] if g else 1.0)
+
+        def silu(h):
+            return h / (1.0 + np.exp(-h))
+
+        D = Wd["all_x_embedder.2-1.weight"].shape[0]
+        hd = D // heads
+        p = patch
+        # 1. timestep embedding (zimage.cpp:148-163), the sinusoid in float as there
+        F = Wd["t_embedder.mlp.0.weight"].shape[1]
+        half = F // 2
+        tt = np.float32(t) * np.float32(t_scale)
+        fr = np.exp(-np.log(np.float32(10000.0)) * np.arange(half, dtype=np.float32) / np.float32(half)).astype(np.float32)
+        freq = np.concatenate([np.cos(tt * fr), np.sin(tt * fr)]).astype(np.float32).astype(f64)[None, :]
+        adaln = lin("t_embedder.mlp.2", silu(lin("t_embedder.mlp.0", freq)))
+        # 2. image tokens: features ordered (ph, pw, c) (tensor.cpp:931-954)
+        _, Cc, H, W = x.shape
+        Ht, Wt = H // p, W // p
+        tok = np.asarray(x, f64)[0].reshape(Cc, Ht, p, Wt, p).transpose(1, 3, 2, 4, 0).reshape(Ht * Wt, p * p * Cc)
+        n_img = Ht * Wt
+        pad32 = lambda n: (n + 31) // 32 * 32
+        n_img_pad = pad32(n_img)
+        img = lin("all_x_embedder.2-1", tok)
+        img = np.concatenate([img, np.repeat(Wd["x_pad_token"].reshape(1, D), n_img_pad - n_img, 0)])
+        # 3. text tokens
+        n_cap = cap.shape[1]
+        n_cap_pad = pad32(n_cap)
+        ct = lin("cap_embedder.1", rms(np.asarray(cap, f64)[0], "cap_embedder.0.weight", eps))
+        ct = np.concatenate([ct, np.repeat(Wd["cap_pad_token"].reshape(1, D), n_cap_pad - n_cap, 0)])
+        # rotary positions (zimage.cpp:177-191) and tables (zimage.cpp:71-88, float angles)
+        cap_pos = [(1 + i, 0, 0) for i in range(n_cap_pad)]
+        img_pos = [(0, 0, 0)] * n_img_pad
+        for hh in range(Ht):
+            for ww in range(Wt):
+                img_pos[hh * Wt + ww] = (n_cap_pad + 1, hh, ww) if plant != 13 else (n_cap_pad + 1, ww, hh)
+
+        def tables(pos):
+            cs = np.zeros((len(pos), hd), np.float32)
+            sn = np.zeros((len(pos), hd), np.float32)
+            off = 0
+            for a in range(3):
+                da = axes[a]
+                fq = 1.0 / np.power(float(theta), (2.0 * np.arange(da // 2)) / da)
+                for si, ps in enumerate(pos):
+                    ang = (ps[a] * fq).astype(np.float32)
+                    cs[si, off:off + da:2] = cs[si, off + 1:off + da:2] = np.cos(ang)
+                    sn[si, off:off + da:2] = sn[si, off + 1:off + da:2] = np.sin(ang)
+                off += da
+            return cs.astype(f64), sn.astype(f64)
+
+        def rope(h, cs, sn):  # interleaved pairs (tensor.cpp:698-730)
+            S = h.shape[0]
+            r = h.reshape(S, heads, hd // 2, 2)
+            c = cs[:, 0::2][:, None, :]
+            s_ = sn[:, 0::2][:, None, :]
+            a, b = r[..., 0], r[..., 1]
+            return np.stack([a * c - b * s_, b * c + a * s_], -1).reshape(S, D)
+
+        def heads_norm(h, g):  # rms_norm_heads_ (tensor.cpp:681-696), eps 1e-5 (zimage.cpp:117-118)
+            S = h.shape[0]
+            r = h.reshape(S, heads, hd)
+            return (r / np.sqrt((r * r).mean(-1, keepdims=True) + 1e-5) * Wd[g]).reshape(S, D)
+
+        def block(pre, xs, cs, sn, modulated):  # zimage.cpp:90-136
+            if modulated:
+                m = lin(pre + ".adaLN_modulation.0", adaln).reshape(4, D)
+                s_msa, g_msa, s_mlp, g_mlp = 1.0 + m[0], np.tanh(m[1]), 1.0 + m[2], np.tanh(m[3])
+                if plant == 14:
+                    s_msa, g_msa = g_msa, s_msa
+            h = rms(xs, pre + ".attention_norm1.weight", eps)
+            if modulated:
+                h = h * s_msa
+            q = rope(heads_norm(lin(pre + ".attention.to_q", h), pre + ".attention.norm_q.weight"), cs, sn)
+            k = rope(heads_norm(lin(pre + ".attention.to_k", h), pre + ".attention.norm_k.weight"), cs, sn)
+            v = lin(pre + ".attention.to_v", h)
+            S = xs.shape[0]
+            qh = q.reshape(S, heads, hd).transpose(1, 0, 2)
+            kh = k.reshape(S, heads, hd).transpose(1, 0, 2)
+            vh = v.reshape(S, heads, hd).transpose(1, 0, 2)
+            sc = qh @ kh.transpose(0, 2, 1) * float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+            sc = np.exp(sc - sc.max(-1, keepdims=True))
+            att = ((sc / sc.sum(-1, keepdims=True)) @ vh).transpose(1, 0, 2).reshape(S, D)
+            a = rms(lin(pre + ".attention.to_out.0", att), pre + ".attention_norm2.weight", eps)
+            xs = xs + (g_msa * a if modulated else a)
+            h = rms(xs, pre + ".ffn_norm1.weight", eps)
+            if modulated:
+                h = h * s_mlp
+            g, u = lin(pre + ".feed_forward.w1", h), lin(pre + ".feed_forward.w3", h)
+            f = rms(lin(pre + ".feed_forward.w2", silu(g) * u), pre + ".ffn_norm2.weight", eps)
+            return xs + (g_mlp * f if modulated else f)
+
+        def count(prefix):
+            i = 0
+            while f"{prefix}.{i}.attention_norm1.weight" in Wd:
+                i += 1
+            return i
+
+        ic, is_ = tables(img_pos)
+        for i in range(count("noise_refiner")):
+            img = block(f"noise_refiner.{i}", img, ic, is_, True)
+        cc, cs_ = tables(cap_pos)
+        for i in range(count("context_refiner")):
+            ct = block(f"context_refiner.{i}", ct, cc, cs_, False)
+        uni = np.concatenate([img, ct])
+        uc, us = tables(img_pos + cap_pos)
+        for i in range(count("layers")):
+            uni = block(f"layers.{i}", uni, uc, us, True)
+        # 5. final layer (zimage.cpp:218-227): LayerNorm without affine, eps 1e-6
+        io = uni[:n_img]
+        scale = 1.0 + lin("all_final_layer.2-1.adaLN_modulation.1", silu(adaln))
+        mu = io.mean(-1, keepdims=True)
+        io = (io - mu) / np.sqrt(((io - mu) ** 2).mean(-1, keepdims=True) + 1e-6) * scale
+        ot = lin("all_final_layer.2-1.linear", io)
+        out = ot.reshape(Ht, Wt, p, p, Cc).transpose(4, 0, 2, 1, 3).reshape(1, Cc, H, W)
+        return out.astype(np.float32)
+
     # -- layout (tensor.cpp:931-1099) --
     def upsample_nearest2x(self, x):
         x = _f32(x)
@@ -446,6 +585,8 @@ class Reference:
             "ref_tensor_data16": (C.POINTER(C.c_uint16), [_vp]),
             "ref_linear": (_vp, [_vp, _vp, _vp]),
             "ref_attention": (_vp, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
+            "ref_zimage_forward": (C.c_int, [C.c_char_p, C.c_int, _i64, C.c_int, _f32p, _i64, _i64, _i64, _fl, _f32p,
+                                             _i64, _i64, _f32p]),
             "ref_patchify2d": (_vp, [_vp, C.c_int]),
             "ref_unpatchify2d": (_vp, [_vp, _i64, _i64, _i64, C.c_int]),
             "ref_slice_rows": (_vp, [_vp, _i64, _i64]),
@@ -652,6 +793,16 @@ class Reference:
         finally:
             self.free(hq, hk, hv)
         return self.take(h, q.shape)
+
+    def zimage_forward(self, path, x, t, cap, heads, keep_bf16=True, bf16_min_numel=1 << 20):
+        """The reference's ZImageTransformer::forward on the CPU (zimage.cpp:
+        138-228) with weights loaded by its own Weights::load_safetensors."""
+        x, cap = _f32(x), _f32(cap)
+        out = np.empty_like(x)
+        self._chk(self.lib.ref_zimage_forward(str(path).encode(), int(bool(keep_bf16)), int(bf16_min_numel), int(heads),
+                                              x, x.shape[1], x.shape[2], x.shape[3], float(t), cap, cap.shape[1],
+                                              cap.shape[2], out))
+        return out
 
     # -- layout --
     def _new_op(self, fn, inputs, out_shape, *args):

@@ -14,6 +14,7 @@
 #include <string>
 
 #include "tensor.h"
+#include "zimage.h"
 
 using sd::Tensor;
 
@@ -105,6 +106,25 @@ void* ref_linear(void* x, void* W, void* b) { return guard_ptr([&] { return wrap
 // ---- attention (new tensor) ----
 void* ref_attention(void* q, void* k, void* v, int heads, int causal, int kv_heads) {
     return guard_ptr([&] { return wrap(sd::attention(*T(q), *T(k), *T(v), heads, causal != 0, kv_heads)); });
+}
+
+// ---- the Z-Image transformer, one forward on the CPU (zimage.cpp:138-228) ----
+// Weights from a .safetensors file as Weights::load_safetensors(path, keep_bf16,
+// bf16_min_numel) loads them; x [1, C, H, W], cap [1, L, cap_dim]; out [1, C, H, W].
+int ref_zimage_forward(const char* path, int keep_bf16, int64_t bf16_min_numel, int heads, const float* x, int64_t C,
+                       int64_t H, int64_t W, float t, const float* cap, int64_t L, int64_t cap_dim, float* out) {
+    return guard([&] {
+        sd::Weights w;
+        w.load_safetensors(path, keep_bf16 != 0, bf16_min_numel);
+        sd::ZImageTransformer::Config cfg;
+        cfg.heads = heads;
+        sd::ZImageTransformer m(w, cfg);
+        Tensor xt({1, C, H, W}), ct({1, L, cap_dim});
+        std::memcpy(xt.ptr(), x, (size_t)xt.numel() * sizeof(float));
+        std::memcpy(ct.ptr(), cap, (size_t)ct.numel() * sizeof(float));
+        Tensor y = m.forward(xt, t, ct);
+        std::memcpy(out, y.ptr(), (size_t)y.numel() * sizeof(float));
+    });
 }
 
 // ---- layout ops (new tensors) ----

@@ -10,8 +10,8 @@
 // backend reports failures (check()/launched(), backend_cuda.cu:41-48, and the
 // stub's throw, backend_cuda_stub.cpp:14).
 //
-// conv2d and attention stay with their existing implementations; they are
-// not part of this backend (GEMM is, for BF16 weights: gemm_nt_bf16).
+// conv2d stays with its existing implementation; the GEMMs (gemm_nt_bf16,
+// gemm_nt_f32) and attention are part of this backend.
 #pragma once
 
 #include <cstddef>
@@ -48,6 +48,10 @@ inline void download(void* dst, const void* src, size_t bytes) {
 }
 inline void copy(void* dst, const void* src, size_t bytes) { detail::check(sdh_copy(dst, src, bytes), "hip::copy"); }
 inline void zero(void* dst, size_t bytes) { detail::check(sdh_zero(dst, bytes), "hip::zero"); }
+// Additive: seeded N(mean, std) fill of device memory (the library's generator).
+inline void fill_normal(float* x, int64_t n, uint64_t seed, float mean, float std) {
+    detail::check(sdh_fill_normal(x, n, seed, mean, std), "hip::fill_normal");
+}
 inline void synchronize() { detail::check(sdh_synchronize(), "hip::synchronize"); }
 
 // backend_cuda.h:41-43
@@ -145,6 +149,11 @@ inline void qknorm_rope(float* q, int64_t inner_q, float* k, int64_t inner_k, in
     detail::check(sdh_qknorm_rope(q, inner_q, k, inner_k, N, S, dim, gamma_q, gamma_k, eps, cos, sin, interleaved ? 1 : 0),
                   "hip::qknorm_rope");
 }
+inline void gemm_nt_f32(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B, int64_t ldb,
+                        float* C, int64_t ldc, const float* bias, bool accumulate) {
+    detail::check(sdh_gemm_nt_f32(M, N, K, A, lda, B, ldb, C, ldc, bias, accumulate ? 1 : 0), "hip::gemm_nt_f32");
+}
+inline void to_bf16(const float* x, uint16_t* y, int64_t n) { detail::check(sdh_to_bf16(x, y, n), "hip::to_bf16"); }
 inline void linear_swiglu(const float* x, const uint16_t* w1, const uint16_t* w3, float* y, int64_t rows, int64_t in,
                           int64_t hidden) {
     detail::check(sdh_linear_swiglu(x, w1, w3, y, rows, in, hidden), "hip::linear_swiglu");

@@ -394,7 +394,7 @@ Tensor repeat_batch(const Tensor& x, int64_t times) {
 
 // ---- linear ------------------------------------------------------------------
 
-// tensor.cpp:481-494, device branch with BF16 weights
+// tensor.cpp:481-494, device branch: BF16 weights on the MFMA GEMM, F32 weights on the fp32 GEMM
 Tensor linear(const Tensor& x, const Tensor& W, const Tensor* b) {
     const int64_t in = x.dim(-1), out = W.dim(0);
     if (W.dim(1) != in) throw std::runtime_error("linear: input dim " + x.shape_str() + " vs weight " + W.shape_str());
@@ -403,10 +403,12 @@ Tensor linear(const Tensor& x, const Tensor& W, const Tensor* b) {
     oshape.back() = out;
     same_device(x, W, "linear");
     need_hip(x, "linear");
-    if (!W.is_bf16()) throw std::runtime_error("linear: F32 weights; backend_hip takes BF16 weights (the tensor-core path)");
     if (b) same_device(x, *b, "linear");
     Tensor y = Tensor::empty(oshape, Device::HIP);
-    sd::hip::gemm_nt_bf16(rows, out, in, x.dptr(), in, W.dptr16(), in, y.dptr(), out, opt(b), false);
+    if (W.is_bf16())
+        sd::hip::gemm_nt_bf16(rows, out, in, x.dptr(), in, W.dptr16(), in, y.dptr(), out, opt(b), false);
+    else
+        sd::hip::gemm_nt_f32(rows, out, in, x.dptr(), in, W.dptr(), in, y.dptr(), out, opt(b), false);
     return y;
 }
 

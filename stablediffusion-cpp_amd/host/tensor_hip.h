@@ -104,9 +104,10 @@ Tensor nlc_to_nchw(const Tensor& x, int64_t H, int64_t W);
 Tensor slice_batch(const Tensor& x, int64_t b);
 Tensor repeat_batch(const Tensor& x, int64_t times);
 
-// ---- linear (tensor.h:146): y = x W^T (+ b) with BF16 weights W [out, in] ----
-// The reference's device branch (tensor.cpp:489-494): x is rounded to bf16,
-// products accumulate in fp32. F32 weights are outside this backend.
+// ---- linear (tensor.h:146): y = x W^T (+ b), W [out, in] ----
+// The reference's device branch (tensor.cpp:489-494): with BF16 weights x is
+// rounded to bf16 and products accumulate in fp32 (MFMA); F32 weights take
+// the fp32 GEMM.
 Tensor linear(const Tensor& x, const Tensor& W, const Tensor* b);
 // swiglu(linear(x, w1), linear(x, w3)) in one GEMM (zimage.cpp:130)
 Tensor linear_swiglu(const Tensor& x, const Tensor& w1, const Tensor& w3);

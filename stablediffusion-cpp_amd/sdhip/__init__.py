@@ -356,3 +356,91 @@ class Backend:
 
     def ln_modulate_gate(self, x, res, scale, shift, gate, y_out, rows, Cc, eps):
         self.call("sdh_ln_modulate_gate", _p(x), _p(res), _p(scale), _p(shift), _p(gate), _p(y_out), rows, Cc, eps)
+
+
+# ---------------------------------------------------------------- the Z-Image transformer
+TENSOR_LIB_PATH = os.path.join(PKG_DIR, "libsdh_tensor.so")
+_MODEL_SIGNATURES = {
+    "sdhm_zimage_load": ([C.c_char_p, _int, _i64, _int, C.POINTER(C.c_void_p)], _int),
+    "sdhm_zimage_random": ([_i64, _int, _i64, _i64, _i64, _i64, _i64, _int, _int, _int, C.c_uint64,
+                            C.POINTER(C.c_void_p)], _int),
+    "sdhm_zimage_forward": ([C.c_void_p, _vp, _i64, _i64, _i64, _fl, _vp, _i64, _i64, _vp], _int),
+    "sdhm_zimage_time": ([C.c_void_p, _i64, _i64, _i64, _i64, _int, _int, C.POINTER(C.c_double)], _int),
+    "sdhm_zimage_params": ([C.c_void_p], _i64),
+    "sdhm_zimage_free": ([C.c_void_p], None),
+    "sdhm_last_error": ([], C.c_char_p),
+}
+_tensor_lib = None
+
+
+def _model_lib():
+    """libsdh_tensor.so (the C++ host library: tensor.h API, weights loader,
+    Z-Image transformer); it runs on the same libsdh.so as Backend."""
+    global _tensor_lib
+    if _tensor_lib is None:
+        if not os.path.exists(TENSOR_LIB_PATH):
+            raise FileNotFoundError(f"{TENSOR_LIB_PATH} is not built; run __graft_entry__.build()")
+        lib = C.CDLL(TENSOR_LIB_PATH)
+        for name, (args, res) in _MODEL_SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _tensor_lib = lib
+    return _tensor_lib
+
+
+class ZImage:
+    """ZImageTransformer (src/zimage.h:40-79) on the device: one denoising step
+    per forward(). Load it from a .safetensors checkpoint, or build one of given
+    shapes with seeded random weights (benchmarks)."""
+
+    def __init__(self, handle):
+        self.h = handle
+
+    @staticmethod
+    def _check(rc):
+        if rc != 0:
+            raise SdhError(SDH_ERR_INVALID, _model_lib().sdhm_last_error().decode())
+
+    @classmethod
+    def load(cls, path, heads=30, keep_bf16=True, bf16_min_numel=1 << 20):
+        h = C.c_void_p()
+        cls._check(_model_lib().sdhm_zimage_load(str(path).encode(), int(bool(keep_bf16)), int(bf16_min_numel),
+                                                 int(heads), C.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def random(cls, dim=3840, heads=30, ffn=10240, in_channels=16, cap_dim=2560, t_hidden=1024, adaln_dim=256,
+               noise_refiners=2, context_refiners=2, layers=30, seed=0):
+        h = C.c_void_p()
+        cls._check(_model_lib().sdhm_zimage_random(dim, heads, ffn, in_channels, cap_dim, t_hidden, adaln_dim,
+                                                   noise_refiners, context_refiners, layers, seed, C.byref(h)))
+        return cls(h)
+
+    def forward(self, x, t, cap):
+        x = np.ascontiguousarray(x, np.float32)
+        cap = np.ascontiguousarray(cap, np.float32)
+        out = np.empty_like(x)
+        self._check(_model_lib().sdhm_zimage_forward(self.h, x.ctypes.data, x.shape[1], x.shape[2], x.shape[3],
+                                                     float(t), cap.ctypes.data, cap.shape[1], cap.shape[2],
+                                                     out.ctypes.data))
+        return out
+
+    def time(self, H, W, L, cap_dim, steps, warmup):
+        ms = C.c_double()
+        self._check(_model_lib().sdhm_zimage_time(self.h, H, W, L, cap_dim, steps, warmup, C.byref(ms)))
+        return ms.value
+
+    def params(self):
+        return int(_model_lib().sdhm_zimage_params(self.h))
+
+    def close(self):
+        if self.h:
+            _model_lib().sdhm_zimage_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

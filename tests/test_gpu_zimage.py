@@ -1,0 +1,87 @@
+"""The Z-Image transformer forward on the device (stablediffusion-cpp_amd/host/
+zimage_hip.cpp through libsdh_tensor.so), on a small model of the checkpoint's
+names and layout (tests/zimage_model.py) loaded from a .safetensors file.
+
+Bars:
+  * F32 weights (no bf16 anywhere): against the reference's own CPU forward
+    (compiled, oracle/_ref), relative RMS 1e-5 (measured 7e-7). This pins the
+    composition: every op, its order, the positions and the modulation.
+  * BF16 weights: against the reference's CPU forward, relative RMS 2e-2, the
+    reference's bar for its device path (test_zimage.cpp:74-77; measured
+    2.5e-3). The device rounds the inputs of BF16-weight linears to bf16
+    (backend_cuda.cu:466-479) and the CPU path does not.
+  * BF16 weights against the float64 oracle with the same rounding: rounding
+    to bf16 is discontinuous, so values that differ by fp32 ulps flip a few
+    roundings and the random network spreads them; the oracle moves by about
+    1.6e-3 when its own input is jittered by 1e-7. The device must stay within
+    3x that floor, measured in the test.
+Two latent sizes (one with image pad tokens), two timesteps.
+"""
+import numpy as np
+import pytest
+
+import zimage_model as zm
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def model(tmp_path_factory):
+    W = zm.make_weights(0)
+    path = tmp_path_factory.mktemp("zimage") / "model.safetensors"
+    zm.write_safetensors(path, W)
+    return W, path
+
+
+CASES = [(16, 16, 20, 0.3), (24, 20, 40, 0.9)]
+
+
+@pytest.mark.parametrize("H,W,L,t", CASES)
+def test_zimage_forward_bf16_weights(be, orc, model, H, W, L, t):
+    import sdhip
+
+    Wt, path = model
+    x, cap = zm.inputs(orc, H=H, W=W, L=L)
+    m = sdhip.ZImage.load(path, heads=zm.SHAPES["heads"], keep_bf16=True, bf16_min_numel=zm.BF16_MIN)
+    try:
+        got = m.forward(x, t, cap)
+    finally:
+        m.close()
+    names = zm.bf16_names(Wt)
+    want = orc.zimage_forward(Wt, x, t, cap, zm.SHAPES["heads"], names, act_bf16=True)
+    jit = (x * (1 + 1e-7 * np.random.default_rng(5).standard_normal(x.shape))).astype(np.float32)
+    floor = zm.rel_rms(orc.zimage_forward(Wt, jit, t, cap, zm.SHAPES["heads"], names, act_bf16=True), want)
+    e = zm.rel_rms(got, want)
+    print(f"{H}x{W} L{L}: relative RMS vs oracle (device numerics) {e:.3g}; oracle under 1e-7 jitter {floor:.3g}")
+    assert e <= 3 * floor
+
+
+@pytest.mark.parametrize("H,W,L,t", CASES)
+def test_zimage_forward_vs_reference_cpu(be, orc, ref, model, H, W, L, t):
+    import sdhip
+
+    _, path = model
+    x, cap = zm.inputs(orc, H=H, W=W, L=L)
+    for keep_bf16, bar in ((True, 2e-2), (False, 1e-5)):
+        m = sdhip.ZImage.load(path, heads=zm.SHAPES["heads"], keep_bf16=keep_bf16, bf16_min_numel=zm.BF16_MIN)
+        try:
+            got = m.forward(x, t, cap)
+        finally:
+            m.close()
+        want = ref.zimage_forward(path, x, t, cap, zm.SHAPES["heads"], keep_bf16, zm.BF16_MIN)
+        e = zm.rel_rms(got, want)
+        print(f"{H}x{W} L{L} keep_bf16={keep_bf16}: relative RMS vs the reference CPU forward {e:.3g}")
+        assert e <= bar
+
+
+def test_zimage_load_errors(be, tmp_path):
+    import sdhip
+
+    bad = tmp_path / "bad.safetensors"
+    bad.write_bytes(b"\x10\x00\x00\x00\x00\x00\x00\x00{not json at all")
+    with pytest.raises(sdhip.SdhError):
+        sdhip.ZImage.load(bad, heads=2)
+    empty = tmp_path / "empty.safetensors"
+    zm.write_safetensors(empty, {"x_pad_token": np.zeros((1, 4), np.float32)})
+    with pytest.raises(sdhip.SdhError, match="missing weight"):
+        sdhip.ZImage.load(empty, heads=2)
