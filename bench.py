@@ -445,6 +445,46 @@ class Attention(Workload):
         return (lambda: [R._ptr(R.lib.ref_attention(hq, hk, hv, 1, 0, 1))]), [hq, hk, hv]
 
 
+class ZImageStep(Workload):
+    """One denoising step of the Z-Image transformer (ZImageTransformer::forward,
+    zimage.cpp:138-228) on the device at 1024x1024: latent [1,16,128,128] ->
+    4096 image tokens, 128 text tokens of 2560 features, 2 noise and 2 context
+    refiner blocks, 30 main blocks of dim 3840 (30 heads x 128, FFN 10240),
+    weights seeded random with the checkpoint's shapes (BF16 from 2^20
+    elements, as pipeline.cpp:113 loads them). Rated in TFLOP/s over the
+    linear layers and attention (2 flop per multiply-add)."""
+
+    name, kernel = "zimage_step_1024", "k_gemm_dl"
+    H = W = 128
+    L, cap_dim = 128, 2560
+    D, F, heads, layers = 3840, 10240, 30, 30
+    algo_bytes = 0
+    cpu = None
+    desc = "Z-Image DiT step at 1024x1024 (4096 image + 128 text tokens, 30+4 blocks, dim 3840), random BF16 weights"
+
+    @property
+    def flops(self):
+        D, F = self.D, self.F
+
+        def block(S):
+            return 2 * S * (4 * D * D + 3 * D * F) + 4 * S * S * D
+
+        n_img, n_cap = (self.H // 2) * (self.W // 2), self.L
+        return (2 * block(n_img) + 2 * block(n_cap) + self.layers * block(n_img + n_cap) +
+                2 * n_img * 64 * D * 2 + 2 * n_cap * self.cap_dim * D)
+
+    def measure(self, steps, warmup):
+        import sdhip
+
+        m = sdhip.ZImage.random(dim=self.D, heads=self.heads, ffn=self.F, layers=self.layers, seed=7)
+        try:
+            ms = m.time(self.H, self.W, self.L, self.cap_dim, steps, warmup)
+            params = m.params()
+        finally:
+            m.close()
+        return dict(event_ms=ms, wall_ms=ms, nsets=1, footprint=0, params=params)
+
+
 class CopyCalibration(Workload):
     """Not a BASELINE config: an in-place x *= 1 stream over [4096,10240]
     (one read + one write of 168 MB), the plain-copy reference for what HBM
@@ -476,7 +516,7 @@ def all_workloads():
         QKNormRope(),
         QKNormRope(unfused=True),
     ] + [Layout(n) for n in Layout.SPECS] + [Linear(k) for k in ("linear_bf16", "linear_swiglu", "linear_swiglu_unfused")] + [
-        Attention()]
+        Attention(), ZImageStep()]
 
 
 # ------------------------------------------------------------------ GPU timing
@@ -715,11 +755,16 @@ def main():
         w = wls[n]
         steps = args.steps if w is head else args.op_steps
         warm = args.warmup if w is head else 3
-        r = measure_gpu(be, w, steps, warm)
+        if hasattr(w, "measure"):  # a whole model step, timed by the model library itself
+            r = w.measure(max(3, min(steps, 10)), 2)
+        else:
+            r = measure_gpu(be, w, steps, warm)
         gbs = w.algo_bytes / (r["event_ms"] * 1e-3) / 1e9
         entry = dict(op=w.name, desc=w.desc, algo_bytes=w.algo_bytes, us_per_op=round(r["event_ms"] * 1e3, 2),
                      GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1), rotation_sets=r["nsets"],
                      rotation_MB=round(r["footprint"] / 2**20), traffic_bytes=read_traffic(w.name))
+        if "params" in r:
+            entry.update(params=r["params"], ms_per_step=round(r["event_ms"], 3))
         flops = getattr(w, "flops", None)
         if flops:
             tfs = flops / (r["event_ms"] * 1e-3) / 1e12
