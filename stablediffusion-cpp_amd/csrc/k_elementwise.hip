@@ -210,6 +210,17 @@ void run_unary(const char* op, float* x, int64_t n, float a, float b) {
 
 }  // namespace
 
+void launch_swiglu(const float* gate, const float* up, float* y, int64_t n) {
+    if (aligned16(gate) && aligned16(up) && aligned16(y)) {
+        const int64_t n4 = n / 4;
+        const int tail = (int)(n - n4 * 4);
+        k_swiglu<<<blocks_for(std::max<int64_t>(n4, 1), kPerBlock), kThreads, 0, stream()>>>(
+            (const f4*)gate, (const f4*)up, (f4*)y, n4, gate + n4 * 4, up + n4 * 4, y + n4 * 4, tail);
+    } else {
+        k_swiglu_scalar<<<stride_grid(n), kThreads, 0, stream()>>>(gate, up, y, n);
+    }
+}
+
 void zero_device(void* p, size_t bytes) {
     if (bytes == 0) return;
     const int64_t n4 = aligned16(p) ? (int64_t)(bytes / 16) : 0;
@@ -234,14 +245,7 @@ int sdh_swiglu(const float* gate, const float* up, float* y, int64_t n) {
         check_range(gate, (size_t)n * 4, op, "gate");
         check_range(up, (size_t)n * 4, op, "up");
         check_range(y, (size_t)n * 4, op, "y");
-        if (aligned16(gate) && aligned16(up) && aligned16(y)) {
-            const int64_t n4 = n / 4;
-            const int tail = (int)(n - n4 * 4);
-            k_swiglu<<<blocks_for(std::max<int64_t>(n4, 1), kPerBlock), kThreads, 0, stream()>>>(
-                (const f4*)gate, (const f4*)up, (f4*)y, n4, gate + n4 * 4, up + n4 * 4, y + n4 * 4, tail);
-        } else {
-            k_swiglu_scalar<<<stride_grid(n), kThreads, 0, stream()>>>(gate, up, y, n);
-        }
+        launch_swiglu(gate, up, y, n);
         launched(op);
     });
 }

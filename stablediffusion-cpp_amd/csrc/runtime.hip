@@ -166,6 +166,8 @@ struct Runtime {
     size_t scratch_bytes = 0;
     unsigned* counters = nullptr;
     size_t counter_count = 0;
+    void* workspace = nullptr;
+    size_t workspace_bytes = 0;
 };
 
 Runtime& rt() {
@@ -280,6 +282,24 @@ void* scratch(size_t bytes) {
     return r.scratch;
 }
 
+void* workspace(size_t bytes) {
+    Runtime& r = rt();
+    std::lock_guard<std::mutex> lk(r.mu);
+    if (bytes > r.workspace_bytes) {
+        if (r.workspace) {
+            hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
+            r.arena.release(r.workspace);
+        }
+        r.workspace_bytes = round_up(bytes, kAlign);
+        r.workspace = r.arena.alloc(r.workspace_bytes);
+        if (!r.workspace) {
+            r.workspace_bytes = 0;
+            fail(SDH_ERR_OOM, "backend_hip: arena exhausted allocating the GEMM workspace");
+        }
+    }
+    return r.workspace;
+}
+
 unsigned* counters(size_t count) {
     Runtime& r = rt();
     std::lock_guard<std::mutex> lk(r.mu);
@@ -352,6 +372,8 @@ int sdh_shutdown(void) {
         r.scratch_bytes = 0;
         r.counters = nullptr;
         r.counter_count = 0;
+        r.workspace = nullptr;
+        r.workspace_bytes = 0;
         for (int i = 0; i < 2; ++i) {
             (void)hipHostFree(r.stage[i]);
             (void)hipEventDestroy(r.stage_ev[i]);

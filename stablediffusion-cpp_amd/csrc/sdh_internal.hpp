@@ -58,6 +58,11 @@ void check_range(const void* p, size_t bytes, const char* op, const char* what);
 // Per-call device scratch of at least `bytes`, owned by the library, valid
 // until the next call that asks for scratch (ops are serialised on one stream).
 void* scratch(size_t bytes);
+// A persistent library-owned device block of at least `bytes` for a library
+// routine's workspace (the BLAS GEMM), distinct from scratch().
+void* workspace(size_t bytes);
+// y = silu(gate) * up over n floats (the SwiGLU kernel of sdh_swiglu, no checks).
+void launch_swiglu(const float* gate, const float* up, float* y, int64_t n);
 // Zero-initialised per-library device counters (uint32), persistent across
 // calls; kernels that use them leave them at zero when they finish.
 unsigned* counters(size_t count);
