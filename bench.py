@@ -365,7 +365,7 @@ class Linear(Workload):
 
     def __init__(self, kind):
         self.name = kind
-        self.kernel = "k_gemm_bf16"
+        self.kernel = "Cijk"  # hipBLASLt's GEMM kernels
         if kind == "linear_bf16":
             self.M, self.N, self.K = T, D, D
             self.flops = 2 * self.M * self.N * self.K
@@ -637,6 +637,9 @@ def gn_dispatches(shape, groups=32):
 
 
 def _kernel_key(full_name):
+    if full_name.startswith("Cijk_"):  # a hipBLASLt GEMM kernel: the library and its macro tile
+        t = re.search(r"_MT(\d+x\d+x\d+)_", full_name)
+        return "hipBLASLt Cijk MT" + (t.group(1) if t else "?")
     m = re.search(r"(k_\w+)(<[^>]*>)?\(", full_name)
     return (m.group(1) + (m.group(2) or "")) if m else full_name
 
