@@ -88,6 +88,13 @@ int sdh_unregister_external(void* p);
  * handed out to live blocks). */
 int sdh_memory_stats(size_t* reserved, size_t* in_use);
 
+/* FUSED for the Z-Image block: a pre-rounded bf16 A (ld lda), as
+ * gemm_nt_bf16 forms it on the device (backend_cuda.cu:183-188), so one
+ * rounding serves several projections of the same input (to_q, to_k, to_v).
+ * Otherwise as sdh_gemm_nt_bf16. */
+int sdh_gemm_nt_bf16_packed(int64_t M, int64_t N, int64_t K, const uint16_t* A, int64_t lda, const uint16_t* B,
+                            int64_t ldb, float* C, int64_t ldc, const float* bias, int accumulate);
+
 /* ---- GEMM with fp32 weights --------------------------------------------- */
 /* backend_cuda.h:38-40 gemm_nt_f32(): C[M,N] = A[M,K] * B[N,K]^T (+ C when
  * accumulate) (+ bias[N]), all fp32, row-major with leading dimensions in
@@ -156,6 +163,22 @@ int sdh_softmax_rows(float* x, int64_t rows, int64_t cols, float scale, int caus
  * stack of [period, cols] score matrices, as the reference's attention launch
  * at backend_cuda.cu:578). */
 int sdh_softmax_rows_batched(float* x, int64_t rows, int64_t cols, float scale, int causal, int64_t period);
+
+/* ---- the Z-Image block's fused row ops (zimage.cpp:114-135) ---------------- */
+/* FUSED: y = bf16 bits of rms_norm(x, gamma, eps) * scale, rows of C floats:
+ * rms_norm then mul_rows_(., scale) then the bf16 rounding gemm_nt_bf16
+ * applies to its A; the bits equal those of that sequence. gamma and scale
+ * may be NULL; y must not overlap x. */
+int sdh_rms_norm_modulate_bf16(const float* x, uint16_t* y, int64_t rows, int64_t C, const float* gamma,
+                               const float* scale, float eps);
+/* FUSED: x += gate * rms_norm(a, gamma, eps), or x += rms_norm(a, gamma, eps)
+ * with gate NULL: rms_norm then add_rows_scaled_ (or add_), with the same
+ * fp32 results. a is not modified; x and a must not overlap. */
+int sdh_rms_norm_gated_add(float* x, const float* a, int64_t rows, int64_t C, const float* gamma, const float* gate,
+                           float eps);
+/* FUSED: y = bf16 bits of swiglu(gate, up): swiglu then the bf16 rounding of
+ * gemm_nt_bf16's A (the input of the FFN's w2, zimage.cpp:130). */
+int sdh_swiglu_bf16(const float* gate, const float* up, uint16_t* y, int64_t n);
 
 /* ---- attention ------------------------------------------------------------ */
 /* backend_cuda.h:57-59 attention(); tensor.h:205-212 (tensor.cpp:776-810).

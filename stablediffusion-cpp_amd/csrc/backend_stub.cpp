@@ -66,6 +66,11 @@ STUB(int sdh_ln_modulate_gate(const float*, float*, const float*, const float*, 
                               int64_t, float))
 STUB(int sdh_qknorm_rope(float*, int64_t, float*, int64_t, int64_t, int64_t, int64_t, const float*, const float*,
                          float, const float*, const float*, int))
+STUB(int sdh_gemm_nt_bf16_packed(int64_t, int64_t, int64_t, const uint16_t*, int64_t, const uint16_t*, int64_t, float*,
+                                 int64_t, const float*, int))
+STUB(int sdh_rms_norm_modulate_bf16(const float*, uint16_t*, int64_t, int64_t, const float*, const float*, float))
+STUB(int sdh_rms_norm_gated_add(float*, const float*, int64_t, int64_t, const float*, const float*, float))
+STUB(int sdh_swiglu_bf16(const float*, const float*, uint16_t*, int64_t))
 STUB(int sdh_gemm_nt_f32(int64_t, int64_t, int64_t, const float*, int64_t, const float*, int64_t, float*, int64_t,
                          const float*, int))
 STUB(int sdh_to_bf16(const float*, uint16_t*, int64_t))

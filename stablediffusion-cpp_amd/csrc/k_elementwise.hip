@@ -97,6 +97,27 @@ __global__ __launch_bounds__(kThreads) void k_swiglu_scalar(const float* __restr
         y[i] = swiglu1(g[i], u[i]);
 }
 
+// y16 = bf16(swiglu(g, u)): swiglu, then the rounding gemm_nt_bf16 applies to
+// its A (the input of the FFN's w2, zimage.cpp:130), bit for bit.
+__global__ __launch_bounds__(kThreads) void k_swiglu_bf16(const f4* __restrict__ g, const f4* __restrict__ u,
+                                                         uint2* __restrict__ y, int64_t n4,
+                                                         const float* __restrict__ gt, const float* __restrict__ ut,
+                                                         unsigned short* __restrict__ yt, int tail) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i < n4) {
+        const f4 a = dev::ld_stream(g + i), b = dev::ld_stream(u + i);
+        y[i] = dev::bf16x4(f4{swiglu1(a.x, b.x), swiglu1(a.y, b.y), swiglu1(a.z, b.z), swiglu1(a.w, b.w)});
+    }
+    if (blockIdx.x == 0 && (int)threadIdx.x < tail) yt[threadIdx.x] = dev::bf16_rne(swiglu1(gt[threadIdx.x], ut[threadIdx.x]));
+}
+
+__global__ __launch_bounds__(kThreads) void k_swiglu_bf16_scalar(const float* __restrict__ g,
+                                                                const float* __restrict__ u,
+                                                                unsigned short* __restrict__ y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+        y[i] = dev::bf16_rne(swiglu1(g[i], u[i]));
+}
+
 // a += b  (tensor.cpp:876)
 __global__ __launch_bounds__(kThreads) void k_add(f4* __restrict__ a, const f4* __restrict__ b, int64_t n4,
                                                  float* __restrict__ at, const float* __restrict__ bt, int tail) {
@@ -235,6 +256,28 @@ void zero_device(void* p, size_t bytes) {
 using namespace sdh;
 
 extern "C" {
+
+int sdh_swiglu_bf16(const float* gate, const float* up, uint16_t* y, int64_t n) {
+    return guarded([&] {
+        const char* op = "sdh_swiglu_bf16";
+        need(n >= 0, op, "negative element count");
+        if (n == 0) return;
+        ensure_init();
+        check_range(gate, (size_t)n * 4, op, "gate");
+        check_range(up, (size_t)n * 4, op, "up");
+        check_range(y, (size_t)n * 2, op, "y");
+        if (aligned16(gate) && aligned16(up) && ((uintptr_t)y & 7) == 0) {
+            const int64_t n4 = n / 4;
+            const int tail = (int)(n - n4 * 4);
+            k_swiglu_bf16<<<blocks_for(std::max<int64_t>(n4, 1), kThreads), kThreads, 0, stream()>>>(
+                (const f4*)gate, (const f4*)up, (uint2*)y, n4, gate + n4 * 4, up + n4 * 4,
+                (unsigned short*)y + n4 * 4, tail);
+        } else {
+            k_swiglu_bf16_scalar<<<stride_grid(n), kThreads, 0, stream()>>>(gate, up, (unsigned short*)y, n);
+        }
+        launched(op);
+    });
+}
 
 int sdh_swiglu(const float* gate, const float* up, float* y, int64_t n) {
     return guarded([&] {

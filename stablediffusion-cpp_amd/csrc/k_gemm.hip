@@ -387,7 +387,7 @@ struct Blas {
     std::mutex mu;
     hipblasLtHandle_t h = nullptr;
     bool tried = false;
-    std::map<std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int>, BlasPlan> plans;
+    std::map<std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int>, BlasPlan> plans;
 };
 Blas& blas() {
     static Blas b;
@@ -400,8 +400,8 @@ void blas_check(hipblasStatus_t st, const char* what) {
 
 // Returns false when hipBLASLt has no algorithm for the shape (the caller then
 // runs its own kernels); throws on a failed launch.
-bool blaslt_gemm(int64_t M, int64_t N, int64_t K, const u16* P, const u16* B, int64_t ldb, float* C, int64_t ldc,
-                 const float* bias, bool accumulate) {
+bool blaslt_gemm(int64_t M, int64_t N, int64_t K, const u16* P, int64_t ldp, const u16* B, int64_t ldb, float* C,
+                 int64_t ldc, const float* bias, bool accumulate) {
     Blas& b = blas();
     std::lock_guard<std::mutex> lk(b.mu);
     if (!b.h) {
@@ -412,7 +412,7 @@ bool blaslt_gemm(int64_t M, int64_t N, int64_t K, const u16* P, const u16* B, in
             return false;
         }
     }
-    const auto key = std::make_tuple(M, N, K, ldb, ldc, bias ? 1 : 0);
+    const auto key = std::make_tuple(M, N, K, ldp, ldb, ldc, bias ? 1 : 0);
     auto it = b.plans.find(key);
     if (it == b.plans.end()) {
         BlasPlan p;
@@ -428,7 +428,7 @@ bool blaslt_gemm(int64_t M, int64_t N, int64_t K, const u16* P, const u16* B, in
                        "bias type");
         }
         blas_check(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, (uint64_t)K, (uint64_t)N, ldb), "layout B");
-        blas_check(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, (uint64_t)K, (uint64_t)M, K), "layout A");
+        blas_check(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, (uint64_t)K, (uint64_t)M, ldp), "layout A");
         blas_check(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, (uint64_t)N, (uint64_t)M, ldc), "layout C");
         hipblasLtMatmulPreference_t pref;
         blas_check(hipblasLtMatmulPreferenceCreate(&pref), "preference");
@@ -490,15 +490,15 @@ void run_gemm(const char* op, int64_t M, int64_t N, int64_t K, const float* A, i
         k_pack_bf16<<<dim3(blocks_for(kg, kGT), gy), kGT, 0, stream()>>>(A, lda, (u32x4*)P, M, (int)K);
         launched(op);
         if constexpr (EPI == E_LINEAR) {
-            if (lt && blaslt_gemm(M, N, K, P, B0, ldb, C, ldc, bias, accumulate)) {
+            if (lt && blaslt_gemm(M, N, K, P, K, B0, ldb, C, ldc, bias, accumulate)) {
                 launched(op);
                 return;
             }
         } else {
             float* G = (float*)(base + pbytes);
             float* U = G + M * N;
-            if (swi_lt && blaslt_gemm(M, N, K, P, B0, ldb, G, N, nullptr, false)) {
-                blaslt_gemm(M, N, K, P, B1, ldb, U, N, nullptr, false);
+            if (swi_lt && blaslt_gemm(M, N, K, P, K, B0, ldb, G, N, nullptr, false)) {
+                blaslt_gemm(M, N, K, P, K, B1, ldb, U, N, nullptr, false);
                 launch_swiglu(G, U, C, M * N);  // tensor.cpp:745 order, as the fused epilogue
                 launched(op);
                 return;
@@ -525,12 +525,62 @@ void run_gemm(const char* op, int64_t M, int64_t N, int64_t K, const float* A, i
     launched(op);
 }
 
+// C[M,N] = A[M,K] x B[N,K]^T (+ bias) (+ C) with A already bf16 (ld lda).
+void run_gemm_packed(int64_t M, int64_t N, int64_t K, const u16* A, int64_t lda, const u16* B, int64_t ldb, float* C,
+                     int64_t ldc, const float* bias, bool accumulate) {
+    const char* op = "sdh_gemm_nt_bf16_packed";
+    need(M >= 0 && N >= 0 && K >= 0, op, "negative size");
+    need(lda >= K && ldb >= K && ldc >= N, op, "leading dimension smaller than the row");
+    if (M == 0 || N == 0) return;
+    ensure_init();
+    if (K > 0) {
+        check_range(A, (size_t)((M - 1) * lda + K) * 2, op, "A");
+        check_range(B, (size_t)((N - 1) * ldb + K) * 2, op, "B");
+    }
+    check_range(C, (size_t)((M - 1) * ldc + N) * 4, op, "C");
+    if (bias) check_range(bias, (size_t)N * 4, op, "bias");
+    const bool lt = K > 0 && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && aligned(A, 16) && aligned(B, 16) &&
+                    aligned(C, 16) && (!bias || aligned(bias, 16));
+    if (lt && blaslt_gemm(M, N, K, A, lda, B, ldb, C, ldc, bias, accumulate)) {
+        launched(op);
+        return;
+    }
+    // the MFMA kernels read A with ld K: rows of a wider A are copied together first
+    need(K > 0 && K % 8 == 0 && ldb % 8 == 0 && aligned(B, 16) && M < (1LL << 31) && N < (1LL << 31), op,
+         "unsupported shape or alignment (K and ldb multiples of 8, 16-byte aligned operands)");
+    const u16* P = A;
+    if (lda != K || !aligned(A, 16)) {
+        u16* Q = (u16*)scratch((size_t)(M * K) * 2);
+        hip_check(hipMemcpy2DAsync(Q, (size_t)K * 2, A, (size_t)lda * 2, (size_t)K * 2, (size_t)M,
+                                   hipMemcpyDeviceToDevice, stream()),
+                  "hipMemcpy2DAsync");
+        P = Q;
+    }
+    if (K % 64 == 0) {
+        const int64_t gx = (N + kDN - 1) / kDN, gym = (M + kDM - 1) / kDM;
+        need(gym <= 65535, op, "too many rows for one launch");
+        k_gemm_dl<E_LINEAR><<<dim3((unsigned)gx, (unsigned)gym), kDT, 0, stream()>>>(
+            P, B, nullptr, ldb, C, ldc, bias, (int)M, (int)N, (int)K, accumulate ? 1 : 0);
+    } else {
+        const int64_t gx = (N + kBN - 1) / kBN, gym = (M + kBM - 1) / kBM;
+        need(gym <= 65535, op, "too many rows for one launch");
+        k_gemm_bf16<E_LINEAR><<<dim3((unsigned)gx, (unsigned)gym), kGT, 0, stream()>>>(
+            P, B, nullptr, ldb, C, ldc, bias, (int)M, (int)N, (int)K, accumulate ? 1 : 0);
+    }
+    launched(op);
+}
+
 }  // namespace
 }  // namespace sdh
 
 using namespace sdh;
 
 extern "C" {
+
+int sdh_gemm_nt_bf16_packed(int64_t M, int64_t N, int64_t K, const uint16_t* A, int64_t lda, const uint16_t* B,
+                            int64_t ldb, float* C, int64_t ldc, const float* bias, int accumulate) {
+    return guarded([&] { run_gemm_packed(M, N, K, A, lda, B, ldb, C, ldc, bias, accumulate != 0); });
+}
 
 int sdh_gemm_nt_bf16(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const uint16_t* B, int64_t ldb,
                      float* C, int64_t ldc, const float* bias, int accumulate) {

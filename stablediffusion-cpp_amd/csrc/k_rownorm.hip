@@ -344,6 +344,117 @@ __global__ __launch_bounds__(kThreads) void k_ln_mod_gate_generic(const float* x
     }
 }
 
+// ---- the Z-Image block's fused row ops ---------------------------------------
+// y16 = bf16(((x * rstd) * gamma) * scale): rms_norm(x, gamma), mul_rows_(.,
+// scale) (zimage.cpp:115-116, :128-129) and the bf16 rounding gemm_nt_bf16
+// applies to its A (backend_cuda.cu:183-188), with the same fp32 products in
+// the same order, so the bits equal those of the three-op sequence. The bf16
+// row is the A operand of the projections that follow.
+template <int V, bool HAS_G, bool HAS_S>
+__global__ __launch_bounds__(kThreads) void k_rms_mod_bf16(const float* __restrict__ x, uint2* __restrict__ y,
+                                                          int64_t rows, int C, const float* __restrict__ gamma,
+                                                          const float* __restrict__ scale, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int n4 = C >> 2;
+    const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const f4* xr = (const f4*)(x + row * C);
+    uint2* yr = y + row * n4;
+    f4 v[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * j;
+        v[j] = idx < n4 ? dev::ld_stream(xr + idx) : zero4();
+    }
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) q += dev::hsum(v[j] * v[j]);
+    const float rstd = rstd_of(dev::wave_sum(q), C, eps);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * j;
+        if (idx < n4) {
+            f4 o = v[j] * rstd;
+            if constexpr (HAS_G) o = o * ((const f4*)gamma)[idx];
+            if constexpr (HAS_S) o = o * ((const f4*)scale)[idx];
+            yr[idx] = dev::bf16x4(o);
+        }
+    }
+}
+
+// x += gate * (a * rstd * gamma): y = rms_norm(a, gamma) then add_rows_scaled_(x,
+// y, gate), or add_(x, y) without a gate (zimage.cpp:124-127, :132-135), with
+// the same fp32 expressions, so x equals the two-op sequence's.
+template <int V, bool HAS_G, bool HAS_GATE>
+__global__ __launch_bounds__(kThreads) void k_rms_gated_add(float* __restrict__ x, const float* __restrict__ a,
+                                                           int64_t rows, int C, const float* __restrict__ gamma,
+                                                           const float* __restrict__ gate, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int n4 = C >> 2;
+    const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const f4* ar = (const f4*)(a + row * C);
+    f4* xr = (f4*)(x + row * C);
+    f4 v[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * j;
+        v[j] = idx < n4 ? dev::ld_stream(ar + idx) : zero4();
+    }
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) q += dev::hsum(v[j] * v[j]);
+    const float rstd = rstd_of(dev::wave_sum(q), C, eps);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * j;
+        if (idx < n4) {
+            // o is rounded on its own as rms_norm's output is: no contraction of
+            // (a rstd) gamma into an FMA with x (the gate's FMA is explicit, as in
+            // add_rows_scaled_)
+#pragma clang fp contract(off)
+            f4 o = v[j] * rstd;
+            if constexpr (HAS_G) o = o * ((const f4*)gamma)[idx];
+            const f4 xv = dev::ld_stream(xr + idx);
+            f4 r;
+            if constexpr (HAS_GATE) {
+                const f4 g = ((const f4*)gate)[idx];
+                r = f4{fmaf(g.x, o.x, xv.x), fmaf(g.y, o.y, xv.y), fmaf(g.z, o.z, xv.z), fmaf(g.w, o.w, xv.w)};
+            } else {
+                r = xv + o;
+            }
+            dev::st_stream(xr + idx, r);
+        }
+    }
+}
+
+// any C / alignment: one wave per row, strided loops over the row
+template <bool GATED>
+__global__ __launch_bounds__(kThreads) void k_rms_fused_generic(const float* __restrict__ src, float* __restrict__ x,
+                                                               unsigned short* __restrict__ y16, int64_t rows,
+                                                               int64_t C, const float* __restrict__ gamma,
+                                                               const float* __restrict__ vec, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t stride = (int64_t)gridDim.x * kWaves;
+    for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows; row += stride) {
+        const float* p = src + row * C;
+        float ss = 0.f;
+        for (int64_t i = lane; i < C; i += 64) ss += p[i] * p[i];
+        const float rstd = rstd_of(dev::wave_sum(ss), C, eps);
+        for (int64_t i = lane; i < C; i += 64) {
+#pragma clang fp contract(off)
+            float o = p[i] * rstd * (gamma ? gamma[i] : 1.0f);
+            if constexpr (GATED) {
+                float* xp = x + row * C + i;
+                *xp = vec ? fmaf(vec[i], o, *xp) : *xp + o;
+            } else {
+                if (vec) o = o * vec[i];
+                y16[row * C + i] = dev::bf16_rne(o);
+            }
+        }
+    }
+}
+
 // ---- dispatch helpers ------------------------------------------------------
 constexpr int kMaxV = 32;
 
@@ -433,12 +544,91 @@ void run_rownorm(const char* op, int mode, const float* x, float* y, int64_t row
     launched(op);
 }
 
+bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return x < y + nb && y < x + na;
+}
+
+void run_rms_mod_bf16(const float* x, uint16_t* y, int64_t rows, int64_t C, const float* gamma, const float* scale,
+                      float eps) {
+    const char* op = "sdh_rms_norm_modulate_bf16";
+    need(rows >= 0 && C >= 0, op, "negative size");
+    if (rows == 0 || C == 0) return;
+    ensure_init();
+    check_range(x, (size_t)(rows * C) * 4, op, "x");
+    check_range(y, (size_t)(rows * C) * 2, op, "y");
+    if (gamma) check_range(gamma, (size_t)C * 4, op, "gamma");
+    if (scale) check_range(scale, (size_t)C * 4, op, "scale");
+    need(!overlaps(x, (size_t)(rows * C) * 4, y, (size_t)(rows * C) * 2), op, "y overlaps x");
+    if (vec_ok(C, {x, gamma, scale}) && ((uintptr_t)y & 7) == 0) {
+        const unsigned grid = exact_grid(rows);
+        with_v(pick_v(C / 4), [&](auto vc) {
+            constexpr int V = decltype(vc)::value;
+            uint2* yy = (uint2*)y;
+            if (gamma && scale)
+                k_rms_mod_bf16<V, true, true><<<grid, kThreads, 0, stream()>>>(x, yy, rows, (int)C, gamma, scale, eps);
+            else if (gamma)
+                k_rms_mod_bf16<V, true, false><<<grid, kThreads, 0, stream()>>>(x, yy, rows, (int)C, gamma, scale, eps);
+            else if (scale)
+                k_rms_mod_bf16<V, false, true><<<grid, kThreads, 0, stream()>>>(x, yy, rows, (int)C, gamma, scale, eps);
+            else
+                k_rms_mod_bf16<V, false, false><<<grid, kThreads, 0, stream()>>>(x, yy, rows, (int)C, gamma, scale, eps);
+        });
+    } else {
+        k_rms_fused_generic<false><<<row_grid(rows, 32), kThreads, 0, stream()>>>(x, nullptr, (unsigned short*)y, rows,
+                                                                                   C, gamma, scale, eps);
+    }
+    launched(op);
+}
+
+void run_rms_gated_add(float* x, const float* a, int64_t rows, int64_t C, const float* gamma, const float* gate,
+                       float eps) {
+    const char* op = "sdh_rms_norm_gated_add";
+    need(rows >= 0 && C >= 0, op, "negative size");
+    if (rows == 0 || C == 0) return;
+    ensure_init();
+    const size_t bytes = (size_t)(rows * C) * 4;
+    check_range(x, bytes, op, "x");
+    check_range(a, bytes, op, "a");
+    if (gamma) check_range(gamma, (size_t)C * 4, op, "gamma");
+    if (gate) check_range(gate, (size_t)C * 4, op, "gate");
+    need(!overlaps(x, bytes, a, bytes), op, "x overlaps a");
+    if (vec_ok(C, {x, a, gamma, gate})) {
+        const unsigned grid = exact_grid(rows);
+        with_v(pick_v(C / 4), [&](auto vc) {
+            constexpr int V = decltype(vc)::value;
+            if (gamma && gate)
+                k_rms_gated_add<V, true, true><<<grid, kThreads, 0, stream()>>>(x, a, rows, (int)C, gamma, gate, eps);
+            else if (gamma)
+                k_rms_gated_add<V, true, false><<<grid, kThreads, 0, stream()>>>(x, a, rows, (int)C, gamma, gate, eps);
+            else if (gate)
+                k_rms_gated_add<V, false, true><<<grid, kThreads, 0, stream()>>>(x, a, rows, (int)C, gamma, gate, eps);
+            else
+                k_rms_gated_add<V, false, false><<<grid, kThreads, 0, stream()>>>(x, a, rows, (int)C, gamma, gate, eps);
+        });
+    } else {
+        k_rms_fused_generic<true><<<row_grid(rows, 32), kThreads, 0, stream()>>>(a, x, nullptr, rows, C, gamma, gate,
+                                                                                  eps);
+    }
+    launched(op);
+}
+
 }  // namespace
 }  // namespace sdh
 
 using namespace sdh;
 
 extern "C" {
+
+int sdh_rms_norm_modulate_bf16(const float* x, uint16_t* y, int64_t rows, int64_t C, const float* gamma,
+                               const float* scale, float eps) {
+    return guarded([&] { run_rms_mod_bf16(x, y, rows, C, gamma, scale, eps); });
+}
+
+int sdh_rms_norm_gated_add(float* x, const float* a, int64_t rows, int64_t C, const float* gamma, const float* gate,
+                           float eps) {
+    return guarded([&] { run_rms_gated_add(x, a, rows, C, gamma, gate, eps); });
+}
 
 int sdh_rms_norm(const float* x, float* y, int64_t rows, int64_t C, const float* gamma, float eps) {
     return guarded([&] { run_rownorm("sdh_rms_norm", M_RMS, x, y, rows, C, gamma, nullptr, eps); });

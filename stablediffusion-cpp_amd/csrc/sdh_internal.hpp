@@ -170,6 +170,19 @@ __device__ __forceinline__ float rstd_fast(float stat, float inv_c, float eps) {
     return __builtin_amdgcn_rsqf(stat * inv_c + eps);
 }
 
+// float -> bf16 bits, nearest even; inf and NaN keep their top 16 bits
+// (tensor.cpp:114-121, the rounding of gemm_nt_bf16's A on the device).
+__device__ __forceinline__ unsigned short bf16_rne(float f) {
+    const unsigned b = __float_as_uint(f);
+    if ((b & 0x7F800000u) == 0x7F800000u) return (unsigned short)(b >> 16);
+    return (unsigned short)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+// four floats -> four bf16 in one 8-byte word (element 0 in the low half)
+__device__ __forceinline__ uint2 bf16x4(const f4& v) {
+    return uint2{(unsigned)bf16_rne(v.x) | ((unsigned)bf16_rne(v.y) << 16),
+                 (unsigned)bf16_rne(v.z) | ((unsigned)bf16_rne(v.w) << 16)};
+}
+
 // Reference-order activations (tensor.cpp:745, :847, :859, :866, :830).
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 __device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }

@@ -81,6 +81,10 @@ SIGNATURES = {
     "sdh_add_rows": [_vp, _vp, _i64, _i64],
     "sdh_gemm_nt_bf16": [_i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, C.c_int],
     "sdh_linear_swiglu": [_vp, _vp, _vp, _vp, _i64, _i64, _i64],
+    "sdh_gemm_nt_bf16_packed": [_i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, C.c_int],
+    "sdh_rms_norm_modulate_bf16": [_vp, _vp, _i64, _i64, _vp, _vp, _fl],
+    "sdh_rms_norm_gated_add": [_vp, _vp, _i64, _i64, _vp, _vp, _fl],
+    "sdh_swiglu_bf16": [_vp, _vp, _vp, _i64],
     "sdh_gemm_nt_f32": [_i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, C.c_int],
     "sdh_to_bf16": [_vp, _vp, _i64],
     "sdh_attention": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
@@ -322,6 +326,19 @@ class Backend:
     # GEMM (bf16 weights held in DArray buffers of uint16)
     def gemm_nt_bf16(self, M, N, K, A, lda, B, ldb, Cm, ldc, bias=None, accumulate=False):
         self.call("sdh_gemm_nt_bf16", M, N, K, _p(A), lda, _p(B), ldb, _p(Cm), ldc, _p(bias), 1 if accumulate else 0)
+
+    def gemm_nt_bf16_packed(self, M, N, K, A16, lda, B, ldb, C, ldc, bias=None, accumulate=False):
+        self.call("sdh_gemm_nt_bf16_packed", M, N, K, _p(A16), lda, _p(B), ldb, _p(C), ldc, _p(bias),
+                  int(bool(accumulate)))
+
+    def rms_norm_modulate_bf16(self, x, y16, rows, C, gamma, scale, eps):
+        self.call("sdh_rms_norm_modulate_bf16", _p(x), _p(y16), rows, C, _p(gamma), _p(scale), eps)
+
+    def rms_norm_gated_add(self, x, a, rows, C, gamma, gate, eps):
+        self.call("sdh_rms_norm_gated_add", _p(x), _p(a), rows, C, _p(gamma), _p(gate), eps)
+
+    def swiglu_bf16(self, g, u, y16, n):
+        self.call("sdh_swiglu_bf16", _p(g), _p(u), _p(y16), n)
 
     def gemm_nt_f32(self, M, N, K, A, lda, B, ldb, C, ldc, bias=None, accumulate=False):
         self.call("sdh_gemm_nt_f32", M, N, K, _p(A), lda, _p(B), ldb, _p(C), ldc, _p(bias), int(bool(accumulate)))

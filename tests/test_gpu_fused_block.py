@@ -1,0 +1,125 @@
+"""GPU tests of the Z-Image block's fused entry points against the op
+sequences they replace, through the C ABI. Each fused op is claimed equal to
+its sequence bit for bit (same fp32 expressions in the same order, then the
+same bf16 rounding), so the bar is exact equality:
+  * sdh_rms_norm_modulate_bf16 == rms_norm -> mul_rows -> to_bf16
+    (zimage.cpp:115-116, :128-129, then gemm_nt_bf16's rounding of A);
+  * sdh_rms_norm_gated_add == rms_norm -> add_rows_scaled (or add_)
+    (zimage.cpp:124-127, :132-135);
+  * sdh_swiglu_bf16 == swiglu -> to_bf16 (zimage.cpp:130, the input of w2);
+  * sdh_gemm_nt_bf16_packed(bf16 A) == sdh_gemm_nt_bf16(the same values in
+    fp32), and within the fp32 accumulation bound of the exact sum for the
+    strided A and the hand-written kernels' shapes.
+Shapes: the Z-Image rows [4224, 3840], small and odd row widths (the generic
+kernels), optional gamma / scale / gate.
+"""
+import numpy as np
+import pytest
+
+from oracle import bf16_to_f32, f32_to_bf16
+from tolerances import assert_gemm
+
+pytestmark = pytest.mark.gpu
+
+ROWS = [(4224, 3840), (5, 64), (33, 100), (7, 30)]
+
+
+def _u16(be, n):
+    return be.array(np.zeros(n, np.uint16))
+
+
+@pytest.mark.parametrize("rows,C", ROWS)
+@pytest.mark.parametrize("with_gamma,with_scale", [(True, True), (True, False), (False, True), (False, False)])
+def test_rms_norm_modulate_bf16(be, orc, rows, C, with_gamma, with_scale):
+    x = orc.randn((rows, C), 700 + C, 0.0, 2.0)
+    g = orc.randn((C,), 701, 1.0, 0.1) if with_gamma else None
+    s = orc.randn((C,), 702, 1.0, 0.3) if with_scale else None
+    dx = be.array(x)
+    dg, ds = (be.array(g) if with_gamma else None), (be.array(s) if with_scale else None)
+    y16 = _u16(be, rows * C)
+    be.rms_norm_modulate_bf16(dx, y16, rows, C, dg, ds, 1e-5)
+    h = be.empty((rows, C))
+    be.rms_norm(dx, h, rows, C, dg, 1e-5)
+    if with_scale:
+        be.mul_rows(h, ds, rows, C)
+    ref16 = _u16(be, rows * C)
+    be.to_bf16(h, ref16, rows * C)
+    got, want = y16.download(), ref16.download()
+    assert np.array_equal(got, want), f"{int(np.sum(got != want))} of {got.size} differ"
+    # and against the oracle's composition: the same value to within one bf16 step
+    o = orc.rms_norm(x, g, 1e-5)
+    if with_scale:
+        o = orc.mul_rows(o, s)
+    assert np.max(np.abs(bf16_to_f32(got).reshape(rows, C) - o) / np.maximum(np.abs(o), 1e-30)) <= 2.0 ** -8
+
+
+@pytest.mark.parametrize("rows,C", ROWS)
+@pytest.mark.parametrize("with_gamma,with_gate", [(True, True), (True, False), (False, True)])
+def test_rms_norm_gated_add(be, orc, rows, C, with_gamma, with_gate):
+    x = orc.randn((rows, C), 710 + C)
+    a = orc.randn((rows, C), 711 + C, 0.0, 3.0)
+    g = orc.randn((C,), 712, 1.0, 0.1) if with_gamma else None
+    gate = orc.randn((C,), 713, 0.0, 0.5) if with_gate else None
+    dg, dgate = (be.array(g) if with_gamma else None), (be.array(gate) if with_gate else None)
+    dx, da = be.array(x), be.array(a)
+    be.rms_norm_gated_add(dx, da, rows, C, dg, dgate, 1e-5)
+    seq_x = be.array(x)
+    an = be.empty((rows, C))
+    be.rms_norm(da, an, rows, C, dg, 1e-5)
+    if with_gate:
+        be.add_rows_scaled(seq_x, an, dgate, rows, C)
+    else:
+        be.add(seq_x, an, rows * C)
+    assert np.array_equal(dx.download(), seq_x.download())
+    assert np.array_equal(da.download(), a)  # a is read only
+
+
+@pytest.mark.parametrize("n,off", [(4224 * 10240, 0), (1001, 0), (1003, 1)])
+def test_swiglu_bf16(be, orc, n, off):
+    g = orc.randn((n + off,), 720, 0.0, 1.5)
+    u = orc.randn((n + off,), 721, 0.0, 1.5)
+    dg, du = be.array(g), be.array(u)
+    y16 = _u16(be, n + 1)
+    # off = 1: unaligned operands take the scalar kernel
+    import sdhip
+
+    gp = sdhip.DArray(be, (n,), ptr=dg.ptr + 4 * off, owned=False)
+    upp = sdhip.DArray(be, (n,), ptr=du.ptr + 4 * off, owned=False)
+    yp = sdhip.DArray(be, (n,), ptr=y16.ptr + 2 * off, owned=False, dtype=np.uint16)
+    be.swiglu_bf16(gp, upp, yp, n)
+    y = be.empty((n,))
+    be.swiglu(gp, upp, y, n)
+    ref16 = _u16(be, n)
+    be.to_bf16(y, ref16, n)
+    assert np.array_equal(y16.download()[off:off + n], ref16.download())
+
+
+@pytest.mark.parametrize("M,N,K,lda", [(4224, 3840, 3840, 3840), (300, 200, 128, 136), (70, 130, 64, 64)])
+def test_gemm_packed_equals_gemm_on_rounded_a(be, orc, M, N, K, lda):
+    A = bf16_to_f32(f32_to_bf16(orc.randn((M, lda), 730 + M))).reshape(M, lda)
+    W = f32_to_bf16(orc.randn((N, K), 731, 0.0, 0.05))
+    b = orc.randn((N,), 732, 0.0, 0.5)
+    dW, db = be.array(W), be.array(b)
+    c1 = be.empty((M, N))
+    be.gemm_nt_bf16_packed(M, N, K, be.array(f32_to_bf16(A)), lda, dW, K, c1, N, db)
+    c0 = be.empty((M, N))
+    be.gemm_nt_bf16(M, N, K, be.array(A), lda, dW, K, c0, N, db)
+    got = c1.download()
+    if lda == K:
+        assert np.array_equal(got, c0.download())
+    rows = np.arange(0, M, max(1, M // 50))
+    want, S = orc.gemm_nt_bf16(A[rows, :K], W, b)
+    assert_gemm(got[rows], want, S + np.abs(b)[None, :], K + 2, f"packed gemm {M}x{N}x{K}")
+
+
+def test_gemm_packed_mfma_kernels(be, orc):
+    """ldc not a multiple of 4: the hand-written MFMA kernels (hipBLASLt needs
+    aligned leading dimensions), K % 64 == 0 and K % 64 != 0."""
+    for (M, N, K) in ((257, 129, 192), (65, 70, 72)):
+        A = bf16_to_f32(f32_to_bf16(orc.randn((M, K), 740 + K))).reshape(M, K)
+        W = f32_to_bf16(orc.randn((N, K), 741, 0.0, 0.05))
+        ldc = N + 1
+        C = be.array(np.zeros((M, ldc), np.float32))
+        be.gemm_nt_bf16_packed(M, N, K, be.array(f32_to_bf16(A)), K, be.array(W), K, C, ldc)
+        want, S = orc.gemm_nt_bf16(A, W)
+        assert_gemm(C.download()[:, :N], want, S, K + 1, f"packed mfma {M}x{N}x{K}")
