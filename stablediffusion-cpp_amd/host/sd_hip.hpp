@@ -154,6 +154,22 @@ inline void gemm_nt_f32(int64_t M, int64_t N, int64_t K, const float* A, int64_t
     detail::check(sdh_gemm_nt_f32(M, N, K, A, lda, B, ldb, C, ldc, bias, accumulate ? 1 : 0), "hip::gemm_nt_f32");
 }
 inline void to_bf16(const float* x, uint16_t* y, int64_t n) { detail::check(sdh_to_bf16(x, y, n), "hip::to_bf16"); }
+inline void gemm_nt_bf16_packed(int64_t M, int64_t N, int64_t K, const uint16_t* A, int64_t lda, const uint16_t* B,
+                                int64_t ldb, float* C, int64_t ldc, const float* bias, bool accumulate) {
+    detail::check(sdh_gemm_nt_bf16_packed(M, N, K, A, lda, B, ldb, C, ldc, bias, accumulate ? 1 : 0),
+                  "hip::gemm_nt_bf16_packed");
+}
+inline void rms_norm_modulate_bf16(const float* x, uint16_t* y, int64_t rows, int64_t C, const float* gamma,
+                                   const float* scale, float eps) {
+    detail::check(sdh_rms_norm_modulate_bf16(x, y, rows, C, gamma, scale, eps), "hip::rms_norm_modulate_bf16");
+}
+inline void rms_norm_gated_add(float* x, const float* a, int64_t rows, int64_t C, const float* gamma,
+                               const float* gate, float eps) {
+    detail::check(sdh_rms_norm_gated_add(x, a, rows, C, gamma, gate, eps), "hip::rms_norm_gated_add");
+}
+inline void swiglu_bf16(const float* gate, const float* up, uint16_t* y, int64_t n) {
+    detail::check(sdh_swiglu_bf16(gate, up, y, n), "hip::swiglu_bf16");
+}
 inline void linear_swiglu(const float* x, const uint16_t* w1, const uint16_t* w3, float* y, int64_t rows, int64_t in,
                           int64_t hidden) {
     detail::check(sdh_linear_swiglu(x, w1, w3, y, rows, in, hidden), "hip::linear_swiglu");

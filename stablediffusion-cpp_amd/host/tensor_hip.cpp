@@ -63,6 +63,15 @@ Tensor Tensor::empty(std::vector<int64_t> s, Device d) {
     return t;
 }
 
+Tensor Tensor::empty_bf16(std::vector<int64_t> s) {
+    Tensor t;
+    t.shape = std::move(s);
+    t.device = Device::HIP;
+    t.dtype = DType::BF16;
+    t.dev = std::make_shared<DeviceBuffer>((size_t)numel_of(t.shape) * sizeof(uint16_t));
+    return t;
+}
+
 float* Tensor::dptr() { return is_hip() && dev ? (float*)dev->p : nullptr; }
 const float* Tensor::dptr() const { return is_hip() && dev ? (const float*)dev->p : nullptr; }
 
@@ -96,6 +105,7 @@ Tensor Tensor::to(Device d) const {
 }
 
 const uint16_t* Tensor::dptr16() const { return is_hip() && dev ? (const uint16_t*)dev->p : nullptr; }
+uint16_t* Tensor::dptr16() { return is_hip() && dev ? (uint16_t*)dev->p : nullptr; }
 
 // tensor.cpp:114-121 rounding (nearest even; inf and NaN keep their top bits)
 void Tensor::to_bf16() {
@@ -405,10 +415,14 @@ Tensor linear(const Tensor& x, const Tensor& W, const Tensor* b) {
     need_hip(x, "linear");
     if (b) same_device(x, *b, "linear");
     Tensor y = Tensor::empty(oshape, Device::HIP);
-    if (W.is_bf16())
+    if (x.is_bf16()) {
+        if (!W.is_bf16()) throw std::runtime_error("linear: a BF16 input needs BF16 weights " + W.shape_str());
+        sd::hip::gemm_nt_bf16_packed(rows, out, in, x.dptr16(), in, W.dptr16(), in, y.dptr(), out, opt(b), false);
+    } else if (W.is_bf16()) {
         sd::hip::gemm_nt_bf16(rows, out, in, x.dptr(), in, W.dptr16(), in, y.dptr(), out, opt(b), false);
-    else
+    } else {
         sd::hip::gemm_nt_f32(rows, out, in, x.dptr(), in, W.dptr(), in, y.dptr(), out, opt(b), false);
+    }
     return y;
 }
 
@@ -441,6 +455,39 @@ Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, int heads, b
     Tensor out = Tensor::empty({N, Sq, inner}, Device::HIP);
     sd::hip::attention(q.dptr(), k.dptr(), v.dptr(), out.dptr(), N, Sq, Skv, heads, kv_heads, d, causal);
     return out;
+}
+
+// ---- the Z-Image block's fused ops ----
+Tensor rms_norm_modulate_bf16(const Tensor& x, const Tensor* gamma, const Tensor* scale, float eps) {
+    need_hip(x, "rms_norm_modulate_bf16");
+    if (gamma) same_device(x, *gamma, "rms_norm_modulate_bf16");
+    if (scale) same_device(x, *scale, "rms_norm_modulate_bf16");
+    const int64_t C = x.dim(-1), rows = x.numel() / C;
+    if ((gamma && gamma->numel() != C) || (scale && scale->numel() != C))
+        throw std::runtime_error("rms_norm_modulate_bf16: vector length vs " + x.shape_str());
+    Tensor y = Tensor::empty_bf16(x.shape);
+    sd::hip::rms_norm_modulate_bf16(x.dptr(), y.dptr16(), rows, C, opt(gamma), opt(scale), eps);
+    return y;
+}
+
+void rms_norm_gated_add_(Tensor& x, const Tensor& a, const Tensor* gamma, const Tensor* gate, float eps) {
+    need_hip(x, "rms_norm_gated_add_");
+    same_device(x, a, "rms_norm_gated_add_");
+    if (x.numel() != a.numel() || x.dim(-1) != a.dim(-1))
+        throw std::runtime_error("add_rows_scaled_: " + x.shape_str() + " vs " + a.shape_str());
+    const int64_t C = x.dim(-1), rows = x.numel() / C;
+    if ((gamma && gamma->numel() != C) || (gate && gate->numel() != C))
+        throw std::runtime_error("rms_norm_gated_add_: vector length vs " + x.shape_str());
+    sd::hip::rms_norm_gated_add(x.dptr(), a.dptr(), rows, C, opt(gamma), opt(gate), eps);
+}
+
+Tensor swiglu_bf16(const Tensor& gate, const Tensor& up) {
+    if (gate.numel() != up.numel()) throw std::runtime_error("swiglu: " + gate.shape_str() + " vs " + up.shape_str());
+    same_device(gate, up, "swiglu");
+    need_hip(gate, "swiglu_bf16");
+    Tensor y = Tensor::empty_bf16(gate.shape);
+    sd::hip::swiglu_bf16(gate.dptr(), up.dptr(), y.dptr16(), gate.numel());
+    return y;
 }
 
 // tensor.cpp:752 (device pointer)

@@ -47,12 +47,15 @@ struct Tensor {
     // Device tensor whose contents are left uninitialised; ops use it for
     // outputs they overwrite completely (no zero-fill pass).
     static Tensor empty(std::vector<int64_t> s, Device d);
+    // Uninitialised BF16 device tensor (bf16 bit patterns, two bytes each).
+    static Tensor empty_bf16(std::vector<int64_t> s);
 
     static int64_t numel_of(const std::vector<int64_t>& s);
     int64_t numel() const { return numel_of(shape); }
     bool is_hip() const { return device == Device::HIP; }
     bool is_bf16() const { return dtype == DType::BF16; }
     const uint16_t* dptr16() const;  // BF16 device storage
+    uint16_t* dptr16();
     // F32 host storage -> BF16, rounding to nearest even (tensor.h:86-87).
     void to_bf16();
     Tensor to(Device d) const;  // tensor.cpp:72-93
@@ -107,10 +110,21 @@ Tensor repeat_batch(const Tensor& x, int64_t times);
 // ---- linear (tensor.h:146): y = x W^T (+ b), W [out, in] ----
 // The reference's device branch (tensor.cpp:489-494): with BF16 weights x is
 // rounded to bf16 and products accumulate in fp32 (MFMA); F32 weights take
-// the fp32 GEMM.
+// the fp32 GEMM. A BF16 x (from rms_norm_modulate_bf16 / swiglu_bf16) is
+// already rounded and is used as is (BF16 weights only).
 Tensor linear(const Tensor& x, const Tensor& W, const Tensor* b);
 // swiglu(linear(x, w1), linear(x, w3)) in one GEMM (zimage.cpp:130)
 Tensor linear_swiglu(const Tensor& x, const Tensor& w1, const Tensor& w3);
+
+// ---- the Z-Image block's fused ops (zimage.cpp:114-135); results equal the
+// op sequences named, bit for bit ----
+// rms_norm(x, gamma, eps), then mul_rows_(., *scale) when scale is given, rounded
+// to BF16: the A operand linear() takes for BF16 weights (no second rounding).
+Tensor rms_norm_modulate_bf16(const Tensor& x, const Tensor* gamma, const Tensor* scale, float eps);
+// x += *gate * rms_norm(a, gamma, eps), or x += rms_norm(a, gamma, eps) without a gate
+void rms_norm_gated_add_(Tensor& x, const Tensor& a, const Tensor* gamma, const Tensor* gate, float eps);
+// swiglu(gate, up) rounded to BF16 (the input of the FFN's w2)
+Tensor swiglu_bf16(const Tensor& gate, const Tensor& up);
 
 // ---- attention (tensor.h:205-212) ----
 // q [N, Sq, heads*d], k and v [N, Skv, kv_heads*d] -> [N, Sq, heads*d];

@@ -12,10 +12,11 @@
 // -> unpatchify. Weights keep the checkpoint's names.
 //
 // Each block runs on backend_hip as the reference's run_block
-// (zimage.cpp:90-136) with two fusions that give the same values: the four
-// QK-norm / RoPE passes are one sdh_qknorm_rope launch, and w2(swiglu(w1 h,
-// w3 h)) computes swiglu in the GEMM epilogue (sdh_linear_swiglu, BF16
-// weights) so g and u never reach memory. Attention is the fused kernel.
+// (zimage.cpp:90-136) with fused ops that give the same values: the four
+// QK-norm / RoPE passes are one sdh_qknorm_rope launch; attention is the
+// fused kernel; with BF16 weights RMSNorm * (1 + scale) emits the GEMMs' bf16
+// A directly (one rounding for to_q, to_k, to_v), swiglu emits w2's bf16 A,
+// and RMSNorm + gated residual is one pass over x.
 #pragma once
 
 #include <array>
