@@ -512,6 +512,7 @@ void run_mfma(const float* q, const float* k, const float* v, float* out, int64_
     u16* tiles = (u16*)base;
     int2* exps = (int2*)(base + (size_t)ntot * tile_bytes);
     const int64_t inner = heads * d, kv_inner = (int64_t)kv_heads * d;
+    need(ntiles * 256 <= kMaxGridItems, "sdh_attention", "too many keys for one launch");
     const dim3 pgrid((unsigned)ntiles, (unsigned)kv_heads, (unsigned)N);
     if (d == DP && kv_inner % 4 == 0 && aligned16(k) && aligned16(v))
         k_attn_pack<DP, true><<<pgrid, 256, 0, stream()>>>(k, v, tiles, exps, (int)Skv, (int)kv_inner, (int)d,
@@ -522,7 +523,7 @@ void run_mfma(const float* q, const float* k, const float* v, float* out, int64_
     launched("sdh_attention");
     const int qvec = d == DP && inner % 4 == 0 && aligned16(q) && aligned16(out);
     const int64_t nqb = (Sq + kBM - 1) / kBM, nblk = nqb * heads * N;
-    need(nblk < (1LL << 31), "sdh_attention", "too many query blocks for one launch");
+    need(nblk * kThreads <= kMaxGridItems, "sdh_attention", "too many query blocks for one launch");
     if (causal)
         k_attn_fwd<DP, true><<<(unsigned)nblk, kThreads, 0, stream()>>>(
             q, tiles, exps, out, (int)Sq, (int)Skv, (int)inner, (int)d, heads / kv_heads, kv_heads, (int)ntiles, c2,
@@ -567,7 +568,9 @@ void run_attention(const float* q, const float* k, const float* v, float* out, i
     } else if (d <= 128) {
         run_mfma<128>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2);
     } else {
-        const dim3 grid((unsigned)((Sq + kGenWaves - 1) / kGenWaves), (unsigned)heads, (unsigned)N);
+        const int64_t gx = (Sq + kGenWaves - 1) / kGenWaves;
+        need(gx * 64 * kGenWaves <= kMaxGridItems, op, "too many queries for one launch");
+        const dim3 grid((unsigned)gx, (unsigned)heads, (unsigned)N);
         if (causal)
             k_attn_generic<true><<<grid, 64 * kGenWaves, 0, stream()>>>(q, k, v, out, (int)Sq, (int)Skv, (int)inner,
                                                                          (int)kv_inner, (int)d, heads / kv_heads, c2);

@@ -25,7 +25,7 @@ __global__ __launch_bounds__(kThreads) void k_rows_vec(f4* __restrict__ x, const
                                                       const f4* __restrict__ v, int64_t n4, unsigned dim4) {
     const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (i >= n4) return;
-    const unsigned c = n4 <= 0xffffffffLL ? (unsigned)i % dim4 : (unsigned)(i % dim4);
+    const unsigned c = (unsigned)i % dim4;  // n4 <= kMaxGridItems per launch
     const f4 vv = v[c];
     const f4 xv = x[i];
     f4 o;
@@ -76,12 +76,16 @@ void run_rows(const char* op, float* x, const float* y, const float* v, int64_t 
     check_range(x, (size_t)(rows * dim) * 4, op, "x");
     if (K == B_ADD_SCALED) check_range(y, (size_t)(rows * dim) * 4, op, "y");
     check_range(v, (size_t)dim * 4, op, K == B_ADD_SCALED ? "g" : "v");
-    const bool vec = dim % 4 == 0 && rows * dim / 4 <= 0x7fffffffLL * kThreads && aligned16(x) && aligned16(v) &&
+    const bool vec = dim % 4 == 0 && dim / 4 <= kMaxGridItems && aligned16(x) && aligned16(v) &&
                      (K != B_ADD_SCALED || aligned16(y));
     if (vec) {
-        const int64_t n4 = rows * dim / 4;
-        k_rows_vec<K><<<blocks_for(n4, kThreads), kThreads, 0, stream()>>>((f4*)x, (const f4*)y, (const f4*)v, n4,
-                                                                            (unsigned)(dim / 4));
+        // whole rows per launch, so the column of element i is i % dim4 in every launch
+        const int64_t dim4 = dim / 4;
+        in_pieces(rows, units_per_launch(dim4), [&](int64_t r0, int64_t nr) {
+            k_rows_vec<K><<<blocks_for(nr * dim4, kThreads), kThreads, 0, stream()>>>(
+                (f4*)x + r0 * dim4, K == B_ADD_SCALED ? (const f4*)y + r0 * dim4 : nullptr, (const f4*)v, nr * dim4,
+                (unsigned)dim4);
+        });
     } else {
         k_rows_scalar<K><<<stride_grid(rows * dim), kThreads, 0, stream()>>>(x, y, v, rows, dim);
     }

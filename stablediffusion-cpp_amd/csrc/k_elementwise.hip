@@ -205,6 +205,17 @@ __global__ __launch_bounds__(kThreads) void k_fill_normal(float* __restrict__ ou
     }
 }
 
+// The float4 kernels above map one work-item to one float4 (kUnroll = 1):
+// calls launch(first, count, last) over [0, n4) in pieces a dispatch can
+// cover; the scalar tail goes with the last piece (n4 = 0: one empty piece
+// that only does the tail).
+template <class F>
+void vec_pieces(int64_t n4, F&& launch) {
+    static_assert(kUnroll == 1, "pieces are sized for one float4 per work-item");
+    const int64_t units = std::max<int64_t>(n4, 1);
+    in_pieces(units, launch_items(), [&](int64_t f, int64_t c) { launch(f, std::min(c, n4 - f), f + c == units); });
+}
+
 // Grid for grid-stride scalar kernels: enough blocks to fill the chip.
 unsigned stride_grid(int64_t n) {
     const int64_t want = (n + kThreads - 1) / kThreads;
@@ -221,8 +232,10 @@ void run_unary(const char* op, float* x, int64_t n, float a, float b) {
     if (aligned16(x)) {
         const int64_t n4 = n / 4;
         const int tail = (int)(n - n4 * 4);
-        k_unary<K><<<blocks_for(std::max<int64_t>(n4, 1), kPerBlock), kThreads, 0, stream()>>>(
-            (f4*)x, n4, x + n4 * 4, tail, a, b);
+        vec_pieces(n4, [&](int64_t f, int64_t c, bool last) {
+            k_unary<K><<<blocks_for(std::max<int64_t>(c, 1), kPerBlock), kThreads, 0, stream()>>>(
+                (f4*)x + f, c, x + n4 * 4, last ? tail : 0, a, b);
+        });
     } else {
         k_unary_scalar<K><<<stride_grid(n), kThreads, 0, stream()>>>(x, n, a, b);
     }
@@ -235,8 +248,11 @@ void launch_swiglu(const float* gate, const float* up, float* y, int64_t n) {
     if (aligned16(gate) && aligned16(up) && aligned16(y)) {
         const int64_t n4 = n / 4;
         const int tail = (int)(n - n4 * 4);
-        k_swiglu<<<blocks_for(std::max<int64_t>(n4, 1), kPerBlock), kThreads, 0, stream()>>>(
-            (const f4*)gate, (const f4*)up, (f4*)y, n4, gate + n4 * 4, up + n4 * 4, y + n4 * 4, tail);
+        vec_pieces(n4, [&](int64_t f, int64_t c, bool last) {
+            k_swiglu<<<blocks_for(std::max<int64_t>(c, 1), kPerBlock), kThreads, 0, stream()>>>(
+                (const f4*)gate + f, (const f4*)up + f, (f4*)y + f, c, gate + n4 * 4, up + n4 * 4, y + n4 * 4,
+                last ? tail : 0);
+        });
     } else {
         k_swiglu_scalar<<<stride_grid(n), kThreads, 0, stream()>>>(gate, up, y, n);
     }
@@ -269,9 +285,11 @@ int sdh_swiglu_bf16(const float* gate, const float* up, uint16_t* y, int64_t n) 
         if (aligned16(gate) && aligned16(up) && ((uintptr_t)y & 7) == 0) {
             const int64_t n4 = n / 4;
             const int tail = (int)(n - n4 * 4);
-            k_swiglu_bf16<<<blocks_for(std::max<int64_t>(n4, 1), kThreads), kThreads, 0, stream()>>>(
-                (const f4*)gate, (const f4*)up, (uint2*)y, n4, gate + n4 * 4, up + n4 * 4,
-                (unsigned short*)y + n4 * 4, tail);
+            vec_pieces(n4, [&](int64_t f, int64_t c, bool last) {
+                k_swiglu_bf16<<<blocks_for(std::max<int64_t>(c, 1), kThreads), kThreads, 0, stream()>>>(
+                    (const f4*)gate + f, (const f4*)up + f, (uint2*)y + f, c, gate + n4 * 4, up + n4 * 4,
+                    (unsigned short*)y + n4 * 4, last ? tail : 0);
+            });
         } else {
             k_swiglu_bf16_scalar<<<stride_grid(n), kThreads, 0, stream()>>>(gate, up, (unsigned short*)y, n);
         }
@@ -301,9 +319,12 @@ int sdh_geglu(const float* x, float* y, int64_t rows, int64_t D) {
         ensure_init();
         check_range(x, (size_t)(rows * 2 * D) * 4, op, "x");
         check_range(y, (size_t)(rows * D) * 4, op, "y");
-        if (D % 4 == 0 && aligned16(x) && aligned16(y)) {
-            const int64_t n4 = rows * D / 4;
-            k_geglu_vec<<<blocks_for(n4, kThreads), kThreads, 0, stream()>>>((const f4*)x, (f4*)y, n4, D / 4);
+        if (D % 4 == 0 && D / 4 <= kMaxGridItems && aligned16(x) && aligned16(y)) {
+            const int64_t D4 = D / 4;
+            in_pieces(rows, units_per_launch(D4), [&](int64_t r0, int64_t nr) {
+                k_geglu_vec<<<blocks_for(nr * D4, kThreads), kThreads, 0, stream()>>>(
+                    (const f4*)x + r0 * 2 * D4, (f4*)y + r0 * D4, nr * D4, D4);
+            });
         } else {
             k_geglu<<<stride_grid(rows * D), kThreads, 0, stream()>>>(x, y, rows, D);
         }
@@ -333,8 +354,10 @@ int sdh_add(float* a, const float* b, int64_t n) {
         if (aligned16(a) && aligned16(b)) {
             const int64_t n4 = n / 4;
             const int tail = (int)(n - n4 * 4);
-            k_add<<<blocks_for(std::max<int64_t>(n4, 1), kPerBlock), kThreads, 0, stream()>>>(
-                (f4*)a, (const f4*)b, n4, a + n4 * 4, b + n4 * 4, tail);
+            vec_pieces(n4, [&](int64_t f, int64_t c, bool last) {
+                k_add<<<blocks_for(std::max<int64_t>(c, 1), kPerBlock), kThreads, 0, stream()>>>(
+                    (f4*)a + f, (const f4*)b + f, c, a + n4 * 4, b + n4 * 4, last ? tail : 0);
+            });
         } else {
             k_add_scalar<<<stride_grid(n), kThreads, 0, stream()>>>(a, b, n);
         }

@@ -507,13 +507,13 @@ void run_gemm(const char* op, int64_t M, int64_t N, int64_t K, const float* A, i
         if (K % 64 == 0) {
             const int bn = EPI == E_SWIGLU ? kDN / 2 : kDN;
             const int64_t gx = (N + bn - 1) / bn, gym = (M + kDM - 1) / kDM;
-            need(gym <= 65535, op, "too many rows for one launch");
+            need(gym <= 65535 && gx * kDT <= kMaxGridItems, op, "matrix too large for one launch");
             k_gemm_dl<EPI><<<dim3((unsigned)gx, (unsigned)gym), kDT, 0, stream()>>>(
                 P, B0, B1, ldb, C, ldc, bias, (int)M, (int)N, (int)K, accumulate ? 1 : 0);
         } else {
             const int bn = EPI == E_SWIGLU ? kBN / 2 : kBN;
             const int64_t gx = (N + bn - 1) / bn, gym = (M + kBM - 1) / kBM;
-            need(gym <= 65535, op, "too many rows for one launch");
+            need(gym <= 65535 && gx * kGT <= kMaxGridItems, op, "matrix too large for one launch");
             k_gemm_bf16<EPI><<<dim3((unsigned)gx, (unsigned)gym), kGT, 0, stream()>>>(
                 P, B0, B1, ldb, C, ldc, bias, (int)M, (int)N, (int)K, accumulate ? 1 : 0);
         }
@@ -558,12 +558,12 @@ void run_gemm_packed(int64_t M, int64_t N, int64_t K, const u16* A, int64_t lda,
     }
     if (K % 64 == 0) {
         const int64_t gx = (N + kDN - 1) / kDN, gym = (M + kDM - 1) / kDM;
-        need(gym <= 65535, op, "too many rows for one launch");
+        need(gym <= 65535 && gx * kDT <= kMaxGridItems, op, "matrix too large for one launch");
         k_gemm_dl<E_LINEAR><<<dim3((unsigned)gx, (unsigned)gym), kDT, 0, stream()>>>(
             P, B, nullptr, ldb, C, ldc, bias, (int)M, (int)N, (int)K, accumulate ? 1 : 0);
     } else {
         const int64_t gx = (N + kBN - 1) / kBN, gym = (M + kBM - 1) / kBM;
-        need(gym <= 65535, op, "too many rows for one launch");
+        need(gym <= 65535 && gx * kGT <= kMaxGridItems, op, "matrix too large for one launch");
         k_gemm_bf16<E_LINEAR><<<dim3((unsigned)gx, (unsigned)gym), kGT, 0, stream()>>>(
             P, B, nullptr, ldb, C, ldc, bias, (int)M, (int)N, (int)K, accumulate ? 1 : 0);
     }

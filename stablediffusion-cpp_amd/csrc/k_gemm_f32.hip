@@ -117,7 +117,7 @@ void run_gemm_f32(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, 
     check_range(C, (size_t)((M - 1) * ldc + N) * 4, op, "C");
     if (bias) check_range(bias, (size_t)N * 4, op, "bias");
     const int64_t gx = (N + kT - 1) / kT, gy = (M + kT - 1) / kT;
-    need(gy <= 65535 && gx < (1LL << 31), op, "matrix too large for one launch");
+    need(gy <= 65535 && gx * kThreads <= kMaxGridItems, op, "matrix too large for one launch");
     const bool vec = K % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 && aligned(A, 16) && aligned(B, 16);
     const dim3 grid((unsigned)gx, (unsigned)gy);
     if (vec)

@@ -329,6 +329,17 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
     check_range(y, bytes, op, "y");
     check_range(gamma, (size_t)C * 4, op, "gamma");
     check_range(beta, (size_t)C * 4, op, "beta");
+    // the single-pass and generic kernels run one workgroup (up to 1024
+    // work-items) per (sample, group) segment: samples beyond what one
+    // dispatch covers go in several launches
+    need((int64_t)groups * 1024 <= kMaxGridItems, op, "too many groups for one launch");
+    const int64_t samples_per_launch = units_per_launch((int64_t)groups * 1024);
+    if (N > samples_per_launch) {
+        in_pieces(N, samples_per_launch, [&](int64_t n0, int64_t nn) {
+            run_gn(op, silu, x + n0 * C * HW, y + n0 * C * HW, nn, C, HW, groups, gamma, beta, eps);
+        });
+        return;
+    }
     const int64_t cg = C / groups, L = cg * HW, nseg = N * groups;
     const bool vec = HW % 4 == 0 && aligned16(x) && aligned16(y) && L < (1LL << 31);
     if (vec && L <= (int64_t)1024 * 4 * 16 && nseg <= 0x7fffffffLL) {

@@ -179,7 +179,8 @@ void run_transpose(const char* op, const float* x, float* y, int64_t B, int64_t 
     check_range(y, bytes, op, "y");
     need(!overlaps(x, bytes, y, bytes), op, "output overlaps input");
     const bool vec = R % 4 == 0 && K % 4 == 0 && aligned16(x) && aligned16(y) && R < (1LL << 31) &&
-                     K < (1LL << 31) && B <= 65535 && (R + kTile - 1) / kTile <= 65535;
+                     K < (1LL << 31) && B <= 65535 && (R + kTile - 1) / kTile <= 65535 &&
+                     (K + kTile - 1) / kTile * kThreads <= kMaxGridItems;
     if (vec) {
         const dim3 grid((unsigned)((K + kTile - 1) / kTile), (unsigned)((R + kTile - 1) / kTile), (unsigned)B);
         k_transpose_vec<<<grid, kThreads, 0, stream()>>>(x, y, (int)R, (int)K);
@@ -257,8 +258,7 @@ int sdh_concat_channels(const float* a, const float* b, float* y, int64_t N, int
         need(!(na && overlaps(a, na, y, ny)) && !(nb && overlaps(b, nb, y, ny)), op, "output overlaps an input");
         const int64_t na4 = Ca * HW / 4, nb4 = Cb * HW / 4;
         const bool vec = (Ca * HW) % 4 == 0 && (Cb * HW) % 4 == 0 && (na == 0 || aligned16(a)) &&
-                         (nb == 0 || aligned16(b)) && aligned16(y) && na4 + nb4 < (1LL << 32) - kThreads &&
-                         N <= 65535;
+                         (nb == 0 || aligned16(b)) && aligned16(y) && na4 + nb4 <= kMaxGridItems && N <= 65535;
         if (vec) {
             const dim3 grid(blocks_for(na4 + nb4, kThreads), (unsigned)N);
             k_concat_vec<<<grid, kThreads, 0, stream()>>>((const f4*)a, (const f4*)b, (f4*)y, (unsigned)na4,

@@ -212,12 +212,30 @@ void run_rope(const char* op, float* q, int64_t inner_q, float* k, int64_t inner
     need(inner_q % dim == 0 && inner_k % dim == 0, op, "inner must be a multiple of dim");
     const int nt = k ? 2 : 1;
     if (N == 0 || S == 0 || (inner_q == 0 && (!k || inner_k == 0))) return;
-    need(N * S <= 0x7fffffffLL, op, "too many token rows");
     ensure_init();
     check_range(q, (size_t)(N * S * inner_q) * 4, op, "x/q");
     if (k) check_range(k, (size_t)(N * S * inner_k) * 4, op, "k");
     check_range(cs, (size_t)(S * dim) * 4, op, "cos");
     check_range(sn, (size_t)(S * dim) * 4, op, "sin");
+    // one workgroup per token row: rows beyond what one dispatch covers go in
+    // several launches, of whole sequences, or of parts of one sequence with
+    // the tables offset to the part's first position
+    const int64_t max_tok = units_per_launch(kThreads);
+    if (N * S > max_tok) {
+        if (S <= max_tok) {
+            in_pieces(N, max_tok / S, [&](int64_t n0, int64_t nn) {
+                run_rope(op, q + n0 * S * inner_q, inner_q, k ? k + n0 * S * inner_k : nullptr, inner_k, nn, S, dim,
+                         cs, sn, interleaved);
+            });
+        } else {
+            for (int64_t n = 0; n < N; ++n)
+                in_pieces(S, max_tok, [&](int64_t s0, int64_t ns) {
+                    run_rope(op, q + (n * S + s0) * inner_q, inner_q, k ? k + (n * S + s0) * inner_k : nullptr,
+                             inner_k, 1, ns, dim, cs + s0 * dim, sn + s0 * dim, interleaved);
+                });
+        }
+        return;
+    }
     RopeArgs a;
     a.x[0] = q;
     a.inner[0] = inner_q;
@@ -379,7 +397,7 @@ bool run_qknorm_rope_fused(float* q, int64_t inner_q, float* k, int64_t inner_k,
                            int interleaved) {
     const bool al = aligned16(q) && aligned16(k) && aligned16(cs) && aligned16(sn) && (!gq || aligned16(gq)) &&
                     (!gk || aligned16(gk));
-    if (!al || dim % 8 != 0 || N * S > 0x7fffffffLL) return false;
+    if (!al || dim % 8 != 0 || N * S * kThreads > kMaxGridItems) return false;
     const int64_t L = interleaved ? dim / 4 : dim / 8;
     if (!(L == 4 || L == 8 || L == 16 || L == 32 || L == 64)) return false;
     const int64_t inner_max = std::max(inner_q, inner_k);

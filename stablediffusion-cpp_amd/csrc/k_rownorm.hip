@@ -475,9 +475,13 @@ unsigned row_grid(int64_t rows, int waves_per_cu) {
 // One wave per row (or per unit), 4 per workgroup, covering all of them.
 unsigned exact_grid(int64_t units) {
     const int64_t b = (units + kWaves - 1) / kWaves;
-    need(b <= 0x7fffffffLL, "backend_hip", "too many rows for one launch");
+    need(b * kThreads <= kMaxGridItems, "backend_hip", "too many rows for one launch");
     return (unsigned)std::max<int64_t>(1, b);
 }
+
+// Rows one launch of the one-wave-per-row kernels covers; the entry points
+// split larger tensors into launches of at most this many rows.
+int64_t rows_per_launch() { return units_per_launch(64); }
 
 // Calls f(std::integral_constant<int, V>) for the runtime V.
 template <class F>
@@ -513,6 +517,12 @@ void run_rownorm(const char* op, int mode, const float* x, float* y, int64_t row
     check_range(y, bytes, op, "y");
     if (gamma) check_range(gamma, (size_t)C * 4, op, "gamma");
     if (beta) check_range(beta, (size_t)C * 4, op, "beta");
+    if (rows > rows_per_launch()) {
+        in_pieces(rows, rows_per_launch(), [&](int64_t r0, int64_t nr) {
+            run_rownorm(op, mode, x + r0 * C, y + r0 * C, nr, C, gamma, beta, eps);
+        });
+        return;
+    }
     if (vec_ok(C, {x, y, gamma, beta})) {
         const int v = pick_v(C / 4);
         const unsigned grid = exact_grid(rows);
@@ -560,6 +570,12 @@ void run_rms_mod_bf16(const float* x, uint16_t* y, int64_t rows, int64_t C, cons
     if (gamma) check_range(gamma, (size_t)C * 4, op, "gamma");
     if (scale) check_range(scale, (size_t)C * 4, op, "scale");
     need(!overlaps(x, (size_t)(rows * C) * 4, y, (size_t)(rows * C) * 2), op, "y overlaps x");
+    if (rows > rows_per_launch()) {
+        in_pieces(rows, rows_per_launch(), [&](int64_t r0, int64_t nr) {
+            run_rms_mod_bf16(x + r0 * C, y + r0 * C, nr, C, gamma, scale, eps);
+        });
+        return;
+    }
     if (vec_ok(C, {x, gamma, scale}) && ((uintptr_t)y & 7) == 0) {
         const unsigned grid = exact_grid(rows);
         with_v(pick_v(C / 4), [&](auto vc) {
@@ -593,6 +609,12 @@ void run_rms_gated_add(float* x, const float* a, int64_t rows, int64_t C, const 
     if (gamma) check_range(gamma, (size_t)C * 4, op, "gamma");
     if (gate) check_range(gate, (size_t)C * 4, op, "gate");
     need(!overlaps(x, bytes, a, bytes), op, "x overlaps a");
+    if (rows > rows_per_launch()) {
+        in_pieces(rows, rows_per_launch(), [&](int64_t r0, int64_t nr) {
+            run_rms_gated_add(x + r0 * C, a + r0 * C, nr, C, gamma, gate, eps);
+        });
+        return;
+    }
     if (vec_ok(C, {x, a, gamma, gate})) {
         const unsigned grid = exact_grid(rows);
         with_v(pick_v(C / 4), [&](auto vc) {
@@ -651,13 +673,16 @@ int sdh_add_rms_norm(float* x, const float* r, float* y, int64_t rows, int64_t C
         check_range(y, bytes, op, "y");
         if (gamma) check_range(gamma, (size_t)C * 4, op, "gamma");
         if (vec_ok(C, {x, r, y, gamma})) {
-            const unsigned grid = exact_grid(rows);
-            with_v(pick_v(C / 4), [&](auto vc) {
-                constexpr int V = decltype(vc)::value;
-                if (gamma)
-                    k_add_rms<V, true><<<grid, kThreads, 0, stream()>>>(x, r, y, rows, (int)C, gamma, eps);
-                else
-                    k_add_rms<V, false><<<grid, kThreads, 0, stream()>>>(x, r, y, rows, (int)C, gamma, eps);
+            in_pieces(rows, rows_per_launch(), [&](int64_t r0, int64_t nr) {
+                const unsigned grid = exact_grid(nr);
+                const int64_t o = r0 * C;
+                with_v(pick_v(C / 4), [&](auto vc) {
+                    constexpr int V = decltype(vc)::value;
+                    if (gamma)
+                        k_add_rms<V, true><<<grid, kThreads, 0, stream()>>>(x + o, r + o, y + o, nr, (int)C, gamma, eps);
+                    else
+                        k_add_rms<V, false><<<grid, kThreads, 0, stream()>>>(x + o, r + o, y + o, nr, (int)C, gamma, eps);
+                });
             });
         } else {
             k_add_rms_generic<<<row_grid(rows, 32), kThreads, 0, stream()>>>(x, r, y, rows, C, gamma, eps);
@@ -684,28 +709,33 @@ int sdh_ln_modulate_gate(const float* x, float* res, const float* scale, const f
         const int64_t n4 = C / 4;
         const int v = n4 <= 128 ? 1 : n4 <= 256 ? 2 : n4 <= 512 ? 4 : n4 <= 1024 ? 8 : n4 <= 1536 ? 12 : n4 <= 2048 ? 16 : 0;
         if (vec_ok(C, {x, res, scale, shift, gate, y_out}) && lds <= 64 * 1024 && v) {
-            const int64_t blocks = (rows + kModRows - 1) / kModRows;
-            need(blocks <= 0x7fffffffLL, op, "too many rows for one launch");
-            const unsigned grid = (unsigned)blocks;
-            auto go = [&](auto vc) {
-                constexpr int V = decltype(vc)::value;
-                if (shift && y_out)
-                    k_ln_mod_gate<V, true, true><<<grid, kModThreads, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
-                else if (shift)
-                    k_ln_mod_gate<V, true, false><<<grid, kModThreads, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
-                else if (y_out)
-                    k_ln_mod_gate<V, false, true><<<grid, kModThreads, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
-                else
-                    k_ln_mod_gate<V, false, false><<<grid, kModThreads, lds, stream()>>>(x, res, scale, shift, gate, y_out, rows, (int)C, eps);
-            };
-            switch (v) {
-                case 1: go(std::integral_constant<int, 1>()); break;
-                case 2: go(std::integral_constant<int, 2>()); break;
-                case 4: go(std::integral_constant<int, 4>()); break;
-                case 8: go(std::integral_constant<int, 8>()); break;
-                case 12: go(std::integral_constant<int, 12>()); break;
-                default: go(std::integral_constant<int, 16>()); break;
-            }
+            // two waves (128 work-items) per row
+            in_pieces(rows, units_per_launch(128), [&](int64_t r0, int64_t nr) {
+                const unsigned grid = blocks_for(nr, kModRows);
+                const int64_t o = r0 * C;
+                const float* xp = x + o;
+                float* rp = res + o;
+                float* yp = y_out ? y_out + o : nullptr;
+                auto go = [&](auto vc) {
+                    constexpr int V = decltype(vc)::value;
+                    if (shift && y_out)
+                        k_ln_mod_gate<V, true, true><<<grid, kModThreads, lds, stream()>>>(xp, rp, scale, shift, gate, yp, nr, (int)C, eps);
+                    else if (shift)
+                        k_ln_mod_gate<V, true, false><<<grid, kModThreads, lds, stream()>>>(xp, rp, scale, shift, gate, yp, nr, (int)C, eps);
+                    else if (y_out)
+                        k_ln_mod_gate<V, false, true><<<grid, kModThreads, lds, stream()>>>(xp, rp, scale, shift, gate, yp, nr, (int)C, eps);
+                    else
+                        k_ln_mod_gate<V, false, false><<<grid, kModThreads, lds, stream()>>>(xp, rp, scale, shift, gate, yp, nr, (int)C, eps);
+                };
+                switch (v) {
+                    case 1: go(std::integral_constant<int, 1>()); break;
+                    case 2: go(std::integral_constant<int, 2>()); break;
+                    case 4: go(std::integral_constant<int, 4>()); break;
+                    case 8: go(std::integral_constant<int, 8>()); break;
+                    case 12: go(std::integral_constant<int, 12>()); break;
+                    default: go(std::integral_constant<int, 16>()); break;
+                }
+            });
         } else {
             k_ln_mod_gate_generic<<<row_grid(rows, 32), kThreads, 0, stream()>>>(x, res, scale, shift, gate, y_out,
                                                                                 rows, C, eps);
@@ -726,22 +756,25 @@ int sdh_rms_norm_heads(float* x, int64_t groups, int64_t dim, const float* gamma
         const bool vec = dim % 4 == 0 && (L == 4 || L == 8 || L == 16 || L == 32 || L == 64) && aligned16(x) &&
                          (!gamma || aligned16(gamma));
         if (vec) {
-            const int64_t waves = (groups + (64 / L) - 1) / (64 / L);
-            const unsigned grid = exact_grid(waves);
-            auto go = [&](auto lc) {
-                constexpr int LL = decltype(lc)::value;
-                if (gamma)
-                    k_heads<LL, true><<<grid, kThreads, 0, stream()>>>(x, groups, (int)dim, gamma, eps);
-                else
-                    k_heads<LL, false><<<grid, kThreads, 0, stream()>>>(x, groups, (int)dim, gamma, eps);
-            };
-            switch (L) {
-                case 4: go(std::integral_constant<int, 4>()); break;
-                case 8: go(std::integral_constant<int, 8>()); break;
-                case 16: go(std::integral_constant<int, 16>()); break;
-                case 32: go(std::integral_constant<int, 32>()); break;
-                default: go(std::integral_constant<int, 64>()); break;
-            }
+            // L work-items per group; pieces of 2^31 / L groups are whole waves
+            in_pieces(groups, units_per_launch(L), [&](int64_t g0, int64_t ng) {
+                const unsigned grid = exact_grid((ng + (64 / L) - 1) / (64 / L));
+                float* xp = x + g0 * dim;
+                auto go = [&](auto lc) {
+                    constexpr int LL = decltype(lc)::value;
+                    if (gamma)
+                        k_heads<LL, true><<<grid, kThreads, 0, stream()>>>(xp, ng, (int)dim, gamma, eps);
+                    else
+                        k_heads<LL, false><<<grid, kThreads, 0, stream()>>>(xp, ng, (int)dim, gamma, eps);
+                };
+                switch (L) {
+                    case 4: go(std::integral_constant<int, 4>()); break;
+                    case 8: go(std::integral_constant<int, 8>()); break;
+                    case 16: go(std::integral_constant<int, 16>()); break;
+                    case 32: go(std::integral_constant<int, 32>()); break;
+                    default: go(std::integral_constant<int, 64>()); break;
+                }
+            });
         } else {
             k_rownorm_generic<M_RMS><<<row_grid(groups, 32), kThreads, 0, stream()>>>(x, x, groups, dim, gamma,
                                                                                      nullptr, eps);

@@ -54,13 +54,13 @@ __device__ __forceinline__ int valid_cols(int64_t row, int64_t period, int cols,
 // One wave per row (n4 <= 64 * V).
 template <int V, bool CAUSAL>
 __global__ __launch_bounds__(kThreads) void k_softmax_wave(float* __restrict__ x, int64_t rows, int cols, float scale,
-                                                          int64_t period) {
+                                                          int64_t period, int64_t row0) {
     const int lane = threadIdx.x & 63;
     const int n4 = cols >> 2;
     const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
     if (row >= rows) return;
     f4* p = (f4*)(x + row * cols);
-    const int valid = valid_cols(row, period, cols, CAUSAL);
+    const int valid = valid_cols(row0 + row, period, cols, CAUSAL);
     f4 v[V];
     float m = -INFINITY;
 #pragma unroll
@@ -85,14 +85,14 @@ __global__ __launch_bounds__(kThreads) void k_softmax_wave(float* __restrict__ x
 
 // One workgroup of TPB threads per row (n4 <= TPB * V).
 template <int TPB, int V, bool CAUSAL>
-__global__ __launch_bounds__(TPB) void k_softmax_block(float* __restrict__ x, int cols, float scale, int64_t period) {
+__global__ __launch_bounds__(TPB) void k_softmax_block(float* __restrict__ x, int cols, float scale, int64_t period, int64_t row0) {
     constexpr int W = TPB / 64;
     __shared__ float sh[2 * W];
     const int w = threadIdx.x >> 6;
     const int n4 = cols >> 2;
     const int64_t row = blockIdx.x;
     f4* p = (f4*)(x + row * cols);
-    const int valid = valid_cols(row, period, cols, CAUSAL);
+    const int valid = valid_cols(row0 + row, period, cols, CAUSAL);
     f4 v[V];
     float m = -INFINITY;
 #pragma unroll
@@ -151,31 +151,33 @@ __global__ __launch_bounds__(kThreads) void k_softmax_generic(float* __restrict_
     }
 }
 
-unsigned exact_grid(int64_t rows) {
-    const int64_t b = (rows + kWaves - 1) / kWaves;
-    need(b <= 0x7fffffffLL, "sdh_softmax_rows", "too many rows for one launch");
-    return (unsigned)std::max<int64_t>(1, b);
-}
-
+// The vector kernels' grids cover their rows exactly, so rows beyond what one
+// dispatch covers go in several launches; row0 keeps the causal phase.
 template <bool CAUSAL>
 bool launch_vec(float* x, int64_t rows, int cols, float scale, int64_t period) {
     const int n4 = cols / 4;
     hipStream_t st = stream();
     if (n4 <= 256) {
-        const unsigned g = exact_grid(rows);
-        if (n4 <= 64) k_softmax_wave<1, CAUSAL><<<g, kThreads, 0, st>>>(x, rows, cols, scale, period);
-        else if (n4 <= 128) k_softmax_wave<2, CAUSAL><<<g, kThreads, 0, st>>>(x, rows, cols, scale, period);
-        else if (n4 <= 192) k_softmax_wave<3, CAUSAL><<<g, kThreads, 0, st>>>(x, rows, cols, scale, period);
-        else k_softmax_wave<4, CAUSAL><<<g, kThreads, 0, st>>>(x, rows, cols, scale, period);
+        in_pieces(rows, units_per_launch(64), [&](int64_t r0, int64_t nr) {
+            const unsigned g = blocks_for(nr, kWaves);
+            float* xp = x + r0 * cols;
+            if (n4 <= 64) k_softmax_wave<1, CAUSAL><<<g, kThreads, 0, st>>>(xp, nr, cols, scale, period, r0);
+            else if (n4 <= 128) k_softmax_wave<2, CAUSAL><<<g, kThreads, 0, st>>>(xp, nr, cols, scale, period, r0);
+            else if (n4 <= 192) k_softmax_wave<3, CAUSAL><<<g, kThreads, 0, st>>>(xp, nr, cols, scale, period, r0);
+            else k_softmax_wave<4, CAUSAL><<<g, kThreads, 0, st>>>(xp, nr, cols, scale, period, r0);
+        });
         return true;
     }
-    need(rows <= 0x7fffffffLL, "sdh_softmax_rows", "too many rows for one launch");
-    const unsigned g = (unsigned)rows;
-    if (n4 <= 512) k_softmax_block<256, 2, CAUSAL><<<g, 256, 0, st>>>(x, cols, scale, period);
-    else if (n4 <= 1024) k_softmax_block<512, 2, CAUSAL><<<g, 512, 0, st>>>(x, cols, scale, period);
-    else if (n4 <= 2048) k_softmax_block<1024, 2, CAUSAL><<<g, 1024, 0, st>>>(x, cols, scale, period);
-    else if (n4 <= 4096) k_softmax_block<1024, 4, CAUSAL><<<g, 1024, 0, st>>>(x, cols, scale, period);
-    else return false;
+    const int tpb = n4 <= 512 ? 256 : n4 <= 1024 ? 512 : 1024;
+    if (n4 > 4096) return false;
+    in_pieces(rows, units_per_launch(tpb), [&](int64_t r0, int64_t nr) {
+        const unsigned g = (unsigned)nr;
+        float* xp = x + r0 * cols;
+        if (n4 <= 512) k_softmax_block<256, 2, CAUSAL><<<g, 256, 0, st>>>(xp, cols, scale, period, r0);
+        else if (n4 <= 1024) k_softmax_block<512, 2, CAUSAL><<<g, 512, 0, st>>>(xp, cols, scale, period, r0);
+        else if (n4 <= 2048) k_softmax_block<1024, 2, CAUSAL><<<g, 1024, 0, st>>>(xp, cols, scale, period, r0);
+        else k_softmax_block<1024, 4, CAUSAL><<<g, 1024, 0, st>>>(xp, cols, scale, period, r0);
+    });
     return true;
 }
 

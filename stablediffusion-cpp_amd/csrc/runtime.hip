@@ -243,6 +243,18 @@ void hip_check(hipError_t e, const char* what) {
     }
 }
 
+int64_t launch_items() {
+    static const int64_t v = [] {
+        const char* e = std::getenv("SDH_LAUNCH_ITEMS");
+        if (!e || !*e) return kMaxGridItems;
+        char* end = nullptr;
+        const long long n = std::strtoll(e, &end, 10);
+        if (!end || *end != 0 || n <= 0) return kMaxGridItems;
+        return std::max<int64_t>(1024, std::min<int64_t>(n, kMaxGridItems));
+    }();
+    return v;
+}
+
 void launched(const char* op) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) fail(SDH_ERR_HIP, std::string(op) + ": kernel launch failed: " + hipGetErrorString(e));

@@ -80,6 +80,33 @@ inline unsigned blocks_for(int64_t items, int64_t per_block) {
     return (unsigned)(b < 1 ? 1 : b);
 }
 
+// A dispatch covers at most 2^32 - 1 work-items per grid dimension (the
+// dispatch packet holds the grid size in work-items as a uint32); a larger
+// grid is not rejected, it wraps and covers less than asked. Launchers whose
+// grid grows with the tensor keep each launch at or below kMaxGridItems
+// work-items and cover larger tensors in several launches.
+constexpr int64_t kMaxGridItems = int64_t(1) << 31;
+// The work-items per launch the splitting launchers aim for: kMaxGridItems,
+// or less when the environment variable SDH_LAUNCH_ITEMS asks for less (at
+// least 1024; a test knob that sends small tensors through the split path).
+int64_t launch_items();
+
+// Calls launch(first, count) for consecutive pieces of [0, units) of at most
+// per_launch units each.
+template <class F>
+inline void in_pieces(int64_t units, int64_t per_launch, F&& launch) {
+    if (per_launch < 1) per_launch = 1;
+    for (int64_t first = 0; first < units; first += per_launch)
+        launch(first, units - first < per_launch ? units - first : per_launch);
+}
+
+// Rows (or other units) one launch may cover when each takes items_per_unit
+// work-items; at least 1.
+inline int64_t units_per_launch(int64_t items_per_unit) {
+    const int64_t u = launch_items() / (items_per_unit < 1 ? 1 : items_per_unit);
+    return u < 1 ? 1 : u;
+}
+
 }  // namespace sdh
 
 // ---------------------------------------------------------------------------
