@@ -265,6 +265,59 @@ class LNModGate(Workload):
         return run, [hx, hr, hsc, hsh, hgt, hones]
 
 
+class RmsModBf16(Workload):
+    """The Z-Image block's norm before the projections, as the bf16 A of the GEMMs."""
+    name, kernel = "rms_norm_modulate_bf16", "k_rms_mod_bf16"
+    desc = ("Z-Image block: y16 = bf16(rms_norm(x) * w * (1 + scale)) (zimage.cpp:115-116, the GEMMs' bf16 A); "
+            "x [4096,3840], w, scale [3840]; eps 1e-5")
+    algo_bytes = T * D * 4 + T * D * 2 + 2 * D * 4
+
+    def make(self, be, i):
+        return dict(x=be.randn((T, D), 15000 + i), w=be.randn((D,), 15500 + i, 1.0, 0.1),
+                    sc=be.randn((D,), 15600 + i, 1.0, 0.2), y16=be.array(np.zeros(T * D, np.uint16)))
+
+    def step(self, be, s):
+        be.rms_norm_modulate_bf16(s["x"], s["y16"], T, D, s["w"], s["sc"], 1e-5)
+
+    def cpu(self, R, orc):
+        x, w, sc = orc.randn((T, D), 15), orc.randn((D,), 16, 1.0, 0.1), orc.randn((D,), 17, 1.0, 0.2)
+        hx, hw, hsc = R.new(x.shape, x), R.new((D,), w), R.new((D,), sc)
+
+        def run():
+            y = R._ptr(R.lib.ref_rms_norm(hx, hw, 1e-5))
+            R._chk(R.lib.ref_mul_rows_(y, hsc))
+            return [y]
+
+        return run, [hx, hw, hsc]
+
+
+class RmsGatedAdd(Workload):
+    """The Z-Image block's norm + gated residual after to_out and w2."""
+    name, kernel = "rms_norm_gated_add", "k_rms_gated_add"
+    desc = ("Z-Image block: x += gate * rms_norm(a) * w (zimage.cpp:124-127); x, a [4096,3840], w, gate [3840]; "
+            "eps 1e-5")
+    algo_bytes = 3 * T * D * 4 + 2 * D * 4
+
+    def make(self, be, i):
+        return dict(x=be.randn((T, D), 16000 + i), a=be.randn((T, D), 16500 + i, 0.0, 3.0),
+                    w=be.randn((D,), 16600 + i, 1.0, 0.1), g=be.randn((D,), 16700 + i, 0.0, 0.5))
+
+    def step(self, be, s):
+        be.rms_norm_gated_add(s["x"], s["a"], T, D, s["w"], s["g"], 1e-5)
+
+    def cpu(self, R, orc):
+        x, a = orc.randn((T, D), 18), orc.randn((T, D), 19, 0.0, 3.0)
+        w, g = orc.randn((D,), 20, 1.0, 0.1), orc.randn((D,), 21, 0.0, 0.5)
+        hx, ha, hw, hg = R.new(x.shape, x), R.new(a.shape, a), R.new((D,), w), R.new((D,), g)
+
+        def run():
+            y = R._ptr(R.lib.ref_rms_norm(ha, hw, 1e-5))
+            R._chk(R.lib.ref_add_rows_scaled_(hx, y, hg))
+            return [y]
+
+        return run, [hx, ha, hw, hg]
+
+
 class Softmax(Workload):
     name, kernel = "softmax_rows", "k_softmax"
     desc = "config 5b: in-place row softmax of scores [30,4096,4096] ~N(0,3), scale 1/sqrt(128), non-causal"
@@ -515,6 +568,8 @@ def all_workloads():
         Softmax(),
         QKNormRope(),
         QKNormRope(unfused=True),
+        RmsModBf16(),
+        RmsGatedAdd(),
     ] + [Layout(n) for n in Layout.SPECS] + [Linear(k) for k in ("linear_bf16", "linear_swiglu", "linear_swiglu_unfused")] + [
         Attention(), ZImageStep()]
 

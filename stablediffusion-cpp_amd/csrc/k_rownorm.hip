@@ -377,7 +377,7 @@ __global__ __launch_bounds__(kThreads) void k_rms_mod_bf16(const float* __restri
             f4 o = v[j] * rstd;
             if constexpr (HAS_G) o = o * ((const f4*)gamma)[idx];
             if constexpr (HAS_S) o = o * ((const f4*)scale)[idx];
-            yr[idx] = dev::bf16x4(o);
+            dev::st_stream(yr + idx, dev::bf16x4(o));
         }
     }
 }
@@ -395,11 +395,18 @@ __global__ __launch_bounds__(kThreads) void k_rms_gated_add(float* __restrict__ 
     if (row >= rows) return;
     const f4* ar = (const f4*)(a + row * C);
     f4* xr = (f4*)(x + row * C);
-    f4 v[V];
+    // both rows are loaded before the reduction, so the x stream is in
+    // flight while the sum of squares is formed
+    f4 v[V], xv[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {
         const int idx = lane + 64 * j;
         v[j] = idx < n4 ? dev::ld_stream(ar + idx) : zero4();
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * j;
+        xv[j] = idx < n4 ? dev::ld_stream(xr + idx) : zero4();
     }
     float q = 0.f;
 #pragma unroll
@@ -415,13 +422,13 @@ __global__ __launch_bounds__(kThreads) void k_rms_gated_add(float* __restrict__ 
 #pragma clang fp contract(off)
             f4 o = v[j] * rstd;
             if constexpr (HAS_G) o = o * ((const f4*)gamma)[idx];
-            const f4 xv = dev::ld_stream(xr + idx);
+            const f4 xo = xv[j];
             f4 r;
             if constexpr (HAS_GATE) {
                 const f4 g = ((const f4*)gate)[idx];
-                r = f4{fmaf(g.x, o.x, xv.x), fmaf(g.y, o.y, xv.y), fmaf(g.z, o.z, xv.z), fmaf(g.w, o.w, xv.w)};
+                r = f4{fmaf(g.x, o.x, xo.x), fmaf(g.y, o.y, xo.y), fmaf(g.z, o.z, xo.z), fmaf(g.w, o.w, xo.w)};
             } else {
-                r = xv + o;
+                r = xo + o;
             }
             dev::st_stream(xr + idx, r);
         }

@@ -175,6 +175,10 @@ __device__ __forceinline__ float hsum(const f4& v) { return (v.x + v.y) + (v.z +
 // stored non-temporally so it does not displace reusable lines in L2/MALL.
 __device__ __forceinline__ f4 ld_stream(const f4* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_stream(f4* p, f4 v) { __builtin_nontemporal_store(v, p); }
+typedef unsigned u2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void st_stream(uint2* p, uint2 v) {
+    __builtin_nontemporal_store(u2v{v.x, v.y}, reinterpret_cast<u2v*>(p));
+}
 
 // exp(x) as 2^(x log2 e) on the hardware exp2 (v_exp_f32). Relative error
 // about |x| 2^-24 (from rounding x log2 e) plus 1 ulp; for ops whose bound

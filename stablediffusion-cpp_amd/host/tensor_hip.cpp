@@ -72,8 +72,8 @@ Tensor Tensor::empty_bf16(std::vector<int64_t> s) {
     return t;
 }
 
-float* Tensor::dptr() { return is_hip() && dev ? (float*)dev->p : nullptr; }
-const float* Tensor::dptr() const { return is_hip() && dev ? (const float*)dev->p : nullptr; }
+float* Tensor::dptr() { return is_hip() && dev ? (float*)dev->p + dev_off : nullptr; }
+const float* Tensor::dptr() const { return is_hip() && dev ? (const float*)dev->p + dev_off : nullptr; }
 
 float* Tensor::ptr() {
     if (is_hip()) throw std::runtime_error("tensor is on the GPU; host pointer requested " + shape_str());
@@ -96,16 +96,16 @@ Tensor Tensor::to(Device d) const {
         if (bytes) sd::hip::upload(t.dev->p, is_bf16() ? (const void*)data16.data() : (const void*)data.data(), bytes);
     } else if (is_bf16()) {
         t.data16.resize((size_t)numel());
-        if (bytes) sd::hip::download(t.data16.data(), dev->p, bytes);
+        if (bytes) sd::hip::download(t.data16.data(), dptr16(), bytes);
     } else {
         t.data.resize((size_t)numel());
-        if (bytes) sd::hip::download(t.data.data(), dev->p, bytes);
+        if (bytes) sd::hip::download(t.data.data(), dptr(), bytes);
     }
     return t;
 }
 
-const uint16_t* Tensor::dptr16() const { return is_hip() && dev ? (const uint16_t*)dev->p : nullptr; }
-uint16_t* Tensor::dptr16() { return is_hip() && dev ? (uint16_t*)dev->p : nullptr; }
+const uint16_t* Tensor::dptr16() const { return is_hip() && dev ? (const uint16_t*)dev->p + dev_off : nullptr; }
+uint16_t* Tensor::dptr16() { return is_hip() && dev ? (uint16_t*)dev->p + dev_off : nullptr; }
 
 // tensor.cpp:114-121 rounding (nearest even; inf and NaN keep their top bits)
 void Tensor::to_bf16() {
@@ -320,6 +320,19 @@ Tensor slice_rows(const Tensor& x, int64_t from, int64_t to) {
     const size_t bytes = (size_t)((to - from) * D) * sizeof(float);
     if (bytes) sd::hip::copy(y.dptr(), x.dptr() + from * D, bytes);
     return y;
+}
+
+Tensor rows_view(const Tensor& x, int64_t from, int64_t to) {
+    need_hip(x, "rows_view");
+    if (x.is_bf16()) throw std::runtime_error("rows_view: F32 tensors only");
+    const int64_t D = x.dim(-1), rows = x.numel() / D;
+    if (from < 0 || to > rows || from > to) throw std::runtime_error("rows_view: range out of bounds");
+    Tensor v;
+    v.shape = {to - from, D};
+    v.device = Device::HIP;
+    v.dev = x.dev;
+    v.dev_off = x.dev_off + from * D;
+    return v;
 }
 
 // tensor.cpp:982-1004

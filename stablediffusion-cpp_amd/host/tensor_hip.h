@@ -38,6 +38,7 @@ struct Tensor {
     DType dtype = DType::F32;
     Device device = Device::CPU;
     std::shared_ptr<DeviceBuffer> dev;  // device storage when device == HIP
+    int64_t dev_off = 0;                // first element within dev (rows_view)
 
     Tensor() = default;
     // Zero-filled host tensor (tensor.h:58).
@@ -99,6 +100,10 @@ void scale_(Tensor& x, float s);
 Tensor patchify2d(const Tensor& x, int p);  // x [1, C, H, W] -> [(H/p)(W/p), p*p*C]
 Tensor unpatchify2d(const Tensor& tokens, int64_t C, int64_t H, int64_t W, int p);
 Tensor slice_rows(const Tensor& x, int64_t from, int64_t to);
+// Rows [from, to) of a device tensor as a tensor that shares x's storage (no
+// copy; in-place ops on it change x). No counterpart in tensor.h, whose
+// slice_rows copies; used where a copy would only feed in-place ops.
+Tensor rows_view(const Tensor& x, int64_t from, int64_t to);
 Tensor upsample_nearest2x(const Tensor& x);
 Tensor concat_channels(const Tensor& a, const Tensor& b);
 Tensor concat_batch(const Tensor& a, const Tensor& b);

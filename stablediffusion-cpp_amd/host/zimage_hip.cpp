@@ -109,10 +109,11 @@ void ZImageTransformer::run_block(const Block& b, Tensor& x, const Tensor& cos, 
     if (mod) {
         Tensor m = b.adaln(*adaln);
         m.reshape({4, D});
-        scale_msa = slice_rows(m, 0, 1);
-        gate_msa = slice_rows(m, 1, 2);
-        scale_mlp = slice_rows(m, 2, 3);
-        gate_mlp = slice_rows(m, 3, 4);
+        // views, not copies: each row only feeds the in-place op that follows
+        scale_msa = rows_view(m, 0, 1);
+        gate_msa = rows_view(m, 1, 2);
+        scale_mlp = rows_view(m, 2, 3);
+        gate_mlp = rows_view(m, 3, 4);
         affine_(scale_msa, 1.0f, 1.0f);
         affine_(scale_mlp, 1.0f, 1.0f);
         tanh_(gate_msa);
