@@ -138,6 +138,10 @@ std::string Tensor::shape_str() const {
 
 namespace {
 
+// total / d, or 0 when d == 0: a zero-width row leaves the op nothing to do
+// (the backend returns at once for an empty extent) instead of dividing by zero
+int64_t count_of(int64_t total, int64_t d) { return d ? total / d : 0; }
+
 // The CPU branch of every op is the reference's tensor.cpp; this library
 // only implements the device branch.
 void need_hip(const Tensor& t, const char* op) {
@@ -159,7 +163,7 @@ Tensor group_norm(const Tensor& x, int groups, const Tensor& gamma, const Tensor
     need_hip(x, "group_norm");
     same_device(x, gamma, "group_norm");
     same_device(x, beta, "group_norm");
-    const int64_t N = x.dim(0), C = x.dim(1), HW = x.numel() / (N * C);
+    const int64_t N = x.dim(0), C = x.dim(1), HW = count_of(x.numel(), (N * C));
     if (C % groups != 0) throw std::runtime_error("group_norm: channels not divisible by groups");
     Tensor y = Tensor::empty(x.shape, Device::HIP);
     sd::hip::group_norm(x.dptr(), y.dptr(), N, C, HW, groups, gamma.dptr(), beta.dptr(), eps);
@@ -171,7 +175,7 @@ Tensor layer_norm(const Tensor& x, const Tensor* gamma, const Tensor* beta, floa
     need_hip(x, "layer_norm");
     if (gamma) same_device(x, *gamma, "layer_norm");
     if (beta) same_device(x, *beta, "layer_norm");
-    const int64_t C = x.dim(-1), rows = x.numel() / C;
+    const int64_t C = x.dim(-1), rows = count_of(x.numel(), C);
     Tensor y = Tensor::empty(x.shape, Device::HIP);
     sd::hip::layer_norm(x.dptr(), y.dptr(), rows, C, opt(gamma), opt(beta), eps);
     return y;
@@ -181,7 +185,7 @@ Tensor layer_norm(const Tensor& x, const Tensor* gamma, const Tensor* beta, floa
 Tensor rms_norm(const Tensor& x, const Tensor* gamma, float eps) {
     need_hip(x, "rms_norm");
     if (gamma) same_device(x, *gamma, "rms_norm");
-    const int64_t C = x.dim(-1), rows = x.numel() / C;
+    const int64_t C = x.dim(-1), rows = count_of(x.numel(), C);
     Tensor y = Tensor::empty(x.shape, Device::HIP);
     sd::hip::rms_norm(x.dptr(), y.dptr(), rows, C, opt(gamma), eps);
     return y;
@@ -191,13 +195,13 @@ Tensor rms_norm(const Tensor& x, const Tensor* gamma, float eps) {
 void rms_norm_heads_(Tensor& x, int64_t dim, const Tensor* gamma, float eps) {
     need_hip(x, "rms_norm_heads_");
     if (gamma) same_device(x, *gamma, "rms_norm_heads_");
-    sd::hip::rms_norm_heads(x.dptr(), x.numel() / dim, dim, opt(gamma), eps);
+    sd::hip::rms_norm_heads(x.dptr(), count_of(x.numel(), dim), dim, opt(gamma), eps);
 }
 
 // tensor.cpp:698-705
 void rope_(Tensor& x, int64_t dim, const Tensor& cos, const Tensor& sin, bool interleaved) {
     need_hip(x, "rope_");
-    const int64_t inner = x.dim(-1), S = x.dim(-2), N = x.numel() / (S * inner);
+    const int64_t inner = x.dim(-1), S = x.dim(-2), N = count_of(x.numel(), (S * inner));
     if (cos.dim(0) < S || cos.dim(1) != dim) throw std::runtime_error("rope_: table shape mismatch");
     same_device(x, cos, "rope_");
     same_device(x, sin, "rope_");
@@ -217,7 +221,7 @@ Tensor swiglu(const Tensor& gate, const Tensor& up) {
 // tensor.cpp:813-821
 Tensor geglu(const Tensor& x) {
     need_hip(x, "geglu");
-    const int64_t D2 = x.dim(-1), D = D2 / 2, rows = x.numel() / D2;
+    const int64_t D2 = x.dim(-1), D = D2 / 2, rows = count_of(x.numel(), D2);
     std::vector<int64_t> oshape = x.shape;
     oshape.back() = D;
     Tensor y = Tensor::empty(oshape, Device::HIP);
@@ -261,7 +265,7 @@ void affine_(Tensor& x, float a, float b) {
 
 // tensor.cpp:889-893
 void mul_rows_(Tensor& x, const Tensor& v) {
-    const int64_t dim = x.dim(-1), rows = x.numel() / dim;
+    const int64_t dim = x.dim(-1), rows = count_of(x.numel(), dim);
     if (v.numel() != dim) throw std::runtime_error("mul_rows_: vector size mismatch");
     same_device(x, v, "mul_rows_");
     need_hip(x, "mul_rows_");
@@ -270,7 +274,7 @@ void mul_rows_(Tensor& x, const Tensor& v) {
 
 // tensor.cpp:903-908
 void add_rows_scaled_(Tensor& x, const Tensor& y, const Tensor& g) {
-    const int64_t dim = x.dim(-1), rows = x.numel() / dim;
+    const int64_t dim = x.dim(-1), rows = count_of(x.numel(), dim);
     if (y.numel() != x.numel() || g.numel() != dim) throw std::runtime_error("add_rows_scaled_: shape mismatch");
     same_device(x, y, "add_rows_scaled_");
     same_device(x, g, "add_rows_scaled_");
@@ -280,7 +284,7 @@ void add_rows_scaled_(Tensor& x, const Tensor& y, const Tensor& g) {
 
 // tensor.cpp:919-923
 void add_channel_bias_(Tensor& x, const Tensor& b) {
-    const int64_t N = x.dim(0), C = x.dim(1), HW = x.numel() / (N * C);
+    const int64_t N = x.dim(0), C = x.dim(1), HW = count_of(x.numel(), (N * C));
     if (b.numel() != N * C) throw std::runtime_error("add_channel_bias_: expected [N, C] bias");
     same_device(x, b, "add_channel_bias_");
     need_hip(x, "add_channel_bias_");
@@ -314,7 +318,7 @@ Tensor unpatchify2d(const Tensor& tokens, int64_t C, int64_t H, int64_t W, int p
 // tensor.cpp:970-980
 Tensor slice_rows(const Tensor& x, int64_t from, int64_t to) {
     need_hip(x, "slice_rows");
-    const int64_t D = x.dim(-1), rows = x.numel() / D;
+    const int64_t D = x.dim(-1), rows = count_of(x.numel(), D);
     if (from < 0 || to > rows || from > to) throw std::runtime_error("slice_rows: range out of bounds");
     Tensor y = Tensor::empty({to - from, D}, Device::HIP);
     const size_t bytes = (size_t)((to - from) * D) * sizeof(float);
@@ -325,7 +329,7 @@ Tensor slice_rows(const Tensor& x, int64_t from, int64_t to) {
 Tensor rows_view(const Tensor& x, int64_t from, int64_t to) {
     need_hip(x, "rows_view");
     if (x.is_bf16()) throw std::runtime_error("rows_view: F32 tensors only");
-    const int64_t D = x.dim(-1), rows = x.numel() / D;
+    const int64_t D = x.dim(-1), rows = count_of(x.numel(), D);
     if (from < 0 || to > rows || from > to) throw std::runtime_error("rows_view: range out of bounds");
     Tensor v;
     v.shape = {to - from, D};
@@ -399,7 +403,7 @@ Tensor slice_batch(const Tensor& x, int64_t b) {
     std::vector<int64_t> s = x.shape;
     s[0] = 1;
     Tensor y = Tensor::empty(s, Device::HIP);
-    const int64_t per = x.numel() / x.dim(0);
+    const int64_t per = count_of(x.numel(), x.dim(0));
     if (per) sd::hip::copy(y.dptr(), x.dptr() + b * per, per * sizeof(float));
     return y;
 }
@@ -421,9 +425,9 @@ Tensor repeat_batch(const Tensor& x, int64_t times) {
 Tensor linear(const Tensor& x, const Tensor& W, const Tensor* b) {
     const int64_t in = x.dim(-1), out = W.dim(0);
     if (W.dim(1) != in) throw std::runtime_error("linear: input dim " + x.shape_str() + " vs weight " + W.shape_str());
-    const int64_t rows = x.numel() / in;
     std::vector<int64_t> oshape = x.shape;
     oshape.back() = out;
+    const int64_t rows = Tensor::numel_of(std::vector<int64_t>(x.shape.begin(), x.shape.end() - 1));
     same_device(x, W, "linear");
     need_hip(x, "linear");
     if (b) same_device(x, *b, "linear");
@@ -450,7 +454,8 @@ Tensor linear_swiglu(const Tensor& x, const Tensor& w1, const Tensor& w3) {
     std::vector<int64_t> oshape = x.shape;
     oshape.back() = hidden;
     Tensor y = Tensor::empty(oshape, Device::HIP);
-    sd::hip::linear_swiglu(x.dptr(), w1.dptr16(), w3.dptr16(), y.dptr(), x.numel() / in, in, hidden);
+    sd::hip::linear_swiglu(x.dptr(), w1.dptr16(), w3.dptr16(), y.dptr(),
+                           Tensor::numel_of(std::vector<int64_t>(x.shape.begin(), x.shape.end() - 1)), in, hidden);
     return y;
 }
 
@@ -475,7 +480,7 @@ Tensor rms_norm_modulate_bf16(const Tensor& x, const Tensor* gamma, const Tensor
     need_hip(x, "rms_norm_modulate_bf16");
     if (gamma) same_device(x, *gamma, "rms_norm_modulate_bf16");
     if (scale) same_device(x, *scale, "rms_norm_modulate_bf16");
-    const int64_t C = x.dim(-1), rows = x.numel() / C;
+    const int64_t C = x.dim(-1), rows = count_of(x.numel(), C);
     if ((gamma && gamma->numel() != C) || (scale && scale->numel() != C))
         throw std::runtime_error("rms_norm_modulate_bf16: vector length vs " + x.shape_str());
     Tensor y = Tensor::empty_bf16(x.shape);
@@ -488,7 +493,7 @@ void rms_norm_gated_add_(Tensor& x, const Tensor& a, const Tensor* gamma, const 
     same_device(x, a, "rms_norm_gated_add_");
     if (x.numel() != a.numel() || x.dim(-1) != a.dim(-1))
         throw std::runtime_error("add_rows_scaled_: " + x.shape_str() + " vs " + a.shape_str());
-    const int64_t C = x.dim(-1), rows = x.numel() / C;
+    const int64_t C = x.dim(-1), rows = count_of(x.numel(), C);
     if ((gamma && gamma->numel() != C) || (gate && gate->numel() != C))
         throw std::runtime_error("rms_norm_gated_add_: vector length vs " + x.shape_str());
     sd::hip::rms_norm_gated_add(x.dptr(), a.dptr(), rows, C, opt(gamma), opt(gate), eps);
@@ -510,7 +515,7 @@ void softmax_rows_(float* x, int64_t rows, int64_t cols, float scale, bool causa
 void softmax_rows_(Tensor& x, float scale, bool causal) {
     need_hip(x, "softmax_rows_");
     const int64_t cols = x.dim(-1);
-    sd::hip::softmax_rows(x.dptr(), x.numel() / cols, cols, scale, causal);
+    sd::hip::softmax_rows(x.dptr(), count_of(x.numel(), cols), cols, scale, causal);
 }
 
 // ---- fused ----
@@ -518,7 +523,7 @@ Tensor add_rms_norm_(Tensor& x, const Tensor& r, const Tensor* gamma, float eps)
     if (x.numel() != r.numel()) throw std::runtime_error("add_: " + x.shape_str() + " vs " + r.shape_str());
     same_device(x, r, "add_rms_norm_");
     need_hip(x, "add_rms_norm_");
-    const int64_t C = x.dim(-1), rows = x.numel() / C;
+    const int64_t C = x.dim(-1), rows = count_of(x.numel(), C);
     Tensor y = Tensor::empty(x.shape, Device::HIP);
     sd::hip::add_rms_norm(x.dptr(), r.dptr(), y.dptr(), rows, C, opt(gamma), eps);
     return y;
@@ -528,7 +533,7 @@ Tensor group_norm_silu(const Tensor& x, int groups, const Tensor& gamma, const T
     need_hip(x, "group_norm_silu");
     same_device(x, gamma, "group_norm_silu");
     same_device(x, beta, "group_norm_silu");
-    const int64_t N = x.dim(0), C = x.dim(1), HW = x.numel() / (N * C);
+    const int64_t N = x.dim(0), C = x.dim(1), HW = count_of(x.numel(), (N * C));
     if (C % groups != 0) throw std::runtime_error("group_norm: channels not divisible by groups");
     Tensor y = Tensor::empty(x.shape, Device::HIP);
     sd::hip::group_norm_silu(x.dptr(), y.dptr(), N, C, HW, groups, gamma.dptr(), beta.dptr(), eps);
@@ -539,7 +544,7 @@ void ln_modulate_gate_(const Tensor& x, Tensor& res, const Tensor& scale, const 
                        float eps, Tensor* y_out) {
     need_hip(x, "ln_modulate_gate_");
     same_device(x, res, "ln_modulate_gate_");
-    const int64_t C = x.dim(-1), rows = x.numel() / C;
+    const int64_t C = x.dim(-1), rows = count_of(x.numel(), C);
     if (res.numel() != x.numel() || scale.numel() != C || gate.numel() != C || (shift && shift->numel() != C))
         throw std::runtime_error("ln_modulate_gate_: shape mismatch");
     if (y_out && (y_out->numel() != x.numel() || !y_out->is_hip()))
@@ -551,8 +556,9 @@ void ln_modulate_gate_(const Tensor& x, Tensor& res, const Tensor& scale, const 
 void rope_qk_(Tensor& q, Tensor& k, int64_t dim, const Tensor& cos, const Tensor& sin, bool interleaved) {
     need_hip(q, "rope_qk_");
     same_device(q, k, "rope_qk_");
-    const int64_t S = q.dim(-2), N = q.numel() / (S * q.dim(-1));
-    if (k.dim(-2) != S || k.numel() / (S * k.dim(-1)) != N) throw std::runtime_error("rope_qk_: q/k token mismatch");
+    const int64_t S = q.dim(-2), N = count_of(q.numel(), (S * q.dim(-1)));
+    if (k.dim(-2) != S || count_of(k.numel(), (S * k.dim(-1))) != N)
+        throw std::runtime_error("rope_qk_: q/k token mismatch");
     if (cos.dim(0) < S || cos.dim(1) != dim) throw std::runtime_error("rope_: table shape mismatch");
     sd::hip::rope_qk(q.dptr(), q.dim(-1), k.dptr(), k.dim(-1), N, S, dim, cos.dptr(), sin.dptr(), interleaved);
 }
@@ -564,8 +570,9 @@ void qknorm_rope_(Tensor& q, Tensor& k, int64_t dim, const Tensor* gamma_q, cons
     same_device(q, k, "qknorm_rope_");
     if (gamma_q) same_device(q, *gamma_q, "qknorm_rope_");
     if (gamma_k) same_device(q, *gamma_k, "qknorm_rope_");
-    const int64_t S = q.dim(-2), N = q.numel() / (S * q.dim(-1));
-    if (k.dim(-2) != S || k.numel() / (S * k.dim(-1)) != N) throw std::runtime_error("qknorm_rope_: q/k token mismatch");
+    const int64_t S = q.dim(-2), N = count_of(q.numel(), (S * q.dim(-1)));
+    if (k.dim(-2) != S || count_of(k.numel(), (S * k.dim(-1))) != N)
+        throw std::runtime_error("qknorm_rope_: q/k token mismatch");
     if (cos.dim(0) < S || cos.dim(1) != dim) throw std::runtime_error("rope_: table shape mismatch");
     sd::hip::qknorm_rope(q.dptr(), q.dim(-1), k.dptr(), k.dim(-1), N, S, dim, opt(gamma_q), opt(gamma_k), eps,
                          cos.dptr(), sin.dptr(), interleaved);
