@@ -670,7 +670,8 @@ KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
     "k_unary<4>": "copy_calibration", "k_add_rms": "add_rms_norm", "k_swiglu": "swiglu",
     "k_rope_il_reg": "rope_qk", "k_ln_mod_gate": "ln_modulate_gate", "k_softmax_block": "softmax_rows",
     "k_upsample2x_vec": "upsample_nearest2x", "k_concat_vec": "concat_channels", "k_patchify": "patchify2d",
-    "k_qknorm_rope_il": "qknorm_rope", "k_attn_fwd": "attention",
+    "k_qknorm_rope_il": "qknorm_rope", "k_attn_fwd": "attention", "k_rms_mod_bf16": "rms_norm_modulate_bf16",
+    "k_rms_gated_add": "rms_norm_gated_add",
 }
 
 
