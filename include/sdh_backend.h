@@ -189,6 +189,12 @@ int sdh_swiglu_bf16(const float* gate, const float* up, uint16_t* y, int64_t n);
  * Fused on the MFMA units (no score matrix in memory) for d <= 128. */
 int sdh_attention(const float* q, const float* k, const float* v, float* out, int64_t N, int64_t Sq, int64_t Skv,
                   int heads, int kv_heads, int64_t d, int causal);
+/* FUSED: out = bf16 bits of attention(q, k, v): sdh_attention then the bf16
+ * rounding gemm_nt_bf16 applies to its A (backend_cuda.h:41-43; the input of
+ * the block's to_out projection, zimage.cpp:121); the bits equal those of
+ * that sequence. out [N, Sq, heads*d] uint16. */
+int sdh_attention_bf16(const float* q, const float* k, const float* v, uint16_t* out, int64_t N, int64_t Sq,
+                       int64_t Skv, int heads, int kv_heads, int64_t d, int causal);
 
 /* ---- activations ----------------------------------------------------------- */
 /* backend_cuda.h:61 swiglu(); tensor.h:191. y = gate / (1 + exp(-gate)) * up. */

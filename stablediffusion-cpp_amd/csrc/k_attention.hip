@@ -45,8 +45,13 @@
 // softmax rescale of O is skipped when no row max of the wave changed
 // (exactly alpha = 1).
 // Head dimensions above 128 take a plain fp32 kernel (one wave per query).
+// Both kernels can store the output rounded to bf16 (sdh_attention_bf16):
+// the operand rounding of the projection that follows (to_out), applied to
+// the same fp32 values, so the next GEMM reads half the bytes and no
+// separate rounding pass runs.
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "sdh_internal.hpp"
 
@@ -209,9 +214,9 @@ __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, 
 // after barrier 1 of t (K(t-1)'s last reader, Y's S^T(t-1), is done), V(t+1)
 // after barrier 2 of t (V(t-1)'s last reader, Y's O(t-1), is done).
 // ---------------------------------------------------------------------------
-template <int DP, bool CAUSAL>
+template <int DP, bool CAUSAL, bool OUT16>
 __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restrict__ Q, const u16* __restrict__ tiles,
-                                                          const int2* __restrict__ exps, float* __restrict__ O, int Sq,
+                                                          const int2* __restrict__ exps, void* __restrict__ O, int Sq,
                                                           int Skv, int inner, int d, int group, int kv_heads,
                                                           int ntiles, float c2, int qvec, int nqb, int heads) {
     constexpr int DS = DP / 16;                    // 16-wide head-dim steps of S^T = K Q^T
@@ -414,19 +419,32 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
     lsum += __shfl_xor(lsum, 32, 64);
     // the reference scales P by 1/sum (tensor.cpp:761-764); O^T carries 2^(14-E) sum(p v), lsum 2^14 sum(p)
     const float inv = ldexpf(1.0f / lsum, E);
-    float* op = O + ((int64_t)nb * Sq + qlane) * inner + (int64_t)h * d;
+    const int64_t obase = ((int64_t)nb * Sq + qlane) * inner + (int64_t)h * d;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int c0 = dt * 32 + g * 8 + fh * 4;
             const f4 v = {o[dt][g * 4] * inv, o[dt][g * 4 + 1] * inv, o[dt][g * 4 + 2] * inv, o[dt][g * 4 + 3] * inv};
-            if (qvec) {
-                *(f4*)(op + c0) = v;
-            } else {
+            if constexpr (OUT16) {
+                // the rounding gemm_nt_bf16 gives its A, applied to the fp32 value above
+                u16* op = (u16*)O + obase;
+                if (qvec) {
+                    *(uint2*)(op + c0) = dev::bf16x4(v);
+                } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (c0 + e < d) op[c0 + e] = v[e];
+                    for (int e = 0; e < 4; ++e)
+                        if (c0 + e < d) op[c0 + e] = dev::bf16_rne(v[e]);
+                }
+            } else {
+                float* op = (float*)O + obase;
+                if (qvec) {
+                    *(f4*)(op + c0) = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (c0 + e < d) op[c0 + e] = v[e];
+                }
             }
         }
 }
@@ -438,9 +456,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
 // ---------------------------------------------------------------------------
 constexpr int kGenWaves = 4, kGenMaxD = 1024;
 
-template <bool CAUSAL>
+template <bool CAUSAL, bool OUT16>
 __global__ __launch_bounds__(64 * kGenWaves) void k_attn_generic(const float* __restrict__ Q, const float* __restrict__ K,
-                                                                 const float* __restrict__ V, float* __restrict__ O,
+                                                                 const float* __restrict__ V, void* __restrict__ O,
                                                                  int Sq, int Skv, int inner, int kv_inner, int d,
                                                                  int group, float c2) {
     __shared__ float sq[kGenWaves][kGenMaxD];
@@ -488,12 +506,15 @@ __global__ __launch_bounds__(64 * kGenWaves) void k_attn_generic(const float* __
         }
     }
     const float inv = 1.0f / lsum;
-    float* op = O + ((int64_t)nb * Sq + q) * inner + (int64_t)h * d;
+    const int64_t obase = ((int64_t)nb * Sq + q) * inner + (int64_t)h * d;
 #pragma unroll
     for (int i = 0; i < kAcc; ++i) {
         const int c = i * 64 + lane;
         if (i * 64 >= d) break;
-        if (c < d) op[c] = acc[i] * inv;
+        if (c < d) {
+            if constexpr (OUT16) ((u16*)O)[obase + c] = dev::bf16_rne(acc[i] * inv);
+            else ((float*)O)[obase + c] = acc[i] * inv;
+        }
     }
 }
 
@@ -502,8 +523,8 @@ bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
     return x < y + nb && y < x + na;
 }
 
-template <int DP>
-void run_mfma(const float* q, const float* k, const float* v, float* out, int64_t N, int64_t Sq, int64_t Skv,
+template <int DP, bool OUT16>
+void run_mfma(const float* q, const float* k, const float* v, void* out, int64_t N, int64_t Sq, int64_t Skv,
               int heads, int kv_heads, int64_t d, bool causal, float c2) {
     const int64_t ntiles = (Skv + kKT - 1) / kKT;
     const int64_t ntot = N * kv_heads * ntiles;
@@ -521,23 +542,24 @@ void run_mfma(const float* q, const float* k, const float* v, float* out, int64_
         k_attn_pack<DP, false><<<pgrid, 256, 0, stream()>>>(k, v, tiles, exps, (int)Skv, (int)kv_inner, (int)d,
                                                             (int)ntiles, kv_heads);
     launched("sdh_attention");
-    const int qvec = d == DP && inner % 4 == 0 && aligned16(q) && aligned16(out);
+    const int qvec = d == DP && inner % 4 == 0 && aligned16(q) && (OUT16 ? ((uintptr_t)out & 7) == 0 : aligned16(out));
     const int64_t nqb = (Sq + kBM - 1) / kBM, nblk = nqb * heads * N;
     need(nblk * kThreads <= kMaxGridItems, "sdh_attention", "too many query blocks for one launch");
     if (causal)
-        k_attn_fwd<DP, true><<<(unsigned)nblk, kThreads, 0, stream()>>>(
+        k_attn_fwd<DP, true, OUT16><<<(unsigned)nblk, kThreads, 0, stream()>>>(
             q, tiles, exps, out, (int)Sq, (int)Skv, (int)inner, (int)d, heads / kv_heads, kv_heads, (int)ntiles, c2,
             qvec, (int)nqb, heads);
     else
-        k_attn_fwd<DP, false><<<(unsigned)nblk, kThreads, 0, stream()>>>(
+        k_attn_fwd<DP, false, OUT16><<<(unsigned)nblk, kThreads, 0, stream()>>>(
             q, tiles, exps, out, (int)Sq, (int)Skv, (int)inner, (int)d, heads / kv_heads, kv_heads, (int)ntiles, c2,
             qvec, (int)nqb, heads);
     launched("sdh_attention");
 }
 
-void run_attention(const float* q, const float* k, const float* v, float* out, int64_t N, int64_t Sq, int64_t Skv,
-                   int heads, int kv_heads, int64_t d, bool causal) {
-    const char* op = "sdh_attention";
+// out is float32, or bf16 (uint16) when out16
+void run_attention(const float* q, const float* k, const float* v, void* out, bool out16, int64_t N, int64_t Sq,
+                   int64_t Skv, int heads, int kv_heads, int64_t d, bool causal) {
+    const char* op = out16 ? "sdh_attention_bf16" : "sdh_attention";
     if (kv_heads <= 0) kv_heads = heads;  // tensor.cpp:777
     need(N >= 0 && Sq >= 0 && Skv >= 0, op, "negative size");
     need(heads > 0 && d > 0, op, "heads and d must be positive");
@@ -549,34 +571,41 @@ void run_attention(const float* q, const float* k, const float* v, float* out, i
     if (N == 0 || Sq == 0) return;
     ensure_init();
     const size_t qb = (size_t)(N * Sq * inner) * 4, kb = (size_t)(N * Skv * kv_inner) * 4;
+    const size_t ob = out16 ? qb / 2 : qb;
     check_range(q, qb, op, "q");
-    check_range(out, qb, op, "out");
+    check_range(out, ob, op, "out");
     if (Skv > 0) {
         check_range(k, kb, op, "k");
         check_range(v, kb, op, "v");
     }
-    need(!overlaps(out, qb, q, qb) && !(Skv > 0 && (overlaps(out, qb, k, kb) || overlaps(out, qb, v, kb))), op,
+    need(!overlaps(out, ob, q, qb) && !(Skv > 0 && (overlaps(out, ob, k, kb) || overlaps(out, ob, v, kb))), op,
          "out overlaps an input");
     if (Skv == 0) {  // empty key set: every weighted sum is empty (the reference's gemm leaves 0)
-        zero_device(out, qb);
+        zero_device(out, ob);
         return;
     }
     const float scale = 1.0f / std::sqrt((float)d);  // tensor.cpp:784
     const float c2 = scale * kLog2e;
-    if (d <= 64) {
-        run_mfma<64>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2);
-    } else if (d <= 128) {
-        run_mfma<128>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2);
+    if (d <= 128) {
+        if (d <= 64)
+            out16 ? run_mfma<64, true>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2)
+                  : run_mfma<64, false>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2);
+        else
+            out16 ? run_mfma<128, true>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2)
+                  : run_mfma<128, false>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2);
     } else {
         const int64_t gx = (Sq + kGenWaves - 1) / kGenWaves;
         need(gx * 64 * kGenWaves <= kMaxGridItems, op, "too many queries for one launch");
         const dim3 grid((unsigned)gx, (unsigned)heads, (unsigned)N);
-        if (causal)
-            k_attn_generic<true><<<grid, 64 * kGenWaves, 0, stream()>>>(q, k, v, out, (int)Sq, (int)Skv, (int)inner,
-                                                                         (int)kv_inner, (int)d, heads / kv_heads, c2);
-        else
-            k_attn_generic<false><<<grid, 64 * kGenWaves, 0, stream()>>>(q, k, v, out, (int)Sq, (int)Skv, (int)inner,
-                                                                          (int)kv_inner, (int)d, heads / kv_heads, c2);
+        auto go = [&](auto cc, auto oc) {
+            constexpr bool C = decltype(cc)::value, O16 = decltype(oc)::value;
+            k_attn_generic<C, O16><<<grid, 64 * kGenWaves, 0, stream()>>>(
+                q, k, v, out, (int)Sq, (int)Skv, (int)inner, (int)kv_inner, (int)d, heads / kv_heads, c2);
+        };
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        if (causal) out16 ? go(T_(), T_()) : go(T_(), F_());
+        else out16 ? go(F_(), T_()) : go(F_(), F_());
         launched(op);
     }
 }
@@ -590,7 +619,12 @@ extern "C" {
 
 int sdh_attention(const float* q, const float* k, const float* v, float* out, int64_t N, int64_t Sq, int64_t Skv,
                   int heads, int kv_heads, int64_t d, int causal) {
-    return guarded([&] { run_attention(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal != 0); });
+    return guarded([&] { run_attention(q, k, v, out, false, N, Sq, Skv, heads, kv_heads, d, causal != 0); });
+}
+
+int sdh_attention_bf16(const float* q, const float* k, const float* v, uint16_t* out, int64_t N, int64_t Sq,
+                       int64_t Skv, int heads, int kv_heads, int64_t d, int causal) {
+    return guarded([&] { run_attention(q, k, v, out, true, N, Sq, Skv, heads, kv_heads, d, causal != 0); });
 }
 
 }  // extern "C"

@@ -88,6 +88,12 @@ inline void attention(const float* q, const float* k, const float* v, float* out
                       int heads, int kv_heads, int64_t d, bool causal) {
     detail::check(sdh_attention(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal ? 1 : 0), "hip::attention");
 }
+// attention with out as the bf16 bits gemm_nt_bf16 would round it to (the next projection's A)
+inline void attention_bf16(const float* q, const float* k, const float* v, uint16_t* out, int64_t N, int64_t Sq,
+                           int64_t Skv, int heads, int kv_heads, int64_t d, bool causal) {
+    detail::check(sdh_attention_bf16(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal ? 1 : 0),
+                  "hip::attention_bf16");
+}
 // backend_cuda.h:60-61
 inline void geglu(const float* x, float* y, int64_t rows, int64_t D) {
     detail::check(sdh_geglu(x, y, rows, D), "hip::geglu");

@@ -460,7 +460,9 @@ Tensor linear_swiglu(const Tensor& x, const Tensor& w1, const Tensor& w3) {
 }
 
 // tensor.cpp:776-790: the reference's shape checks and messages, device branch
-Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal, int kv_heads) {
+namespace {
+Tensor attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal, int kv_heads,
+                      bool bf16) {
     if (kv_heads <= 0) kv_heads = heads;
     const int64_t N = q.dim(0), Sq = q.dim(1), inner = q.dim(2), Skv = k.dim(1), kv_inner = k.dim(2);
     if (inner % heads != 0 || heads % kv_heads != 0) throw std::runtime_error("attention: heads mismatch");
@@ -470,9 +472,23 @@ Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, int heads, b
     same_device(q, k, "attention");
     same_device(q, v, "attention");
     need_hip(q, "attention");
+    if (bf16) {
+        Tensor out = Tensor::empty_bf16({N, Sq, inner});
+        sd::hip::attention_bf16(q.dptr(), k.dptr(), v.dptr(), out.dptr16(), N, Sq, Skv, heads, kv_heads, d, causal);
+        return out;
+    }
     Tensor out = Tensor::empty({N, Sq, inner}, Device::HIP);
     sd::hip::attention(q.dptr(), k.dptr(), v.dptr(), out.dptr(), N, Sq, Skv, heads, kv_heads, d, causal);
     return out;
+}
+}  // namespace
+
+Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal, int kv_heads) {
+    return attention_impl(q, k, v, heads, causal, kv_heads, false);
+}
+
+Tensor attention_bf16(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal, int kv_heads) {
+    return attention_impl(q, k, v, heads, causal, kv_heads, true);
 }
 
 // ---- the Z-Image block's fused ops ----

@@ -135,6 +135,9 @@ Tensor swiglu_bf16(const Tensor& gate, const Tensor& up);
 // q [N, Sq, heads*d], k and v [N, Skv, kv_heads*d] -> [N, Sq, heads*d];
 // query head h reads key/value head h / (heads / kv_heads); kv_heads 0 = heads.
 Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal = false, int kv_heads = 0);
+// attention rounded to BF16 (the input of the block's to_out projection)
+Tensor attention_bf16(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal = false,
+                      int kv_heads = 0);
 
 // ---- softmax (tensor.h:236) ----
 // Same parameters as the reference; x is a DEVICE pointer here (rows x cols

@@ -129,12 +129,12 @@ void ZImageTransformer::run_block(const Block& b, Tensor& x, const Tensor& cos, 
         // BF16 weights: the same values through the fused ops, each equal to the
         // sequence it replaces bit for bit. The normalised, modulated rows are
         // emitted as the GEMMs' bf16 A once for to_q, to_k and to_v (and once
-        // for w1, w3), and the norm + gated residual after to_out and w2 is one
-        // pass over x.
+        // for w1, w3), attention and swiglu emit the bf16 A of to_out and w2,
+        // and the norm + gated residual after to_out and w2 is one pass over x.
         Tensor h16 = rms_norm_modulate_bf16(x, b.attn_norm1, mod ? &scale_msa : nullptr, cfg_.norm_eps);
         Tensor q = b.to_q(h16), k = b.to_k(h16), v = b.to_v(h16);
         qknorm_rope_(q, k, head_dim_, b.norm_q, b.norm_k, 1e-5f, cos, sin, true);
-        Tensor a = b.to_out(attention(q, k, v, cfg_.heads, false));
+        Tensor a = b.to_out(attention_bf16(q, k, v, cfg_.heads, false));
         rms_norm_gated_add_(x, a, b.attn_norm2, mod ? &gate_msa : nullptr, cfg_.norm_eps);
         h16 = rms_norm_modulate_bf16(x, b.ffn_norm1, mod ? &scale_mlp : nullptr, cfg_.norm_eps);
         Tensor f = b.w2(swiglu_bf16(b.w1(h16), b.w3(h16)));

@@ -88,6 +88,7 @@ SIGNATURES = {
     "sdh_gemm_nt_f32": [_i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, C.c_int],
     "sdh_to_bf16": [_vp, _vp, _i64],
     "sdh_attention": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
+    "sdh_attention_bf16": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
     "sdh_upsample_nearest2x": [_vp, _vp, _i64, _i64, _i64],
     "sdh_concat_channels": [_vp, _vp, _vp, _i64, _i64, _i64, _i64],
     "sdh_nchw_to_nlc": [_vp, _vp, _i64, _i64, _i64],
@@ -283,6 +284,11 @@ class Backend:
     def attention(self, q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal=False):
         """out [N, Sq, heads*d] = softmax(q k^T / sqrt(d)) v per head (tensor.cpp:776-810)."""
         self.call("sdh_attention", _p(q), _p(k), _p(v), _p(out), N, Sq, Skv, heads, kv_heads, d, int(bool(causal)))
+
+    def attention_bf16(self, q, k, v, out16, N, Sq, Skv, heads, kv_heads, d, causal=False):
+        """As attention, out16 (uint16) holding the bf16 rounding of the result."""
+        self.call("sdh_attention_bf16", _p(q), _p(k), _p(v), _p(out16), N, Sq, Skv, heads, kv_heads, d,
+                  int(bool(causal)))
 
     def swiglu(self, g, u, y, n):
         self.call("sdh_swiglu", _p(g), _p(u), _p(y), n)

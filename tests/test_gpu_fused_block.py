@@ -123,3 +123,27 @@ def test_gemm_packed_mfma_kernels(be, orc):
         be.gemm_nt_bf16_packed(M, N, K, be.array(f32_to_bf16(A)), K, be.array(W), K, C, ldc)
         want, S = orc.gemm_nt_bf16(A, W)
         assert_gemm(C.download()[:, :N], want, S, K + 1, f"packed mfma {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("N,Sq,Skv,heads,kvh,d,causal", [(1, 300, 300, 3, 3, 128, False), (2, 70, 130, 4, 2, 64, True),
+                                                          (1, 33, 40, 2, 2, 200, False), (1, 65, 65, 2, 1, 100, True),
+                                                          (1, 5, 0, 2, 2, 64, False)])
+def test_attention_bf16(be, orc, N, Sq, Skv, heads, kvh, d, causal):
+    """sdh_attention_bf16 == sdh_attention then the GEMM's rounding of A, bit
+    for bit: the MFMA kernel (d = 64, 128; d = 100 takes its scalar stores),
+    the generic kernel (d = 200), grouped heads, causal, no keys."""
+    q = orc.randn((N, Sq, heads * d), 750 + d)
+    k = orc.randn((N, Skv, kvh * d), 751 + d)
+    v = orc.randn((N, Skv, kvh * d), 752 + d)
+    dq = be.array(q)
+    dk = be.array(k) if Skv else be.empty((1,))
+    dv = be.array(v) if Skv else be.empty((1,))
+    n = N * Sq * heads * d
+    o16 = _u16(be, n)
+    be.attention_bf16(dq, dk, dv, o16, N, Sq, Skv, heads, kvh, d, causal)
+    o = be.empty((N, Sq, heads * d))
+    be.attention(dq, dk, dv, o, N, Sq, Skv, heads, kvh, d, causal)
+    ref16 = _u16(be, n)
+    be.to_bf16(o, ref16, n)
+    got, want = o16.download(), ref16.download()
+    assert np.array_equal(got, want), f"{int(np.sum(got != want))} of {got.size} differ"
