@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kModThreads) void k_ln_mod_gate(const float* __rest
                                                             const float* __restrict__ gate, float* __restrict__ yout,
                                                             int64_t rows, int C, float eps) {
     extern __shared__ f4 lds[];  // [3][n4]: 1+scale | shift | tanh(gate)
-    __shared__ float red[2 * kModRows * 2];
+    __shared__ double red[2 * kModRows * 2];
     const int n4 = C >> 2;
     f4* s1 = lds;
     f4* sh = lds + n4;
@@ -207,26 +207,29 @@ __global__ __launch_bounds__(kModThreads) void k_ln_mod_gate(const float* __rest
             tg[i] = sgt[k];
         }
     }
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < V; ++j) s += dev::hsum(v[j]);
-    s = dev::wave_sum(s);
-    if ((threadIdx.x & 63) == 0) red[w] = s;
-    __syncthreads();  // also publishes the staged vectors
-    const float mean = (float)((double)(red[2 * sub] + red[2 * sub + 1]) / (double)C);
-    float q = 0.f;
+    // One pass of statistics: sum and sum of squares in double (every fp32
+    // square is exact in double), so var = E[x^2] - mean^2 keeps the precision
+    // of the reference's two-pass double form for any offset; one reduction
+    // and one barrier instead of two.
+    double s = 0.0, q = 0.0;
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-        if (t + 128 * j < n4) {
-            const f4 d = v[j] - mean;
-            q += dev::hsum(d * d);
-        }
+        const double a = v[j].x, b = v[j].y, c = v[j].z, e = v[j].w;
+        s += (a + b) + (c + e);
+        q += fma(a, a, fma(b, b, fma(c, c, e * e)));
     }
-    q = dev::wave_sum(q);
-    if ((threadIdx.x & 63) == 0) red[2 * kModRows + w] = q;
-    __syncthreads();
+    s = dev::wave_sum_d(s);
+    q = dev::wave_sum_d(q);
+    if ((threadIdx.x & 63) == 0) {
+        red[w] = s;
+        red[2 * kModRows + w] = q;
+    }
+    __syncthreads();  // also publishes the staged vectors
     if (!ok) return;
-    const float rstd = rstd_of(red[2 * kModRows + 2 * sub] + red[2 * kModRows + 2 * sub + 1], C, eps);
+    const double ms = (red[2 * sub] + red[2 * sub + 1]) / (double)C;
+    const double var = fmax((red[2 * kModRows + 2 * sub] + red[2 * kModRows + 2 * sub + 1]) / (double)C - ms * ms, 0.0);
+    const float mean = (float)ms;
+    const float rstd = (float)(1.0 / sqrt(var + (double)eps));
 #pragma unroll
     for (int j = 0; j < V; ++j) {
         const int idx = t + 128 * j;

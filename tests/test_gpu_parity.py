@@ -173,6 +173,22 @@ def test_ln_modulate_gate(be, orc, rows, C, shift, store_y):
         assert_reduction(dy.download(), y_ref, "ln_modulate_gate y")
 
 
+@pytest.mark.parametrize("mean,std", [(300.0, 0.5), (-40.0, 1e-3), (0.0, 1e-30)])
+def test_ln_modulate_gate_offset_rows(be, orc, mean, std):
+    """Rows far from zero mean (and nearly constant rows): the statistics in
+    one double pass must match the reference's two-pass form (mean, then the
+    sum of squared deviations, tensor.cpp:640-648)."""
+    rows, C = 64, 3840
+    x = orc.randn((rows, C), _seed("lmg_off", int(mean)), mean, std)
+    res = orc.randn((rows, C), _seed("lmg_off_r"))
+    sc, sh, gt = (orc.randn((C,), _seed("lmg_off_v", i), 0.0, 0.2) for i in range(3))
+    dres, dy = be.array(res), be.empty((rows, C))
+    be.ln_modulate_gate(be.array(x), dres, be.array(sc), be.array(sh), be.array(gt), dy, rows, C, 1e-6)
+    r_ref, y_ref = orc.ln_modulate_gate(x, res, sc, sh, gt, 1e-6)
+    assert_reduction(dy.download(), y_ref, f"ln_modulate_gate y, rows ~N({mean}, {std})")
+    assert_reduction(dres.download(), r_ref, f"ln_modulate_gate res, rows ~N({mean}, {std})")
+
+
 GN_SHAPES = [
     ((2, 64, 5, 7), 32, 1e-6),          # test_ops.cpp:391-392
     ((1, 512, 128, 128), 32, 1e-6),     # config 4a (FLUX VAE)
