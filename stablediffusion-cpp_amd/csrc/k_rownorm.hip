@@ -142,6 +142,14 @@ __global__ __launch_bounds__(kThreads) void k_add_rms(float* __restrict__ x, con
     }
 }
 
+// Rows of 2048 < C <= 8192 floats can take one 256-thread workgroup per row,
+// wave p lane l holding float4 l + 64 (p + 4 j). Measured on MI355X at
+// [4096, 3840] against one wave per row: the norm + gated residual (two row
+// reads, one write) gains 6-8 points of HBM peak; rms_norm (one read, one
+// write) loses 5 and add + rms_norm (two reads, two writes) loses 2, so
+// those keep one wave per row.
+constexpr int kRowThreads = 256;
+
 // Fused adaLN chain (see sdh_ln_modulate_gate). A 512-thread workgroup owns
 // kModRows = 4 rows, two waves (128 threads, V float4 each) per row. It
 // stages 1 + scale (affine_(scale, 1, 1)), shift and tanh(gate) for all C
@@ -438,6 +446,67 @@ __global__ __launch_bounds__(kThreads) void k_rms_gated_add(float* __restrict__ 
     }
 }
 
+// k_rms_gated_add with one 256-thread workgroup per row (2048 < C <= 8192).
+// The sum of squares is formed in exactly the one-wave kernels' order (per
+// lane l: float4 l, l + 64, l + 128, ... in sequence, then the wave tree),
+// through LDS, so rstd has the bits rms_norm's has and x stays bit-equal to
+// rms_norm then add_rows_scaled_.
+template <int V, bool HAS_G, bool HAS_GATE>
+__global__ __launch_bounds__(kRowThreads) void k_rms_gated_add_row(float* __restrict__ x, const float* __restrict__ a,
+                                                                  int C, const float* __restrict__ gamma,
+                                                                  const float* __restrict__ gate, float eps) {
+    __shared__ float hs[4 * V][64];  // hs[k][l]: squared sum of float4 l + 64 k
+    const int lane = threadIdx.x & 63, p = threadIdx.x >> 6;
+    const int n4 = C >> 2;
+    const int64_t row = blockIdx.x;
+    const f4* ar = (const f4*)(a + row * C);
+    f4* xr = (f4*)(x + row * C);
+    f4 v[V], xv[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * (p + 4 * j);
+        v[j] = idx < n4 ? dev::ld_stream(ar + idx) : zero4();
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * (p + 4 * j);
+        xv[j] = idx < n4 ? dev::ld_stream(xr + idx) : zero4();
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) hs[p + 4 * j][lane] = dev::hsum(v[j] * v[j]);
+    __syncthreads();
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4 * V; ++k) q += hs[k][lane];  // zero entries past the row add exactly 0
+    const float rstd = rstd_of(dev::wave_sum(q), C, eps);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * (p + 4 * j);
+        if (idx < n4) {
+#pragma clang fp contract(off)
+            f4 o = v[j] * rstd;
+            if constexpr (HAS_G) o = o * ((const f4*)gamma)[idx];
+            const f4 xo = xv[j];
+            f4 r;
+            if constexpr (HAS_GATE) {
+                const f4 g = ((const f4*)gate)[idx];
+                r = f4{fmaf(g.x, o.x, xo.x), fmaf(g.y, o.y, xo.y), fmaf(g.z, o.z, xo.z), fmaf(g.w, o.w, xo.w)};
+            } else {
+                r = xo + o;
+            }
+            dev::st_stream(xr + idx, r);
+        }
+    }
+}
+
+// the row-per-workgroup kernels' float4 per lane for a row of n4 float4, or 0
+int pick_row_v(int64_t n4) {
+    if (n4 <= 512) return 0;  // narrower rows: one wave per row
+    if (n4 <= 1024) return 4;
+    if (n4 <= 2048) return 8;
+    return 0;
+}
+
 // any C / alignment: one wave per row, strided loops over the row
 template <bool GATED>
 __global__ __launch_bounds__(kThreads) void k_rms_fused_generic(const float* __restrict__ src, float* __restrict__ x,
@@ -625,7 +694,28 @@ void run_rms_gated_add(float* x, const float* a, int64_t rows, int64_t C, const 
         });
         return;
     }
-    if (vec_ok(C, {x, a, gamma, gate})) {
+    const int rv = pick_row_v(C / 4);
+    if (rv && vec_ok(C, {x, a, gamma, gate})) {
+        // one workgroup per row
+        in_pieces(rows, units_per_launch(kRowThreads), [&](int64_t r0, int64_t nr) {
+            float* xp = x + r0 * C;
+            const float* ap = a + r0 * C;
+            auto go = [&](auto vc) {
+                constexpr int V = decltype(vc)::value;
+                const unsigned g = (unsigned)nr;
+                if (gamma && gate)
+                    k_rms_gated_add_row<V, true, true><<<g, kRowThreads, 0, stream()>>>(xp, ap, (int)C, gamma, gate, eps);
+                else if (gamma)
+                    k_rms_gated_add_row<V, true, false><<<g, kRowThreads, 0, stream()>>>(xp, ap, (int)C, gamma, gate, eps);
+                else if (gate)
+                    k_rms_gated_add_row<V, false, true><<<g, kRowThreads, 0, stream()>>>(xp, ap, (int)C, gamma, gate, eps);
+                else
+                    k_rms_gated_add_row<V, false, false><<<g, kRowThreads, 0, stream()>>>(xp, ap, (int)C, gamma, gate, eps);
+            };
+            if (rv == 4) go(std::integral_constant<int, 4>());
+            else go(std::integral_constant<int, 8>());
+        });
+    } else if (vec_ok(C, {x, a, gamma, gate})) {
         const unsigned grid = exact_grid(rows);
         with_v(pick_v(C / 4), [&](auto vc) {
             constexpr int V = decltype(vc)::value;

@@ -90,6 +90,17 @@ def main():
     dx = be.array(x)
     be.rms_norm_gated_add(dx, be.array(y), rows, C, dg, dv, 1e-5)
     assert_reduction(dx.download(), orc.add_rows_scaled(x, orc.rms_norm(y, gam, 1e-5), v), "rms_norm_gated_add")
+    # rows of 3840 (the gated add runs one workgroup per row: 16 rows per launch here)
+    xw, yw = orc.randn((40, 3840), 20), orc.randn((40, 3840), 21, 0.0, 3.0)
+    gw, vw = orc.randn((3840,), 22, 1.0, 0.1), orc.randn((3840,), 23, 0.0, 0.5)
+    dxw, dyw = be.array(xw), be.empty((40, 3840))
+    be.add_rms_norm(dxw, be.array(yw), dyw, 40, 3840, be.array(gw), 1e-6)
+    s_want, y_want = orc.add_rms_norm(xw, yw, gw, 1e-6)
+    assert_elementwise(dxw.download(), s_want, "add_rms_norm sum, wide rows")
+    assert_reduction(dyw.download(), y_want, "add_rms_norm, wide rows")
+    dxw = be.array(xw)
+    be.rms_norm_gated_add(dxw, be.array(yw), 40, 3840, be.array(gw), be.array(vw), 1e-5)
+    assert_reduction(dxw.download(), orc.add_rows_scaled(xw, orc.rms_norm(yw, gw, 1e-5), vw), "gated_add, wide rows")
     h = orc.randn((3000, 128), 12)
     gh = orc.randn((128,), 13, 1.0, 0.1)
     dh = be.array(h)
