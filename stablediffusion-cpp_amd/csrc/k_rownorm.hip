@@ -159,7 +159,7 @@ constexpr int kRowThreads = 256;
 // halve the live registers per lane against one wave per row (168 -> ~90
 // VGPRs), doubling the waves in flight; measured the fastest of the variants
 // tried (1 wave/row with 8 rows per block, L2 gathers of the vectors, 2 or 8
-// rows per block).
+// rows per block, 4 waves per row: 69.4 against 71 % of HBM peak).
 constexpr int kModRows = 4;
 constexpr int kModThreads = kModRows * 128;
 
