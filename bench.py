@@ -795,8 +795,8 @@ def main():
             print(f"{w.name:24s} {w.algo_bytes:>14,d} B  {w.desc}")
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this build measures one GPU only: every op shards by rows with no exchange "
-                                   "(see DESIGN.md); run with --gpus 1"}), flush=True)
+        print(json.dumps({"error": "this build measures one GPU only (every op shards by rows with no exchange); "
+                                   "run with --gpus 1"}), flush=True)
         return 2
     if args.workload not in wls:
         print(f"unknown workload {args.workload}; --list shows them", file=sys.stderr)
