@@ -9,7 +9,9 @@
 //     the statistics pass and the apply pass both run on registers.
 //   * Reductions are wave-only (DPP + readlane, sdh_internal.hpp); no LDS and
 //     no barrier, except the adaLN kernel (two waves per row, column vectors
-//     staged in LDS once per 4 rows).
+//     staged in LDS once per 4 rows) and the norm + gated residual on rows
+//     wider than 2048 floats (one 256-thread workgroup per row, measured
+//     faster for that op's three row streams).
 //   * The grid covers the rows exactly (4 rows per 256-thread workgroup, no
 //     persistent loop): measured on MI355X, letting the dispatcher refill CUs
 //     with fresh workgroups streams ~10 points of peak better than persistent
