@@ -387,7 +387,7 @@ struct Blas {
     std::mutex mu;
     hipblasLtHandle_t h = nullptr;
     bool tried = false;
-    std::map<std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int>, BlasPlan> plans;
+    std::map<std::tuple<int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int, int>, BlasPlan> plans;
 };
 Blas& blas() {
     static Blas b;
@@ -398,10 +398,14 @@ void blas_check(hipblasStatus_t st, const char* what) {
     if (st != HIPBLAS_STATUS_SUCCESS) fail(SDH_ERR_HIP, std::string(what) + ": hipBLASLt status " + std::to_string((int)st));
 }
 
-// Returns false when hipBLASLt has no algorithm for the shape (the caller then
-// runs its own kernels); throws on a failed launch.
-bool blaslt_gemm(int64_t M, int64_t N, int64_t K, const u16* P, int64_t ldp, const u16* B, int64_t ldb, float* C,
-                 int64_t ldc, const float* bias, bool accumulate) {
+}  // namespace
+
+// C[M,N] = P[M,K] B[N,K]^T (+ bias) (+ C) on hipBLASLt with fp32 accumulation,
+// P and B bf16 (f32 = false) or fp32 (f32 = true; fp32 products). Returns
+// false when hipBLASLt has no algorithm for the shape (the caller then runs
+// its own kernels); throws on a failed launch.
+bool blaslt_gemm(bool f32, int64_t M, int64_t N, int64_t K, const void* P, int64_t ldp, const void* B, int64_t ldb,
+                 float* C, int64_t ldc, const float* bias, bool accumulate) {
     Blas& b = blas();
     std::lock_guard<std::mutex> lk(b.mu);
     if (!b.h) {
@@ -412,7 +416,8 @@ bool blaslt_gemm(int64_t M, int64_t N, int64_t K, const u16* P, int64_t ldp, con
             return false;
         }
     }
-    const auto key = std::make_tuple(M, N, K, ldp, ldb, ldc, bias ? 1 : 0);
+    const auto key = std::make_tuple(M, N, K, ldp, ldb, ldc, bias ? 1 : 0, f32 ? 1 : 0);
+    const hipDataType ab = f32 ? HIP_R_32F : HIP_R_16BF;
     auto it = b.plans.find(key);
     if (it == b.plans.end()) {
         BlasPlan p;
@@ -427,8 +432,8 @@ bool blaslt_gemm(int64_t M, int64_t N, int64_t K, const u16* P, int64_t ldp, con
             blas_check(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof bt),
                        "bias type");
         }
-        blas_check(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, (uint64_t)K, (uint64_t)N, ldb), "layout B");
-        blas_check(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, (uint64_t)K, (uint64_t)M, ldp), "layout A");
+        blas_check(hipblasLtMatrixLayoutCreate(&p.la, ab, (uint64_t)K, (uint64_t)N, ldb), "layout B");
+        blas_check(hipblasLtMatrixLayoutCreate(&p.lb, ab, (uint64_t)K, (uint64_t)M, ldp), "layout A");
         blas_check(hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_32F, (uint64_t)N, (uint64_t)M, ldc), "layout C");
         hipblasLtMatmulPreference_t pref;
         blas_check(hipblasLtMatmulPreferenceCreate(&pref), "preference");
@@ -458,6 +463,8 @@ bool blaslt_gemm(int64_t M, int64_t N, int64_t K, const u16* P, int64_t ldp, con
                "hipblasLtMatmul");
     return true;
 }
+
+namespace {
 
 template <int EPI>
 void run_gemm(const char* op, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const u16* B0,
@@ -490,15 +497,15 @@ void run_gemm(const char* op, int64_t M, int64_t N, int64_t K, const float* A, i
         k_pack_bf16<<<dim3(blocks_for(kg, kGT), gy), kGT, 0, stream()>>>(A, lda, (u32x4*)P, M, (int)K);
         launched(op);
         if constexpr (EPI == E_LINEAR) {
-            if (lt && blaslt_gemm(M, N, K, P, K, B0, ldb, C, ldc, bias, accumulate)) {
+            if (lt && blaslt_gemm(false, M, N, K, P, K, B0, ldb, C, ldc, bias, accumulate)) {
                 launched(op);
                 return;
             }
         } else {
             float* G = (float*)(base + pbytes);
             float* U = G + M * N;
-            if (swi_lt && blaslt_gemm(M, N, K, P, K, B0, ldb, G, N, nullptr, false)) {
-                blaslt_gemm(M, N, K, P, K, B1, ldb, U, N, nullptr, false);
+            if (swi_lt && blaslt_gemm(false, M, N, K, P, K, B0, ldb, G, N, nullptr, false)) {
+                blaslt_gemm(false, M, N, K, P, K, B1, ldb, U, N, nullptr, false);
                 launch_swiglu(G, U, C, M * N);  // tensor.cpp:745 order, as the fused epilogue
                 launched(op);
                 return;
@@ -541,7 +548,7 @@ void run_gemm_packed(int64_t M, int64_t N, int64_t K, const u16* A, int64_t lda,
     if (bias) check_range(bias, (size_t)N * 4, op, "bias");
     const bool lt = K > 0 && lda % 8 == 0 && ldb % 8 == 0 && ldc % 4 == 0 && aligned(A, 16) && aligned(B, 16) &&
                     aligned(C, 16) && (!bias || aligned(bias, 16));
-    if (lt && blaslt_gemm(M, N, K, A, lda, B, ldb, C, ldc, bias, accumulate)) {
+    if (lt && blaslt_gemm(false, M, N, K, A, lda, B, ldb, C, ldc, bias, accumulate)) {
         launched(op);
         return;
     }

@@ -116,6 +116,12 @@ void run_gemm_f32(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, 
     }
     check_range(C, (size_t)((M - 1) * ldc + N) * 4, op, "C");
     if (bias) check_range(bias, (size_t)N * 4, op, "bias");
+    // the library GEMM for aligned operands (fp32 products, fp32 accumulation)
+    if (K > 0 && lda % 4 == 0 && ldb % 4 == 0 && ldc % 4 == 0 && aligned(A, 16) && aligned(B, 16) && aligned(C, 16) &&
+        (!bias || aligned(bias, 16)) && blaslt_gemm(true, M, N, K, A, lda, B, ldb, C, ldc, bias, accumulate)) {
+        launched(op);
+        return;
+    }
     const int64_t gx = (N + kT - 1) / kT, gy = (M + kT - 1) / kT;
     need(gy <= 65535 && gx * kThreads <= kMaxGridItems, op, "matrix too large for one launch");
     const bool vec = K % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 && aligned(A, 16) && aligned(B, 16);

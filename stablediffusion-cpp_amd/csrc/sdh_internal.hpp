@@ -61,6 +61,11 @@ void* scratch(size_t bytes);
 // A persistent library-owned device block of at least `bytes` for a library
 // routine's workspace (the BLAS GEMM), distinct from scratch().
 void* workspace(size_t bytes);
+// C[M,N] = P[M,K] B[N,K]^T (+ bias[N]) (+ C) on hipBLASLt, fp32 accumulation;
+// P and B bf16 (f32 false) or fp32 (f32 true), leading dimensions in elements
+// (k_gemm.hip). False when hipBLASLt has no algorithm for the shape.
+bool blaslt_gemm(bool f32, int64_t M, int64_t N, int64_t K, const void* P, int64_t ldp, const void* B, int64_t ldb,
+                 float* C, int64_t ldc, const float* bias, bool accumulate);
 // y = silu(gate) * up over n floats (the SwiGLU kernel of sdh_swiglu, no checks).
 void launch_swiglu(const float* gate, const float* up, float* y, int64_t n);
 // Zero-initialised per-library device counters (uint32), persistent across

@@ -134,13 +134,15 @@ def test_gemm_invalid_arguments(be):
 @pytest.mark.parametrize("M,N,K,lda,with_bias,acc", [
     (5, 7, 16, 16, False, False), (70, 130, 64, 64, True, False), (4096, 64, 3840, 3840, True, False),
     (129, 3840, 64, 64, True, True), (9, 33, 13, 13, True, False), (65, 64, 100, 104, False, True),
-    (1, 1024, 256, 256, True, False),
+    (1, 1024, 256, 256, True, False), (300, 64, 3840, 3841, True, False),
 ])
 def test_gemm_nt_f32(be, orc, M, N, K, lda, with_bias, acc):
     """The fp32-weight linear (sdh_gemm_nt_f32) against the exact sum, within
     the fp32 accumulation bound; the Z-Image final projection [4096,3840] x
     [64,3840]^T and patch embedding [*, 64] x [3840, 64]^T shapes; K not a
-    multiple of 4 (scalar loads), padded rows, accumulate and bias."""
+    multiple of 4 (scalar loads), padded rows, accumulate and bias. Aligned
+    operands run on hipBLASLt, the others (ldc or lda not a multiple of 4) on
+    the hand-written kernel."""
     A = orc.randn((M, lda), 600 + M + K)
     W = orc.randn((N, K), 601 + N, 0.0, 0.05)
     b = orc.randn((N,), 602, 0.0, 0.5) if with_bias else None
