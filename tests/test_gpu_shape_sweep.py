@@ -1,13 +1,12 @@
-"""GPU sweep of seeded pseudo-random shapes per op, through the C ABI, against
-the oracle with the usual tolerances.
+"""GPU sweep of shapes across every dispatch boundary, through the C ABI,
+against the oracle with the usual tolerances (seeded inputs).
 
 The parity tests pin each op at its config shapes and hand-picked edge cases;
 the launchers also choose among kernels by row width (the float4 count per
-lane, one wave or one workgroup per row), alignment of the width, head size
-and group size. This sweep draws widths across those buckets (including
-widths just above and below each boundary) so every dispatch branch runs on
-shapes nobody picked by hand. Sizes stay small; the whole sweep takes
-seconds.
+lane, one wave or one workgroup per row), alignment of the width, head size,
+group size and key/query tiling. This sweep takes widths just below, at and
+just above each of those boundaries, so every dispatch branch runs. Sizes
+stay small; the whole sweep takes seconds.
 """
 import math
 
@@ -123,3 +122,23 @@ def test_broadcast_sweep(be, orc, dim):
         dz = be.empty((rows, dim // 2))
         be.geglu(be.array(x), dz, rows, dim // 2)
         assert_elementwise(dz.download(), orc.geglu(x), f"geglu D={dim // 2}")
+
+
+ATTN_TOL = 1e-4  # max-abs on unit-variance inputs, as tests/test_gpu_attention.py
+
+
+@pytest.mark.parametrize("d", [1, 8, 15, 16, 33, 63, 64, 65, 100, 127, 128, 129, 200, 256])
+@pytest.mark.parametrize("Sq,Skv,causal", [(1, 1, False), (17, 70, False), (70, 17, True), (300, 300, True),
+                                           (257, 129, False)])
+def test_attention_sweep(be, orc, d, Sq, Skv, causal):
+    """Head sizes across the MFMA kernel's two paddings (64, 128), its scalar
+    loads (d below the padding) and the generic kernel (d > 128); query and key
+    counts off the 256-query and 64-key tiles; grouped heads."""
+    N, heads, kvh = 1, 4, 2
+    q = orc.randn((N, Sq, heads * d), 5400 + d)
+    k = orc.randn((N, Skv, kvh * d), 5401 + d)
+    v = orc.randn((N, Skv, kvh * d), 5402 + d)
+    out = be.empty((N, Sq, heads * d))
+    be.attention(be.array(q), be.array(k), be.array(v), out, N, Sq, Skv, heads, kvh, d, causal)
+    err = float(np.max(np.abs(out.download() - orc.attention(q, k, v, heads, causal, kvh))))
+    assert err <= ATTN_TOL, f"attention d={d} Sq={Sq} Skv={Skv} causal={causal}: max-abs {err:.3g}"
