@@ -101,6 +101,13 @@ int sdh_gemm_nt_bf16_packed(int64_t M, int64_t N, int64_t K, const uint16_t* A, 
  * elements; bias may be NULL. The linear layers whose weights stay fp32. */
 int sdh_gemm_nt_f32(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B, int64_t ldb,
                     float* C, int64_t ldc, const float* bias, int accumulate);
+/* backend_cuda.h:45-47 conv2d(); tensor.h:159 (tensor.cpp:520-560).
+ * x [N, Cin, H, W], w [Cout, Cin, kh, kw] fp32, bias [Cout] or NULL,
+ * out [N, Cout, Ho, Wo] with Ho = (H + 2 pad - kh) / stride + 1 (and Wo
+ * alike); zero padding. Patches gathered per pixel chunk, then the fp32
+ * GEMM: completes the reference's backend interface, not a tuned path. */
+int sdh_conv2d(const float* x, int64_t N, int64_t Cin, int64_t H, int64_t W, const float* w, int64_t Cout, int64_t kh,
+               int64_t kw, const float* bias, int stride, int pad, float* out, int64_t Ho, int64_t Wo);
 /* Tensor::to_bf16 (tensor.cpp:131-137) on device memory: y[i] = bf16 bits of
  * x[i] (nearest even; inf and NaN keep their top 16 bits). */
 int sdh_to_bf16(const float* x, uint16_t* y, int64_t n);

@@ -317,6 +317,38 @@ class Oracle:
             acc = acc + np.asarray(bias, np.float64)[None, :]
         return acc.astype(np.float32), np.abs(a) @ np.abs(b).T
 
+    def conv2d(self, x, w, b=None, stride=1, pad=0):
+        """float64 conv2d as the reference defines it (tensor.cpp:520-560): out
+        [N, Cout, Ho, Wo], Ho = (H + 2 pad - kh) / stride + 1, out[n, co, oy, ox]
+        = b[co] + sum over (ci, ky, kx) of w[co, ci, ky, kx] x[n, ci, oy*stride
+        - pad + ky, ox*stride - pad + kx], zero outside the image. Returns
+        (out as fp32, S = the same sum of absolute products) for the fp32
+        accumulation bound."""
+        x = np.asarray(x, np.float32).astype(np.float64)
+        w = np.asarray(w, np.float32).astype(np.float64)
+        N, Cin, H, W = x.shape
+        Cout, _, kh, kw = w.shape
+        Ho, Wo = (H + 2 * pad - kh) // stride + 1, (W + 2 * pad - kw) // stride + 1
+        xp = np.zeros((N, Cin, H + 2 * pad, W + 2 * pad))
+        xp[:, :, pad:pad + H, pad:pad + W] = x
+        plant = getattr(self, "_plant_py", 0)
+        cols = np.empty((N, Ho, Wo, Cin, kh, kw))
+        for ky in range(kh):
+            for kx in range(kw):
+                win = xp[:, :, ky:ky + stride * (Ho - 1) + 1:stride, kx:kx + stride * (Wo - 1) + 1:stride]
+                if plant == 15 and kh == kw:  # planted: kernel taps transposed (ky, kx swapped)
+                    cols[..., kx, ky] = win.transpose(0, 2, 3, 1)
+                else:
+                    cols[..., ky, kx] = win.transpose(0, 2, 3, 1)
+        cols = cols.reshape(N, Ho * Wo, Cin * kh * kw)
+        wm = w.reshape(Cout, -1)
+        out = np.matmul(cols, wm.T).transpose(0, 2, 1)
+        S = np.matmul(np.abs(cols), np.abs(wm).T).transpose(0, 2, 1)
+        if b is not None and plant != 16:  # planted 16: bias dropped
+            out = out + np.asarray(b, np.float64)[None, :, None]
+            S = S + np.abs(np.asarray(b, np.float64))[None, :, None]
+        return out.reshape(N, Cout, Ho, Wo).astype(np.float32), S.reshape(N, Cout, Ho, Wo)
+
     def linear_swiglu(self, x, w1_16, w3_16):
         """y = swiglu(x w1^T, x w3^T) with exact products, plus the exact g,
         u and their accumulation scales (for the test's error bound)."""
@@ -585,6 +617,7 @@ class Reference:
             "ref_tensor_data16": (C.POINTER(C.c_uint16), [_vp]),
             "ref_linear": (_vp, [_vp, _vp, _vp]),
             "ref_attention": (_vp, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
+            "ref_conv2d": (_vp, [_vp, _vp, _vp, C.c_int, C.c_int]),
             "ref_zimage_forward": (C.c_int, [C.c_char_p, C.c_int, _i64, C.c_int, _f32p, _i64, _i64, _i64, _fl, _f32p,
                                              _i64, _i64, _f32p]),
             "ref_patchify2d": (_vp, [_vp, C.c_int]),
@@ -793,6 +826,20 @@ class Reference:
         finally:
             self.free(hq, hk, hv)
         return self.take(h, q.shape)
+
+    def conv2d(self, x, w, b=None, stride=1, pad=0):
+        """The reference's CPU conv2d (tensor.cpp:520-560: im2col rows, then the
+        fp32 GEMM seeded with the bias)."""
+        x, w = _f32(x), _f32(w)
+        hx, hw = self.new(x.shape, x), self.new(w.shape, w)
+        hb = self.new(b.shape, _f32(b)) if b is not None else None
+        try:
+            h = self._ptr(self.lib.ref_conv2d(hx, hw, hb, stride, pad))
+        finally:
+            self.free(hx, hw, hb)
+        N, _, H, W = x.shape
+        Cout, _, kh, kw = w.shape
+        return self.take(h, (N, Cout, (H + 2 * pad - kh) // stride + 1, (W + 2 * pad - kw) // stride + 1))
 
     def zimage_forward(self, path, x, t, cap, heads, keep_bf16=True, bf16_min_numel=1 << 20):
         """The reference's ZImageTransformer::forward on the CPU (zimage.cpp:

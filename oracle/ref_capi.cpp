@@ -103,6 +103,11 @@ int ref_tensor_to_bf16(void* h) { return guard([&] { T(h)->to_bf16(); }); }
 const uint16_t* ref_tensor_data16(void* h) { return T(h)->ptr16(); }
 void* ref_linear(void* x, void* W, void* b) { return guard_ptr([&] { return wrap(sd::linear(*T(x), *T(W), opt(b))); }); }
 
+// ---- conv2d (new tensor, tensor.cpp:520-560) ----
+void* ref_conv2d(void* x, void* w, void* b, int stride, int pad) {
+    return guard_ptr([&] { return wrap(sd::conv2d(*T(x), *T(w), opt(b), stride, pad)); });
+}
+
 // ---- attention (new tensor) ----
 void* ref_attention(void* q, void* k, void* v, int heads, int causal, int kv_heads) {
     return guard_ptr([&] { return wrap(sd::attention(*T(q), *T(k), *T(v), heads, causal != 0, kv_heads)); });

@@ -76,6 +76,8 @@ STUB(int sdh_swiglu_bf16(const float*, const float*, uint16_t*, int64_t))
 STUB(int sdh_gemm_nt_f32(int64_t, int64_t, int64_t, const float*, int64_t, const float*, int64_t, float*, int64_t,
                          const float*, int))
 STUB(int sdh_to_bf16(const float*, uint16_t*, int64_t))
+STUB(int sdh_conv2d(const float*, int64_t, int64_t, int64_t, int64_t, const float*, int64_t, int64_t, int64_t,
+                    const float*, int, int, float*, int64_t, int64_t))
 STUB(int sdh_gemm_nt_bf16(int64_t, int64_t, int64_t, const float*, int64_t, const uint16_t*, int64_t, float*, int64_t,
                           const float*, int))
 STUB(int sdh_linear_swiglu(const float*, const uint16_t*, const uint16_t*, float*, int64_t, int64_t, int64_t))

@@ -160,6 +160,11 @@ inline void gemm_nt_f32(int64_t M, int64_t N, int64_t K, const float* A, int64_t
     detail::check(sdh_gemm_nt_f32(M, N, K, A, lda, B, ldb, C, ldc, bias, accumulate ? 1 : 0), "hip::gemm_nt_f32");
 }
 inline void to_bf16(const float* x, uint16_t* y, int64_t n) { detail::check(sdh_to_bf16(x, y, n), "hip::to_bf16"); }
+// backend_cuda.h:45-47
+inline void conv2d(const float* x, int64_t N, int64_t Cin, int64_t H, int64_t W, const float* w, int64_t Cout,
+                   int64_t kh, int64_t kw, const float* bias, int stride, int pad, float* out, int64_t Ho, int64_t Wo) {
+    detail::check(sdh_conv2d(x, N, Cin, H, W, w, Cout, kh, kw, bias, stride, pad, out, Ho, Wo), "hip::conv2d");
+}
 inline void gemm_nt_bf16_packed(int64_t M, int64_t N, int64_t K, const uint16_t* A, int64_t lda, const uint16_t* B,
                                 int64_t ldb, float* C, int64_t ldc, const float* bias, bool accumulate) {
     detail::check(sdh_gemm_nt_bf16_packed(M, N, K, A, lda, B, ldb, C, ldc, bias, accumulate ? 1 : 0),

@@ -459,6 +459,21 @@ Tensor linear_swiglu(const Tensor& x, const Tensor& w1, const Tensor& w3) {
     return y;
 }
 
+// tensor.cpp:529-541: the reference's shape checks and messages, device branch
+Tensor conv2d(const Tensor& x, const Tensor& W, const Tensor* b, int stride, int pad) {
+    const int64_t N = x.dim(0), Cin = x.dim(1), H = x.dim(2), Wd = x.dim(3);
+    const int64_t Cout = W.dim(0), kh = W.dim(2), kw = W.dim(3);
+    if (W.dim(1) != Cin) throw std::runtime_error("conv2d: input " + x.shape_str() + " vs weight " + W.shape_str());
+    const int64_t Ho = (H + 2 * pad - kh) / stride + 1, Wo = (Wd + 2 * pad - kw) / stride + 1;
+    same_device(x, W, "conv2d");
+    need_hip(x, "conv2d");
+    if (W.is_bf16()) throw std::runtime_error("conv2d: bf16 conv weights are not supported");
+    if (b) same_device(x, *b, "conv2d");
+    Tensor out = Tensor::empty({N, Cout, Ho, Wo}, Device::HIP);
+    sd::hip::conv2d(x.dptr(), N, Cin, H, Wd, W.dptr(), Cout, kh, kw, opt(b), stride, pad, out.dptr(), Ho, Wo);
+    return out;
+}
+
 // tensor.cpp:776-790: the reference's shape checks and messages, device branch
 namespace {
 Tensor attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal, int kv_heads,

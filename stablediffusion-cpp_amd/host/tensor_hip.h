@@ -120,6 +120,8 @@ Tensor repeat_batch(const Tensor& x, int64_t times);
 Tensor linear(const Tensor& x, const Tensor& W, const Tensor* b);
 // swiglu(linear(x, w1), linear(x, w3)) in one GEMM (zimage.cpp:130)
 Tensor linear_swiglu(const Tensor& x, const Tensor& w1, const Tensor& w3);
+// tensor.h:159: x [N, Cin, H, W], W [Cout, Cin, kh, kw] (F32), b [Cout] or null
+Tensor conv2d(const Tensor& x, const Tensor& W, const Tensor* b, int stride, int pad);
 
 // ---- the Z-Image block's fused ops (zimage.cpp:114-135); results equal the
 // op sequences named, bit for bit ----

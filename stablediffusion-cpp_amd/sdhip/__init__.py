@@ -86,6 +86,7 @@ SIGNATURES = {
     "sdh_rms_norm_gated_add": [_vp, _vp, _i64, _i64, _vp, _vp, _fl],
     "sdh_swiglu_bf16": [_vp, _vp, _vp, _i64],
     "sdh_gemm_nt_f32": [_i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, C.c_int],
+    "sdh_conv2d": [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, C.c_int, C.c_int, _vp, _i64, _i64],
     "sdh_to_bf16": [_vp, _vp, _i64],
     "sdh_attention": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
     "sdh_attention_bf16": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
@@ -348,6 +349,9 @@ class Backend:
 
     def gemm_nt_f32(self, M, N, K, A, lda, B, ldb, C, ldc, bias=None, accumulate=False):
         self.call("sdh_gemm_nt_f32", M, N, K, _p(A), lda, _p(B), ldb, _p(C), ldc, _p(bias), int(bool(accumulate)))
+
+    def conv2d(self, x, N, Cin, H, W, w, Cout, kh, kw, bias, stride, pad, out, Ho, Wo):
+        self.call("sdh_conv2d", _p(x), N, Cin, H, W, _p(w), Cout, kh, kw, _p(bias), stride, pad, _p(out), Ho, Wo)
 
     def to_bf16(self, x, y, n):
         self.call("sdh_to_bf16", _p(x), _p(y), n)
