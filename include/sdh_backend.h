@@ -3,8 +3,10 @@
  * elementwise / reduction / broadcast ops of StableDiffusion-cpp's tensor
  * library.
  *
- * It replaces the non-GEMM part of the reference's GPU boundary,
- * src/backend_cuda.h (namespace sd::cuda, raw device pointers + int64 sizes).
+ * It implements every function of the reference's GPU boundary,
+ * src/backend_cuda.h (namespace sd::cuda, raw device pointers + int64 sizes):
+ * the elementwise / reduction / broadcast ops it is built for, and the
+ * GEMMs, attention and conv2d that complete the interface.
  * Each entry point keeps the parameters of the function it replaces, in the
  * same order and with the same meaning; the comment on each cites that
  * declaration. Differences, all at the ABI level:
