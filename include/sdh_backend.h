@@ -26,8 +26,12 @@
  *   - additive entry points (marked FUSED) have no single reference
  *     function; their comment names the reference composition they equal.
  *
- * Thread safety: calls may come from any thread; the allocator is
- * mutex-guarded; ops on one stream are serialised in call order.
+ * Thread safety: calls may come from any thread. Each entry point holds
+ * one library lock while it checks its arguments and queues its kernels,
+ * so the launches of one op reach the single library stream together and
+ * ops that run several kernels through the shared scratch buffer cannot
+ * interleave; ops run in the order their calls took the lock. A call that
+ * waits (sdh_download, sdh_synchronize) holds the lock while it waits.
  */
 #ifndef SDH_BACKEND_H
 #define SDH_BACKEND_H

@@ -175,6 +175,15 @@ Runtime& rt() {
     return r;
 }
 
+}  // namespace
+
+std::recursive_mutex& op_mutex() {
+    static std::recursive_mutex m;
+    return m;
+}
+
+namespace {
+
 void probe_locked(Runtime& r) {
     if (r.probed) return;
     r.probed = true;

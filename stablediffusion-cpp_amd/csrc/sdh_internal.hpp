@@ -8,6 +8,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <stdexcept>
+#include <mutex>
 #include <string>
 
 #include "sdh_backend.h"
@@ -27,9 +28,16 @@ struct Error : std::runtime_error {
 [[noreturn]] void fail(int status, const std::string& msg);
 void hip_check(hipError_t e, const char* what);
 void set_last_error(const char* msg);
+// Held by every C entry point while it checks arguments and queues its
+// work, so an op's launches reach the stream together: ops that run several
+// kernels through the shared scratch buffer (GroupNorm's split schedule,
+// attention, the bf16 GEMM's packed A, conv2d) cannot interleave with
+// another thread's. Recursive: entry points call entry points.
+std::recursive_mutex& op_mutex();
 
 template <class F>
 int guarded(F&& f) noexcept {
+    std::lock_guard<std::recursive_mutex> lk(op_mutex());
     try {
         f();
         set_last_error("");
