@@ -7,10 +7,15 @@
 // apply step uses the reference's folded form y = x * a + (beta - mean * a),
 // a = rstd * gamma[c], then SiLU as x / (1 + exp(-x)).
 //
-// Two schedules:
+// Three schedules:
 //   * single: one workgroup (256 or 1024 threads) per segment when the
 //     segment fits in its registers (<= 65536 floats). One HBM read, one
 //     write. Used by the SD 1.5 shapes.
+//   * resident (larger segments, large tensors): teams of workgroups hold a
+//     segment in registers across a team wait, so x is read once (two
+//     streams); pipelined over two register buffers when a team has several
+//     rounds. Described at k_gn_resident; run_gn_resident says when it is
+//     chosen.
 //   * split: the segment is cut into chunks of kChunk floats.
 //       pass A (k_gn_partial): one workgroup per chunk computes the chunk's
 //         sum and its M2 around the chunk mean from registers and stores the
@@ -31,9 +36,11 @@
 //     Measured on MI355X the Infinity Cache does not keep streamed reads
 //     (re-reading 64-512 MB is no faster than the first read), so for
 //     tensors much larger than L2 this schedule moves three streams (x, x,
-//     y) against the two of the algorithmic minimum.
+//     y) against the two of the algorithmic minimum: the resident schedule
+//     takes those.
 #include <algorithm>
 #include <cstdlib>
+#include <string>
 
 #include "sdh_internal.hpp"
 
@@ -256,6 +263,254 @@ __global__ __launch_bounds__(kThreads) void k_gn_apply(const float* __restrict__
     }
 }
 
+// ---- resident schedule -------------------------------------------------------
+// One launch of at most as many 1024-thread workgroups as the GPU holds at
+// once (occupancy x CUs). A team of P consecutive workgroups owns one segment at a time
+// (segments team, team + T, ...; T = teams), each workgroup a share of
+// 4096 * V floats kept in registers: it loads its share once, publishes the
+// share's (sum, M2 around the share mean), waits for its team's P pairs,
+// merges them in double (the split schedule's finalize arithmetic, in the
+// same fixed order in every workgroup of the team) and writes y from its
+// registers. x is read once: two streams, the algorithmic minimum.
+//
+// Publication without fences: each value travels in one 64-bit agent-scope
+// atomic store together with a 32-bit tag (round + 1), so a reader that sees
+// the tag sees the value, and no device-scope release (which would write
+// back the per-XCD L2s) is needed. Slots alternate between two parities by
+// round: a workgroup's round r + 2 store, the next into round r's slot,
+// follows its own wait for every teammate's round r + 1 value, which each
+// teammate publishes only after its round r reads. The last workgroup to
+// finish clears the slots and the finish counter, so every launch starts
+// from zeroed slots and tags 1, 2, ... never match a stale value.
+//
+// Teams wait only on their own members: P consecutive workgroups, which the
+// dispatcher places in order, in a grid no larger than the GPU holds at
+// once, so once earlier work on the GPU drains every member of a waiting
+// team is resident. (Not a cooperative launch: measured, a cooperative
+// launch fails with hipErrorIllegalState in a second process while another
+// process that made one is alive.) Each wait is still bounded (spin_limit
+// polls): on expiry the workgroup sets ctl[1], writes NaN for its share and
+// goes on, so the kernel always drains; the host reports ctl[1] at the next
+// synchronisation.
+constexpr int kResThreads = 1024;
+constexpr int kResMaxTeam = 64;  // workgroups per segment per slot of a polling lane
+constexpr int kCtlWords = 64;     // ctl[0] finished workgroups, ctl[1] error word; slots from ctl + 64
+constexpr unsigned kSpinLimit = 1u << 20;  // polls of about 1 us: a wait ends within about a second
+
+using u64 = unsigned long long;
+
+__device__ __forceinline__ void put_slot(u64* s, float v, unsigned tag) {
+    __hip_atomic_store(s, ((u64)tag << 32) | (u64)__float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 get_slot(const u64* s) {
+    return __hip_atomic_load(s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct ResArgs {
+    const float* x;
+    float* y;
+    const float* gamma;
+    const float* beta;
+    unsigned* ctl;
+    int L, HW, cg, groups, nseg, P;
+    unsigned spin_limit;
+    float eps;
+};
+
+// UNIFORM: every share is full and lies in one channel (HW % (4096 V) ==
+// 0), so one (a, b) per workgroup.
+template <int V, bool UNIFORM>
+__device__ __forceinline__ void res_load(f4 (&v)[V], const float* x, int64_t base, int n4) {
+    const f4* p = (const f4*)(x + base);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = threadIdx.x + kResThreads * j;
+        v[j] = (UNIFORM || idx < n4) ? dev::ld_stream(p + idx) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+}
+
+// Wave 0: waits for the team's (sum, M2) pairs of this round (lane i holds
+// parts i, i + 64, ...; KS slots per lane), merges them in double and
+// leaves (mean, rstd) in *stat.
+template <int KS>
+__device__ __forceinline__ void res_team_stats(const ResArgs& a, const u64* slots, int team, int par, unsigned tag,
+                                               int share, float2* stat) {
+    const int lane = threadIdx.x;
+    float sv[KS], mv[KS];
+    unsigned pending = 0;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+        sv[k] = 0.f;
+        mv[k] = 0.f;
+        if (lane + 64 * k < a.P) pending |= 1u << k;
+    }
+    const u64* ts = slots + (size_t)team * a.P * 4 + par * 2;
+    bool timed_out = false;
+    for (unsigned it = 0;; ++it) {
+        if (it >= a.spin_limit) {
+            timed_out = true;
+            break;
+        }
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            if (pending & (1u << k)) {
+                const u64* q = ts + (size_t)(lane + 64 * k) * 4;
+                const u64 u = get_slot(q), w = get_slot(q + 1);
+                if ((unsigned)(u >> 32) == tag && (unsigned)(w >> 32) == tag) {
+                    sv[k] = __uint_as_float((unsigned)u);
+                    mv[k] = __uint_as_float((unsigned)w);
+                    pending &= ~(1u << k);
+                }
+            }
+        }
+        if (!__any(pending != 0)) break;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    double tot = 0.0;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) tot += (double)sv[k];
+    const double mean = wave_dsum(tot) / (double)a.L;
+    double m2t = 0.0;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+        const int i = lane + 64 * k;
+        if (i < a.P) {
+            const double ni = (double)min(share, a.L - i * share);
+            const double dm = (double)sv[k] / ni - mean;
+            m2t += (double)mv[k] + ni * dm * dm;
+        }
+    }
+    const double m2s = wave_dsum(m2t);
+    if (lane == 0) {
+        float meanf = (float)mean, rstd = (float)(1.0 / sqrt(m2s / (double)a.L + (double)a.eps));
+        if (timed_out) {
+            __hip_atomic_store(a.ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            meanf = rstd = __builtin_nanf("");
+        }
+        *stat = make_float2(meanf, rstd);
+    }
+}
+
+// One round of one workgroup: share statistics from registers, publication,
+// (PREFETCH: the next round's loads into nxt, issued before the wait so
+// they run under it), the team wait, and y from registers.
+template <int V, bool SILU, bool UNIFORM, int KS, bool PREFETCH>
+__device__ __forceinline__ void res_round(const ResArgs& a, f4 (&cur)[V], f4 (&nxt)[V], int seg, int next_seg,
+                                          int round, int team, int off, int n4, float* sh, float2* stat) {
+    constexpr int kShare = kResThreads * V * 4;
+    u64* slots = (u64*)(a.ctl + kCtlWords);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) s += dev::hsum(cur[j]);  // masked entries are zero
+    const float sum = block_sum<kResThreads>(s, sh);
+    const float mc = sum / (float)(n4 * 4);
+    float m2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = threadIdx.x + kResThreads * j;
+        if (UNIFORM || idx < n4) {
+            const f4 d = cur[j] - mc;
+            m2 += dev::hsum(d * d);
+        }
+    }
+    const float M2 = block_sum<kResThreads>(m2, sh);
+    const unsigned tag = (unsigned)round + 1;
+    const int par = round & 1;
+    if (threadIdx.x == 0) {
+        u64* mine = slots + ((size_t)blockIdx.x * 2 + par) * 2;
+        put_slot(mine, sum, tag);
+        put_slot(mine + 1, M2, tag);
+    }
+    if constexpr (PREFETCH) {
+        if (next_seg < a.nseg) res_load<V, UNIFORM>(nxt, a.x, (int64_t)next_seg * a.L + off, n4);
+    }
+    if (threadIdx.x < 64) res_team_stats<KS>(a, slots, team, par, tag, kShare, stat);
+    __syncthreads();
+    const float meanf = stat->x, rstd = stat->y;
+    f4* q = (f4*)(a.y + (int64_t)seg * a.L + off);
+    const int gc = (seg % a.groups) * a.cg;
+    if constexpr (UNIFORM) {
+        const int ch = gc + off / a.HW;
+        const float ca = rstd * a.gamma[ch];
+        const float cb = a.beta[ch] - meanf * ca;
+#pragma unroll
+        for (int j = 0; j < V; ++j) dev::st_stream(q + threadIdx.x + kResThreads * j, apply4<SILU>(cur[j], ca, cb));
+    } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const int idx = threadIdx.x + kResThreads * j;
+            if (idx < n4) {
+                const int ch = gc + (int)((unsigned)(off + idx * 4) / (unsigned)a.HW);
+                const float ca = rstd * a.gamma[ch];
+                const float cb = a.beta[ch] - meanf * ca;
+                dev::st_stream(q + idx, apply4<SILU>(cur[j], ca, cb));
+            }
+        }
+    }
+}
+
+// Every workgroup has finished its reads of the slots before it counts
+// itself finished; the last one clears the slots of this launch and the
+// counter.
+__device__ __forceinline__ void res_finish(unsigned* ctl, unsigned* last) {
+    u64* slots = (u64*)(ctl + kCtlWords);
+    if (threadIdx.x == 0)
+        *last = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    __syncthreads();
+    if (*last) {
+        for (unsigned i = threadIdx.x; i < gridDim.x * 4; i += kResThreads)
+            __hip_atomic_store(slots + i, (u64)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) __hip_atomic_store(ctl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// grid = T * P workgroups of kResThreads; segments team, team + T, ... one
+// round each; P <= 64.
+template <int V, bool SILU, bool UNIFORM>
+__global__ __launch_bounds__(kResThreads) void k_gn_resident(ResArgs a) {
+    constexpr int kShare4 = kResThreads * V;
+    __shared__ float sh[kResThreads / 64];
+    __shared__ float2 stat;
+    __shared__ unsigned last;
+    const int team = blockIdx.x / a.P, part = blockIdx.x - team * a.P, T = gridDim.x / a.P;
+    const int off = part * kShare4 * 4;
+    const int n4 = UNIFORM ? kShare4 : min(kShare4, (a.L - off) >> 2);
+    int round = 0;
+    for (int seg = team; seg < a.nseg; seg += T, ++round) {
+        f4 v[V];
+        res_load<V, UNIFORM>(v, a.x, (int64_t)seg * a.L + off, n4);
+        res_round<V, SILU, UNIFORM, 1, false>(a, v, v, seg, 0, round, team, off, n4, sh, &stat);
+    }
+    res_finish(a.ctl, &last);
+}
+
+// The same schedule software-pipelined over two register buffers: round
+// r + 1's share is loaded while round r waits for its team, so the waits
+// (and the share reductions) overlap HBM traffic. P <= 128 (two slots per
+// polling lane).
+template <int V, bool SILU, bool UNIFORM>
+__global__ __launch_bounds__(kResThreads) void k_gn_resident_pipe(ResArgs a) {
+    constexpr int kShare4 = kResThreads * V;
+    __shared__ float sh[kResThreads / 64];
+    __shared__ float2 stat;
+    __shared__ unsigned last;
+    const int team = blockIdx.x / a.P, part = blockIdx.x - team * a.P, T = gridDim.x / a.P;
+    const int off = part * kShare4 * 4;
+    const int n4 = UNIFORM ? kShare4 : min(kShare4, (a.L - off) >> 2);
+    f4 va[V], vb[V];
+    int seg = team;
+    if (seg < a.nseg) res_load<V, UNIFORM>(va, a.x, (int64_t)seg * a.L + off, n4);
+    for (int round = 0; seg < a.nseg; round += 2) {
+        const int s1 = seg + T;
+        res_round<V, SILU, UNIFORM, 2, true>(a, va, vb, seg, s1, round, team, off, n4, sh, &stat);
+        if (s1 >= a.nseg) break;
+        const int s2 = s1 + T;
+        res_round<V, SILU, UNIFORM, 2, true>(a, vb, va, s1, s2, round + 1, team, off, n4, sh, &stat);
+        seg = s2;
+    }
+    res_finish(a.ctl, &last);
+}
+
 // ---- generic (any HW / alignment): one workgroup per segment, three strided
 // passes; statistics in double per thread, like the reference's loops.
 template <bool SILU>
@@ -317,6 +572,147 @@ int64_t gn_block_bytes() {
     return v;
 }
 
+long env_long(const char* name, long dflt) {
+    const char* e = std::getenv(name);
+    if (!e || !*e) return dflt;
+    char* end = nullptr;
+    const long v = std::strtol(e, &end, 10);
+    return (end && *end == 0 && v >= 0) ? v : dflt;
+}
+
+// One resident kernel: pipelined or not, V float4 per thread.
+struct ResKind {
+    bool pipe;
+    int V;
+};
+
+// Calls f with the instantiation for (kind, silu, uniform). Instantiated:
+// k_gn_resident V = 4, 8, 16 (16 only uniform: the per-vector channel lookup
+// would spill) and k_gn_resident_pipe V = 4, 8.
+template <class F>
+void with_resident(ResKind k, bool silu, bool uniform, F&& f) {
+    auto go = [&](auto vc, auto pc) {
+        constexpr int VV = decltype(vc)::value;
+        constexpr bool PP = decltype(pc)::value;
+        if constexpr (PP) {
+            if (silu) uniform ? f(k_gn_resident_pipe<VV, true, true>) : f(k_gn_resident_pipe<VV, true, false>);
+            else uniform ? f(k_gn_resident_pipe<VV, false, true>) : f(k_gn_resident_pipe<VV, false, false>);
+        } else {
+            if (silu) uniform ? f(k_gn_resident<VV, true, true>) : f(k_gn_resident<VV, true, false>);
+            else uniform ? f(k_gn_resident<VV, false, true>) : f(k_gn_resident<VV, false, false>);
+        }
+    };
+    using P1 = std::true_type;
+    using P0 = std::false_type;
+    if (k.V == 4) k.pipe ? go(std::integral_constant<int, 4>(), P1()) : go(std::integral_constant<int, 4>(), P0());
+    else if (k.V == 8) k.pipe ? go(std::integral_constant<int, 8>(), P1()) : go(std::integral_constant<int, 8>(), P0());
+    else if (k.V == 16 && !k.pipe && uniform) {
+        if (silu) f(k_gn_resident<16, true, true>);
+        else f(k_gn_resident<16, false, true>);
+    } else
+        fail(SDH_ERR_INVALID, "k_gn_resident: no such instantiation");
+}
+
+bool instantiated(ResKind k, bool uniform) { return k.pipe ? (k.V == 4 || k.V == 8) : (k.V != 16 || uniform); }
+
+// Resident workgroups per CU of one instantiation (0 if none); cached (calls
+// are serialised by the op lock).
+int resident_occupancy(ResKind k, bool silu, bool uniform) {
+    static int cache[2][3][2][2];
+    static bool filled = false;
+    if (!filled) {
+        for (auto& a : cache)
+            for (auto& b : a)
+                for (auto& c : b)
+                    for (int& d : c) d = -1;
+        filled = true;
+    }
+    if (!instantiated(k, uniform)) return 0;
+    int& c = cache[k.pipe][k.V == 4 ? 0 : k.V == 8 ? 1 : 2][silu][uniform];
+    if (c < 0) {
+        c = 0;
+        with_resident(k, silu, uniform, [&](auto kern) {
+            int nb = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kern), kResThreads, 0) ==
+                hipSuccess)
+                c = nb;
+            else
+                (void)hipGetLastError();
+        });
+    }
+    return c;
+}
+
+// The resident schedule for segments of L floats (HW % 4 == 0, 16-byte
+// aligned, L < 2^31), when it is expected to beat the split schedule
+// (measured on MI355X, GroupNorm + SiLU, 32 groups):
+//   * x of at least 64 MB: the split schedule's re-read comes from HBM; the
+//     k_gn_resident_pipe plan with the fewest rounds (smaller share on
+//     ties; else k_gn_resident's), e.g. [1,128,1024,1024] 247 -> 187 us,
+//     [1,256,256,256] 29.6 -> 25.8 us;
+//   * smaller x when one round of k_gn_resident covers it and the split
+//     schedule would run fewer than 1024 workgroups per pass (too few to
+//     fill the GPU): [2,640,64,64] 18.8 -> 12.7 us. Otherwise the split
+//     schedule, which re-reads from L2 at these sizes, is as fast or faster
+//     ([1,512,128,128] 15.6 vs 16.2 us; [2,320,128,128], two unbalanced
+//     rounds, 18.8 vs 22.3 us).
+// False: use the split schedule. Knobs for tests and tuning:
+// SDH_GN_RESIDENT=0 never, =2 always when a plan exists (the plan chosen as
+// for large x); SDH_GN_RESIDENT_V=4|8|16 fixes the share;
+// SDH_GN_RESIDENT_PIPE=0|1 allows only the plain or only the pipelined
+// kernel; SDH_GN_SPIN_LIMIT bounds each wait (polls; 0 expires every wait
+// at once).
+bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_t L, int64_t HW, int64_t cg,
+                     int groups, int64_t nseg, const float* gamma, const float* beta, float eps) {
+    static const long mode = env_long("SDH_GN_RESIDENT", 1);
+    static const long force_v = env_long("SDH_GN_RESIDENT_V", 0);
+    static const long force_pipe = env_long("SDH_GN_RESIDENT_PIPE", -1);
+    static const unsigned spin = (unsigned)std::min<long>(env_long("SDH_GN_SPIN_LIMIT", kSpinLimit), 0x7fffffffL);
+    if (mode == 0 || nseg > 0x7fffffffLL) return false;
+    struct Plan {
+        ResKind k{false, 0};
+        int64_t P = 0, T = 0, rounds = INT64_MAX;
+    };
+    Plan best_pipe, best_plain, best_one;
+    for (bool pipe : {false, true}) {
+        if (force_pipe >= 0 && pipe != (force_pipe != 0)) continue;
+        for (int V : {4, 8, 16}) {
+            if (force_v && V != force_v) continue;
+            const int64_t share = (int64_t)kResThreads * 4 * V;
+            const int64_t P = (L + share - 1) / share;
+            if (P > (pipe ? 2 : 1) * kResMaxTeam) continue;
+            const ResKind k{pipe, V};
+            const int64_t T = (int64_t)resident_occupancy(k, silu, HW % share == 0) * num_cus() / P;
+            if (T == 0) continue;
+            const Plan pl{k, P, T, (nseg + T - 1) / T};
+            Plan& slot = pipe ? best_pipe : best_plain;
+            if (pl.rounds < slot.rounds) slot = pl;
+            if (!pipe && pl.rounds == 1 && !best_one.k.V) best_one = pl;
+        }
+    }
+    const bool large = nseg * L * 4 >= (int64_t(64) << 20);
+    const int64_t split_wgs = nseg * ((L + kChunk - 1) / kChunk);
+    Plan pl;
+    if (large || mode == 2) pl = best_pipe.k.V ? best_pipe : best_plain;
+    else if (best_one.k.V && split_wgs < 1024) pl = best_one;
+    if (!pl.k.V) return false;
+    const bool uniform = HW % ((int64_t)kResThreads * 4 * pl.k.V) == 0;
+    const int64_t grid = std::min(pl.T, nseg) * pl.P;
+    ResArgs args{x, y, gamma, beta, nullptr, (int)L, (int)HW, (int)cg, groups, (int)nseg, (int)pl.P, spin, eps};
+    args.ctl = counters((size_t)kCtlWords + (size_t)grid * 8);
+    void* argv[] = {&args};
+    with_resident(pl.k, silu, uniform, [&](auto kern) {
+        const std::string what = std::string(op) + ": launch of " + std::to_string(grid) + " resident workgroups (" +
+                                 (pl.k.pipe ? "pipelined, " : "") + "V " + std::to_string(pl.k.V) + ", " +
+                                 std::to_string(resident_occupancy(pl.k, silu, uniform)) + " per CU)";
+        hip_check(hipLaunchKernel(reinterpret_cast<const void*>(kern), dim3((unsigned)grid), dim3(kResThreads), argv,
+                                  0, stream()),
+                  what.c_str());
+    });
+    arm_device_check(args.ctl + 1, op);
+    return true;
+}
+
 void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups,
             const float* gamma, const float* beta, float eps) {
     need(N >= 0 && C >= 0 && HW >= 0, op, "negative size");
@@ -363,6 +759,9 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
         else if (n4 <= 8192) go(K(), std::integral_constant<int, 8>());
         else if (n4 <= 12288) go(K(), std::integral_constant<int, 12>());
         else go(K(), std::integral_constant<int, 16>());
+    } else if (vec && gn_block_bytes() == 0 &&
+               run_gn_resident(op, silu, x, y, L, HW, cg, groups, nseg, gamma, beta, eps)) {
+        return;
     } else if (vec) {
         const int64_t nchunks = (L + kChunk - 1) / kChunk;
         // segments per block: the apply pass re-reads a block right after

@@ -168,6 +168,8 @@ struct Runtime {
     size_t counter_count = 0;
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
+    unsigned* check_word = nullptr;  // see arm_device_check
+    const char* check_what = nullptr;
 };
 
 Runtime& rt() {
@@ -234,6 +236,24 @@ void range_check_locked(Runtime& r, const void* p, size_t bytes, const char* op,
     if (inside(r.arena.requested) || inside(r.external)) return;
     fail(SDH_ERR_INVALID, std::string(op) + ": " + what + " (" + std::to_string(bytes) +
                               " bytes) is not inside a live backend_hip allocation");
+}
+
+// Reads and clears the word registered by arm_device_check; the stream must
+// be synchronised.
+void device_check_locked(Runtime& r) {
+    if (!r.check_word) return;
+    unsigned* w = r.check_word;
+    r.check_word = nullptr;
+    unsigned v = 0;
+    hip_check(hipMemcpyAsync(&v, w, sizeof v, hipMemcpyDeviceToHost, r.stream), "hipMemcpyAsync(device check)");
+    hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
+    if (v) {
+        const unsigned z = 0;
+        hip_check(hipMemcpyAsync(w, &z, sizeof z, hipMemcpyHostToDevice, r.stream), "hipMemcpyAsync(device check)");
+        hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
+        fail(SDH_ERR_HIP, std::string(r.check_what) +
+                              ": a bounded wait inside the kernel expired; the affected outputs hold NaN");
+    }
 }
 
 }  // namespace
@@ -321,12 +341,20 @@ void* workspace(size_t bytes) {
     return r.workspace;
 }
 
+void arm_device_check(unsigned* word, const char* what) {
+    Runtime& r = rt();
+    std::lock_guard<std::mutex> lk(r.mu);
+    r.check_word = word;
+    r.check_what = what;
+}
+
 unsigned* counters(size_t count) {
     Runtime& r = rt();
     std::lock_guard<std::mutex> lk(r.mu);
     if (count > r.counter_count) {
         if (r.counters) {
             hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
+            device_check_locked(r);  // the registered word may live in the old block
             r.arena.release(r.counters);
         }
         const size_t n = std::max(count, (size_t)4096);
@@ -393,6 +421,7 @@ int sdh_shutdown(void) {
         r.scratch_bytes = 0;
         r.counters = nullptr;
         r.counter_count = 0;
+        r.check_word = nullptr;
         r.workspace = nullptr;
         r.workspace_bytes = 0;
         for (int i = 0; i < 2; ++i) {
@@ -489,6 +518,7 @@ int sdh_download(void* dst, const void* src, size_t bytes) {
         hip_check(hipEventSynchronize(r.stage_ev[b ^ 1]), "hipEventSynchronize(staging)");
         std::memcpy((char*)dst + prev_off, r.stage[b ^ 1], prev_n);
         hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
+        device_check_locked(r);
     });
 }
 
@@ -510,6 +540,7 @@ int sdh_synchronize(void) {
         std::lock_guard<std::mutex> lk(r.mu);
         if (!r.inited) return;
         hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
+        device_check_locked(r);
     });
 }
 

@@ -80,6 +80,11 @@ void launch_swiglu(const float* gate, const float* up, float* y, int64_t n);
 // calls; kernels that use them leave them at zero when they finish.
 unsigned* counters(size_t count);
 void launched(const char* op);
+// Registers a device word that the kernel just queued sets nonzero on a
+// failure it cannot return as a status (a bounded wait that expired). The
+// next sdh_synchronize or sdh_download reads the word after its stream
+// synchronisation, clears it and fails with SDH_ERR_HIP naming `what`.
+void arm_device_check(unsigned* word, const char* what);
 // Queues a zero fill of [p, p + bytes) on the library stream (a kernel, not a memset).
 void zero_device(void* p, size_t bytes);
 
