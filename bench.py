@@ -675,12 +675,20 @@ KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
 }
 
 
-def gn_dispatches(shape, groups=32):
+# Resident workgroups per CU of the gfx950 build of each resident GroupNorm
+# kernel (its VGPR count at 1024 threads): k_gn_resident V=4 (59-62 VGPRs)
+# 2, V=8 (70-94) 1, V=16 (107) 1; k_gn_resident_pipe V=4 (80-89) 1, V=8
+# (112-124) 1.
+GN_RESIDENT_OCC = {(False, 4): 2, (False, 8): 1, (False, 16): 1, (True, 4): 1, (True, 8): 1}
+
+
+def gn_dispatches(shape, groups=32, cus=256):
     """(kernel prefix, grid work-items) of the launches that carry a GroupNorm
     workload's HBM traffic, following run_gn's choice of schedule: one
-    k_gn_single launch for segments up to 65536 floats, else k_gn_partial and
-    k_gn_apply over 8192-float chunks (k_gn_finalize moves a few KB and is
-    left out)."""
+    k_gn_single launch for segments up to 65536 floats; else the resident
+    plan of run_gn_resident when its policy takes the tensor (one launch of
+    k_gn_resident or k_gn_resident_pipe); else k_gn_partial and k_gn_apply
+    over 8192-float chunks (k_gn_finalize moves a few KB and is left out)."""
     N, Cc = shape[0], shape[1]
     HW = int(np.prod(shape[2:]))
     L, nseg = Cc // groups * HW, N * groups
@@ -688,6 +696,28 @@ def gn_dispatches(shape, groups=32):
         n4 = L // 4
         tpb = 256 if n4 <= 2048 else 1024
         return [("k_gn_single", nseg * tpb)]
+    best = {}
+    for pipe in (False, True):
+        for V in (4, 8, 16):
+            share = 4096 * V
+            P = -(-L // share)
+            if (pipe, V) not in GN_RESIDENT_OCC or P > (128 if pipe else 64) or (V == 16 and HW % share):
+                continue
+            T = GN_RESIDENT_OCC[(pipe, V)] * cus // P
+            if T == 0:
+                continue
+            rounds = -(-nseg // T)
+            key = "pipe" if pipe else "plain"
+            if key not in best or rounds < best[key][0]:
+                best[key] = (rounds, pipe, P, T)
+            if not pipe and rounds == 1 and "one" not in best:
+                best["one"] = (rounds, pipe, P, T)
+    large = nseg * L * 4 >= 64 << 20
+    split_wgs = nseg * -(-L // 8192)
+    plan = (best.get("pipe") or best.get("plain")) if large else (best.get("one") if split_wgs < 1024 else None)
+    if plan:
+        _, pipe, P, T = plan
+        return [("k_gn_resident_pipe<" if pipe else "k_gn_resident<", min(T, nseg) * P * 1024)]
     grid = (L + 8191) // 8192 * 256 * nseg
     return [("k_gn_partial", grid), ("k_gn_apply", grid)]
 

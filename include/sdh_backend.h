@@ -77,13 +77,16 @@ int sdh_free(void* p);
 /* backend_cuda.h:32 upload(): host -> device. Staged through pinned buffers
  * with hipMemcpyAsync; the host buffer may be reused when the call returns. */
 int sdh_upload(void* dst, const void* src, size_t bytes);
-/* backend_cuda.h:33 download(): device -> host; waits for all queued work. */
+/* backend_cuda.h:33 download(): device -> host; waits for all queued work.
+ * Also reports a failure found on the device since the last wait (an expired
+ * GroupNorm team wait, see sdh_group_norm) as SDH_ERR_HIP, after the copy. */
 int sdh_download(void* dst, const void* src, size_t bytes);
 /* backend_cuda.h:34 copy(): device -> device, asynchronous. */
 int sdh_copy(void* dst, const void* src, size_t bytes);
 /* backend_cuda.h:35 zero(): fills with zero bytes, asynchronous. */
 int sdh_zero(void* dst, size_t bytes);
-/* backend_cuda.h:36 synchronize(): waits for all queued work. */
+/* backend_cuda.h:36 synchronize(): waits for all queued work; reports a
+ * failure found on the device as sdh_download does. */
 int sdh_synchronize(void);
 /* No reference counterpart: lets ops accept device memory that the library did
  * not allocate (for example a framework's tensor). The range must stay valid
@@ -133,7 +136,10 @@ int sdh_linear_swiglu(const float* x, const uint16_t* w1, const uint16_t* w3, fl
 
 /* ---- norms -------------------------------------------------------------- */
 /* backend_cuda.h:48 group_norm(); tensor.h:166. x, y [N, C, HW]; gamma, beta
- * [C]; C % groups == 0. y may equal x. */
+ * [C]; C % groups == 0. y may equal x. Large segments may run on the
+ * resident schedule, whose workgroups wait for each other inside the kernel;
+ * each wait is bounded, and one that expires leaves NaN in y and is reported
+ * by the next sdh_synchronize or sdh_download. */
 int sdh_group_norm(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups, const float* gamma,
                    const float* beta, float eps);
 /* backend_cuda.h:50 layer_norm(); tensor.h:170. x, y [rows, C]; gamma, beta
