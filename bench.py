@@ -685,17 +685,15 @@ GN_RESIDENT_OCC = {(False, 4): 2, (False, 8): 1, (False, 16): 1, (True, 4): 1, (
 def gn_dispatches(shape, groups=32, cus=256):
     """(kernel prefix, grid work-items) of the launches that carry a GroupNorm
     workload's HBM traffic, following run_gn's choice of schedule: one
-    k_gn_single launch for segments up to 65536 floats; else the resident
-    plan of run_gn_resident when its policy takes the tensor (one launch of
-    k_gn_resident or k_gn_resident_pipe); else k_gn_partial and k_gn_apply
-    over 8192-float chunks (k_gn_finalize moves a few KB and is left out)."""
+    k_gn_single launch for segments up to 65536 floats, unless a segment
+    holds more than 24576 floats and one resident round takes the tensor;
+    else the resident plan of run_gn_resident when its policy takes the
+    tensor (one launch of k_gn_resident or k_gn_resident_pipe); else
+    k_gn_partial and k_gn_apply over 8192-float chunks (k_gn_finalize moves a
+    few KB and is left out)."""
     N, Cc = shape[0], shape[1]
     HW = int(np.prod(shape[2:]))
     L, nseg = Cc // groups * HW, N * groups
-    if L <= 65536:
-        n4 = L // 4
-        tpb = 256 if n4 <= 2048 else 1024
-        return [("k_gn_single", nseg * tpb)]
     best = {}
     for pipe in (False, True):
         for V in (4, 8, 16):
@@ -714,7 +712,14 @@ def gn_dispatches(shape, groups=32, cus=256):
                 best["one"] = (rounds, pipe, P, T)
     large = nseg * L * 4 >= 64 << 20
     split_wgs = nseg * -(-L // 8192)
-    plan = (best.get("pipe") or best.get("plain")) if large else (best.get("one") if split_wgs < 1024 else None)
+    if L <= 65536:
+        plan = best.get("one") if L > 24576 and split_wgs < 1024 else None
+        if not plan:
+            n4 = L // 4
+            tpb = 256 if n4 <= 2048 else 1024
+            return [("k_gn_single", nseg * tpb)]
+    else:
+        plan = (best.get("pipe") or best.get("plain")) if large else (best.get("one") if split_wgs < 1024 else None)
     if plan:
         _, pipe, P, T = plan
         return [("k_gn_resident_pipe<" if pipe else "k_gn_resident<", min(T, nseg) * P * 1024)]

@@ -10,7 +10,8 @@
 // Three schedules:
 //   * single: one workgroup (256 or 1024 threads) per segment when the
 //     segment fits in its registers (<= 65536 floats). One HBM read, one
-//     write. Used by the SD 1.5 shapes.
+//     write. Used by the SD 1.5 shapes up to 24576 floats per segment;
+//     longer segments of few-segment tensors take one resident round.
 //   * resident (larger segments, large tensors): teams of workgroups hold a
 //     segment in registers across a team wait, so x is read once (two
 //     streams); pipelined over two register buffers when a team has several
@@ -53,6 +54,9 @@ constexpr int kThreads = 256;
 constexpr int kChunkV = 8;                               // float4 per thread per chunk
 constexpr int64_t kChunk = (int64_t)kThreads * 4 * kChunkV;  // floats per chunk (8192)
 constexpr int64_t kGnBlockMB = 0;
+// Segments longer than this (up to 65536 floats) try one resident round
+// before the single-workgroup schedule (run_gn_resident).
+constexpr int64_t kSmallResidentMin = 24576;
 
 // SiLU on the hardware exp2 and reciprocal: x * rcp(1 + 2^(-x log2 e)). Its
 // error against the correctly rounded x / (1 + expf(-x)) is a few ulp (the
@@ -652,7 +656,12 @@ int resident_occupancy(ResKind k, bool silu, bool uniform) {
 //     [1,256,256,256] 29.6 -> 25.8 us;
 //   * smaller x when one round of k_gn_resident covers it and the split
 //     schedule would run fewer than 1024 workgroups per pass (too few to
-//     fill the GPU): [2,640,64,64] 18.8 -> 12.7 us. Otherwise the split
+//     fill the GPU): [2,640,64,64] 18.8 -> 12.7 us; with one_round_only
+//     (segments of kSmallResidentMin + 1 to 65536 floats, ahead of the
+//     single-workgroup schedule) only this case: [2,320,64,64] 11.5 ->
+//     9.3 us, [2,1280,32,32] 11.6 -> 9.4 us, [2,960,32,32] 9.5 -> 8.6 us,
+//     while [2,640,32,32] (20480 floats: shares of 16384 + 4096) measured
+//     7.6 single against 7.9 resident. Otherwise the split
 //     schedule, which re-reads from L2 at these sizes, is as fast or faster
 //     ([1,512,128,128] 15.6 vs 16.2 us; [2,320,128,128], two unbalanced
 //     rounds, 18.8 vs 22.3 us).
@@ -663,7 +672,8 @@ int resident_occupancy(ResKind k, bool silu, bool uniform) {
 // kernel; SDH_GN_SPIN_LIMIT bounds each wait (polls; 0 expires every wait
 // at once).
 bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_t L, int64_t HW, int64_t cg,
-                     int groups, int64_t nseg, const float* gamma, const float* beta, float eps) {
+                     int groups, int64_t nseg, const float* gamma, const float* beta, float eps,
+                     bool one_round_only) {
     static const long mode = env_long("SDH_GN_RESIDENT", 1);
     static const long force_v = env_long("SDH_GN_RESIDENT_V", 0);
     static const long force_pipe = env_long("SDH_GN_RESIDENT_PIPE", -1);
@@ -693,7 +703,9 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
     const bool large = nseg * L * 4 >= (int64_t(64) << 20);
     const int64_t split_wgs = nseg * ((L + kChunk - 1) / kChunk);
     Plan pl;
-    if (large || mode == 2) pl = best_pipe.k.V ? best_pipe : best_plain;
+    if (one_round_only) {
+        if (best_one.k.V && split_wgs < 1024) pl = best_one;
+    } else if (large || mode == 2) pl = best_pipe.k.V ? best_pipe : best_plain;
     else if (best_one.k.V && split_wgs < 1024) pl = best_one;
     if (!pl.k.V) return false;
     const bool uniform = HW % ((int64_t)kResThreads * 4 * pl.k.V) == 0;
@@ -738,6 +750,11 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
     }
     const int64_t cg = C / groups, L = cg * HW, nseg = N * groups;
     const bool vec = HW % 4 == 0 && aligned16(x) && aligned16(y) && L < (1LL << 31);
+    // segments of 24577-65536 floats: a resident round spreads each over
+    // 2-4 workgroups, where the single schedule runs one per segment
+    if (vec && L > kSmallResidentMin && L <= (int64_t)1024 * 4 * 16 && gn_block_bytes() == 0 &&
+        run_gn_resident(op, silu, x, y, L, HW, cg, groups, nseg, gamma, beta, eps, true))
+        return;
     if (vec && L <= (int64_t)1024 * 4 * 16 && nseg <= 0x7fffffffLL) {
         const int64_t n4 = L / 4;
         auto go = [&](auto tc, auto vc) {
@@ -760,7 +777,7 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
         else if (n4 <= 12288) go(K(), std::integral_constant<int, 12>());
         else go(K(), std::integral_constant<int, 16>());
     } else if (vec && gn_block_bytes() == 0 &&
-               run_gn_resident(op, silu, x, y, L, HW, cg, groups, nseg, gamma, beta, eps)) {
+               run_gn_resident(op, silu, x, y, L, HW, cg, groups, nseg, gamma, beta, eps, false)) {
         return;
     } else if (vec) {
         const int64_t nchunks = (L + kChunk - 1) / kChunk;

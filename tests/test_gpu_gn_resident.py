@@ -191,7 +191,7 @@ def test_expired_wait_is_reported():
         "    assert e.status == sdhip.SDH_ERR_HIP and 'sdh_group_norm_silu' in str(e) and 'bounded wait' in str(e), e\n"
         "be.synchronize()\n"
         "assert np.isnan(o.download()).all()\n"
-        "o2, want2 = run((2, 320, 64, 64), 32, 1e-5, True, 4601)\n"
+        "o2, want2 = run((2, 320, 32, 32), 32, 1e-5, True, 4601)\n"
         "assert_reduction(o2.download(), want2, 'single after expiry')\n"
         "a = be.array(np.ones(1000, np.float32)); be.add(a, be.array(np.ones(1000, np.float32)), 1000)\n"
         "assert (a.download() == 2.0).all()\n"
@@ -225,3 +225,32 @@ def test_two_processes_at_once():
         outs.append((p.returncode, out, err[-2000:]))
     print(outs)
     assert all(rc == 0 and "concurrent ok" in out for rc, out, _ in outs)
+
+
+# Segments of 24577-65536 floats: one resident round ahead of the
+# single-workgroup schedule when the split would run fewer than 1024
+# workgroups (SD 1.5 UNet shapes); shares of 16384 floats, the last short.
+SMALL_SEG_SHAPES = [((2, 320, 64, 64), 32, 1e-5), ((2, 1280, 32, 32), 32, 1e-5), ((2, 960, 32, 32), 32, 1e-5),
+                    ((1, 64, 128, 128), 32, 1e-6), ((2, 512, 64, 64), 32, 1e-5), ((2, 96, 30, 36), 3, 1e-6)]
+
+
+@pytest.mark.parametrize("shape,groups,eps", SMALL_SEG_SHAPES)
+@pytest.mark.parametrize("silu", [True, False])
+def test_small_segments_resident_round(be, orc, shape, groups, eps, silu):
+    got, want = _run(be, orc, shape, groups, eps, silu, 5200 + shape[1])
+    assert_reduction(got, want, f"small-segment group_norm {shape} g{groups} silu={silu}")
+
+
+def test_small_segments_single_schedule_still_reachable():
+    """SDH_GN_RESIDENT=0: the same shapes on the single-workgroup kernels
+    (V = 8, 12 and 16 float4 per thread of 1024), which larger batches of
+    these shapes still take."""
+    body = (
+        "for shape, groups, eps in %r:\n"
+        "    for silu in (True, False):\n"
+        "        o, want = run(shape, groups, eps, silu, 5300)\n"
+        "        assert_reduction(o.download(), want, f'single {shape} {silu}')\n"
+        "print('single ok')\n"
+    ) % (SMALL_SEG_SHAPES,)
+    r = _child({"SDH_GN_RESIDENT": "0"}, body)
+    assert r.returncode == 0 and "single ok" in r.stdout
