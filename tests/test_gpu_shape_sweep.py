@@ -95,7 +95,11 @@ def test_rotary_sweep(be, orc, dim, interleaved):
 
 @pytest.mark.parametrize("shape,groups", [((1, 32, 1, 1), 32), ((2, 64, 3, 5), 32), ((1, 8, 100, 100), 4),
                                           ((1, 64, 128, 128), 32), ((3, 96, 17, 17), 32), ((1, 32, 512, 129), 32),
-                                          ((1, 4, 256, 260), 2), ((2, 6, 7, 9), 3), ((1, 32, 256, 256), 1)])
+                                          ((1, 4, 256, 260), 2), ((2, 6, 7, 9), 3), ((1, 32, 256, 256), 1),
+                                          # segments at the single / one-resident-round boundary (24576
+                                          # floats) and at the single schedule's 65536-float limit
+                                          ((1, 1, 1, 24572), 1), ((1, 1, 1, 24576), 1), ((1, 1, 1, 24580), 1),
+                                          ((2, 3, 4, 8196), 3), ((1, 1, 1, 65536), 1), ((1, 1, 1, 65540), 1)])
 def test_group_norm_sweep(be, orc, shape, groups):
     x = orc.randn(shape, 5000 + shape[1], 0.5, 2.0)
     g, b = orc.randn((shape[1],), 5001, 1.0, 0.1), orc.randn((shape[1],), 5002, 0.0, 0.1)
