@@ -710,6 +710,8 @@ def gn_dispatches(shape, groups=32, cus=256):
                 best[key] = (rounds, pipe, P, T)
             if not pipe and rounds == 1 and "one" not in best:
                 best["one"] = (rounds, pipe, P, T)
+    if "pipe" in best and best["pipe"][0] == 1:  # run_gn_resident prefers a one-round pipelined plan
+        best["one"] = best["pipe"]
     large = nseg * L * 4 >= 64 << 20
     split_wgs = nseg * -(-L // 8192)
     if L <= 65536:

@@ -669,8 +669,10 @@ int resident_occupancy(ResKind k, bool silu, bool uniform) {
 // SDH_GN_RESIDENT=0 never, =2 always when a plan exists (the plan chosen as
 // for large x); SDH_GN_RESIDENT_V=4|8|16 fixes the share;
 // SDH_GN_RESIDENT_PIPE=0|1 allows only the plain or only the pipelined
-// kernel; SDH_GN_SPIN_LIMIT bounds each wait (polls; 0 expires every wait
-// at once).
+// kernel; SDH_GN_ONE_ROUND_PIPE=0 keeps the plain kernel's plan for one
+// round (the pipelined plan measured 2-7 % faster there: [2,640,64,64]
+// 12.65 -> 11.9 us, [2,320,64,64] 9.31 -> 9.09 us); SDH_GN_SPIN_LIMIT
+// bounds each wait (polls; 0 expires every wait at once).
 bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_t L, int64_t HW, int64_t cg,
                      int groups, int64_t nseg, const float* gamma, const float* beta, float eps,
                      bool one_round_only) {
@@ -702,6 +704,10 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
     }
     const bool large = nseg * L * 4 >= (int64_t(64) << 20);
     const int64_t split_wgs = nseg * ((L + kChunk - 1) / kChunk);
+    // one round: the pipelined kernel's plan when it also covers the tensor
+    // in one round (shares of 8 float4 where the plain one has 4: fewer
+    // workgroups, each holding more in flight), else the plain kernel's
+    if (best_pipe.k.V && best_pipe.rounds == 1 && env_long("SDH_GN_ONE_ROUND_PIPE", 1)) best_one = best_pipe;
     Plan pl;
     if (one_round_only) {
         if (best_one.k.V && split_wgs < 1024) pl = best_one;
