@@ -287,18 +287,27 @@ __global__ __launch_bounds__(kThreads) void k_gn_apply(const float* __restrict__
 // finish clears the slots and the finish counter, so every launch starts
 // from zeroed slots and tags 1, 2, ... never match a stale value.
 //
-// Teams wait only on their own members: P consecutive workgroups, which the
-// dispatcher places in order, in a grid no larger than the GPU holds at
-// once, so once earlier work on the GPU drains every member of a waiting
-// team is resident. (Not a cooperative launch: measured, a cooperative
+// Teams are formed by arrival, not by blockIdx: each workgroup takes a
+// ticket (ctl[2]) when it starts and ticket / P is its team, ticket % P its
+// share. Workgroups that have started hold tickets 0 .. k-1, so every team
+// but the one holding ticket k-1 is complete and running, and at most one
+// team per launch waits on members that are not yet on the GPU. Teams fixed
+// by blockIdx could all be incomplete at once: the dispatcher fills each
+// XCD in blockIdx order on its own, so when another process's kernel holds
+// one XCD's CUs, every team with a member there waits, and two such
+// launches can hold every slot. With tickets, a launch's complete teams
+// always finish and free their CUs for the incomplete one. The ticket costs
+// one atomic round trip before the first load (about 0.5 us at a 32 MB
+// tensor, measured). (Not a cooperative launch: measured, a cooperative
 // launch fails with hipErrorIllegalState in a second process while another
 // process that made one is alive.) Each wait is still bounded (spin_limit
 // polls): on expiry the workgroup sets ctl[1], writes NaN for its share and
 // goes on, so the kernel always drains; the host reports ctl[1] at the next
-// synchronisation.
+// synchronisation, and from then on this process runs the split schedule
+// instead (an in-place call, y == x, has then lost the expired shares of x).
 constexpr int kResThreads = 1024;
 constexpr int kResMaxTeam = 64;  // workgroups per segment per slot of a polling lane
-constexpr int kCtlWords = 64;     // ctl[0] finished workgroups, ctl[1] error word; slots from ctl + 64
+constexpr int kCtlWords = 64;     // ctl[0] finished workgroups, ctl[1] error word, ctl[2] ticket; slots from ctl + 64
 constexpr unsigned kSpinLimit = 1u << 20;  // polls of about 1 us: a wait ends within about a second
 
 using u64 = unsigned long long;
@@ -400,7 +409,8 @@ __device__ __forceinline__ void res_team_stats(const ResArgs& a, const u64* slot
 // they run under it), the team wait, and y from registers.
 template <int V, bool SILU, bool UNIFORM, int KS, bool PREFETCH>
 __device__ __forceinline__ void res_round(const ResArgs& a, f4 (&cur)[V], f4 (&nxt)[V], int seg, int next_seg,
-                                          int round, int team, int off, int n4, float* sh, float2* stat) {
+                                          int round, int team, int ticket, int off, int n4, float* sh,
+                                          float2* stat) {
     constexpr int kShare = kResThreads * V * 4;
     u64* slots = (u64*)(a.ctl + kCtlWords);
     float s = 0.f;
@@ -421,7 +431,7 @@ __device__ __forceinline__ void res_round(const ResArgs& a, f4 (&cur)[V], f4 (&n
     const unsigned tag = (unsigned)round + 1;
     const int par = round & 1;
     if (threadIdx.x == 0) {
-        u64* mine = slots + ((size_t)blockIdx.x * 2 + par) * 2;
+        u64* mine = slots + ((size_t)ticket * 2 + par) * 2;
         put_slot(mine, sum, tag);
         put_slot(mine + 1, M2, tag);
     }
@@ -453,9 +463,9 @@ __device__ __forceinline__ void res_round(const ResArgs& a, f4 (&cur)[V], f4 (&n
     }
 }
 
-// Every workgroup has finished its reads of the slots before it counts
-// itself finished; the last one clears the slots of this launch and the
-// counter.
+// Every workgroup has taken its ticket and finished its reads of the slots
+// before it counts itself finished; the last one clears the slots of this
+// launch, the ticket and the counter.
 __device__ __forceinline__ void res_finish(unsigned* ctl, unsigned* last) {
     u64* slots = (u64*)(ctl + kCtlWords);
     if (threadIdx.x == 0)
@@ -464,8 +474,17 @@ __device__ __forceinline__ void res_finish(unsigned* ctl, unsigned* last) {
     if (*last) {
         for (unsigned i = threadIdx.x; i < gridDim.x * 4; i += kResThreads)
             __hip_atomic_store(slots + i, (u64)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (threadIdx.x == 0) __hip_atomic_store(ctl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0 || threadIdx.x == 2)
+            __hip_atomic_store(ctl + threadIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+// This workgroup's ticket: its place in arrival order (see above).
+__device__ __forceinline__ int res_ticket(unsigned* ctl, int* sh_ticket) {
+    if (threadIdx.x == 0)
+        *sh_ticket = (int)__hip_atomic_fetch_add(ctl + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    return *sh_ticket;
 }
 
 // grid = T * P workgroups of kResThreads; segments team, team + T, ... one
@@ -476,14 +495,16 @@ __global__ __launch_bounds__(kResThreads) void k_gn_resident(ResArgs a) {
     __shared__ float sh[kResThreads / 64];
     __shared__ float2 stat;
     __shared__ unsigned last;
-    const int team = blockIdx.x / a.P, part = blockIdx.x - team * a.P, T = gridDim.x / a.P;
+    __shared__ int sh_ticket;
+    const int ticket = res_ticket(a.ctl, &sh_ticket);
+    const int team = ticket / a.P, part = ticket - team * a.P, T = gridDim.x / a.P;
     const int off = part * kShare4 * 4;
     const int n4 = UNIFORM ? kShare4 : min(kShare4, (a.L - off) >> 2);
     int round = 0;
     for (int seg = team; seg < a.nseg; seg += T, ++round) {
         f4 v[V];
         res_load<V, UNIFORM>(v, a.x, (int64_t)seg * a.L + off, n4);
-        res_round<V, SILU, UNIFORM, 1, false>(a, v, v, seg, 0, round, team, off, n4, sh, &stat);
+        res_round<V, SILU, UNIFORM, 1, false>(a, v, v, seg, 0, round, team, ticket, off, n4, sh, &stat);
     }
     res_finish(a.ctl, &last);
 }
@@ -498,7 +519,9 @@ __global__ __launch_bounds__(kResThreads) void k_gn_resident_pipe(ResArgs a) {
     __shared__ float sh[kResThreads / 64];
     __shared__ float2 stat;
     __shared__ unsigned last;
-    const int team = blockIdx.x / a.P, part = blockIdx.x - team * a.P, T = gridDim.x / a.P;
+    __shared__ int sh_ticket;
+    const int ticket = res_ticket(a.ctl, &sh_ticket);
+    const int team = ticket / a.P, part = ticket - team * a.P, T = gridDim.x / a.P;
     const int off = part * kShare4 * 4;
     const int n4 = UNIFORM ? kShare4 : min(kShare4, (a.L - off) >> 2);
     f4 va[V], vb[V];
@@ -506,10 +529,10 @@ __global__ __launch_bounds__(kResThreads) void k_gn_resident_pipe(ResArgs a) {
     if (seg < a.nseg) res_load<V, UNIFORM>(va, a.x, (int64_t)seg * a.L + off, n4);
     for (int round = 0; seg < a.nseg; round += 2) {
         const int s1 = seg + T;
-        res_round<V, SILU, UNIFORM, 2, true>(a, va, vb, seg, s1, round, team, off, n4, sh, &stat);
+        res_round<V, SILU, UNIFORM, 2, true>(a, va, vb, seg, s1, round, team, ticket, off, n4, sh, &stat);
         if (s1 >= a.nseg) break;
         const int s2 = s1 + T;
-        res_round<V, SILU, UNIFORM, 2, true>(a, vb, va, s1, s2, round + 1, team, off, n4, sh, &stat);
+        res_round<V, SILU, UNIFORM, 2, true>(a, vb, va, s1, s2, round + 1, team, ticket, off, n4, sh, &stat);
         seg = s2;
     }
     res_finish(a.ctl, &last);
@@ -673,9 +696,16 @@ int resident_occupancy(ResKind k, bool silu, bool uniform) {
 // round (the pipelined plan measured 2-7 % faster there: [2,640,64,64]
 // 12.65 -> 11.9 us, [2,320,64,64] 9.31 -> 9.09 us); SDH_GN_SPIN_LIMIT
 // bounds each wait (polls; 0 expires every wait at once).
+// Set when a resident launch's bounded wait expired (the host learns it at
+// the next synchronisation): later calls in this process take the other
+// schedules, which never wait across workgroups.
+bool g_resident_off = false;
+void resident_expired() { g_resident_off = true; }
+
 bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_t L, int64_t HW, int64_t cg,
                      int groups, int64_t nseg, const float* gamma, const float* beta, float eps,
                      bool one_round_only) {
+    if (g_resident_off) return false;
     static const long mode = env_long("SDH_GN_RESIDENT", 1);
     static const long force_v = env_long("SDH_GN_RESIDENT_V", 0);
     static const long force_pipe = env_long("SDH_GN_RESIDENT_PIPE", -1);
@@ -727,7 +757,7 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
                                   0, stream()),
                   what.c_str());
     });
-    arm_device_check(args.ctl + 1, op);
+    arm_device_check(args.ctl + 1, op, resident_expired);
     return true;
 }
 

@@ -170,6 +170,7 @@ struct Runtime {
     size_t workspace_bytes = 0;
     unsigned* check_word = nullptr;  // see arm_device_check
     const char* check_what = nullptr;
+    void (*check_failure)() = nullptr;
 };
 
 Runtime& rt() {
@@ -251,8 +252,10 @@ void device_check_locked(Runtime& r) {
         const unsigned z = 0;
         hip_check(hipMemcpyAsync(w, &z, sizeof z, hipMemcpyHostToDevice, r.stream), "hipMemcpyAsync(device check)");
         hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
+        if (r.check_failure) r.check_failure();
         fail(SDH_ERR_HIP, std::string(r.check_what) +
-                              ": a bounded wait inside the kernel expired; the affected outputs hold NaN");
+                              ": a bounded wait inside the kernel expired; the affected outputs hold NaN (and, for "
+                              "a call made in place, the same parts of its input)");
     }
 }
 
@@ -341,11 +344,12 @@ void* workspace(size_t bytes) {
     return r.workspace;
 }
 
-void arm_device_check(unsigned* word, const char* what) {
+void arm_device_check(unsigned* word, const char* what, void (*on_failure)()) {
     Runtime& r = rt();
     std::lock_guard<std::mutex> lk(r.mu);
     r.check_word = word;
     r.check_what = what;
+    r.check_failure = on_failure;
 }
 
 unsigned* counters(size_t count) {

@@ -83,8 +83,9 @@ void launched(const char* op);
 // Registers a device word that the kernel just queued sets nonzero on a
 // failure it cannot return as a status (a bounded wait that expired). The
 // next sdh_synchronize or sdh_download reads the word after its stream
-// synchronisation, clears it and fails with SDH_ERR_HIP naming `what`.
-void arm_device_check(unsigned* word, const char* what);
+// synchronisation, clears it, calls on_failure (if given) and fails with
+// SDH_ERR_HIP naming `what`.
+void arm_device_check(unsigned* word, const char* what, void (*on_failure)() = nullptr);
 // Queues a zero fill of [p, p + bytes) on the library stream (a kernel, not a memset).
 void zero_device(void* p, size_t bytes);
 

@@ -182,7 +182,9 @@ def test_expired_wait_is_reported():
     """SDH_GN_SPIN_LIMIT=0: every team wait expires before its first poll,
     every workgroup still finishes (NaN output), the download fails with
     SDH_ERR_HIP naming the op, the word is then clear, and the library keeps
-    working (a non-resident GroupNorm and an add afterwards are correct)."""
+    working (a non-resident GroupNorm and an add afterwards are correct).
+    After the expiry the process no longer takes the resident schedule: the
+    same shape, whose waits would all expire again, now comes out right."""
     body = (
         "o, want = run((1, 256, 256, 256), 32, 1e-6, True, 4600)\n"
         "try:\n"
@@ -193,6 +195,8 @@ def test_expired_wait_is_reported():
         "assert np.isnan(o.download()).all()\n"
         "o2, want2 = run((2, 320, 32, 32), 32, 1e-5, True, 4601)\n"
         "assert_reduction(o2.download(), want2, 'single after expiry')\n"
+        "o3, want3 = run((1, 256, 256, 256), 32, 1e-6, True, 4602)\n"
+        "assert_reduction(o3.download(), want3, 'resident shape after expiry')\n"
         "a = be.array(np.ones(1000, np.float32)); be.add(a, be.array(np.ones(1000, np.float32)), 1000)\n"
         "assert (a.download() == 2.0).all()\n"
         "print('expiry ok')\n"
