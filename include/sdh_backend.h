@@ -272,6 +272,19 @@ int sdh_add_rms_norm(float* x, const float* r, float* y, int64_t rows, int64_t C
  * (modules.cpp:34-35, vae.cpp:48-49, unet.cpp:120-121). y may equal x. */
 int sdh_group_norm_silu(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups, const float* gamma,
                         const float* beta, float eps);
+/* ALLOCATION-FREE: no counterpart in the reference. For callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The same kernels and result as
+ * sdh_group_norm_silu, with the scratch they need (team slots and counters,
+ * chunk statistics) in a fixed 1 MiB device array per GPU instead of the
+ * arena; it calls no hipMalloc, hipFree or allocating routine, so sdh_init
+ * must have run first (SDH_ERR_INVALID otherwise). A tensor whose split
+ * schedule needs more than the array's 960 KiB of chunk statistics is
+ * rejected with SDH_ERR_INVALID; the resident and single-workgroup schedules
+ * need at most 17 KiB. Calls that overlap on one GPU share the array and
+ * would race; the library's own calls are serialised on its one stream. */
+int sdh_group_norm_silu_noalloc(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups,
+                                const float* gamma, const float* beta, float eps);
 /* FUSED adaLN: y = layer_norm(x, no affine, eps) * (1 + scale) + shift;
  * res += tanh(gate) * y. Equals layer_norm -> affine_(scale, 1, 1) ->
  * tanh_(gate) -> mul_rows_(y, 1+scale) -> add_rows_scaled_(y, ones, shift) ->

@@ -64,6 +64,7 @@ STUB(int sdh_add_channel_bias(float*, const float*, int64_t, int64_t, int64_t))
 STUB(int sdh_add_rows(float*, const float*, int64_t, int64_t))
 STUB(int sdh_add_rms_norm(float*, const float*, float*, int64_t, int64_t, const float*, float))
 STUB(int sdh_group_norm_silu(const float*, float*, int64_t, int64_t, int64_t, int, const float*, const float*, float))
+STUB(int sdh_group_norm_silu_noalloc(const float*, float*, int64_t, int64_t, int64_t, int, const float*, const float*, float))
 STUB(int sdh_ln_modulate_gate(const float*, float*, const float*, const float*, const float*, float*, int64_t,
                               int64_t, float))
 STUB(int sdh_qknorm_rope(float*, int64_t, float*, int64_t, int64_t, int64_t, int64_t, const float*, const float*,

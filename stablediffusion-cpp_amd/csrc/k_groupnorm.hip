@@ -45,10 +45,25 @@
 
 #include "sdh_internal.hpp"
 
+// Device scratch of the allocation-free entry point
+// (sdh_group_norm_silu_noalloc): the resident schedule's team slots and
+// counters in its first kFixedCtlBytes, the split schedule's chunk pairs and
+// statistics after them. Each GPU the library runs on holds its own copy
+// until the process ends. In host code this name is a stand-in, not a device
+// address: host code uses the address hipGetSymbolAddress returns for the
+// current device (sdh::gn_fixed_scratch_setup), never the name.
+static constexpr size_t kFixedScratchBytes = size_t(1) << 20;
+static __device__ __align__(256) unsigned char scratch[kFixedScratchBytes];
+
 namespace sdh {
 namespace {
 
 using dev::f4;
+
+constexpr size_t kFixedCtlBytes = size_t(64) << 10;
+constexpr int kMaxDevices = 64;
+// Device address of `scratch` per device, from gn_fixed_scratch_setup.
+unsigned char* g_fixed_scratch[kMaxDevices] = {};
 
 constexpr int kThreads = 256;
 constexpr int kChunkV = 8;                               // float4 per thread per chunk
@@ -702,9 +717,11 @@ int resident_occupancy(ResKind k, bool silu, bool uniform) {
 bool g_resident_off = false;
 void resident_expired() { g_resident_off = true; }
 
+// fixed: the allocation-free entry point's scratch (slots and counters at
+// its start), or null for the library's counters.
 bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_t L, int64_t HW, int64_t cg,
                      int groups, int64_t nseg, const float* gamma, const float* beta, float eps,
-                     bool one_round_only) {
+                     bool one_round_only, unsigned char* fixed) {
     if (g_resident_off) return false;
     static const long mode = env_long("SDH_GN_RESIDENT", 1);
     static const long force_v = env_long("SDH_GN_RESIDENT_V", 0);
@@ -747,7 +764,15 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
     const bool uniform = HW % ((int64_t)kResThreads * 4 * pl.k.V) == 0;
     const int64_t grid = std::min(pl.T, nseg) * pl.P;
     ResArgs args{x, y, gamma, beta, nullptr, (int)L, (int)HW, (int)cg, groups, (int)nseg, (int)pl.P, spin, eps};
-    args.ctl = counters((size_t)kCtlWords + (size_t)grid * 8);
+    const size_t ctl_words = (size_t)kCtlWords + (size_t)grid * 8;
+    if (fixed) {
+        if (ctl_words * sizeof(unsigned) > kFixedCtlBytes)
+            fail(SDH_ERR_INVALID, std::string(op) + ": " + std::to_string(grid) +
+                                      " resident workgroups need more team slots than the fixed scratch holds");
+        args.ctl = (unsigned*)fixed;  // zero at set-up; every launch leaves it zero when it ends
+    } else {
+        args.ctl = counters(ctl_words);
+    }
     void* argv[] = {&args};
     with_resident(pl.k, silu, uniform, [&](auto kern) {
         const std::string what = std::string(op) + ": launch of " + std::to_string(grid) + " resident workgroups (" +
@@ -761,8 +786,10 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
     return true;
 }
 
+// fixed: the allocation-free entry point's scratch, or null for the
+// library's scratch and counters (which may allocate from the arena).
 void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups,
-            const float* gamma, const float* beta, float eps) {
+            const float* gamma, const float* beta, float eps, unsigned char* fixed = nullptr) {
     need(N >= 0 && C >= 0 && HW >= 0, op, "negative size");
     need(groups > 0, op, "groups must be positive");
     need(C % groups == 0, op, "channels not divisible by groups");
@@ -780,7 +807,7 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
     const int64_t samples_per_launch = units_per_launch((int64_t)groups * 1024);
     if (N > samples_per_launch) {
         in_pieces(N, samples_per_launch, [&](int64_t n0, int64_t nn) {
-            run_gn(op, silu, x + n0 * C * HW, y + n0 * C * HW, nn, C, HW, groups, gamma, beta, eps);
+            run_gn(op, silu, x + n0 * C * HW, y + n0 * C * HW, nn, C, HW, groups, gamma, beta, eps, fixed);
         });
         return;
     }
@@ -789,7 +816,7 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
     // segments of 24577-65536 floats: a resident round spreads each over
     // 2-4 workgroups, where the single schedule runs one per segment
     if (vec && L > kSmallResidentMin && L <= (int64_t)1024 * 4 * 16 && gn_block_bytes() == 0 &&
-        run_gn_resident(op, silu, x, y, L, HW, cg, groups, nseg, gamma, beta, eps, true))
+        run_gn_resident(op, silu, x, y, L, HW, cg, groups, nseg, gamma, beta, eps, true, fixed))
         return;
     if (vec && L <= (int64_t)1024 * 4 * 16 && nseg <= 0x7fffffffLL) {
         const int64_t n4 = L / 4;
@@ -813,7 +840,7 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
         else if (n4 <= 12288) go(K(), std::integral_constant<int, 12>());
         else go(K(), std::integral_constant<int, 16>());
     } else if (vec && gn_block_bytes() == 0 &&
-               run_gn_resident(op, silu, x, y, L, HW, cg, groups, nseg, gamma, beta, eps, false)) {
+               run_gn_resident(op, silu, x, y, L, HW, cg, groups, nseg, gamma, beta, eps, false, fixed)) {
         return;
     } else if (vec) {
         const int64_t nchunks = (L + kChunk - 1) / kChunk;
@@ -824,7 +851,19 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
         if (budget > 0) sb = std::max<int64_t>(1, std::min<int64_t>(nseg, budget / (L * 4)));
         sb = std::min<int64_t>(sb, 65535);
         const size_t part_bytes = ((size_t)(sb * nchunks) * sizeof(float2) + 255) / 256 * 256;
-        char* scr = (char*)scratch(part_bytes + (size_t)sb * sizeof(float2));
+        const size_t scr_bytes = part_bytes + (size_t)sb * sizeof(float2);
+        char* scr = nullptr;
+        if (fixed) {
+            // every pair and statistic is written before it is read: nothing here must start at zero
+            if (scr_bytes > kFixedScratchBytes - kFixedCtlBytes)
+                fail(SDH_ERR_INVALID, std::string(op) + ": " + std::to_string(nseg) + " segments of " +
+                                          std::to_string(L) + " floats need " + std::to_string(scr_bytes) +
+                                          " bytes of scratch; this entry point holds " +
+                                          std::to_string(kFixedScratchBytes - kFixedCtlBytes));
+            scr = (char*)fixed + kFixedCtlBytes;
+        } else {
+            scr = (char*)scratch(scr_bytes);
+        }
         float2* part = (float2*)scr;
         float2* stats = (float2*)(scr + part_bytes);
         const bool uniform = HW % kChunk == 0;
@@ -870,6 +909,17 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
 }
 
 }  // namespace
+
+void gn_fixed_scratch_setup() {
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) fail(SDH_ERR_INVALID, "backend_hip: device index out of range");
+    void* p = nullptr;
+    hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(::scratch)), "hipGetSymbolAddress(scratch)");
+    zero_device(p, kFixedScratchBytes);
+    g_fixed_scratch[dev] = (unsigned char*)p;
+}
+
 }  // namespace sdh
 
 using namespace sdh;
@@ -884,6 +934,24 @@ int sdh_group_norm(const float* x, float* y, int64_t N, int64_t C, int64_t HW, i
 int sdh_group_norm_silu(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups, const float* gamma,
                         const float* beta, float eps) {
     return guarded([&] { run_gn("sdh_group_norm_silu", true, x, y, N, C, HW, groups, gamma, beta, eps); });
+}
+
+// The kernels and schedules of sdh_group_norm_silu, with their scratch in
+// the file-scope `scratch` array instead of the arena: no allocation of any
+// kind, the library's set-up included (which is why it requires sdh_init
+// first). Calls that overlap on one GPU would share the array and race; the
+// library's lock and single stream keep its own calls in order.
+int sdh_group_norm_silu_noalloc(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups,
+                                const float* gamma, const float* beta, float eps) {
+    return guarded([&] {
+        const char* op = "sdh_group_norm_silu_noalloc";
+        need(initialized(), op, "call sdh_init first (this entry point allocates nothing, set-up included)");
+        int dev = 0;
+        hip_check(hipGetDevice(&dev), "hipGetDevice");
+        unsigned char* f = dev >= 0 && dev < kMaxDevices ? g_fixed_scratch[dev] : nullptr;
+        need(f != nullptr, op, "the current device has no scratch address (it was not set up by sdh_init)");
+        run_gn(op, true, x, y, N, C, HW, groups, gamma, beta, eps, f);
+    });
 }
 
 }  // extern "C"

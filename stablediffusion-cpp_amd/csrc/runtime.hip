@@ -221,6 +221,7 @@ void init_locked(Runtime& r, size_t arena_bytes) {
     const size_t first = arena_bytes ? arena_bytes : env_mb("SDH_ARENA_MB", (size_t)1024 << 20);
     if (first && !r.arena.grow(first))
         fail(SDH_ERR_OOM, "backend_hip: cannot reserve the initial arena segment of " + std::to_string(first) + " bytes");
+    gn_fixed_scratch_setup();
     r.inited = true;
 }
 
@@ -296,6 +297,12 @@ void ensure_init() {
     Runtime& r = rt();
     std::lock_guard<std::mutex> lk(r.mu);
     init_locked(r, 0);
+}
+
+bool initialized() {
+    Runtime& r = rt();
+    std::lock_guard<std::mutex> lk(r.mu);
+    return r.inited;
 }
 
 hipStream_t stream() { return rt().stream; }

@@ -58,6 +58,12 @@ int guarded(F&& f) noexcept {
 // Runtime (runtime.hip)
 // ---------------------------------------------------------------------------
 void ensure_init();
+// True once sdh_init (or any entry point's implicit set-up) has run.
+bool initialized();
+// Looks up, for the current device, the address of the allocation-free
+// GroupNorm entry point's fixed scratch and zeroes it (k_groupnorm.hip);
+// called by the library's set-up.
+void gn_fixed_scratch_setup();
 hipStream_t stream();
 int num_cus();
 // Throws SDH_ERR_INVALID unless [p, p + bytes) lies inside one live arena

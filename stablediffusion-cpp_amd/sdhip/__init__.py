@@ -98,6 +98,7 @@ SIGNATURES = {
     "sdh_unpatchify": [_vp, _vp, _i64, _i64, _i64, C.c_int],
     "sdh_add_rms_norm": [_vp, _vp, _vp, _i64, _i64, _vp, _fl],
     "sdh_group_norm_silu": [_vp, _vp, _i64, _i64, _i64, _int, _vp, _vp, _fl],
+    "sdh_group_norm_silu_noalloc": [_vp, _vp, _i64, _i64, _i64, _int, _vp, _vp, _fl],
     "sdh_ln_modulate_gate": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _fl],
     "sdh_fill_normal": [_vp, _i64, C.c_uint64, _fl, _fl],
     "sdh_timer_record": [_int],
