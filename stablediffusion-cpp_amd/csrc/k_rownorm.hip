@@ -40,6 +40,18 @@ constexpr int kWaves = kThreads / 64;
 enum Mode { M_LN = 0, M_RMS = 1 };
 
 __device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
+// The four floats summed in double, and their squares (each exact in double).
+__device__ __forceinline__ double dsum4(const f4& v) {
+    return ((double)v.x + (double)v.y) + ((double)v.z + (double)v.w);
+}
+__device__ __forceinline__ double dsq4(const f4& d) {
+    return ((double)d.x * (double)d.x + (double)d.y * (double)d.y) +
+           ((double)d.z * (double)d.z + (double)d.w * (double)d.w);
+}
+// rstd from a statistic summed in double: (float)(1 / sqrt(stat / C + eps)).
+__device__ __forceinline__ float rstd_of_d(double stat, int64_t C, float eps) {
+    return (float)(1.0 / sqrt(stat / (double)C + (double)eps));
+}
 
 using dev::rstd_of;
 
@@ -62,19 +74,19 @@ __global__ __launch_bounds__(kThreads) void k_rownorm(const float* __restrict__ 
     }
     float mean = 0.f, rstd;
     if constexpr (MODE == M_LN) {
-        float s = 0.f;
+        // both sums in double, as tensor.cpp:640-647 forms them: an fp32
+        // sum moves the mean by ~1e-5 / C and rstd by ~1e-6 relative, which
+        // outputs near zero (x near the mean, or cancelling beta) magnify
+        double s = 0.0;
 #pragma unroll
-        for (int j = 0; j < V; ++j) s += dev::hsum(v[j]);
-        mean = (float)((double)dev::wave_sum(s) / (double)C);
-        float q = 0.f;
+        for (int j = 0; j < V; ++j) s += dsum4(v[j]);  // masked entries are zero
+        mean = (float)(dev::wave_sum_d(s) / (double)C);
+        double q = 0.0;
 #pragma unroll
         for (int j = 0; j < V; ++j) {
-            if (lane + 64 * j < n4) {
-                const f4 d = v[j] - mean;
-                q += dev::hsum(d * d);
-            }
+            if (lane + 64 * j < n4) q += dsq4(v[j] - mean);
         }
-        rstd = rstd_of(dev::wave_sum(q), C, eps);
+        rstd = rstd_of_d(dev::wave_sum_d(q), C, eps);
     } else {
         float q = 0.f;
 #pragma unroll
@@ -285,18 +297,22 @@ __global__ __launch_bounds__(kThreads) void k_rownorm_generic(const float* x, fl
     for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows; row += stride) {
         const float* p = x + row * C;
         float* q = y + row * C;
-        float mean = 0.f;
+        float mean = 0.f, rstd;
         if constexpr (MODE == M_LN) {
-            float s = 0.f;
-            for (int64_t i = lane; i < C; i += 64) s += p[i];
-            mean = (float)((double)dev::wave_sum(s) / (double)C);
+            double s = 0.0;
+            for (int64_t i = lane; i < C; i += 64) s += (double)p[i];
+            mean = (float)(dev::wave_sum_d(s) / (double)C);
+            double ss = 0.0;
+            for (int64_t i = lane; i < C; i += 64) {
+                const float d = p[i] - mean;
+                ss += (double)d * (double)d;
+            }
+            rstd = rstd_of_d(dev::wave_sum_d(ss), C, eps);
+        } else {
+            float ss = 0.f;
+            for (int64_t i = lane; i < C; i += 64) ss += p[i] * p[i];
+            rstd = rstd_of(dev::wave_sum(ss), C, eps);
         }
-        float ss = 0.f;
-        for (int64_t i = lane; i < C; i += 64) {
-            const float d = p[i] - mean;
-            ss += d * d;
-        }
-        const float rstd = rstd_of(dev::wave_sum(ss), C, eps);
         for (int64_t i = lane; i < C; i += 64) {
             if constexpr (MODE == M_LN) {
                 float o = (p[i] - mean) * rstd;

@@ -253,17 +253,31 @@ void Weights::load_safetensors(const std::string& path, bool keep_bf16, int64_t 
         const JValue* off = kv.second.find("data_offsets");
         if (!dt || !sh || !off || off->arr.size() != 2) throw std::runtime_error("safetensors: bad entry for " + name);
         const std::string& dtype = dt->str;
+        // Dimensions and offsets must be non-negative integers that fit the
+        // file; the element count is formed with overflow checks, so a shape
+        // can never disagree with the bytes it describes.
+        auto whole = [&](const JValue& v, double hi, const char* what) {
+            if (v.kind != JValue::Number || !(v.num >= 0.0) || v.num > hi || v.num != (double)(int64_t)v.num)
+                throw std::runtime_error(std::string("safetensors: bad ") + what + " for " + name);
+            return (int64_t)v.num;
+        };
         std::vector<int64_t> shape;
-        for (const JValue& d : sh->arr) shape.push_back((int64_t)d.num);
-        const size_t b = (size_t)off->arr[0].num, e = (size_t)off->arr[1].num;
+        int64_t n = 1;
+        for (const JValue& d : sh->arr) {
+            shape.push_back(whole(d, 9.0e15, "dimension"));
+            if (__builtin_mul_overflow(n, shape.back(), &n))
+                throw std::runtime_error("safetensors: element count overflows for " + name);
+        }
+        const size_t b = (size_t)whole(off->arr[0], 9.0e15, "offset"), e = (size_t)whole(off->arr[1], 9.0e15, "offset");
         if (e > data_size || b > e) throw std::runtime_error("safetensors: bad offsets for " + name);
         if (dtype != "F32" && dtype != "F16" && dtype != "BF16") {
             std::fprintf(stderr, "  skipping %s (dtype %s)\n", name.c_str(), dtype.c_str());
             continue;
         }
-        const int64_t n = Tensor::numel_of(shape);
         const size_t elem = dtype == "F32" ? 4 : 2;
-        if (e - b != (size_t)n * elem) throw std::runtime_error("safetensors: size mismatch for " + name);
+        int64_t nbytes = 0;
+        if (__builtin_mul_overflow(n, (int64_t)elem, &nbytes) || (size_t)nbytes != e - b)
+            throw std::runtime_error("safetensors: size mismatch for " + name);
         const uint8_t* src = data + b;
         Tensor t(shape);  // host staging
         if (keep_bf16 && n >= bf16_min_numel) {

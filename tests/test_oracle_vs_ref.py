@@ -51,6 +51,18 @@ def test_softmax_bitexact(orc, ref, rows, cols, causal):
     _eq(orc.softmax_rows(x, 0.0883883, causal), ref.softmax_rows(x, 0.0883883, causal), "softmax")
 
 
+@pytest.mark.parametrize("blocks,p,cols", [(3, 37, 37), (4, 9, 9), (2, 16, 40), (5, 1, 7), (3, 13, 4096)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_softmax_period_bitexact(orc, ref, blocks, p, cols, causal):
+    """The batched form (rows in blocks of `period`, the causal mask restarting
+    at each block: backend_cuda.cu:351-367, one block per attention head) is
+    the reference's softmax_rows_ (tensor.cpp:752-769) applied to each block
+    of p rows on its own, bit for bit."""
+    x = orc.randn((blocks * p, cols), 31 + p + cols, 0.0, 3.0)
+    want = np.concatenate([ref.softmax_rows(x[i * p:(i + 1) * p], 0.0883883, causal) for i in range(blocks)])
+    _eq(orc.softmax_rows(x, 0.0883883, causal, period=p), want, f"softmax period {p}")
+
+
 @pytest.mark.parametrize("interleaved", [True, False])
 def test_rope_bitexact(orc, ref, interleaved):
     S = 64
