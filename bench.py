@@ -51,19 +51,60 @@ MAX_SETS = 32
 
 # ------------------------------------------------------------------ workloads
 class Workload:
-    """One BASELINE config: how to make a buffer set, run one step, and the
-    reference CPU composition of the same step."""
+    """One BASELINE config (or calibration / model line): its inputs, one step
+    on the device, and the reference's CPU composition of the same step.
+
+    inputs:  (name, shape, mean, std, seed) of each fp32 input ~N(mean, std),
+             generated on the device by the library's seeded generator
+             (sdh_fill_normal: splitmix64 + Box-Muller), seed + 1000 i for
+             set i. Set 0 is downloaded before the timed steps, and the
+             reference's CPU step runs on exactly those arrays.
+    outputs: (name, shape) allocated uninitialised on the device.
+    results: the arrays compared with the reference after one step (outputs,
+             or inputs updated in place), with the tolerance of each:
+             ("abs", b) max-abs, ("rel", b) |d| / max(|want|, 1),
+             ("softmax", b) elementwise relative with exact causal zeros,
+             ("normrel", b) max|d| / max|want|."""
 
     name = ""
     desc = ""
     kernel = ""  # substring of the dominant kernel's name (for rocprof)
     algo_bytes = 0
+    inputs = ()
+    outputs = ()
+    results = {}
 
     def make(self, be, i):
-        raise NotImplementedError
+        d = {}
+        for n, shape, mean, std, seed in self.inputs:
+            d[n] = be.randn(shape, seed + 1000 * i, mean, std)
+        for n, shape in self.outputs:
+            d[n] = be.empty(shape)
+        return d
+
+    def host_inputs(self, s):
+        """Set s's inputs on the host (what the reference's CPU step gets)."""
+        return {n: s[n].download() for n, *_ in self.inputs}
+
+    def reload(self, be, s, host):
+        """Set 0's inputs uploaded again (in-place steps changed them)."""
+        for n, *_ in self.inputs:
+            s[n].upload(host[n])
 
     def step(self, be, s):
         raise NotImplementedError
+
+    def gpu_results(self, be, s):
+        return {n: s[n].download() for n in self.results}
+
+    def cpu(self, R, h):
+        """(run, handles, collect): run() executes the reference composition
+        once and returns the handles it allocated; collect(outs) copies the
+        results of one run out of the reference's tensors."""
+        return None
+
+    def seeds(self):
+        return {n: seed for n, _, _, _, seed in self.inputs}
 
 
 def _tables_3axis(S, side):
@@ -82,45 +123,45 @@ def _tables_3axis(S, side):
     return cs, sn
 
 
+def _peek(R, h, shape):
+    return R.view(h).copy().reshape(shape)
+
+
 class AddRmsNorm(Workload):
     name, kernel = "add_rms_norm", "k_add_rms"
     desc = "config 1: x += r; y = rms_norm(x) * w; x, r [4096,3840], w [3840], eps 1e-6"
     algo_bytes = 4 * T * D * 4 + D * 4
-
-    def make(self, be, i):
-        return dict(x=be.randn((T, D), 1000 + i), r=be.randn((T, D), 2000 + i), w=be.randn((D,), 3000 + i, 1.0, 0.1),
-                    y=be.empty((T, D)))
+    inputs = (("x", (T, D), 0.0, 1.0, 1), ("r", (T, D), 0.0, 1.0, 2), ("w", (D,), 1.0, 0.1, 3))
+    outputs = (("y", (T, D)),)
+    results = {"x": ("abs", 1e-5), "y": ("rel", 1e-4)}
 
     def step(self, be, s):
         be.add_rms_norm(s["x"], s["r"], s["y"], T, D, s["w"], 1e-6)
 
-    def cpu(self, R, orc):
-        x, r = orc.randn((T, D), 1), orc.randn((T, D), 2)
-        w = orc.randn((D,), 3, 1.0, 0.1)
-        hx, hr, hw = R.new(x.shape, x), R.new(r.shape, r), R.new(w.shape, w)
+    def cpu(self, R, h):
+        hx, hr, hw = R.new((T, D), h["x"]), R.new((T, D), h["r"]), R.new((D,), h["w"])
 
         def run():
             R._chk(R.lib.ref_add_(hx, hr))
             return [R._ptr(R.lib.ref_rms_norm(hx, hw, 1e-6))]
 
-        return run, [hx, hr, hw]
+        return run, [hx, hr, hw], lambda outs: {"x": _peek(R, hx, (T, D)), "y": _peek(R, outs[0], (T, D))}
 
 
 class SwiGLU(Workload):
     name, kernel = "swiglu", "k_swiglu"
     desc = "config 2: y = silu(g) * u; g, u [4096,10240] ~N(0,1.5)"
     algo_bytes = 3 * T * F * 4
-
-    def make(self, be, i):
-        return dict(g=be.randn((T, F), 4000 + i, 0.0, 1.5), u=be.randn((T, F), 5000 + i, 0.0, 1.5), y=be.empty((T, F)))
+    inputs = (("g", (T, F), 0.0, 1.5, 4), ("u", (T, F), 0.0, 1.5, 5))
+    outputs = (("y", (T, F)),)
+    results = {"y": ("abs", 1e-5)}
 
     def step(self, be, s):
         be.swiglu(s["g"], s["u"], s["y"], T * F)
 
-    def cpu(self, R, orc):
-        g, u = orc.randn((T, F), 4, 0.0, 1.5), orc.randn((T, F), 5, 0.0, 1.5)
-        hg, hu = R.new(g.shape, g), R.new(u.shape, u)
-        return (lambda: [R._ptr(R.lib.ref_swiglu(hg, hu))]), [hg, hu]
+    def cpu(self, R, h):
+        hg, hu = R.new((T, F), h["g"]), R.new((T, F), h["u"])
+        return (lambda: [R._ptr(R.lib.ref_swiglu(hg, hu))]), [hg, hu], lambda outs: {"y": _peek(R, outs[0], (T, F))}
 
 
 class RopeQK(Workload):
@@ -128,19 +169,22 @@ class RopeQK(Workload):
     desc = ("config 3: 3-axis interleaved RoPE in place on q and k [4096,30*128] in one launch, axes (32,48,48), "
             "theta 256, reference-format duplicated cos/sin tables [4096,128]")
     algo_bytes = 4 * T * D * 4 + 2 * T * 128 * 4
+    inputs = (("q", (T, D), 0.0, 1.0, 6), ("k", (T, D), 0.0, 1.0, 7))
+    results = {"q": ("abs", 1e-5), "k": ("abs", 1e-5)}
 
     def __init__(self):
         self.cs, self.sn = _tables_3axis(T, 64)
 
     def make(self, be, i):
-        return dict(q=be.randn((T, D), 6000 + i), k=be.randn((T, D), 7000 + i), c=be.array(self.cs), s=be.array(self.sn))
+        d = super().make(be, i)
+        d.update(c=be.array(self.cs), s=be.array(self.sn))
+        return d
 
     def step(self, be, s):
         be.rope_qk(s["q"], D, s["k"], D, 1, T, 128, s["c"], s["s"], True)
 
-    def cpu(self, R, orc):
-        q, k = orc.randn((1, T, D), 6), orc.randn((1, T, D), 7)
-        hq, hk = R.new(q.shape, q), R.new(k.shape, k)
+    def cpu(self, R, h):
+        hq, hk = R.new((1, T, D), h["q"]), R.new((1, T, D), h["k"])
         hc, hs = R.new(self.cs.shape, self.cs), R.new(self.sn.shape, self.sn)
 
         def run():
@@ -148,7 +192,7 @@ class RopeQK(Workload):
             R._chk(R.lib.ref_rope_(hk, 128, hc, hs, 1))
             return []
 
-        return run, [hq, hk, hc, hs]
+        return run, [hq, hk, hc, hs], lambda outs: {"q": _peek(R, hq, (T, D)), "k": _peek(R, hk, (T, D))}
 
 
 class QKNormRope(Workload):
@@ -156,6 +200,10 @@ class QKNormRope(Workload):
     unfused=True the same result through the op sequence the reference calls
     (two rms_norm_heads_ and the two rope_), for comparison; both are rated
     on the fused op's algorithmic bytes."""
+
+    results = {"q": ("rel", 1e-4), "k": ("rel", 1e-4)}
+    inputs = (("q", (T, D), 0.0, 1.0, 17), ("k", (T, D), 0.0, 1.0, 18), ("gq", (128,), 1.0, 0.1, 19),
+              ("gk", (128,), 1.0, 0.1, 20))
 
     def __init__(self, unfused=False):
         self.unfused = unfused
@@ -166,13 +214,11 @@ class QKNormRope(Workload):
                       if unfused else ", one launch"))
         self.algo_bytes = 4 * T * D * 4 + 2 * T * 128 * 4 + 2 * 128 * 4
         self.cs, self.sn = _tables_3axis(T, 64)
-        if unfused:
-            self.cpu = None  # the CPU sequence is the fused line's baseline
 
     def make(self, be, i):
-        return dict(q=be.randn((T, D), 17000 + i), k=be.randn((T, D), 17500 + i), c=be.array(self.cs),
-                    s=be.array(self.sn), gq=be.randn((128,), 17900 + i, 1.0, 0.1),
-                    gk=be.randn((128,), 17950 + i, 1.0, 0.1))
+        d = super().make(be, i)
+        d.update(c=be.array(self.cs), s=be.array(self.sn))
+        return d
 
     def step(self, be, s):
         if self.unfused:
@@ -182,10 +228,9 @@ class QKNormRope(Workload):
         else:
             be.qknorm_rope(s["q"], D, s["k"], D, 1, T, 128, s["gq"], s["gk"], 1e-5, s["c"], s["s"], True)
 
-    def cpu(self, R, orc):
-        q, k = orc.randn((1, T, D), 17), orc.randn((1, T, D), 18)
-        gq, gk = orc.randn((128,), 19, 1.0, 0.1), orc.randn((128,), 20, 1.0, 0.1)
-        hq, hk, hgq, hgk = R.new(q.shape, q), R.new(k.shape, k), R.new(gq.shape, gq), R.new(gk.shape, gk)
+    def cpu(self, R, h):
+        hq, hk = R.new((1, T, D), h["q"]), R.new((1, T, D), h["k"])
+        hgq, hgk = R.new((128,), h["gq"]), R.new((128,), h["gk"])
         hc, hs = R.new(self.cs.shape, self.cs), R.new(self.sn.shape, self.sn)
 
         def run():
@@ -195,11 +240,12 @@ class QKNormRope(Workload):
             R._chk(R.lib.ref_rope_(hk, 128, hc, hs, 1))
             return []
 
-        return run, [hq, hk, hgq, hgk, hc, hs]
+        return run, [hq, hk, hgq, hgk, hc, hs], lambda outs: {"q": _peek(R, hq, (T, D)), "k": _peek(R, hk, (T, D))}
 
 
 class GNSiLU(Workload):
     kernel = "k_gn_"
+    results = {"y": ("rel", 1e-4)}
 
     def __init__(self, tag, shape, eps, note):
         self.shape, self.eps = shape, eps
@@ -207,29 +253,25 @@ class GNSiLU(Workload):
         self.desc = f"config {note}: y = silu(group_norm(x, 32 groups, eps {eps:g})), x {list(shape)} ~N(0,2)"
         n = int(np.prod(shape))
         self.algo_bytes = 2 * n * 4 + 2 * shape[1] * 4
-
-    def make(self, be, i):
-        Cc = self.shape[1]
-        return dict(x=be.randn(self.shape, 8000 + i, 0.0, 2.0), y=be.empty(self.shape),
-                    g=be.randn((Cc,), 9000 + i, 1.0, 0.1), b=be.randn((Cc,), 9500 + i, 0.0, 0.1))
+        Cc = shape[1]
+        self.inputs = (("x", shape, 0.0, 2.0, 8), ("g", (Cc,), 1.0, 0.1, 9), ("b", (Cc,), 0.0, 0.1, 10))
+        self.outputs = (("y", shape),)
 
     def step(self, be, s):
         N, Cc = self.shape[0], self.shape[1]
         HW = int(np.prod(self.shape[2:]))
         be.group_norm(s["x"], s["y"], N, Cc, HW, 32, s["g"], s["b"], self.eps, silu=True)
 
-    def cpu(self, R, orc):
-        x = orc.randn(self.shape, 8, 0.0, 2.0)
+    def cpu(self, R, h):
         Cc = self.shape[1]
-        g, b = orc.randn((Cc,), 9, 1.0, 0.1), orc.randn((Cc,), 10, 0.0, 0.1)
-        hx, hg, hb = R.new(x.shape, x), R.new(g.shape, g), R.new(b.shape, b)
+        hx, hg, hb = R.new(self.shape, h["x"]), R.new((Cc,), h["g"]), R.new((Cc,), h["b"])
 
         def run():
-            h = R._ptr(R.lib.ref_group_norm(hx, 32, hg, hb, self.eps))
-            R._chk(R.lib.ref_silu_(h))
-            return [h]
+            o = R._ptr(R.lib.ref_group_norm(hx, 32, hg, hb, self.eps))
+            R._chk(R.lib.ref_silu_(o))
+            return [o]
 
-        return run, [hx, hg, hb]
+        return run, [hx, hg, hb], lambda outs: {"y": _peek(R, outs[0], self.shape)}
 
 
 class LNModGate(Workload):
@@ -237,23 +279,22 @@ class LNModGate(Workload):
     desc = ("config 5a: y = layer_norm(x)*(1+scale)+shift; res += tanh(gate)*y (y not stored); x, res [4096,3840]; "
             "scale, shift, gate [3840] ~N(0,0.2); eps 1e-6")
     algo_bytes = 3 * T * D * 4 + 3 * D * 4
-
-    def make(self, be, i):
-        return dict(x=be.randn((T, D), 10000 + i), res=be.randn((T, D), 11000 + i),
-                    sc=be.randn((D,), 12000 + i, 0.0, 0.2), sh=be.randn((D,), 13000 + i, 0.0, 0.2),
-                    gt=be.randn((D,), 14000 + i, 0.0, 0.2))
+    inputs = (("x", (T, D), 0.0, 1.0, 11), ("res", (T, D), 0.0, 1.0, 12), ("sc", (D,), 0.0, 0.2, 13),
+              ("sh", (D,), 0.0, 0.2, 14), ("gt", (D,), 0.0, 0.2, 15))
+    results = {"res": ("rel", 1e-4)}
 
     def step(self, be, s):
         be.ln_modulate_gate(s["x"], s["res"], s["sc"], s["sh"], s["gt"], None, T, D, 1e-6)
 
-    def cpu(self, R, orc):
-        x, res = orc.randn((T, D), 10), orc.randn((T, D), 11)
-        sc, sh, gt = (orc.randn((D,), 12 + i, 0.0, 0.2) for i in range(3))
-        hx, hr = R.new(x.shape, x), R.new(res.shape, res)
-        hsc, hsh, hgt = R.new((D,), sc), R.new((D,), sh), R.new((D,), gt)
+    def cpu(self, R, h):
+        hx, hr = R.new((T, D), h["x"]), R.new((T, D), h["res"])
+        hsc, hsh, hgt = R.new((D,), h["sc"]), R.new((D,), h["sh"]), R.new((D,), h["gt"])
         hones = R.new((T, D), np.ones((T, D), np.float32))
 
         def run():
+            # scale and gate are transformed in place by the composition: fresh copies each run
+            R.view(hsc)[...] = h["sc"]
+            R.view(hgt)[...] = h["gt"]
             y = R._ptr(R.lib.ref_layer_norm(hx, None, None, 1e-6))
             R._chk(R.lib.ref_affine_(hsc, 1.0, 1.0))
             R._chk(R.lib.ref_tanh_(hgt))
@@ -262,7 +303,21 @@ class LNModGate(Workload):
             R._chk(R.lib.ref_add_rows_scaled_(hr, y, hgt))
             return [y]
 
-        return run, [hx, hr, hsc, hsh, hgt, hones]
+        return run, [hx, hr, hsc, hsh, hgt, hones], lambda outs: {"res": _peek(R, hr, (T, D))}
+
+
+def _bf16_bits(a):
+    """fp32 -> bf16 bit patterns, nearest even (inf/NaN keep their top half):
+    the device's rounding of a GEMM's A (backend_cuda.cu:183-188)."""
+    w = np.ascontiguousarray(a, np.float32).view(np.uint32)
+    top = (w >> np.uint32(16)).astype(np.uint32)
+    r = (w + np.uint32(0x7FFF) + (top & np.uint32(1))) >> np.uint32(16)
+    special = (w & np.uint32(0x7F800000)) == np.uint32(0x7F800000)
+    return np.where(special, top, r).astype(np.uint16)
+
+
+def _bf16_to_f32(b):
+    return (b.astype(np.uint32) << np.uint32(16)).view(np.float32)
 
 
 class RmsModBf16(Workload):
@@ -271,24 +326,30 @@ class RmsModBf16(Workload):
     desc = ("Z-Image block: y16 = bf16(rms_norm(x) * w * (1 + scale)) (zimage.cpp:115-116, the GEMMs' bf16 A); "
             "x [4096,3840], w, scale [3840]; eps 1e-5")
     algo_bytes = T * D * 4 + T * D * 2 + 2 * D * 4
+    inputs = (("x", (T, D), 0.0, 1.0, 21), ("w", (D,), 1.0, 0.1, 22), ("sc", (D,), 1.0, 0.2, 23))
+    results = {"y16": ("rel", 1e-2)}  # bf16 output: half an ulp of bf16 is 2^-9 relative
 
     def make(self, be, i):
-        return dict(x=be.randn((T, D), 15000 + i), w=be.randn((D,), 15500 + i, 1.0, 0.1),
-                    sc=be.randn((D,), 15600 + i, 1.0, 0.2), y16=be.array(np.zeros(T * D, np.uint16)))
+        d = super().make(be, i)
+        d["y16"] = be.array(np.zeros(T * D, np.uint16))
+        return d
 
     def step(self, be, s):
         be.rms_norm_modulate_bf16(s["x"], s["y16"], T, D, s["w"], s["sc"], 1e-5)
 
-    def cpu(self, R, orc):
-        x, w, sc = orc.randn((T, D), 15), orc.randn((D,), 16, 1.0, 0.1), orc.randn((D,), 17, 1.0, 0.2)
-        hx, hw, hsc = R.new(x.shape, x), R.new((D,), w), R.new((D,), sc)
+    def gpu_results(self, be, s):
+        return {"y16": _bf16_to_f32(s["y16"].download()).reshape(T, D)}
+
+    def cpu(self, R, h):
+        hx, hw, hsc = R.new((T, D), h["x"]), R.new((D,), h["w"]), R.new((D,), h["sc"])
 
         def run():
             y = R._ptr(R.lib.ref_rms_norm(hx, hw, 1e-5))
             R._chk(R.lib.ref_mul_rows_(y, hsc))
             return [y]
 
-        return run, [hx, hw, hsc]
+        # the reference's device path rounds the GEMM's A to bf16 (backend_cuda.cu:183-188)
+        return run, [hx, hw, hsc], lambda outs: {"y16": _bf16_to_f32(_bf16_bits(_peek(R, outs[0], (T, D))))}
 
 
 class RmsGatedAdd(Workload):
@@ -297,48 +358,42 @@ class RmsGatedAdd(Workload):
     desc = ("Z-Image block: x += gate * rms_norm(a) * w (zimage.cpp:124-127); x, a [4096,3840], w, gate [3840]; "
             "eps 1e-5")
     algo_bytes = 3 * T * D * 4 + 2 * D * 4
-
-    def make(self, be, i):
-        return dict(x=be.randn((T, D), 16000 + i), a=be.randn((T, D), 16500 + i, 0.0, 3.0),
-                    w=be.randn((D,), 16600 + i, 1.0, 0.1), g=be.randn((D,), 16700 + i, 0.0, 0.5))
+    inputs = (("x", (T, D), 0.0, 1.0, 24), ("a", (T, D), 0.0, 3.0, 25), ("w", (D,), 1.0, 0.1, 26),
+              ("g", (D,), 0.0, 0.5, 27))
+    results = {"x": ("rel", 1e-4)}
 
     def step(self, be, s):
         be.rms_norm_gated_add(s["x"], s["a"], T, D, s["w"], s["g"], 1e-5)
 
-    def cpu(self, R, orc):
-        x, a = orc.randn((T, D), 18), orc.randn((T, D), 19, 0.0, 3.0)
-        w, g = orc.randn((D,), 20, 1.0, 0.1), orc.randn((D,), 21, 0.0, 0.5)
-        hx, ha, hw, hg = R.new(x.shape, x), R.new(a.shape, a), R.new((D,), w), R.new((D,), g)
+    def cpu(self, R, h):
+        hx, ha, hw, hg = R.new((T, D), h["x"]), R.new((T, D), h["a"]), R.new((D,), h["w"]), R.new((D,), h["g"])
 
         def run():
             y = R._ptr(R.lib.ref_rms_norm(ha, hw, 1e-5))
             R._chk(R.lib.ref_add_rows_scaled_(hx, y, hg))
             return [y]
 
-        return run, [hx, ha, hw, hg]
+        return run, [hx, ha, hw, hg], lambda outs: {"x": _peek(R, hx, (T, D))}
 
 
 class Softmax(Workload):
     name, kernel = "softmax_rows", "k_softmax"
     desc = "config 5b: in-place row softmax of scores [30,4096,4096] ~N(0,3), scale 1/sqrt(128), non-causal"
     algo_bytes = 2 * 30 * T * T * 4
-
-    def make(self, be, i):
-        return dict(x=be.randn((30 * T, T), 15000 + i, 0.0, 3.0))
+    inputs = (("x", (30 * T, T), 0.0, 3.0, 28),)
+    results = {"x": ("softmax", 1e-4)}
 
     def step(self, be, s):
         be.softmax_rows(s["x"], 30 * T, T, 1.0 / math.sqrt(128.0), False)
 
-    def cpu(self, R, orc):
-        x = orc.randn((30 * T, T), 15, 0.0, 3.0)
-        hx = R.new(x.shape, x)
-        del x
+    def cpu(self, R, h):
+        hx = R.new((30 * T, T), h["x"])
 
         def run():
             R._chk(R.lib.ref_softmax_rows_(hx, 30 * T, T, 1.0 / math.sqrt(128.0), 0))
             return []
 
-        return run, [hx]
+        return run, [hx], lambda outs: {"x": _peek(R, hx, (30 * T, T))}
 
 
 class Layout(Workload):
@@ -358,17 +413,15 @@ class Layout(Workload):
         "patchify2d": ("Z-Image latent to tokens (zimage.cpp:165): [1,16,128,128], p 2 -> [4096,64]",
                        [(1, 16, 128, 128)], (4096, 64), "k_patchify"),
     }
+    results = {"y": ("abs", 0.0)}
 
     def __init__(self, name):
         self.name = name
         self.desc, self.ins, self.out, self.kernel = self.SPECS[name]
         n_in = sum(int(np.prod(s)) for s in self.ins)
         self.algo_bytes = 4 * (n_in + int(np.prod(self.out)))
-
-    def make(self, be, i):
-        d = {f"x{k}": be.randn(s, 16000 + 100 * k + i) for k, s in enumerate(self.ins)}
-        d["y"] = be.empty(self.out)
-        return d
+        self.inputs = tuple((f"x{k}", sh, 0.0, 1.0, 30 + k) for k, sh in enumerate(self.ins))
+        self.outputs = (("y", self.out),)
 
     def step(self, be, s):
         a, y = s["x0"], s["y"]
@@ -388,24 +441,22 @@ class Layout(Workload):
             _, Cc, H, W = self.ins[0]
             be.patchify(a, y, Cc, H, W, 2)
 
-    def cpu(self, R, orc):
-        xs = [orc.randn(sh, 16 + k) for k, sh in enumerate(self.ins)]
-        hs = [R.new(x.shape, x) for x in xs]
-        del xs
+    def cpu(self, R, h):
+        hs = [R.new(sh, h[f"x{k}"]) for k, sh in enumerate(self.ins)]
         L = R.lib
         fn = {"upsample_nearest2x": lambda: L.ref_upsample_nearest2x(hs[0]),
               "nchw_to_nlc": lambda: L.ref_nchw_to_nlc(hs[0]),
               "nlc_to_nchw": lambda: L.ref_nlc_to_nchw(hs[0], 128, 128),
               "concat_channels": lambda: L.ref_concat_channels(hs[0], hs[1]),
               "patchify2d": lambda: L.ref_patchify2d(hs[0], 2)}[self.name]
-        return (lambda: [R._ptr(fn())]), hs
+        return (lambda: [R._ptr(fn())]), hs, lambda outs: {"y": _peek(R, outs[0], self.out)}
 
 
 def _bf16_weights(shape, seed, std):
     """Synthetic bf16 weights (uint16 bit patterns): seeded normals rounded to
     nearest even."""
-    w = (np.random.default_rng(seed).standard_normal(shape, dtype=np.float32) * np.float32(std)).view(np.uint32)
-    return ((w + np.uint32(0x7FFF) + ((w >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+    w = (np.random.default_rng(seed).standard_normal(shape, dtype=np.float32) * np.float32(std))
+    return _bf16_bits(w)
 
 
 class Linear(Workload):
@@ -414,7 +465,11 @@ class Linear(Workload):
     [4096,3840] x [3840,3840]^T + bias, and the FFN front half
     swiglu(x w1^T, x w3^T) with w1, w3 [10240,3840] -- fused, and unfused as the
     reference runs it (two GEMMs, then swiglu). Rated in TFLOP/s against the
-    dense bf16 MFMA peak."""
+    dense bf16 MFMA peak. Parity: the reference's CPU linear on the same
+    weights with x rounded to bf16 as its device path rounds it
+    (backend_cuda.cu:466-467); then only the fp32 summation order differs."""
+
+    _want = {}  # the swiglu lines share one reference result
 
     def __init__(self, kind):
         self.name = kind
@@ -424,26 +479,28 @@ class Linear(Workload):
             self.flops = 2 * self.M * self.N * self.K
             self.algo_bytes = self.M * self.K * 4 + self.N * self.K * 2 + self.M * self.N * 4 + self.N * 4
             self.desc = "linear, bf16 weights: y = x W^T + b, x [4096,3840] fp32, W [3840,3840] bf16 (Z-Image to_q/k/v/out)"
+            self.inputs = (("x", (T, D), 0.0, 1.0, 40), ("b", (D,), 0.0, 0.1, 41))
+            self.wseeds = {"w": 42}
         else:
             self.M, self.N, self.K = T, F, D
             self.flops = 2 * 2 * self.M * self.N * self.K
             self.algo_bytes = self.M * self.K * 4 + 2 * self.N * self.K * 2 + self.M * self.N * 4
             self.desc = ("swiglu(x w1^T, x w3^T), x [4096,3840] fp32, w1, w3 [10240,3840] bf16 (Z-Image FFN, zimage.cpp:130)" +
                          (": the reference's sequence (two GEMMs, then swiglu)" if kind.endswith("unfused") else ", one GEMM"))
+            self.inputs = (("x", (T, D), 0.0, 1.0, 43),)
+            self.wseeds = {"w1": 44, "w3": 45}
+        self.outputs = (("y", (self.M, self.N)),)
+        self.results = {"y": ("normrel", 1e-5)}
+        self.weights = {n: _bf16_weights((self.N, self.K), sd, 0.02) for n, sd in self.wseeds.items()}
         if kind != "linear_bf16":
-            self.cpu = None  # tens of seconds per step on the host; the projection line carries the CPU baseline
+            self.cpu_time = False  # tens of seconds per step on the host: parity only, no timing
 
     def make(self, be, i):
-        d = dict(x=be.randn((self.M, self.K), 18000 + i))
-        if self.name == "linear_bf16":
-            d["w"] = be.array(_bf16_weights((self.N, self.K), 18100 + i, 0.02))
-            d["b"] = be.randn((self.N,), 18200 + i, 0.0, 0.1)
-        else:
-            d["w1"] = be.array(_bf16_weights((self.N, self.K), 18300 + i, 0.02))
-            d["w3"] = be.array(_bf16_weights((self.N, self.K), 18400 + i, 0.02))
-            if self.name.endswith("unfused"):
-                d["g"], d["u"] = be.empty((self.M, self.N)), be.empty((self.M, self.N))
-        d["y"] = be.empty((self.M, self.N))
+        d = super().make(be, i)
+        for n, w in self.weights.items():
+            d[n] = be.array(w)
+        if self.name.endswith("unfused"):
+            d["g"], d["u"] = be.empty((self.M, self.N)), be.empty((self.M, self.N))
         return d
 
     def step(self, be, s):
@@ -457,13 +514,37 @@ class Linear(Workload):
             be.gemm_nt_bf16(M, N, K, s["x"], K, s["w3"], K, s["u"], N)
             be.swiglu(s["g"], s["u"], s["y"], M * N)
 
-    def cpu(self, R, orc):
-        x = orc.randn((self.M, self.K), 18)
-        W = orc.randn((self.N, self.K), 19, 0.0, 0.02)
-        b = orc.randn((self.N,), 20, 0.0, 0.1)
-        hx, hw, hb = R.new(x.shape, x), R.new(W.shape, W), R.new(b.shape, b)
-        R._chk(R.lib.ref_tensor_to_bf16(hw))
-        return (lambda: [R._ptr(R.lib.ref_linear(hx, hw, hb))]), [hx, hw, hb]
+    def _ref_weight(self, R, n):
+        hw = R.new((self.N, self.K), _bf16_to_f32(self.weights[n]))
+        R._chk(R.lib.ref_tensor_to_bf16(hw))  # exact: the values are bf16 already
+        return hw
+
+    def cpu(self, R, h):
+        hx = R.new((self.M, self.K), _bf16_to_f32(_bf16_bits(h["x"])))
+        hws = {n: self._ref_weight(R, n) for n in self.weights}
+        if self.name == "linear_bf16":
+            hb = R.new((self.N,), h["b"])
+            return ((lambda: [R._ptr(R.lib.ref_linear(hx, hws["w"], hb))]), [hx, hb] + list(hws.values()),
+                    lambda outs: {"y": _peek(R, outs[0], (self.M, self.N))})
+
+        def run():
+            g = R._ptr(R.lib.ref_linear(hx, hws["w1"], None))
+            u = R._ptr(R.lib.ref_linear(hx, hws["w3"], None))
+            y = R._ptr(R.lib.ref_swiglu(g, u))
+            R.free(g, u)
+            return [y]
+
+        return run, [hx] + list(hws.values()), lambda outs: {"y": _peek(R, outs[0], (self.M, self.N))}
+
+    def reference_results(self, R, h):
+        """The swiglu lines have the same inputs: one reference computation."""
+        key = "swiglu" if self.name != "linear_bf16" else self.name
+        if key not in Linear._want:
+            run, handles, collect = self.cpu(R, h)
+            outs = run()
+            Linear._want[key] = collect(outs)
+            R.free(*outs, *handles)
+        return Linear._want[key]
 
 
 class Attention(Workload):
@@ -473,7 +554,8 @@ class Attention(Workload):
     formula 4 S^2 d H (test_ops.cpp:352); the MFMA units execute three bf16
     products per fp32 product (split operands), which pct_mfma_peak counts.
     The CPU baseline times the reference's attention on one of the 30 heads
-    and scales it by 30 (heads are independent, tensor.cpp:793-808)."""
+    and scales it by 30 (heads are independent, tensor.cpp:793-808); parity
+    runs the reference on all 30 heads."""
 
     name, kernel = "attention", "k_attn_fwd"
     S, H, d = T, 30, 128
@@ -482,20 +564,30 @@ class Attention(Workload):
     algo_bytes = 4 * T * 30 * 128 * 4
     cpu_scale = 30
     desc = "attention, q k v [1,4096,30x128] fp32, softmax(q k^T / sqrt(128)) v per head (Z-Image DiT layer)"
-
-    def make(self, be, i):
-        shp = (1, self.S, self.H * self.d)
-        return dict(q=be.randn(shp, 19000 + i), k=be.randn(shp, 19100 + i), v=be.randn(shp, 19200 + i),
-                    o=be.empty(shp))
+    inputs = (("q", (1, T, 30 * 128), 0.0, 1.0, 50), ("k", (1, T, 30 * 128), 0.0, 1.0, 51),
+              ("v", (1, T, 30 * 128), 0.0, 1.0, 52))
+    outputs = (("o", (1, T, 30 * 128)),)
+    results = {"o": ("abs", 1e-4)}  # the reference's attention bar (test_ops.cpp:442-451)
 
     def step(self, be, s):
         be.attention(s["q"], s["k"], s["v"], s["o"], 1, self.S, self.S, self.H, self.H, self.d, False)
 
-    def cpu(self, R, orc):
-        shp = (1, self.S, self.d)  # one head
-        q, k, v = orc.randn(shp, 21), orc.randn(shp, 22), orc.randn(shp, 23)
-        hq, hk, hv = R.new(shp, q), R.new(shp, k), R.new(shp, v)
-        return (lambda: [R._ptr(R.lib.ref_attention(hq, hk, hv, 1, 0, 1))]), [hq, hk, hv]
+    def _head(self, h, n, i):
+        return np.ascontiguousarray(h[n].reshape(T, 30, 128)[:, i, :]).reshape(1, T, 128)
+
+    def cpu(self, R, h):
+        shp = (1, self.S, self.d)  # one head timed
+        hq, hk, hv = (R.new(shp, self._head(h, n, 0)) for n in ("q", "k", "v"))
+        return (lambda: [R._ptr(R.lib.ref_attention(hq, hk, hv, 1, 0, 1))]), [hq, hk, hv], None
+
+    def reference_results(self, R, h):
+        o = np.empty((T, 30, 128), np.float32)
+        for i in range(30):
+            hs = [R.new((1, T, 128), self._head(h, n, i)) for n in ("q", "k", "v")]
+            ho = R._ptr(R.lib.ref_attention(*hs, 1, 0, 1))
+            o[:, i, :] = _peek(R, ho, (T, 128))
+            R.free(ho, *hs)
+        return {"o": o.reshape(1, T, 30 * 128)}
 
 
 class ZImageStep(Workload):
@@ -505,14 +597,16 @@ class ZImageStep(Workload):
     refiner blocks, 30 main blocks of dim 3840 (30 heads x 128, FFN 10240),
     weights seeded random with the checkpoint's shapes (BF16 from 2^20
     elements, as pipeline.cpp:113 loads them). Rated in TFLOP/s over the
-    linear layers and attention (2 flop per multiply-add)."""
+    linear layers and attention (2 flop per multiply-add). Its parity against
+    the reference's own forward runs in tests/test_gpu_zimage.py on a model of
+    the same layout and fewer layers (the full model's CPU forward takes
+    minutes)."""
 
     name, kernel = "zimage_step_1024", "k_gemm_dl"
     H = W = 128
     L, cap_dim = 128, 2560
     D, F, heads, layers = 3840, 10240, 30, 30
     algo_bytes = 0
-    cpu = None
     desc = "Z-Image DiT step at 1024x1024 (4096 image + 128 text tokens, 30+4 blocks, dim 3840), random BF16 weights"
 
     @property
@@ -540,23 +634,50 @@ class ZImageStep(Workload):
 
 class CopyCalibration(Workload):
     """Not a BASELINE config: an in-place x *= 1 stream over [4096,10240]
-    (one read + one write of 168 MB), the plain-copy reference for what HBM
-    streaming reaches on this box and the calibration for the traffic counters."""
+    (one read + one write of 168 MB, non-temporal loads and stores), the
+    plain-copy reference for what HBM streaming reaches on this box and the
+    calibration for the traffic counters."""
 
     name, kernel = "copy_calibration", "k_unary"
     desc = "calibration (not a config): in-place x *= 1.0 over [4096,10240] fp32, 1 read + 1 write"
     algo_bytes = 2 * T * F * 4
-
-    def make(self, be, i):
-        return dict(x=be.randn((T, F), 16000 + i))
+    inputs = (("x", (T, F), 0.0, 1.0, 60),)
+    results = {"x": ("abs", 0.0)}
 
     def step(self, be, s):
         be.scale(s["x"], 1.0, T * F)
+
+    def cpu(self, R, h):
+        hx = R.new((T, F), h["x"])
+        return (lambda: (R._chk(R.lib.ref_scale_(hx, 1.0)), [])[1]), [hx], lambda outs: {"x": _peek(R, hx, (T, F))}
+
+
+class BlitCalibration(Workload):
+    """Not a BASELINE config: the HIP runtime's device-to-device copy
+    (sdh_copy -> hipMemcpyAsync) of [4096,10240] fp32, a second calibration
+    kernel of known traffic whose loads and stores are ordinary (cached)
+    ones, to check the counters' scale on kernels that do not stream
+    non-temporally."""
+
+    name, kernel = "blit_calibration", "copyBuffer"
+    desc = "calibration (not a config): hipMemcpyAsync device-to-device of [4096,10240] fp32, 1 read + 1 write"
+    algo_bytes = 2 * T * F * 4
+    inputs = (("x", (T, F), 0.0, 1.0, 61),)
+    outputs = (("y", (T, F)),)
+    results = {"y": ("abs", 0.0)}
+
+    def step(self, be, s):
+        be.copy(s["y"], s["x"], T * F * 4)
+
+    def cpu(self, R, h):
+        hx = R.new((T, F), h["x"])
+        return (lambda: []), [hx], lambda outs: {"y": _peek(R, hx, (T, F))}
 
 
 def all_workloads():
     return [
         CopyCalibration(),
+        BlitCalibration(),
         AddRmsNorm(),
         SwiGLU(),
         RopeQK(),
@@ -575,8 +696,13 @@ def all_workloads():
 
 
 # ------------------------------------------------------------------ GPU timing
-def measure_gpu(be, w, steps, warmup):
+def measure_gpu(be, w, steps, warmup, check=False):
+    """Times `steps` steps over rotating buffer sets. With check, set 0's
+    inputs are downloaded before the timed steps, and afterwards, outside the
+    timed region, set 0 is reloaded from them, stepped once and its results
+    returned for the parity check."""
     first = w.make(be, 0)
+    host = w.host_inputs(first) if check and w.results else None
     footprint = sum(a.nbytes for a in first.values())
     nsets = max(2, min(MAX_SETS, math.ceil(MIN_ROTATION_BYTES / max(footprint, 1))))
     sets = [first] + [w.make(be, i) for i in range(1, nsets)]
@@ -592,63 +718,118 @@ def measure_gpu(be, w, steps, warmup):
     be.synchronize()
     wall = time.perf_counter() - t0
     ev_ms = be.timer_elapsed(0, 1)
-    for s in sets:
-        for a in s.values():
+    got = None
+    if host is not None and w.results:
+        w.reload(be, sets[0], host)
+        w.step(be, sets[0])
+        got = w.gpu_results(be, sets[0])
+    for st in sets:
+        for a in st.values():
             a.free()
-    return dict(nsets=nsets, footprint=footprint * nsets, wall_ms=wall * 1e3 / steps, event_ms=ev_ms / steps)
+    return dict(nsets=nsets, footprint=footprint * nsets, wall_ms=wall * 1e3 / steps, event_ms=ev_ms / steps,
+                got=got, host=host)
 
 
-# ------------------------------------------------------------------ CPU baseline
-def cpu_threads():
+# ------------------------------------------------------------------ CPU leg: reference timing and parity
+REF_V3 = os.path.join(ROOT, "oracle", "_ref", "libsdref.so")
+REF_V4 = os.path.join(ROOT, "oracle", "_ref", "libsdref_v4.so")
+REF_FLAGS = "g++ -std=c++17 -O3 {march} -pthread -fPIC (the reference Makefile's flags; -march=native there)"
+
+
+def _host_has_avx512():
     try:
-        n = len(os.sched_getaffinity(0))
+        flags = next(l for l in open("/proc/cpuinfo") if l.startswith("flags")).split()
     except Exception:
-        n = os.cpu_count() or 1
-    return max(1, min(16, n))
+        return False
+    return all(f in flags for f in ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"))
 
 
-def measure_cpu(w, reps):
-    """Times the reference's CPU composition of one step (median of reps)."""
+def reference_library():
+    """The compiled reference tensor library (oracle/_ref) for the CPU leg:
+    the x86-64-v4 (AVX-512) build where this host has AVX-512, else the
+    x86-64-v3 (AVX2 + FMA) build the parity tests pin. None if neither is
+    built (the reference tree was absent when build() ran)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    from oracle import Oracle, Reference, have_reference
+    from oracle import Reference
 
-    if getattr(w, "cpu", None) is None:
-        return None
-    orc = Oracle()
-    threads = cpu_threads()
-    orc.set_threads(threads)
-    if not have_reference():
-        return measure_cpu_port(w, orc, reps, threads)
-    R = Reference()
-    R.lib.ref_set_threads(threads)
-    run, handles = w.cpu(R, orc)
+    if os.path.exists(REF_V4) and _host_has_avx512():
+        return Reference(REF_V4), REF_FLAGS.format(march="-march=x86-64-v4")
+    if os.path.exists(REF_V3):
+        return Reference(REF_V3), REF_FLAGS.format(march="-march=x86-64-v3")
+    return None, None
+
+
+def cpu_threads():
+    """Threads for the reference's pool: this process's CPU share -- the
+    OMP_NUM_THREADS the GPU box sets (its CPUs per GPU), else the CPUs this
+    process may run on."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except Exception:
+        avail = os.cpu_count() or 1
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    n = int(share) if share.isdigit() and int(share) > 0 else avail
+    return max(1, min(n, avail)), avail
+
+
+def run_reference(R, w, host, reps):
+    """The reference's CPU composition of one step on the host inputs: its
+    results after exactly one run (for parity) and, when reps > 0, the
+    median time of reps further runs after that one (output allocation
+    included, as the op is called)."""
+    if hasattr(w, "reference_results"):
+        want = w.reference_results(R, host)
+        if reps <= 0 or getattr(w, "cpu_time", True) is False:
+            return dict(want=want, ms=None)
+        made = w.cpu(R, host)
+        run, handles, _ = made
+        collect = None
+    else:
+        made = w.cpu(R, host)
+        if made is None:
+            return None
+        run, handles, collect = made
+        want = None
     times = []
-    for i in range(reps + 1):
+    for i in range((reps if getattr(w, "cpu_time", True) else 0) + 1):
         t0 = time.perf_counter()
         outs = run()
         dt = time.perf_counter() - t0
+        if i == 0 and collect is not None:
+            want = collect(outs)
         R.free(*outs)
         if i:
             times.append(dt)
     R.free(*handles)
-    # a workload may time a fixed fraction of its step (independent heads) and scale it
-    return dict(ms=statistics.median(times) * 1e3 * getattr(w, "cpu_scale", 1), reps=reps, threads=threads,
-                kind="reference")
+    ms = statistics.median(times) * 1e3 * getattr(w, "cpu_scale", 1) if times else None
+    return dict(want=want, ms=ms)
 
 
-def measure_cpu_port(w, orc, reps, threads):
-    """Fallback when oracle/_ref is absent: the C restatement of the same
-    step (SwiGLU only; other configs report no CPU time then)."""
-    if not isinstance(w, SwiGLU):
-        return None
-    g, u = orc.randn((T, F), 4, 0.0, 1.5), orc.randn((T, F), 5, 0.0, 1.5)
-    times = []
-    for i in range(reps + 1):
-        t0 = time.perf_counter()
-        orc.swiglu(g, u)
-        if i:
-            times.append(time.perf_counter() - t0)
-    return dict(ms=statistics.median(times) * 1e3, reps=reps, threads=threads, kind="port")
+def parity(got, want, results):
+    """max-abs error and the tolerance metric of each result, GPU against the
+    reference on the same inputs."""
+    per, worst = {}, None
+    for n, (kind, bound) in results.items():
+        g = np.asarray(got[n], np.float64).reshape(-1)
+        r = np.asarray(want[n], np.float64).reshape(-1)
+        d = np.abs(g - r)
+        mx = float(np.max(d)) if d.size else 0.0
+        if kind == "softmax":
+            zeros = r == 0
+            metric = float("inf") if np.any(g[zeros] != 0) else float(np.max(d / np.maximum(np.abs(r), 1e-30)))
+        elif kind == "normrel":
+            metric = mx / max(float(np.max(np.abs(r))), 1e-30)
+        elif kind == "rel":
+            metric = float(np.max(d / np.maximum(np.abs(r), 1.0)))
+        else:  # abs
+            metric = mx
+        e = dict(max_abs_err=mx, rel_err=float(np.max(d / np.maximum(np.abs(r), 1.0))) if kind != "softmax" else metric,
+                 metric=kind, bound=bound, value=metric, within_tolerance=bool(metric <= bound),
+                 bitexact=bool(mx == 0.0))
+        per[n] = e
+        if worst is None or e["max_abs_err"] > worst["max_abs_err"]:
+            worst = e
+    return per, worst
 
 
 # ------------------------------------------------------------------ traffic (rocprof pmc)
@@ -844,9 +1025,13 @@ def main():
     be = sdhip.Backend()
     head = wls[args.workload]
     names = [n.strip() for n in args.only.split(",")] if args.only else list(wls)
+    R, ref_build = (None, None) if args.no_cpu else reference_library()
+    threads, avail = cpu_threads()
+    if R is not None:
+        R.lib.ref_set_threads(threads)
 
     ops = []
-    head_res = None
+    head_res, head_cpu, head_err = None, None, None
     for n in names:
         w = wls[n]
         steps = args.steps if w is head else args.op_steps
@@ -854,11 +1039,13 @@ def main():
         if hasattr(w, "measure"):  # a whole model step, timed by the model library itself
             r = w.measure(max(3, min(steps, 10)), 2)
         else:
-            r = measure_gpu(be, w, steps, warm)
+            r = measure_gpu(be, w, steps, warm, check=R is not None)
         gbs = w.algo_bytes / (r["event_ms"] * 1e-3) / 1e9
         entry = dict(op=w.name, desc=w.desc, algo_bytes=w.algo_bytes, us_per_op=round(r["event_ms"] * 1e3, 2),
                      GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1), rotation_sets=r["nsets"],
                      rotation_MB=round(r["footprint"] / 2**20), traffic_bytes=read_traffic(w.name))
+        if w.inputs:
+            entry["seeds"] = w.seeds()
         if "params" in r:
             entry.update(params=r["params"], ms_per_step=round(r["event_ms"], 3))
         flops = getattr(w, "flops", None)
@@ -867,17 +1054,32 @@ def main():
             mult = getattr(w, "mfma_mult", 1)  # bf16 MFMA products per counted product
             entry.update(flops=flops, TFLOPs=round(tfs, 1),
                          pct_mfma_peak=round(100 * tfs * mult / MFMA_BF16_PEAK_TFS, 1))
-        if args.cpu_all and not args.no_cpu:
+        if r.get("got") is not None:
             heavy = w.algo_bytes > (1 << 30) or (flops or 0) > 1e10
-            c = measure_cpu(w, 1 if (flops or 0) > 1e10 else 3 if heavy else args.cpu_reps)
-            if c:
-                entry.update(cpu_ms=round(c["ms"], 3), cpu_threads=c["threads"],
-                             speedup_vs_cpu=round(c["ms"] / (r["event_ms"]), 1))
+            reps = (args.cpu_reps if w is head else
+                    (1 if (flops or 0) > 1e10 else 3 if heavy else args.cpu_reps) if args.cpu_all else 0)
+            c = run_reference(R, w, r["host"], reps)
+            if c is not None and c["want"] is not None:
+                per, worst = parity(r["got"], c["want"], w.results)
+                entry.update(max_abs_err=float(f"{worst['max_abs_err']:.3e}"), rel_err=float(f"{worst['rel_err']:.3e}"),
+                             within_tolerance=all(e["within_tolerance"] for e in per.values()),
+                             parity={k: {kk: (float(f"{vv:.3e}") if isinstance(vv, float) else vv)
+                                         for kk, vv in e.items()} for k, e in per.items()})
+                if w is head:
+                    head_err = entry
+            if c is not None and c["ms"]:
+                entry.update(cpu_ms=round(c["ms"], 3), cpu_threads=threads, speedup_vs_cpu=round(c["ms"] / r["event_ms"], 1))
+                if w is head:
+                    head_cpu = c
+        r.pop("got", None)
+        r.pop("host", None)
         ops.append(entry)
         rate = (f"{entry['TFLOPs']:8.1f} TFLOP/s {entry['pct_mfma_peak']:5.1f}% of 2.5 PF bf16" if flops else
                 f"{entry['GBps']:8.1f} GB/s  {entry['pct_hbm_peak']:5.1f}% of 8 TB/s")
+        err = (f"  err {entry['max_abs_err']:.1e} abs {entry['rel_err']:.1e} rel "
+               f"{'ok' if entry['within_tolerance'] else 'OUT OF TOLERANCE'}") if "max_abs_err" in entry else ""
         print(f"# {w.name:22s} {entry['us_per_op']:10.2f} us  {rate}" +
-              (f"  cpu {entry['cpu_ms']:.2f} ms" if 'cpu_ms' in entry else ""), file=sys.stderr, flush=True)
+              (f"  cpu {entry['cpu_ms']:.2f} ms" if 'cpu_ms' in entry else "") + err, file=sys.stderr, flush=True)
         if w is head:
             head_res = r
 
@@ -888,17 +1090,16 @@ def main():
     achieved = head.algo_bytes / (head_res["event_ms"] * 1e-3) / 1e9
     traffic = read_traffic(head.name)
     cpu = None
-    if not args.no_cpu:
-        c = measure_cpu(head, args.cpu_reps)
-        if c:
-            cpu = dict(value=round(head.algo_bytes / (c["ms"] * 1e-3) / 1e9, 2), unit="GB/s", cores=c["threads"],
-                       kind=c["kind"],
-                       sample=f"the full {head.name} step at the config shape through "
-                              + ("the reference's tensor.cpp (compiled from /root/reference)" if c["kind"] == "reference"
-                                 else "the C restatement of tensor.cpp")
-                              + f", output allocation included, median of {c['reps']} runs after 1 warm-up: "
-                              f"{c['ms']:.2f} ms per step",
-                       ms_per_step=round(c["ms"], 3))
+    if head_cpu is not None:
+        cpu = dict(value=round(head.algo_bytes / (head_cpu["ms"] * 1e-3) / 1e9, 2), unit="GB/s", cores=threads,
+                   cores_available=avail, kind="reference",
+                   sample=f"the full {head.name} step at the config shape through the reference's tensor.cpp "
+                          f"(oracle/_ref, compiled from /root/reference), on the same input arrays as the GPU's "
+                          f"set 0, output allocation included, median of {args.cpu_reps} runs after 1 warm-up: "
+                          f"{head_cpu['ms']:.2f} ms per step",
+                   build=ref_build, ms_per_step=round(head_cpu["ms"], 3),
+                   threads_note="the reference's thread pool sized to this process's CPU share (OMP_NUM_THREADS "
+                                "where set, which the GPU box sets to its CPUs per GPU; else the CPUs it may run on)")
     value = head.algo_bytes / (head_res["wall_ms"] * 1e-3) / 1e9
     line = {
         "metric": METRIC,
@@ -912,7 +1113,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded N(mu,sigma) fp32 inputs generated on the device, resident in HBM)",
+        "data": "synthetic: seeded N(mu,sigma) fp32 inputs generated on the device (sdh_fill_normal, seeds per "
+                "tensor under ops[].seeds), resident in HBM; set 0 is also the reference CPU path's input",
         "config": {"workload": head.desc, "algorithmic_bytes": head.algo_bytes,
                    "rotation_sets": head_res["nsets"], "rotation_MB": round(head_res["footprint"] / 2**20)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -920,6 +1122,12 @@ def main():
                      "kernel": head.kernel, "kernel_us": round(head_res["event_ms"] * 1e3, 3)},
         "cpu_baseline": cpu,
         "speedup_vs_cpu": round(cpu["ms_per_step"] / head_res["wall_ms"], 1) if cpu else None,
+        "max_abs_err": head_err["max_abs_err"] if head_err else None,
+        "rel_err": head_err["rel_err"] if head_err else None,
+        "within_tolerance": head_err["within_tolerance"] if head_err else None,
+        "parity_note": ("every op line compares the GPU result of set 0 with the reference's tensor.cpp on the same "
+                        "arrays, outside the timed region: max_abs_err = max|gpu - ref|, rel_err = max |gpu - ref| / "
+                        "max(|ref|, 1); within_tolerance applies the op's bar (parity.metric, parity.bound)"),
         "ops": ops,
     }
     print(json.dumps(line), flush=True)

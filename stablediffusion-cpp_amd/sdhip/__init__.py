@@ -225,6 +225,10 @@ class Backend:
     def synchronize(self):
         self.check(self.lib.sdh_synchronize())
 
+    def copy(self, dst, src, nbytes: int):
+        """Device-to-device copy on the library stream (sdh_copy)."""
+        self.check(self.lib.sdh_copy(_p(dst), _p(src), nbytes))
+
     def memory_stats(self):
         r, u = C.c_size_t(), C.c_size_t()
         self.check(self.lib.sdh_memory_stats(C.byref(r), C.byref(u)))

@@ -3,6 +3,8 @@
 seeded random inputs, for every op on the path, at tiny, odd and mid-size
 shapes. Skipped where oracle/_ref was not built.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -138,3 +140,34 @@ def test_qknorm_rope_bitexact(orc, ref, interleaved):
     rk = ref.rope(ref.rms_norm_heads(k, dim, gk, 1e-5).reshape(k.shape), dim, cs, sn, interleaved)
     _eq(q2, rq, "qknorm_rope q")
     _eq(k2, rk, "qknorm_rope k")
+
+
+REF_V4 = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle", "_ref", "libsdref_v4.so")
+
+
+def _avx512():
+    try:
+        flags = next(l for l in open("/proc/cpuinfo") if l.startswith("flags")).split()
+    except Exception:
+        return False
+    return all(f in flags for f in ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"))
+
+
+@pytest.mark.skipif(not (os.path.exists(REF_V4) and _avx512()), reason="no AVX-512 build of the reference or host")
+def test_reference_v4_build_equals_v3(orc, ref):
+    """The AVX-512 build of the reference (bench.py's CPU baseline on AVX-512
+    hosts) computes the same bits as the x86-64-v3 build the parity tests
+    pin, on every op the benchmark times."""
+    from oracle import Reference
+
+    r4 = Reference(REF_V4)
+    x = orc.randn((64, 3840), 91)
+    w = orc.randn((3840,), 92, 1.0, 0.1)
+    g, u = orc.randn((64, 3840), 93, 0.0, 1.5), orc.randn((64, 3840), 94, 0.0, 1.5)
+    _eq(r4.rms_norm(x, w, 1e-6), ref.rms_norm(x, w, 1e-6), "rms_norm v4")
+    _eq(r4.layer_norm(x, None, None, 1e-6), ref.layer_norm(x, None, None, 1e-6), "layer_norm v4")
+    _eq(r4.swiglu(g, u), ref.swiglu(g, u), "swiglu v4")
+    _eq(r4.softmax_rows(x, 0.0883883), ref.softmax_rows(x, 0.0883883), "softmax v4")
+    xg = orc.randn((1, 64, 32, 32), 95, 0.0, 2.0)
+    gg, bb = orc.randn((64,), 96, 1.0, 0.1), orc.randn((64,), 97, 0.0, 0.1)
+    _eq(r4.group_norm(xg, 32, gg, bb, 1e-6, silu=True), ref.group_norm(xg, 32, gg, bb, 1e-6, silu=True), "gn v4")
