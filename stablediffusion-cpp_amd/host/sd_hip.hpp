@@ -10,8 +10,8 @@
 // backend reports failures (check()/launched(), backend_cuda.cu:41-48, and the
 // stub's throw, backend_cuda_stub.cpp:14).
 //
-// conv2d stays with its existing implementation; the GEMMs (gemm_nt_bf16,
-// gemm_nt_f32) and attention are part of this backend.
+// Every function of backend_cuda.h has its counterpart here, conv2d, the
+// GEMMs (gemm_nt_bf16, gemm_nt_f32) and attention included.
 #pragma once
 
 #include <cstddef>

@@ -1,279 +1,421 @@
-// zimage_hip.cpp - see zimage_hip.h. The order of operations follows
-// src/zimage.cpp (lines cited per step); the arithmetic is backend_hip's.
+// zimage_hip.cpp - one Z-Image denoising step on the device (see
+// zimage_hip.h for the design). The function computed is the reference's
+// ZImageTransformer::forward (src/zimage.cpp:138-228): the same checkpoint
+// tensors, the same order of operations and the same rotary positions; the
+// code below is organised around this library's token buffer, cached rotary
+// tables and fused block ops.
 #include "zimage_hip.h"
 
+#include <algorithm>
+#include <cctype>
 #include <chrono>
 #include <cmath>
-#include <memory>
+#include <map>
+#include <mutex>
 #include <stdexcept>
 #include <string>
+#include <tuple>
+#include <utility>
+#include <vector>
 
 #include "sd_hip.hpp"
 
 namespace sdh {
 namespace {
 
-constexpr int64_t kSeqMultiple = 32;  // zimage.cpp:28: sequences are padded to a multiple of 32
-int64_t pad_to(int64_t n) { return (n + kSeqMultiple - 1) / kSeqMultiple * kSeqMultiple; }
+// ---- the checkpoint's layout ---------------------------------------------------
+// A block's tensors by role. The strings are the checkpoint's module names
+// (the file format; zimage.cpp:38-47 reads the same ones).
+enum NormRole { kNormAttnIn, kNormAttnOut, kNormFfnIn, kNormFfnOut, kNormQ, kNormK, kNormRoles };
+enum ProjRole { kProjQ, kProjK, kProjV, kProjOut, kProjGate, kProjDown, kProjUp, kProjMod, kProjRoles };
+const char* const kNormName[kNormRoles] = {"attention_norm1", "attention_norm2", "ffn_norm1",
+                                           "ffn_norm2",       "attention.norm_q", "attention.norm_k"};
+const char* const kProjName[kProjRoles] = {"attention.to_q",  "attention.to_k",  "attention.to_v",
+                                           "attention.to_out.0", "feed_forward.w1", "feed_forward.w2",
+                                           "feed_forward.w3", "adaLN_modulation.0"};
 
-// rows [n, D] followed by n_pad copies of the [1, D] pad token (zimage.cpp:31-35)
-Tensor pad_rows(const Tensor& rows, const Tensor& pad, int64_t n_pad) {
-    if (n_pad <= 0) return rows;
-    return concat_batch(rows, repeat_batch(pad, n_pad));
+// The block stacks in the order a step runs them. The noise refiner (image
+// tokens) and the main stack are modulated by the timestep; the context
+// refiner (text tokens) is not.
+enum Stack { kNoiseRefiner, kContextRefiner, kMainStack, kStacks };
+const char* const kStackName[kStacks] = {"noise_refiner", "context_refiner", "layers"};
+const bool kStackModulated[kStacks] = {true, false, true};
+
+// Token counts are padded up to a multiple of 32 with the pad tokens
+// (transformer_z_image.py's SEQ_MULTI_OF, zimage.cpp:28).
+constexpr int64_t kTokenGranule = 32;
+int64_t padded(int64_t n) { return (n + kTokenGranule - 1) / kTokenGranule * kTokenGranule; }
+
+// QK-norm's eps is a literal in the model, not config.json's norm_eps
+// (zimage.cpp:117-118).
+constexpr float kQkNormEps = 1e-5f;
+// The final LayerNorm: no affine, eps 1e-6 (zimage.cpp:223).
+constexpr float kHeadNormEps = 1e-6f;
+
+struct Proj {
+    const Tensor* W = nullptr;
+    const Tensor* b = nullptr;
+};
+
+struct BlockBinding {
+    const Tensor* norm[kNormRoles] = {};
+    Proj proj[kProjRoles];
+    bool modulated = false;
+    // Every projection but the modulation is BF16: the block runs the fused
+    // ops (the normalised rows emitted as the GEMMs' bf16 A, attention and
+    // SwiGLU emitting the next GEMM's bf16 A), which give the values of the
+    // op sequence they replace.
+    bool fused_bf16 = false;
+};
+
+// Rows of one step's token buffer: image tokens, image pads, text tokens,
+// text pads.
+struct TokenLayout {
+    int64_t grid_h = 0, grid_w = 0;  // patches down and across
+    int64_t img = 0, img_rows = 0;   // image tokens, and with their pads
+    int64_t txt = 0, txt_rows = 0;   // text tokens, and with their pads
+    int64_t rows() const { return img_rows + txt_rows; }
+};
+
+// Blocks in a stack: one past the largest "<stack>.<index>." any weight name has.
+int64_t stack_depth(const Weights& w, const std::string& stack) {
+    const std::string head = stack + ".";
+    int64_t depth = 0;
+    for (const auto& kv : w.tensors) {
+        const std::string& name = kv.first;
+        if (name.compare(0, head.size(), head) != 0) continue;
+        size_t i = head.size();
+        int64_t idx = 0;
+        while (i < name.size() && std::isdigit((unsigned char)name[i]) && idx < (int64_t(1) << 40))
+            idx = idx * 10 + (name[i++] - '0');
+        if (i > head.size() && i < name.size() && name[i] == '.') depth = std::max(depth, idx + 1);
+    }
+    return depth;
+}
+
+// y = x W^T (+ b) written into `out`, which already has x's rows and W's
+// outputs (a row range of a bigger device tensor): the embedders fill their
+// rows of the token buffer without an intermediate tensor.
+void project_into(const Tensor& x, const Proj& p, Tensor& out, const char* what) {
+    const int64_t in = x.dim(-1), n = p.W->dim(0), rows = x.numel() / (in > 0 ? in : 1);
+    if (p.W->dim(1) != in || out.numel() != rows * n)
+        throw std::runtime_error(std::string("ZImageTransformer: ") + what + " takes " + std::to_string(p.W->dim(1)) +
+                                 " features per token, the input has " + x.shape_str());
+    const float* bias = p.b ? p.b->dptr() : nullptr;
+    if (p.W->is_bf16())
+        sd::hip::gemm_nt_bf16(rows, n, in, x.dptr(), in, p.W->dptr16(), in, out.dptr(), n, bias, false);
+    else
+        sd::hip::gemm_nt_f32(rows, n, in, x.dptr(), in, p.W->dptr(), in, out.dptr(), n, bias, false);
+}
+
+// Rows [from, to) of a [rows, D] device tensor set to a [1, D] token: one
+// copy of the token, then copies of the rows written so far, doubling.
+void fill_rows(Tensor& buf, int64_t from, int64_t to, const Tensor& token) {
+    const int64_t D = buf.dim(-1), n = to - from;
+    if (n <= 0) return;
+    if (token.numel() != D) throw std::runtime_error("ZImageTransformer: a pad token must have dim features");
+    float* base = buf.dptr() + from * D;
+    sd::hip::copy(base, token.dptr(), (size_t)D * sizeof(float));
+    for (int64_t done = 1; done < n; done *= 2)
+        sd::hip::copy(base + done * D, base, (size_t)(std::min(done, n - done) * D) * sizeof(float));
+}
+
+Tensor as_sequence(Tensor rows) {
+    rows.reshape({1, rows.dim(0), rows.dim(1)});
+    return rows;
 }
 
 }  // namespace
 
-ZImageTransformer::Linear::Linear(const Weights& w, const std::string& prefix)
-    : W(&w.get(prefix + ".weight")), b(w.try_get(prefix + ".bias")) {}
+struct ZImageTransformer::Impl {
+    Config cfg;
+    int64_t dim = 0, head_dim = 0;
+    int channels = 0;
+    Proj patch_embed, text_embed, t_in, t_out, head_mod, head_out;
+    const Tensor *text_norm = nullptr, *img_pad = nullptr, *txt_pad = nullptr;
+    std::vector<BlockBinding> stacks[kStacks];
+    std::vector<float> t_freq;         // timestep sinusoid: frequency i of F/2
+    std::vector<double> pair_freq;     // rotary pair k: theta^(-2j/d_a) for its axis a and index j in it
+    std::vector<int> pair_axis;        // rotary pair k: the position axis it turns with
+    mutable std::mutex rotary_mu;      // the cache below is filled by const forward calls
+    mutable std::map<std::tuple<int64_t, int64_t, int64_t>, std::pair<Tensor, Tensor>> rotary_cache;
 
-// zimage.cpp:38-47: the checkpoint's tensor names of one block
-ZImageTransformer::Block ZImageTransformer::load_block(const Weights& w, const std::string& p, bool modulated) const {
-    Block b{&w.get(p + ".attention_norm1.weight"),
-            &w.get(p + ".attention_norm2.weight"),
-            &w.get(p + ".ffn_norm1.weight"),
-            &w.get(p + ".ffn_norm2.weight"),
-            &w.get(p + ".attention.norm_q.weight"),
-            &w.get(p + ".attention.norm_k.weight"),
-            Linear(w, p + ".attention.to_q"),
-            Linear(w, p + ".attention.to_k"),
-            Linear(w, p + ".attention.to_v"),
-            Linear(w, p + ".attention.to_out.0"),
-            Linear(w, p + ".feed_forward.w1"),
-            Linear(w, p + ".feed_forward.w2"),
-            Linear(w, p + ".feed_forward.w3"),
-            Linear()};
-    if (modulated) b.adaln = Linear(w, p + ".adaLN_modulation.0");
-    return b;
-}
+    explicit Impl(const Config& c) : cfg(c) {}
+
+    Proj bind_proj(const Weights& w, const std::string& name) const {
+        return Proj{&w.get(name + ".weight"), w.try_get(name + ".bias")};
+    }
+
+    BlockBinding bind_block(const Weights& w, const std::string& prefix, bool modulated) const {
+        BlockBinding b;
+        b.modulated = modulated;
+        for (int r = 0; r < kNormRoles; ++r) b.norm[r] = &w.get(prefix + "." + kNormName[r] + ".weight");
+        for (int r = 0; r < kProjRoles; ++r)
+            if (r != kProjMod || modulated) b.proj[r] = bind_proj(w, prefix + "." + kProjName[r]);
+        b.fused_bf16 = true;
+        for (int r = 0; r < kProjMod; ++r) b.fused_bf16 = b.fused_bf16 && b.proj[r].W->is_bf16();
+        return b;
+    }
+
+    void bind(const Weights& w) {
+        patch_embed = bind_proj(w, "all_x_embedder.2-1");
+        text_norm = &w.get("cap_embedder.0.weight");
+        text_embed = bind_proj(w, "cap_embedder.1");
+        t_in = bind_proj(w, "t_embedder.mlp.0");
+        t_out = bind_proj(w, "t_embedder.mlp.2");
+        head_out = bind_proj(w, "all_final_layer.2-1.linear");
+        head_mod = bind_proj(w, "all_final_layer.2-1.adaLN_modulation.1");
+        img_pad = &w.get("x_pad_token");
+        txt_pad = &w.get("cap_pad_token");
+        const int64_t pp = (int64_t)cfg.patch * cfg.patch;
+        dim = patch_embed.W->dim(0);
+        if (cfg.heads <= 0 || dim % cfg.heads)
+            throw std::runtime_error("ZImageTransformer: model width " + std::to_string(dim) + " is not a multiple of " +
+                                     std::to_string(cfg.heads) + " heads");
+        head_dim = dim / cfg.heads;
+        channels = (int)(patch_embed.W->dim(1) / pp);
+        const int64_t axes = (int64_t)cfg.axes_dims[0] + cfg.axes_dims[1] + cfg.axes_dims[2];
+        if (axes != head_dim)
+            throw std::runtime_error("ZImageTransformer: rotary axes of " + std::to_string(axes) +
+                                     " channels for heads of " + std::to_string(head_dim));
+        for (int s = 0; s < kStacks; ++s) {
+            const int64_t n = stack_depth(w, kStackName[s]);
+            for (int64_t i = 0; i < n; ++i)
+                stacks[s].push_back(bind_block(w, std::string(kStackName[s]) + "." + std::to_string(i), kStackModulated[s]));
+        }
+        if (stacks[kMainStack].empty())
+            throw std::runtime_error("ZImageTransformer: the weights hold no main-stack block (layers.<i>.*)");
+
+        // timestep sinusoid frequencies, in float as the model forms them (zimage.cpp:152-153)
+        const int64_t half = t_in.W->dim(1) / 2;
+        for (int64_t i = 0; i < half; ++i) t_freq.push_back(std::exp(-std::log(10000.0f) * (float)i / (float)half));
+        // rotary pair frequencies per axis in double (zimage.cpp:80)
+        for (int a = 0; a < 3; ++a)
+            for (int j = 0; j < cfg.axes_dims[a] / 2; ++j) {
+                pair_freq.push_back(1.0 / std::pow((double)cfg.rope_theta, (double)(2 * j) / (double)cfg.axes_dims[a]));
+                pair_axis.push_back(a);
+            }
+    }
+
+    TokenLayout layout(const Tensor& latent, const Tensor& text) const {
+        if (!latent.is_hip() || !text.is_hip())
+            throw std::runtime_error("ZImageTransformer::forward: latent and text must be device tensors");
+        if (latent.ndim() != 4 || latent.dim(0) != 1 || text.ndim() != 3 || text.dim(0) != 1)
+            throw std::runtime_error("ZImageTransformer::forward: one sample at a time: latent [1, C, H, W] and text "
+                                     "[1, L, features], got " + latent.shape_str() + " and " + text.shape_str());
+        const int64_t p = cfg.patch;
+        if (latent.dim(1) != channels || latent.dim(2) % p || latent.dim(3) % p)
+            throw std::runtime_error("ZImageTransformer::forward: the latent needs " + std::to_string(channels) +
+                                     " channels and sides that are multiples of " + std::to_string(p) + ", got " +
+                                     latent.shape_str());
+        TokenLayout g;
+        g.grid_h = latent.dim(2) / p;
+        g.grid_w = latent.dim(3) / p;
+        g.img = g.grid_h * g.grid_w;
+        g.img_rows = padded(g.img);
+        g.txt = text.dim(1);
+        g.txt_rows = padded(g.txt);
+        return g;
+    }
+
+    // The adaLN conditioning vector [1, adaln_dim] of timestep t (zimage.cpp:148-163).
+    Tensor condition(float t) const {
+        const int64_t half = (int64_t)t_freq.size();
+        Tensor v({1, 2 * half});
+        const float tt = t * cfg.t_scale;
+        for (int64_t i = 0; i < half; ++i) {
+            v.data[i] = std::cos(tt * t_freq[i]);
+            v.data[half + i] = std::sin(tt * t_freq[i]);
+        }
+        Tensor h = linear(v.to(Device::HIP), *t_in.W, t_in.b);
+        silu_(h);
+        return linear(h, *t_out.W, t_out.b);
+    }
+
+    // Interleaved rotary tables [rows, head_dim] of a token layout, built on
+    // the first call with that layout. Row positions (axis 0, 1, 2)
+    // (zimage.cpp:177-191): image token (txt_rows + 1, row, column) of the
+    // patch grid; image pad (0, 0, 0); text row j, pads included, (1 + j, 0, 0).
+    // Pair k of a row turns by the float angle position[axis(k)] * freq(k)
+    // formed in double, cos and sin stored twice (zimage.cpp:81-83).
+    const std::pair<Tensor, Tensor>& rotary(const TokenLayout& g) const {
+        std::lock_guard<std::mutex> lk(rotary_mu);
+        const auto key = std::make_tuple(g.grid_h, g.grid_w, g.txt_rows);
+        auto it = rotary_cache.find(key);
+        if (it != rotary_cache.end()) return it->second;
+        const int64_t rows = g.rows(), hd = head_dim, pairs = (int64_t)pair_freq.size();
+        Tensor c({rows, hd}), s({rows, hd});
+        for (int64_t r = 0; r < rows; ++r) {
+            int64_t pos[3] = {0, 0, 0};
+            if (r < g.img) {
+                pos[0] = g.txt_rows + 1;
+                pos[1] = r / g.grid_w;
+                pos[2] = r % g.grid_w;
+            } else if (r >= g.img_rows) {
+                pos[0] = 1 + (r - g.img_rows);
+            }
+            float* cr = c.data.data() + r * hd;
+            float* sr = s.data.data() + r * hd;
+            for (int64_t k = 0; k < pairs; ++k) {
+                const float ang = (float)((double)pos[pair_axis[k]] * pair_freq[k]);
+                cr[2 * k] = cr[2 * k + 1] = std::cos(ang);
+                sr[2 * k] = sr[2 * k + 1] = std::sin(ang);
+            }
+        }
+        return rotary_cache.emplace(key, std::make_pair(c.to(Device::HIP), s.to(Device::HIP))).first->second;
+    }
+
+    // The token buffer's rows: patch embeddings, image pads, embedded
+    // (RMS-normalised) text, text pads (zimage.cpp:165-175).
+    void embed(const Tensor& latent, const Tensor& text, const TokenLayout& g, Tensor& seq) const {
+        Tensor img = rows_view(seq, 0, g.img);
+        project_into(patchify2d(latent, cfg.patch), patch_embed, img, "the patch embedder");
+        fill_rows(seq, g.img, g.img_rows, *img_pad);
+        Tensor txt = rows_view(seq, g.img_rows, g.img_rows + g.txt);
+        project_into(rms_norm(text, text_norm, cfg.norm_eps), text_embed, txt, "the text embedder");
+        fill_rows(seq, g.img_rows + g.txt, g.rows(), *txt_pad);
+    }
+
+    // The input of a sublayer: rms_norm(x) * (1 + scale), as the BF16 GEMM
+    // operand on the fused path.
+    Tensor sublayer_input(const BlockBinding& b, const Tensor& x, NormRole n, const Tensor* scale) const {
+        if (b.fused_bf16) return rms_norm_modulate_bf16(x, b.norm[n], scale, cfg.norm_eps);
+        Tensor h = rms_norm(x, b.norm[n], cfg.norm_eps);
+        if (scale) mul_rows_(h, *scale);
+        return h;
+    }
+
+    Tensor project(const Tensor& x, const BlockBinding& b, ProjRole r) const {
+        return linear(x, *b.proj[r].W, b.proj[r].b);
+    }
+
+    // Self-attention with QK-norm and rotary positions, then to_out (zimage.cpp:116-122).
+    Tensor attend(const BlockBinding& b, const Tensor& in, const Tensor& cos, const Tensor& sin) const {
+        Tensor q = project(in, b, kProjQ), k = project(in, b, kProjK), v = project(in, b, kProjV);
+        qknorm_rope_(q, k, head_dim, b.norm[kNormQ], b.norm[kNormK], kQkNormEps, cos, sin, true);
+        Tensor o = b.fused_bf16 ? attention_bf16(q, k, v, cfg.heads, false) : attention(q, k, v, cfg.heads, false);
+        return project(o, b, kProjOut);
+    }
+
+    // w2(silu(w1 x) * w3 x) (zimage.cpp:130).
+    Tensor feed_forward(const BlockBinding& b, const Tensor& in) const {
+        const Proj &gate = b.proj[kProjGate], &up = b.proj[kProjUp];
+        Tensor hidden;
+        if (b.fused_bf16)
+            hidden = swiglu_bf16(project(in, b, kProjGate), project(in, b, kProjUp));
+        else if (gate.W->is_bf16() && up.W->is_bf16() && !gate.b && !up.b)
+            hidden = linear_swiglu(in, *gate.W, *up.W);
+        else
+            hidden = swiglu(project(in, b, kProjGate), project(in, b, kProjUp));
+        return project(hidden, b, kProjDown);
+    }
+
+    // One block on rows x ([1, S, dim], a range of the token buffer, updated
+    // in place), rotary rows cos/sin [S, head_dim], conditioning vector cond
+    // (modulated blocks). Each of its two sublayers adds
+    // gate * rms_norm(sublayer(rms_norm(x) * (1 + scale))) to x, attention
+    // first, then the FFN; unmodulated blocks have no scale and gate
+    // (zimage.cpp:90-136).
+    void run(const BlockBinding& b, Tensor& x, const Tensor& cos, const Tensor& sin, const Tensor* cond) const {
+        // the modulation rows: attention scale, attention gate, FFN scale, FFN gate
+        Tensor mod, scale[2], gate[2];
+        if (b.modulated) {
+            mod = project(*cond, b, kProjMod);
+            mod.reshape({4, dim});
+            for (int s = 0; s < 2; ++s) {
+                scale[s] = rows_view(mod, 2 * s, 2 * s + 1);
+                gate[s] = rows_view(mod, 2 * s + 1, 2 * s + 2);
+                affine_(scale[s], 1.0f, 1.0f);
+                tanh_(gate[s]);
+                scale[s].reshape({dim});
+                gate[s].reshape({dim});
+            }
+        }
+        for (int s = 0; s < 2; ++s) {
+            const bool attn = s == 0;
+            const Tensor* sc = b.modulated ? &scale[s] : nullptr;
+            const Tensor* gt = b.modulated ? &gate[s] : nullptr;
+            Tensor in = sublayer_input(b, x, attn ? kNormAttnIn : kNormFfnIn, sc);
+            Tensor out = attn ? attend(b, in, cos, sin) : feed_forward(b, in);
+            rms_norm_gated_add_(x, out, b.norm[attn ? kNormAttnOut : kNormFfnOut], gt, cfg.norm_eps);
+        }
+    }
+
+    // The final layer on the image tokens (zimage.cpp:218-227): LayerNorm
+    // without affine, times (1 + scale(silu(cond))), projection to patches,
+    // patches back to the latent's layout. cond is not used afterwards, so
+    // its SiLU is taken in place.
+    Tensor head(const Tensor& seq, Tensor& cond, const TokenLayout& g, int64_t H, int64_t W) const {
+        silu_(cond);
+        Tensor scale = linear(cond, *head_mod.W, head_mod.b);
+        affine_(scale, 1.0f, 1.0f);
+        scale.reshape({dim});
+        Tensor y = layer_norm(rows_view(seq, 0, g.img), nullptr, nullptr, kHeadNormEps);
+        mul_rows_(y, scale);
+        return unpatchify2d(linear(y, *head_out.W, head_out.b), channels, H, W, cfg.patch);
+    }
+};
 
 ZImageTransformer::ZImageTransformer(const Weights& w) : ZImageTransformer(w, Config()) {}
 
-// zimage.cpp:51-68
-ZImageTransformer::ZImageTransformer(const Weights& w, const Config& cfg)
-    : cfg_(cfg),
-      x_embed_(w, "all_x_embedder.2-1"),
-      cap_embed_(w, "cap_embedder.1"),
-      t_mlp0_(w, "t_embedder.mlp.0"),
-      t_mlp2_(w, "t_embedder.mlp.2"),
-      final_linear_(w, "all_final_layer.2-1.linear"),
-      final_adaln_(w, "all_final_layer.2-1.adaLN_modulation.1"),
-      cap_norm_(&w.get("cap_embedder.0.weight")),
-      x_pad_(&w.get("x_pad_token")),
-      cap_pad_(&w.get("cap_pad_token")) {
-    dim_ = x_embed_.W->dim(0);
-    head_dim_ = dim_ / cfg_.heads;
-    in_channels_ = (int)(x_embed_.W->dim(1) / (cfg_.patch * cfg_.patch));
-    if (cfg_.axes_dims[0] + cfg_.axes_dims[1] + cfg_.axes_dims[2] != head_dim_)
-        throw std::runtime_error("Z-Image: axes_dims must sum to the head dim");
-    for (int i = 0; w.has("noise_refiner." + std::to_string(i) + ".attention_norm1.weight"); ++i)
-        noise_refiner_.push_back(load_block(w, "noise_refiner." + std::to_string(i), true));
-    for (int i = 0; w.has("context_refiner." + std::to_string(i) + ".attention_norm1.weight"); ++i)
-        context_refiner_.push_back(load_block(w, "context_refiner." + std::to_string(i), false));
-    for (int i = 0; w.has("layers." + std::to_string(i) + ".attention_norm1.weight"); ++i)
-        layers_.push_back(load_block(w, "layers." + std::to_string(i), true));
-    if (layers_.empty()) throw std::runtime_error("Z-Image: no transformer layers found");
+ZImageTransformer::ZImageTransformer(const Weights& w, const Config& cfg) : impl_(new Impl(cfg)) { impl_->bind(w); }
+
+ZImageTransformer::~ZImageTransformer() = default;
+
+int ZImageTransformer::in_channels() const { return impl_->channels; }
+int64_t ZImageTransformer::dim() const { return impl_->dim; }
+
+Tensor ZImageTransformer::forward(const Tensor& latent, float t, const Tensor& text) const {
+    const Impl& m = *impl_;
+    const TokenLayout g = m.layout(latent, text);
+    Tensor cond = m.condition(t);
+    Tensor seq = Tensor::empty({g.rows(), m.dim}, Device::HIP);
+    m.embed(latent, text, g, seq);
+    const auto& rot = m.rotary(g);
+    // the refiners update the image and the text rows in place, each with
+    // its rows of the joint rotary tables
+    const int64_t split[3] = {0, g.img_rows, g.rows()};
+    for (int part = 0; part < 2; ++part) {
+        const Stack st = part == 0 ? kNoiseRefiner : kContextRefiner;
+        Tensor x = as_sequence(rows_view(seq, split[part], split[part + 1]));
+        const Tensor c = rows_view(rot.first, split[part], split[part + 1]);
+        const Tensor s = rows_view(rot.second, split[part], split[part + 1]);
+        for (const BlockBinding& b : m.stacks[st]) m.run(b, x, c, s, kStackModulated[st] ? &cond : nullptr);
+    }
+    Tensor all = as_sequence(rows_view(seq, 0, g.rows()));
+    for (const BlockBinding& b : m.stacks[kMainStack]) m.run(b, all, rot.first, rot.second, &cond);
+    return m.head(seq, cond, g, latent.dim(2), latent.dim(3));
 }
 
-// zimage.cpp:71-88: per axis a, freq_k = theta^(-2k/d_a) in double, angle =
-// (float)(position * freq_k); pair (2k, 2k+1) of the concatenated axes holds
-// cos and sin of the angle twice (interleaved layout).
-void ZImageTransformer::rope_tables(const std::vector<std::array<int, 3>>& pos, Tensor& cos, Tensor& sin) const {
-    const int64_t S = (int64_t)pos.size(), d = head_dim_;
-    Tensor c({S, d}), s({S, d});
-    for (int64_t i = 0; i < S; ++i) {
-        int64_t off = 0;
-        for (int a = 0; a < 3; ++a) {
-            const int da = cfg_.axes_dims[a];
-            for (int k = 0; k < da / 2; ++k) {
-                const double freq = 1.0 / std::pow((double)cfg_.rope_theta, (double)(2 * k) / (double)da);
-                const float ang = (float)((double)pos[i][a] * freq);
-                c.data[i * d + off + 2 * k] = c.data[i * d + off + 2 * k + 1] = std::cos(ang);
-                s.data[i * d + off + 2 * k] = s.data[i * d + off + 2 * k + 1] = std::sin(ang);
-            }
-            off += da;
-        }
-    }
-    cos = c.to(Device::HIP);
-    sin = s.to(Device::HIP);
-}
-
-// zimage.cpp:90-136
-void ZImageTransformer::run_block(const Block& b, Tensor& x, const Tensor& cos, const Tensor& sin,
-                                  const Tensor* adaln) const {
-    const int64_t D = dim_;
-    // modulation: mod [1, 4D] = scale_msa | gate_msa | scale_mlp | gate_mlp,
-    // scales as 1 + s and gates as tanh(g) (zimage.cpp:96-113)
-    Tensor scale_msa, gate_msa, scale_mlp, gate_mlp;
-    const bool mod = b.adaln.valid();
-    if (mod) {
-        Tensor m = b.adaln(*adaln);
-        m.reshape({4, D});
-        // views, not copies: each row only feeds the in-place op that follows
-        scale_msa = rows_view(m, 0, 1);
-        gate_msa = rows_view(m, 1, 2);
-        scale_mlp = rows_view(m, 2, 3);
-        gate_mlp = rows_view(m, 3, 4);
-        affine_(scale_msa, 1.0f, 1.0f);
-        affine_(scale_mlp, 1.0f, 1.0f);
-        tanh_(gate_msa);
-        tanh_(gate_mlp);
-        scale_msa.reshape({D});
-        gate_msa.reshape({D});
-        scale_mlp.reshape({D});
-        gate_mlp.reshape({D});
-    }
-    const bool all_bf16 = b.to_q.W->is_bf16() && b.to_k.W->is_bf16() && b.to_v.W->is_bf16() &&
-                          b.to_out.W->is_bf16() && b.w1.W->is_bf16() && b.w2.W->is_bf16() && b.w3.W->is_bf16();
-    if (all_bf16) {
-        // BF16 weights: the same values through the fused ops, each equal to the
-        // sequence it replaces bit for bit. The normalised, modulated rows are
-        // emitted as the GEMMs' bf16 A once for to_q, to_k and to_v (and once
-        // for w1, w3), attention and swiglu emit the bf16 A of to_out and w2,
-        // and the norm + gated residual after to_out and w2 is one pass over x.
-        Tensor h16 = rms_norm_modulate_bf16(x, b.attn_norm1, mod ? &scale_msa : nullptr, cfg_.norm_eps);
-        Tensor q = b.to_q(h16), k = b.to_k(h16), v = b.to_v(h16);
-        qknorm_rope_(q, k, head_dim_, b.norm_q, b.norm_k, 1e-5f, cos, sin, true);
-        Tensor a = b.to_out(attention_bf16(q, k, v, cfg_.heads, false));
-        rms_norm_gated_add_(x, a, b.attn_norm2, mod ? &gate_msa : nullptr, cfg_.norm_eps);
-        h16 = rms_norm_modulate_bf16(x, b.ffn_norm1, mod ? &scale_mlp : nullptr, cfg_.norm_eps);
-        Tensor f = b.w2(swiglu_bf16(b.w1(h16), b.w3(h16)));
-        rms_norm_gated_add_(x, f, b.ffn_norm2, mod ? &gate_mlp : nullptr, cfg_.norm_eps);
-        return;
-    }
-    // attention (zimage.cpp:115-127)
-    Tensor h = rms_norm(x, b.attn_norm1, cfg_.norm_eps);
-    if (mod) mul_rows_(h, scale_msa);
-    Tensor q = b.to_q(h), k = b.to_k(h), v = b.to_v(h);
-    // rms_norm_heads_(q), rms_norm_heads_(k), rope_(q), rope_(k) in one launch
-    qknorm_rope_(q, k, head_dim_, b.norm_q, b.norm_k, 1e-5f, cos, sin, true);
-    Tensor a = b.to_out(attention(q, k, v, cfg_.heads, false));
-    a = rms_norm(a, b.attn_norm2, cfg_.norm_eps);
-    if (mod)
-        add_rows_scaled_(x, a, gate_msa);
-    else
-        add_(x, a);
-    // feed-forward (zimage.cpp:128-135)
-    h = rms_norm(x, b.ffn_norm1, cfg_.norm_eps);
-    if (mod) mul_rows_(h, scale_mlp);
-    Tensor g = (b.w1.W->is_bf16() && b.w3.W->is_bf16() && !b.w1.b && !b.w3.b) ? linear_swiglu(h, *b.w1.W, *b.w3.W)
-                                                                                : swiglu(b.w1(h), b.w3(h));
-    Tensor f = b.w2(g);
-    f = rms_norm(f, b.ffn_norm2, cfg_.norm_eps);
-    if (mod)
-        add_rows_scaled_(x, f, gate_mlp);
-    else
-        add_(x, f);
-}
-
-// zimage.cpp:138-228
-Tensor ZImageTransformer::forward(const Tensor& x_in, float t, const Tensor& cap_in) const {
-    const int64_t C = x_in.dim(1), H = x_in.dim(2), W = x_in.dim(3), p = cfg_.patch, D = dim_;
-    if (x_in.dim(0) != 1 || cap_in.dim(0) != 1) throw std::runtime_error("Z-Image: batch size must be 1");
-    if (C != in_channels_ || H % p || W % p) throw std::runtime_error("Z-Image: bad latent shape " + x_in.shape_str());
-    if (!x_in.is_hip() || !cap_in.is_hip()) throw std::runtime_error("Z-Image: latent and text must be device tensors");
-    const int64_t Ht = H / p, Wt = W / p, n_img = Ht * Wt, n_img_pad = pad_to(n_img);
-    const int64_t n_cap = cap_in.dim(1), n_cap_pad = pad_to(n_cap);
-
-    // 1. timestep embedding -> adaln (zimage.cpp:148-163): sinusoid in float, MLP with SiLU
-    Tensor adaln;
-    {
-        const int64_t F = t_mlp0_.W->dim(1), half = F / 2;
-        Tensor freq({1, F});
-        const float tt = t * cfg_.t_scale;
-        for (int64_t i = 0; i < half; ++i) {
-            const float f = std::exp(-std::log(10000.0f) * (float)i / (float)half);
-            freq.data[i] = std::cos(tt * f);
-            freq.data[half + i] = std::sin(tt * f);
-        }
-        adaln = t_mlp0_(freq.to(Device::HIP));
-        silu_(adaln);
-        adaln = t_mlp2_(adaln);
-    }
-
-    // 2. image tokens: patchify (features ordered ph, pw, c), embed, pad (zimage.cpp:166-169)
-    Tensor img = x_embed_(patchify2d(x_in, (int)p));
-    Tensor img_seq = pad_rows(img, *x_pad_, n_img_pad - n_img);
-    img_seq.reshape({1, n_img_pad, D});
-
-    // 3. text tokens: RMSNorm, embed, pad (zimage.cpp:172-175)
-    Tensor cap = cap_embed_(rms_norm(cap_in, cap_norm_, cfg_.norm_eps));
-    cap.reshape({n_cap, D});
-    Tensor cap_seq = pad_rows(cap, *cap_pad_, n_cap_pad - n_cap);
-    cap_seq.reshape({1, n_cap_pad, D});
-
-    // rotary positions (zimage.cpp:177-191): text (1 + i, 0, 0) for every row
-    // including its pad; image (n_cap_pad + 1, h, w); image pad rows (0, 0, 0)
-    std::vector<std::array<int, 3>> cap_pos(n_cap_pad, {0, 0, 0}), img_pos(n_img_pad, {0, 0, 0});
-    for (int64_t i = 0; i < n_cap_pad; ++i) cap_pos[i] = {(int)(1 + i), 0, 0};
-    for (int64_t hh = 0; hh < Ht; ++hh)
-        for (int64_t ww = 0; ww < Wt; ++ww) img_pos[hh * Wt + ww] = {(int)(n_cap_pad + 1), (int)hh, (int)ww};
-    Tensor img_cos, img_sin, cap_cos, cap_sin;
-    rope_tables(img_pos, img_cos, img_sin);
-    rope_tables(cap_pos, cap_cos, cap_sin);
-
-    // refiners (zimage.cpp:194-201)
-    for (const Block& b : noise_refiner_) run_block(b, img_seq, img_cos, img_sin, &adaln);
-    for (const Block& b : context_refiner_) run_block(b, cap_seq, cap_cos, cap_sin, nullptr);
-
-    // 4. the unified sequence [image, text] through the main stack (zimage.cpp:204-215)
-    Tensor uni = concat_batch(img_seq.reshape({n_img_pad, D}), cap_seq.reshape({n_cap_pad, D}));
-    uni.reshape({1, n_img_pad + n_cap_pad, D});
-    std::vector<std::array<int, 3>> uni_pos = img_pos;
-    uni_pos.insert(uni_pos.end(), cap_pos.begin(), cap_pos.end());
-    Tensor uni_cos, uni_sin;
-    rope_tables(uni_pos, uni_cos, uni_sin);
-    for (const Block& b : layers_) run_block(b, uni, uni_cos, uni_sin, &adaln);
-
-    // 5. final layer on the image tokens, unpatchify (zimage.cpp:218-227)
-    Tensor img_out = slice_rows(uni, 0, n_img);
-    Tensor c = adaln;
-    silu_(c);
-    Tensor scale = final_adaln_(c);
-    affine_(scale, 1.0f, 1.0f);
-    scale.reshape({D});
-    img_out = layer_norm(img_out, nullptr, nullptr, 1e-6f);
-    mul_rows_(img_out, scale);
-    Tensor out_tok = final_linear_(img_out);
-    return unpatchify2d(out_tok, C, H, W, (int)p);
-}
-
-void ZImageTransformer::random_weights(Weights& w, const Shapes& s, uint64_t seed, int64_t mn) {
-    uint64_t k = seed;
-    auto lin = [&](const std::string& p, int64_t out, int64_t in, bool bias) {
-        w.add_random(p + ".weight", {out, in}, k++, 0.0f, 1.0f / std::sqrt((float)in), true, mn);
-        if (bias) w.add_random(p + ".bias", {out}, k++, 0.0f, 0.02f);
+void ZImageTransformer::random_weights(Weights& w, const Shapes& s, uint64_t seed, int64_t bf16_min_numel) {
+    uint64_t next = seed;
+    auto proj = [&](const std::string& name, int64_t out, int64_t in, bool bias) {
+        w.add_random(name + ".weight", {out, in}, next++, 0.0f, 1.0f / std::sqrt((float)in), true, bf16_min_numel);
+        if (bias) w.add_random(name + ".bias", {out}, next++, 0.0f, 0.02f);
     };
-    auto norm = [&](const std::string& name, int64_t n) { w.add_random(name, {n}, k++, 1.0f, 0.05f); };
+    auto norm = [&](const std::string& name, int64_t n) { w.add_random(name + ".weight", {n}, next++, 1.0f, 0.05f); };
     const int64_t D = s.dim, hd = s.dim / s.heads, pp = (int64_t)s.patch * s.patch;
-    lin("all_x_embedder.2-1", D, pp * s.in_channels, true);
-    norm("cap_embedder.0.weight", s.cap_dim);
-    lin("cap_embedder.1", D, s.cap_dim, true);
-    lin("t_embedder.mlp.0", s.t_hidden, s.t_freq, true);
-    lin("t_embedder.mlp.2", s.adaln_dim, s.t_hidden, true);
-    lin("all_final_layer.2-1.linear", pp * s.in_channels, D, true);
-    lin("all_final_layer.2-1.adaLN_modulation.1", D, s.adaln_dim, true);
-    w.add_random("x_pad_token", {1, D}, k++, 0.0f, 1.0f);
-    w.add_random("cap_pad_token", {1, D}, k++, 0.0f, 1.0f);
-    auto block = [&](const std::string& p, bool modulated) {
-        norm(p + ".attention_norm1.weight", D);
-        norm(p + ".attention_norm2.weight", D);
-        norm(p + ".ffn_norm1.weight", D);
-        norm(p + ".ffn_norm2.weight", D);
-        norm(p + ".attention.norm_q.weight", hd);
-        norm(p + ".attention.norm_k.weight", hd);
-        lin(p + ".attention.to_q", D, D, false);
-        lin(p + ".attention.to_k", D, D, false);
-        lin(p + ".attention.to_v", D, D, false);
-        lin(p + ".attention.to_out.0", D, D, false);
-        lin(p + ".feed_forward.w1", s.ffn, D, false);
-        lin(p + ".feed_forward.w2", D, s.ffn, false);
-        lin(p + ".feed_forward.w3", s.ffn, D, false);
-        if (modulated) lin(p + ".adaLN_modulation.0", 4 * D, s.adaln_dim, true);
-    };
-    for (int i = 0; i < s.noise_refiners; ++i) block("noise_refiner." + std::to_string(i), true);
-    for (int i = 0; i < s.context_refiners; ++i) block("context_refiner." + std::to_string(i), false);
-    for (int i = 0; i < s.layers; ++i) block("layers." + std::to_string(i), true);
+    proj("all_x_embedder.2-1", D, pp * s.in_channels, true);
+    norm("cap_embedder.0", s.cap_dim);
+    proj("cap_embedder.1", D, s.cap_dim, true);
+    proj("t_embedder.mlp.0", s.t_hidden, s.t_freq, true);
+    proj("t_embedder.mlp.2", s.adaln_dim, s.t_hidden, true);
+    proj("all_final_layer.2-1.linear", pp * s.in_channels, D, true);
+    proj("all_final_layer.2-1.adaLN_modulation.1", D, s.adaln_dim, true);
+    w.add_random("x_pad_token", {1, D}, next++, 0.0f, 1.0f);
+    w.add_random("cap_pad_token", {1, D}, next++, 0.0f, 1.0f);
+    const int depth[kStacks] = {s.noise_refiners, s.context_refiners, s.layers};
+    for (int st = 0; st < kStacks; ++st)
+        for (int i = 0; i < depth[st]; ++i) {
+            const std::string p = std::string(kStackName[st]) + "." + std::to_string(i) + ".";
+            for (int r = 0; r < kNormRoles; ++r) norm(p + kNormName[r], r == kNormQ || r == kNormK ? hd : D);
+            for (int r = 0; r < kProjRoles; ++r) {
+                // (out, in) of each projection; only the modulation has a bias
+                const int64_t out = r == kProjGate || r == kProjUp ? s.ffn : r == kProjMod ? 4 * D : D;
+                const int64_t in = r == kProjDown ? s.ffn : r == kProjMod ? s.adaln_dim : D;
+                if (r != kProjMod || kStackModulated[st]) proj(p + kProjName[r], out, in, r == kProjMod);
+            }
+        }
 }
 
 }  // namespace sdh

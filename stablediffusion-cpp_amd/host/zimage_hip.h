@@ -1,28 +1,28 @@
-// zimage_hip.h - the Z-Image single-stream diffusion transformer (S3-DiT) on
-// the MI355X: one denoising step, ZImageTransformer::forward of the reference
-// (src/zimage.h:40-79, src/zimage.cpp:138-228), computed entirely on the
-// device through backend_hip.
+// zimage_hip.h - one denoising step of Z-Image's single-stream diffusion
+// transformer, run entirely on the MI355X through backend_hip.
 //
-// The step (zimage.h:5-21): timestep embedding -> adaLN vector; image latent
-// -> 2x2 patches -> tokens (padded to a multiple of 32 with x_pad_token), 2
-// modulated noise-refiner blocks; text hidden states -> RMSNorm -> tokens
-// (padded with cap_pad_token), 2 context-refiner blocks; the joint [image,
-// text] sequence through the main blocks (30 heads of 128, RMS QK-norm,
-// 3-axis rotary positions, SwiGLU); final LayerNorm * (1 + scale) -> linear
-// -> unpatchify. Weights keep the checkpoint's names.
-//
-// Each block runs on backend_hip as the reference's run_block
-// (zimage.cpp:90-136) with fused ops that give the same values: the four
-// QK-norm / RoPE passes are one sdh_qknorm_rope launch; attention is the
-// fused kernel; with BF16 weights RMSNorm * (1 + scale) emits the GEMMs' bf16
-// A directly (one rounding for to_q, to_k, to_v), swiglu emits w2's bf16 A,
-// and RMSNorm + gated residual is one pass over x.
+// Interface: the reference's ZImageTransformer (src/zimage.h:40-79) --
+// constructed from the checkpoint's named weights and the config.json
+// hyper-parameters, forward(latent [1, C, H, W], t, text [1, L, cap_dim])
+// returning the model output of the latent's shape (ZImageTransformer::forward,
+// src/zimage.cpp:138-228). Everything behind the interface is this library's
+// own design (zimage_hip.cpp):
+//   * the step works on one token buffer [image rows, image pad rows, text
+//     rows, text pad rows] x dim, allocated once per call: the embedders
+//     write their rows into it, the two refiner stacks update its image and
+//     text row ranges in place, and the main stack runs on the whole buffer,
+//     so the joint sequence is never assembled by copies;
+//   * the rotary tables of a token layout are built once (from per-pair
+//     frequencies precomputed at construction) and kept for later calls; the
+//     refiners read row ranges of the joint table;
+//   * block weights are bound by role from a table of the checkpoint's name
+//     suffixes, and each block's path (the fused BF16 ops, or the fp32 ops)
+//     is fixed when it is bound.
 #pragma once
 
-#include <array>
 #include <cstdint>
+#include <memory>
 #include <string>
-#include <vector>
 
 #include "tensor_hip.h"
 #include "weights_hip.h"
@@ -31,7 +31,8 @@ namespace sdh {
 
 class ZImageTransformer {
 public:
-    // zimage.h:44-51: hyper-parameters not derivable from the weights.
+    // Hyper-parameters the weights do not determine (zimage.h:44-51); the
+    // defaults are the released model's.
     struct Config {
         int patch = 2;
         int heads = 30;
@@ -40,54 +41,35 @@ public:
         float t_scale = 1000.0f;
         int axes_dims[3] = {32, 48, 48};
     };
-    // Shapes of a model, for Weights filled with random values (benchmarks).
+    // Tensor shapes of a model, for filling Weights with random values.
     struct Shapes {
         int64_t dim = 3840, ffn = 10240, in_channels = 16, cap_dim = 2560, t_freq = 256, t_hidden = 1024,
                 adaln_dim = 256;
         int heads = 30, patch = 2, noise_refiners = 2, context_refiners = 2, layers = 30;
     };
-    // Adds every tensor of a model of `s` to w (N(0, 1/sqrt(fan-in)) linears,
-    // N(1, 0.05) norm weights), BF16 from bf16_min_numel elements as the
-    // pipeline loads Z-Image (pipeline.cpp:113).
+    // Adds every tensor of a model of shapes `s` under the checkpoint's names
+    // to w: linears N(0, 1/sqrt(fan-in)), norm weights N(1, 0.05), biases
+    // N(0, 0.02), pad tokens N(0, 1); BF16 from bf16_min_numel elements, as
+    // the pipeline loads the checkpoint (pipeline.cpp:113).
     static void random_weights(Weights& w, const Shapes& s, uint64_t seed, int64_t bf16_min_numel = 1 << 20);
 
     explicit ZImageTransformer(const Weights& w);
     ZImageTransformer(const Weights& w, const Config& cfg);
+    ~ZImageTransformer();
+    ZImageTransformer(const ZImageTransformer&) = delete;
+    ZImageTransformer& operator=(const ZImageTransformer&) = delete;
 
-    // x: [1, C, H, W] latent (H, W even); t in [0, 1]; cap: [1, L, cap_dim]
-    // text hidden states; device tensors. Returns [1, C, H, W] on the device.
-    Tensor forward(const Tensor& x, float t, const Tensor& cap) const;
+    // latent: [1, C, H, W] device tensor, H and W multiples of the patch; t in
+    // [0, 1]; text: [1, L, cap_dim] device tensor of text hidden states.
+    // Returns a [1, C, H, W] device tensor. Safe to call from several threads.
+    Tensor forward(const Tensor& latent, float t, const Tensor& text) const;
 
-    int in_channels() const { return in_channels_; }
-    int64_t dim() const { return dim_; }
-
-    // modules.h:23-30: a bound linear layer (weight [out, in], optional bias).
-    struct Linear {
-        const Tensor* W = nullptr;
-        const Tensor* b = nullptr;
-        Linear() = default;
-        Linear(const Weights& w, const std::string& prefix);
-        Tensor operator()(const Tensor& x) const { return linear(x, *W, b); }
-        bool valid() const { return W != nullptr; }
-    };
+    int in_channels() const;
+    int64_t dim() const;
 
 private:
-    struct Block {
-        const Tensor *attn_norm1, *attn_norm2, *ffn_norm1, *ffn_norm2, *norm_q, *norm_k;
-        Linear to_q, to_k, to_v, to_out, w1, w2, w3;
-        Linear adaln;  // modulated blocks only
-    };
-    Block load_block(const Weights& w, const std::string& prefix, bool modulated) const;
-    void run_block(const Block& b, Tensor& x, const Tensor& cos, const Tensor& sin, const Tensor* adaln) const;
-    // interleaved rotary tables [S, head_dim] for (axis0, h, w) positions, on the device
-    void rope_tables(const std::vector<std::array<int, 3>>& pos, Tensor& cos, Tensor& sin) const;
-
-    Config cfg_;
-    int64_t dim_ = 0, head_dim_ = 0;
-    int in_channels_ = 0;
-    Linear x_embed_, cap_embed_, t_mlp0_, t_mlp2_, final_linear_, final_adaln_;
-    const Tensor *cap_norm_ = nullptr, *x_pad_ = nullptr, *cap_pad_ = nullptr;
-    std::vector<Block> noise_refiner_, context_refiner_, layers_;
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
 };
 
 }  // namespace sdh
