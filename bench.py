@@ -195,6 +195,30 @@ class RopeQK(Workload):
         return run, [hq, hk, hc, hs], lambda outs: {"q": _peek(R, hq, (T, D)), "k": _peek(R, hk, (T, D))}
 
 
+class RopeQKAxes(RopeQK):
+    """Config 3 with sin/cos computed on the device (sdh_rope_qk_axes): the
+    angles come from the positions (0, h, w) of the 64 x 64 grid [4096, 3]
+    int32, axes (32, 48, 48), theta 256; no table crosses HBM. The reference's
+    CPU rope_ runs with the tables of the same positions."""
+
+    name, kernel = "rope_qk_axes", "k_rope_il_axes"
+    desc = ("config 3: 3-axis interleaved RoPE in place on q and k [4096,30*128] in one launch, axes (32,48,48), "
+            "theta 256, sin/cos computed on the device from the [4096,3] int32 positions (0,h,w)")
+    algo_bytes = 4 * T * D * 4 + T * 3 * 4
+
+    def __init__(self):
+        super().__init__()
+        self.pos = np.array([[0, h, w] for h in range(64) for w in range(64)], np.int32)
+
+    def make(self, be, i):
+        d = Workload.make(self, be, i)
+        d["p"] = be.array(self.pos.view(np.float32))
+        return d
+
+    def step(self, be, s):
+        be.rope_qk_axes(s["q"], D, s["k"], D, 1, T, 128, s["p"], (32, 48, 48), 256.0)
+
+
 class QKNormRope(Workload):
     """Fused QK-norm + RoPE at the config-3 shape (zimage.cpp:117-120). With
     unfused=True the same result through the op sequence the reference calls
@@ -681,6 +705,7 @@ def all_workloads():
         AddRmsNorm(),
         SwiGLU(),
         RopeQK(),
+        RopeQKAxes(),
         GNSiLU("4a", (1, 512, 128, 128), 1e-6, "4a (FLUX VAE)"),
         GNSiLU("4b", (1, 128, 1024, 1024), 1e-6, "4b (FLUX VAE norm_out)"),
         GNSiLU("4c", (2, 320, 64, 64), 1e-5, "4c (SD 1.5, reported only)"),
@@ -849,7 +874,7 @@ def read_traffic(name):
 # ------------------------------------------------------------------ rocprofv3 summaries
 KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
     "k_unary<4>": "copy_calibration", "k_add_rms": "add_rms_norm", "k_swiglu": "swiglu",
-    "k_rope_il_reg": "rope_qk", "k_ln_mod_gate": "ln_modulate_gate", "k_softmax_block": "softmax_rows",
+    "k_rope_il_reg": "rope_qk", "k_rope_il_axes": "rope_qk_axes", "k_ln_mod_gate": "ln_modulate_gate", "k_softmax_block": "softmax_rows",
     "k_upsample2x_vec": "upsample_nearest2x", "k_concat_vec": "concat_channels", "k_patchify": "patchify2d",
     "k_qknorm_rope_il": "qknorm_rope", "k_attn_fwd": "attention", "k_rms_mod_bf16": "rms_norm_modulate_bf16",
     "k_rms_gated_add": "rms_norm_gated_add",

@@ -164,6 +164,16 @@ int sdh_rope(float* x, int64_t N, int64_t S, int64_t inner, int64_t dim, const f
  * equals rope_(q, ...) then rope_(k, ...) (zimage.cpp:119-120). */
 int sdh_rope_qk(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
                 const float* cos, const float* sin, int interleaved);
+/* VARIANT of sdh_rope_qk (interleaved) with the tables formed on the device
+ * from positions, as zimage.cpp:71-88 forms them on the host: pos [S, 3]
+ * int32 (device); the head's dim = axis0 + axis1 + axis2 channels are the
+ * concatenated axes, pair j of axis a turns by the float angle
+ * (float)((double)pos[s, a] * theta^(-2j/d_a)) whose cos and sin (float)
+ * rotate it. Equals building those [S, dim] tables and calling
+ * sdh_rope_qk(..., interleaved = 1). q, k 16-byte aligned, rows of at most
+ * 8192 floats, dim a multiple of 4 and at most 256. */
+int sdh_rope_qk_axes(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
+                     const int32_t* pos, int axis0, int axis1, int axis2, float theta);
 /* FUSED: QK-norm then RoPE on q [N, S, inner_q] and k [N, S, inner_k] in one
  * launch; equals rms_norm_heads_(q, dim, gamma_q, eps),
  * rms_norm_heads_(k, dim, gamma_k, eps), rope_(q, ...), rope_(k, ...)

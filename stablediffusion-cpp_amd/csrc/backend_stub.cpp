@@ -67,6 +67,7 @@ STUB(int sdh_group_norm_silu(const float*, float*, int64_t, int64_t, int64_t, in
 STUB(int sdh_group_norm_silu_noalloc(const float*, float*, int64_t, int64_t, int64_t, int, const float*, const float*, float))
 STUB(int sdh_ln_modulate_gate(const float*, float*, const float*, const float*, const float*, float*, int64_t,
                               int64_t, float))
+STUB(int sdh_rope_qk_axes(float*, int64_t, float*, int64_t, int64_t, int64_t, int64_t, const int32_t*, int, int, int, float))
 STUB(int sdh_qknorm_rope(float*, int64_t, float*, int64_t, int64_t, int64_t, int64_t, const float*, const float*,
                          float, const float*, const float*, int))
 STUB(int sdh_gemm_nt_bf16_packed(int64_t, int64_t, int64_t, const uint16_t*, int64_t, const uint16_t*, int64_t, float*,

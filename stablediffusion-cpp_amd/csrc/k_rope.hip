@@ -15,6 +15,7 @@
 //   rotate_half: the float4 at head offset i < dim/2 pairs with the float4 at
 //                i + dim/2 (tensor.cpp:722-724); one thread updates both.
 #include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 #include "sdh_internal.hpp"
@@ -280,6 +281,96 @@ void run_rope(const char* op, float* q, int64_t inner_q, float* k, int64_t inner
     launched(op);
 }
 
+// ---- interleaved RoPE with the angles formed on the device ----------------------------
+// The tables of zimage.cpp:71-88 come from positions: pair k of a head turns
+// with position axis a(k) (the concatenated axes) by the float angle
+// (float)((double)pos[s, a(k)] * freq(k)), freq(k) = theta^(-2j/d_a) in
+// double for index j of the pair within its axis. The host forms the
+// frequencies (with the same double pow as the reference) and passes them as
+// kernel arguments; each workgroup turns its token's dim/2 angles into cos and
+// sin in LDS while its row loads are in flight, so no table crosses HBM. The
+// positions are [S, 3] int32 on the device; the rotation is k_rope_il_reg's.
+constexpr int kMaxAxisPairs = 128;  // dim <= 256
+
+struct RopeAxes {
+    double freq[kMaxAxisPairs];
+    unsigned char axis[kMaxAxisPairs];
+};
+
+template <int RV>
+__global__ __launch_bounds__(kThreads) void k_rope_il_axes(RopeArgs a, int64_t S, int dim, int64_t s0,
+                                                          const int* __restrict__ pos, RopeAxes ax) {
+    __shared__ float cl[kMaxAxisPairs], sl[kMaxAxisPairs];
+    const int t = blockIdx.y;
+    const int64_t ns = blockIdx.x;
+    const int64_t inner = a.inner[t];
+    const int64_t s = ns % S;
+    f4* row = (f4*)(a.x[t] + ns * inner);
+    const int n4 = (int)(inner >> 2), d4 = dim >> 2;
+    f4 v[RV];
+#pragma unroll
+    for (int j = 0; j < RV; ++j) {
+        const int i = threadIdx.x + kThreads * j;
+        if (i < n4) v[j] = dev::ld_stream(row + i);
+    }
+    if ((int)threadIdx.x < (dim >> 1)) {
+        const int k = threadIdx.x;
+        const float ang = (float)((double)pos[(s0 + s) * 3 + ax.axis[k]] * ax.freq[k]);
+        cl[k] = cosf(ang);
+        sl[k] = sinf(ang);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < RV; ++j) {
+        const int i = threadIdx.x + kThreads * j;
+        if (i < n4) {
+            const int h = 2 * (i % d4);  // first of the float4's two pairs
+            const float c0 = cl[h], s0v = sl[h], c1 = cl[h + 1], s1v = sl[h + 1];
+            f4 o;
+            o.x = v[j].x * c0 - v[j].y * s0v;
+            o.y = v[j].y * c0 + v[j].x * s0v;
+            o.z = v[j].z * c1 - v[j].w * s1v;
+            o.w = v[j].w * c1 + v[j].z * s1v;
+            dev::st_stream(row + i, o);
+        }
+    }
+}
+
+void run_rope_axes(const char* op, float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S,
+                   int64_t dim, const int* pos, int64_t s0, const RopeAxes& ax) {
+    const int64_t max_tok = units_per_launch(kThreads);
+    if (N * S > max_tok) {
+        if (S <= max_tok) {
+            in_pieces(N, max_tok / S, [&](int64_t n0, int64_t nn) {
+                run_rope_axes(op, q + n0 * S * inner_q, inner_q, k + n0 * S * inner_k, inner_k, nn, S, dim, pos, s0, ax);
+            });
+        } else {
+            for (int64_t n = 0; n < N; ++n)
+                in_pieces(S, max_tok, [&](int64_t p0, int64_t ns) {
+                    run_rope_axes(op, q + (n * S + p0) * inner_q, inner_q, k + (n * S + p0) * inner_k, inner_k, 1, ns,
+                                  dim, pos, s0 + p0, ax);
+                });
+        }
+        return;
+    }
+    RopeArgs a;
+    a.x[0] = q;
+    a.inner[0] = inner_q;
+    a.x[1] = k;
+    a.inner[1] = inner_k;
+    const dim3 grid((unsigned)(N * S), 2);
+    const int64_t steps = (std::max(inner_q, inner_k) / 4 + kThreads - 1) / kThreads;
+    auto go = [&](auto rc) {
+        constexpr int RV = decltype(rc)::value;
+        k_rope_il_axes<RV><<<grid, kThreads, 0, stream()>>>(a, S, (int)dim, s0, pos, ax);
+    };
+    if (steps <= 1) go(std::integral_constant<int, 1>());
+    else if (steps <= 2) go(std::integral_constant<int, 2>());
+    else if (steps <= 4) go(std::integral_constant<int, 4>());
+    else go(std::integral_constant<int, 8>());
+    launched(op);
+}
+
 // ---- fused QK-norm + RoPE (zimage.cpp:117-120) ---------------------------------------
 // rms_norm_heads_ then rope_, for Q and K in one launch: each row is read and
 // written once instead of twice. A workgroup owns one token row of one tensor
@@ -453,6 +544,39 @@ int sdh_rope_qk(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N,
         need(k != nullptr, "sdh_rope_qk", "k is NULL");
         need(k != q, "sdh_rope_qk", "q and k must be distinct tensors");
         run_rope("sdh_rope_qk", q, inner_q, k, inner_k, N, S, dim, cos, sin, interleaved);
+    });
+}
+
+int sdh_rope_qk_axes(float* q, int64_t inner_q, float* k, int64_t inner_k, int64_t N, int64_t S, int64_t dim,
+                     const int32_t* pos, int axis0, int axis1, int axis2, float theta) {
+    return guarded([&] {
+        const char* op = "sdh_rope_qk_axes";
+        need(q != nullptr && k != nullptr && k != q, op, "q and k must be two distinct tensors");
+        need(N >= 0 && S >= 0 && inner_q >= 0 && inner_k >= 0, op, "negative size");
+        const int axes[3] = {axis0, axis1, axis2};
+        need(axis0 >= 0 && axis1 >= 0 && axis2 >= 0 && axis0 % 2 == 0 && axis1 % 2 == 0 && axis2 % 2 == 0, op,
+             "axis sizes must be even and non-negative");
+        need((int64_t)axis0 + axis1 + axis2 == dim, op, "the axis sizes must add up to dim");
+        need(dim > 0 && dim % 4 == 0 && dim / 2 <= kMaxAxisPairs, op, "dim must be a positive multiple of 4, at most 256");
+        need(inner_q % dim == 0 && inner_k % dim == 0, op, "inner must be a multiple of dim");
+        need(inner_q <= (int64_t)kThreads * 4 * 8 && inner_k <= (int64_t)kThreads * 4 * 8, op,
+             "rows of at most 8192 floats");
+        need(theta > 0.0f, op, "theta must be positive");
+        if (N == 0 || S == 0) return;
+        ensure_init();
+        check_range(q, (size_t)(N * S * inner_q) * 4, op, "q");
+        check_range(k, (size_t)(N * S * inner_k) * 4, op, "k");
+        check_range(pos, (size_t)(S * 3) * 4, op, "pos");
+        need(aligned16(q) && aligned16(k) && inner_q % 4 == 0 && inner_k % 4 == 0, op,
+             "q and k must be 16-byte aligned with rows of whole float4");
+        RopeAxes ax;
+        int kk = 0;
+        for (int a = 0; a < 3; ++a)
+            for (int j = 0; j < axes[a] / 2; ++j, ++kk) {
+                ax.freq[kk] = 1.0 / std::pow((double)theta, (double)(2 * j) / (double)axes[a]);
+                ax.axis[kk] = (unsigned char)a;
+            }
+        run_rope_axes(op, q, inner_q, k, inner_k, N, S, dim, pos, 0, ax);
     });
 }
 

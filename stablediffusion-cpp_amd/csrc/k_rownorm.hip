@@ -131,6 +131,10 @@ __global__ __launch_bounds__(kThreads) void k_add_rms(float* __restrict__ x, con
     f4* xr = (f4*)(x + row * C);
     const f4* rr = (const f4*)(r + row * C);
     f4* yr = (f4*)(y + row * C);
+    // a load pair per vector and lane, added as it arrives: measured faster
+    // (42.2 us at [4096,3840]) than issuing the whole row's loads first
+    // (44.8 us), which needs 168 VGPRs and no longer fits every row on the GPU
+    // at once
     f4 v[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {

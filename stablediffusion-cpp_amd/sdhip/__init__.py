@@ -63,6 +63,7 @@ SIGNATURES = {
     "sdh_rms_norm_heads": [_vp, _i64, _i64, _vp, _fl],
     "sdh_rope": [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _int],
     "sdh_rope_qk": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _int],
+    "sdh_rope_qk_axes": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _int, _int, _int, _fl],
     "sdh_qknorm_rope": [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _fl, _vp, _vp, C.c_int],
     "sdh_softmax_rows": [_vp, _i64, _i64, _fl, _int],
     "sdh_softmax_rows_batched": [_vp, _i64, _i64, _fl, _int, _i64],
@@ -266,6 +267,12 @@ class Backend:
 
     def rms_norm(self, x, y, rows, Cc, gamma, eps):
         self.call("sdh_rms_norm", _p(x), _p(y), rows, Cc, _p(gamma), eps)
+
+    def rope_qk_axes(self, q, inner_q, k, inner_k, N, S, dim, pos, axes, theta):
+        """RoPE on q and k with the angles formed on the device from int32
+        positions pos [S, 3] (a DArray of int32 bits), axes (d0, d1, d2)."""
+        self.call("sdh_rope_qk_axes", _p(q), inner_q, _p(k), inner_k, N, S, dim, _p(pos), int(axes[0]),
+                  int(axes[1]), int(axes[2]), float(theta))
 
     def rms_norm_heads(self, x, groups, dim, gamma, eps):
         self.call("sdh_rms_norm_heads", _p(x), groups, dim, _p(gamma), eps)

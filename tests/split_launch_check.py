@@ -127,6 +127,17 @@ def main():
             assert_elementwise(dq.download(), orc.rope(q, dim, cs, sn, inter), f"rope q N={N} S={S} {inter}")
             assert_elementwise(dk.download(), orc.rope(k, dim, cs, sn, inter), f"rope k N={N} S={S} {inter}")
 
+    step("rope_qk_axes")
+    for N, S in ((2, 40), (50, 8)):  # parts of one sequence (positions offset), and whole sequences per launch
+        pos = np.array([[i % 7, (3 * i) % 11, i] for i in range(S)], np.int32)
+        cs, sn = orc.rope_tables_3axis(pos, [4, 6, 6], 16, 256.0)
+        q = orc.randn((N, S, 3 * 16), 20)
+        k = orc.randn((N, S, 2 * 16), 21)
+        dq, dk = be.array(q), be.array(k)
+        be.rope_qk_axes(dq, 3 * 16, dk, 2 * 16, N, S, 16, be.array(pos.view(np.float32)), (4, 6, 6), 256.0)
+        assert_elementwise(dq.download(), orc.rope(q, 16, cs, sn, True), f"rope_qk_axes q N={N} S={S}")
+        assert_elementwise(dk.download(), orc.rope(k, 16, cs, sn, True), f"rope_qk_axes k N={N} S={S}")
+
     step("group_norm")
     shape, groups = (5, 64, 8, 8), 32
     x = orc.randn(shape, 17, 0.5, 2.0)

@@ -355,6 +355,64 @@ def test_rope_qk_config_3(be, orc):
     assert_elementwise(dk.download(), orc.rope(k, 128, cs, sn, True), "rope_qk k")
 
 
+def _pos_array(be, pos):
+    """int32 positions [S, 3] on the device (uploaded as their raw bytes)."""
+    return be.array(np.ascontiguousarray(pos, np.int32).view(np.float32))
+
+
+def test_rope_qk_axes_config_3(be, orc):
+    """Config 3 with the angles formed on the device (sdh_rope_qk_axes):
+    positions (0, h, w) of the 64 x 64 grid, axes (32, 48, 48), theta 256,
+    against the oracle's rope_ with its tables (the restatement of
+    zimage.cpp:71-88) at max-abs 1e-5, and against the table kernel fed
+    those tables."""
+    pos = np.array([[0, h, w] for h in range(64) for w in range(64)], np.int32)
+    cs, sn = orc.rope_tables_3axis(pos, [32, 48, 48], 128, 256.0)
+    q = orc.randn((1, T, 30 * 128), _seed("q3a"))
+    k = orc.randn((1, T, 30 * 128), _seed("k3a"))
+    dq, dk = be.array(q), be.array(k)
+    be.rope_qk_axes(dq, 30 * 128, dk, 30 * 128, 1, T, 128, _pos_array(be, pos), (32, 48, 48), 256.0)
+    gq, gk = dq.download(), dk.download()
+    assert_elementwise(gq, orc.rope(q, 128, cs, sn, True), "rope_qk_axes q")
+    assert_elementwise(gk, orc.rope(k, 128, cs, sn, True), "rope_qk_axes k")
+    tq, tk = be.array(q), be.array(k)
+    be.rope_qk(tq, 30 * 128, tk, 30 * 128, 1, T, 128, be.array(cs), be.array(sn), True)
+    d = max(float(np.max(np.abs(gq - tq.download()))), float(np.max(np.abs(gk - tk.download()))))
+    print("device angles vs tables: max |diff|", d)
+    assert d <= 1e-6
+
+
+@pytest.mark.parametrize("N,S,hq,hk,dim,axes,theta", [
+    (2, 37, 3, 1, 64, (16, 24, 24), 256.0),     # odd length, unequal head counts
+    (1, 160, 30, 30, 128, (32, 48, 48), 256.0),  # Z-Image text rows: positions (1 + i, 0, 0)
+    (1, 9, 2, 2, 8, (4, 0, 4), 10000.0),         # an empty axis
+    (3, 5, 64, 64, 128, (32, 48, 48), 256.0),    # 8192-float rows (eight float4 per thread)
+])
+def test_rope_qk_axes_shapes(be, orc, N, S, hq, hk, dim, axes, theta):
+    rng = np.random.default_rng(S + dim)
+    pos = rng.integers(0, 200, size=(S, 3)).astype(np.int32)
+    if S == 160:
+        pos = np.array([[1 + i, 0, 0] for i in range(S)], np.int32)
+    cs, sn = orc.rope_tables_3axis(pos, list(axes), dim, theta)
+    q = orc.randn((N, S, hq * dim), _seed("qax", S, dim))
+    k = orc.randn((N, S, hk * dim), _seed("kax", S, dim))
+    dq, dk = be.array(q), be.array(k)
+    be.rope_qk_axes(dq, hq * dim, dk, hk * dim, N, S, dim, _pos_array(be, pos), axes, theta)
+    assert_elementwise(dq.download(), orc.rope(q, dim, cs, sn, True), f"rope_qk_axes q {N}x{S} {axes}")
+    assert_elementwise(dk.download(), orc.rope(k, dim, cs, sn, True), f"rope_qk_axes k {N}x{S} {axes}")
+
+
+def test_rope_qk_axes_rejects(be):
+    q, k = be.empty((1, 4, 128)), be.empty((1, 4, 128))
+    pos = _pos_array(be, np.zeros((4, 3), np.int32))
+    for args, msg in [(((32, 48, 40), 256.0), "add up to dim"), (((33, 47, 48), 256.0), "even"),
+                      (((32, 48, 48), 0.0), "theta")]:
+        with pytest.raises(sdhip.SdhError, match=msg):
+            be.rope_qk_axes(q, 128, k, 128, 1, 4, 128, pos, *args)
+    with pytest.raises(sdhip.SdhError, match="distinct"):
+        be.rope_qk_axes(q, 128, q, 128, 1, 4, 128, pos, (32, 48, 48), 256.0)
+
+
 def test_rope_qk_gqa_half(be, orc):
     """rotate_half with fewer K heads (Qwen3-style tables, qwen3.cpp:46-53)."""
     S, dim = 37, 128
