@@ -877,7 +877,7 @@ KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
     "k_rope_il_reg": "rope_qk", "k_rope_il_axes": "rope_qk_axes", "k_ln_mod_gate": "ln_modulate_gate", "k_softmax_block": "softmax_rows",
     "k_upsample2x_vec": "upsample_nearest2x", "k_concat_vec": "concat_channels", "k_patchify": "patchify2d",
     "k_qknorm_rope_il": "qknorm_rope", "k_attn_fwd": "attention", "k_rms_mod_bf16": "rms_norm_modulate_bf16",
-    "k_rms_gated_add": "rms_norm_gated_add",
+    "k_rms_gated_add": "rms_norm_gated_add", "copyBuffer": "blit_calibration",
 }
 
 
@@ -936,6 +936,8 @@ def gn_dispatches(shape, groups=32, cus=256):
 
 
 def _kernel_key(full_name):
+    if "copyBuffer" in full_name:  # the HIP runtime's device-to-device copy kernel
+        return "copyBuffer"
     if full_name.startswith("Cijk_"):  # a hipBLASLt GEMM kernel: the library and its macro tile
         t = re.search(r"_MT(\d+x\d+x\d+)_", full_name)
         return "hipBLASLt Cijk MT" + (t.group(1) if t else "?")
@@ -943,18 +945,26 @@ def _kernel_key(full_name):
     return (m.group(1) + (m.group(2) or "")) if m else full_name
 
 
-def rocprof_summary(trace_dir, fetch_dir=None, write_dir=None):
+def rocprof_summary(trace_dir, read_dir=None, write_dir=None):
     """Markdown summary of a `rocprofv3 --kernel-trace --stats --output-format
-    csv` run of this script (and, optionally, of its --pmc FETCH_SIZE and
-    WRITE_SIZE runs). Traffic is calibrated against the in-place copy kernel
-    (copy_calibration: known 1 read + 1 write of [4096,10240] fp32)."""
+    csv` run of this script and, optionally, of its two counter runs:
+      read_dir:  --pmc TCC_EA0_RDREQ_sum TCC_EA0_RDREQ_128B_sum
+                       TCC_EA0_RDREQ_64B_sum TCC_EA0_RDREQ_32B_sum
+      write_dir: --pmc TCC_EA0_WRREQ_sum TCC_EA0_WRREQ_64B_sum
+    HBM bytes per dispatch come from the L2-to-memory requests by size:
+    read = 128 n128 + 64 n64 + 32 n32, write = 64 n64 + 32 (n - n64). No
+    calibration factor: the derived FETCH_SIZE of this ROCm counts a 128-byte
+    request as 64 bytes (its expression takes 128-byte requests from
+    TCC_BUBBLE), which a factor of 2 used to correct. The two copy kernels
+    (non-temporal and the runtime's ordinary-load copy) check the method
+    against their known traffic."""
     import collections
     import csv
     import glob
 
     def rows_of(d, suffix):
-        files = glob.glob(os.path.join(d, "*" + suffix))
-        return list(csv.DictReader(open(files[0]))) if files else []
+        files = glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True)
+        return [r for f in files for r in csv.DictReader(open(f))]
 
     trace = rows_of(trace_dir, "_kernel_trace.csv")
     dur = collections.defaultdict(list)
@@ -969,41 +979,55 @@ def rocprof_summary(trace_dir, fetch_dir=None, write_dir=None):
         out.append(f"| `{k}` | {g} | {len(v)} | {statistics.mean(v):.2f} | {v[len(v) // 2]:.2f} | {v[0]:.2f} |")
     text = "\n".join(out) + "\n"
     traffic_lines = []
-    if fetch_dir and write_dir:
+    if read_dir and write_dir:
         def counters(d):
-            agg = collections.defaultdict(list)
+            per = collections.defaultdict(lambda: collections.defaultdict(float))
             for r in rows_of(d, "_counter_collection.csv"):
-                k = (_kernel_key(r["Kernel_Name"]), int(r["Grid_Size"]))
-                agg[k].append(float(r["Counter_Value"]))
-            return {k: statistics.median(v) for k, v in agg.items()}
+                key = (_kernel_key(r["Kernel_Name"]), int(r["Grid_Size"]), r.get("Dispatch_Id", r.get("Correlation_Id")))
+                per[key][r["Counter_Name"]] += float(r["Counter_Value"])
+            agg = collections.defaultdict(list)
+            for (kn, g, _), c in per.items():
+                agg[(kn, g)].append(c)
+            return agg
 
-        f, w = counters(fetch_dir), counters(write_dir)
-        cal = [k for k in f if k[0] == "k_unary<4>" and k[1] == T * F // 4]
-        copy_kib = T * F * 4 / 1024.0
-        ff = copy_kib / f[cal[0]] if cal else 1.0
-        wf = copy_kib / w[cal[0]] if cal else 1.0
-        text += (f"\nCalibration (in-place copy, {copy_kib:.0f} KiB read + {copy_kib:.0f} KiB written): "
-                 f"FETCH_SIZE factor {ff:.3f}, WRITE_SIZE factor {wf:.3f}.\n\n")
-        text += "| kernel | grid | FETCH_SIZE KiB | WRITE_SIZE KiB | calibrated HBM bytes per dispatch |\n|---|---|---|---|---|\n"
-        for k in sorted(f, key=lambda k: -f[k]):
+        rd, wr = counters(read_dir), counters(write_dir)
+
+        def med(cs, name):
+            return statistics.median(c.get(name, 0.0) for c in cs)
+
+        def read_bytes(cs):
+            n128, n64, n32 = med(cs, "TCC_EA0_RDREQ_128B_sum"), med(cs, "TCC_EA0_RDREQ_64B_sum"), med(cs, "TCC_EA0_RDREQ_32B_sum")
+            return 128 * n128 + 64 * n64 + 32 * n32, med(cs, "TCC_EA0_RDREQ_sum") - (n128 + n64 + n32)
+
+        def write_bytes(cs):
+            n, n64 = med(cs, "TCC_EA0_WRREQ_sum"), med(cs, "TCC_EA0_WRREQ_64B_sum")
+            return 64 * n64 + 32 * (n - n64)
+
+        text += ("\nHBM traffic per dispatch from the L2/EA request counters by size (read = 128 n128 + 64 n64 + "
+                 "32 n32; write = 64 n64 + 32 n32); no calibration factor.\n\n")
+        text += ("| kernel | grid | read bytes | write bytes | HBM bytes per dispatch | requests of no listed size |\n"
+                 "|---|---|---|---|---|---|\n")
+        for k in sorted(rd, key=lambda k: -read_bytes(rd[k])[0]):
             if k[0].startswith("k_fill_normal") or k[0].startswith("k_zero"):
                 continue
-            tb = int(round((f[k] * ff + w.get(k, 0.0) * wf) * 1024))
-            text += f"| `{k[0]}` | {k[1]} | {f[k]:.0f} | {w.get(k, 0.0):.0f} | {tb:,} |\n"
+            rb, other = read_bytes(rd[k])
+            wb = write_bytes(wr[k]) if k in wr else 0.0
+            tb = int(round(rb + wb))
+            text += f"| `{k[0]}` | {k[1]} | {rb:,.0f} | {wb:,.0f} | {tb:,} | {other:.0f} |\n"
             wl = next((v for kk, v in KERNEL_OF.items() if k[0].startswith(kk)), None)
             if wl:
-                traffic_lines.append(f"{wl} kernel={k[0]} grid={k[1]} fetch_kib={f[k]:.1f} write_kib={w.get(k, 0.0):.1f} "
-                                     f"fetch_factor={ff:.4f} write_factor={wf:.4f} traffic_bytes={tb}")
+                traffic_lines.append(f"{wl} kernel={k[0]} grid={k[1]} read_bytes={rb:.0f} write_bytes={wb:.0f} "
+                                     f"traffic_bytes={tb}")
         for wl in all_workloads():
             if not isinstance(wl, GNSiLU):
                 continue
-            ks = [k for pre, g in gn_dispatches(wl.shape) for k in f if k[0].startswith(pre) and k[1] == g]
+            ks = [k for pre, g in gn_dispatches(wl.shape) for k in rd if k[0].startswith(pre) and k[1] == g]
             if ks:
-                fk, wk = sum(f[k] for k in ks), sum(w.get(k, 0.0) for k in ks)
-                tb = int(round((fk * ff + wk * wf) * 1024))
+                rb = sum(read_bytes(rd[k])[0] for k in ks)
+                wb = sum(write_bytes(wr[k]) for k in ks if k in wr)
                 names = "+".join(k[0] for k in ks)
-                traffic_lines.append(f"{wl.name} kernel={names} grid={ks[0][1]} fetch_kib={fk:.1f} write_kib={wk:.1f} "
-                                     f"fetch_factor={ff:.4f} write_factor={wf:.4f} traffic_bytes={tb}")
+                traffic_lines.append(f"{wl.name} kernel={names} grid={ks[0][1]} read_bytes={rb:.0f} write_bytes={wb:.0f} "
+                                     f"traffic_bytes={int(round(rb + wb))}")
     return text, traffic_lines
 
 
@@ -1020,7 +1044,7 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--list", action="store_true")
     ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR",
-                    help="print a markdown summary of rocprofv3 csv output: TRACE_DIR [FETCH_DIR WRITE_DIR]")
+                    help="print a markdown summary of rocprofv3 csv output: TRACE_DIR [READ_DIR WRITE_DIR]")
     args = ap.parse_args()
 
     if args.rocprof_summary:

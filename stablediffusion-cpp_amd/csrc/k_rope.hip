@@ -297,10 +297,15 @@ struct RopeAxes {
     unsigned char axis[kMaxAxisPairs];
 };
 
-template <int RV>
+// WAVE: dim <= 128, so the token's dim/2 pairs fit one per lane: every wave
+// forms them itself (lane k, pair k) and fetches the two pairs of each of
+// its float4 by cross-lane reads, with no LDS and no workgroup barrier
+// (measured: the barrier behind one wave's 64 sin/cos cost 2 us at config 3).
+// Otherwise the pairs go through LDS.
+template <int RV, bool WAVE>
 __global__ __launch_bounds__(kThreads) void k_rope_il_axes(RopeArgs a, int64_t S, int dim, int64_t s0,
                                                           const int* __restrict__ pos, RopeAxes ax) {
-    __shared__ float cl[kMaxAxisPairs], sl[kMaxAxisPairs];
+    __shared__ float cl[WAVE ? 1 : kMaxAxisPairs], sl[WAVE ? 1 : kMaxAxisPairs];
     const int t = blockIdx.y;
     const int64_t ns = blockIdx.x;
     const int64_t inner = a.inner[t];
@@ -313,19 +318,41 @@ __global__ __launch_bounds__(kThreads) void k_rope_il_axes(RopeArgs a, int64_t S
         const int i = threadIdx.x + kThreads * j;
         if (i < n4) v[j] = dev::ld_stream(row + i);
     }
-    if ((int)threadIdx.x < (dim >> 1)) {
-        const int k = threadIdx.x;
-        const float ang = (float)((double)pos[(s0 + s) * 3 + ax.axis[k]] * ax.freq[k]);
-        cl[k] = cosf(ang);
-        sl[k] = sinf(ang);
+    const int* ps = pos + (s0 + s) * 3;
+    float cw = 1.0f, sw = 0.0f;
+    if constexpr (WAVE) {
+        const int k = threadIdx.x & 63;
+        if (k < (dim >> 1)) {
+            const float ang = (float)((double)ps[ax.axis[k]] * ax.freq[k]);
+            cw = cosf(ang);
+            sw = sinf(ang);
+        }
+    } else {
+        if ((int)threadIdx.x < (dim >> 1)) {
+            const int k = threadIdx.x;
+            const float ang = (float)((double)ps[ax.axis[k]] * ax.freq[k]);
+            cl[k] = cosf(ang);
+            sl[k] = sinf(ang);
+        }
+        __syncthreads();
     }
-    __syncthreads();
 #pragma unroll
     for (int j = 0; j < RV; ++j) {
         const int i = threadIdx.x + kThreads * j;
+        const int h = 2 * (i % d4);  // first of the float4's two pairs
+        float c0, s0v, c1, s1v;
+        if constexpr (WAVE) {
+            c0 = __shfl(cw, h, 64);
+            s0v = __shfl(sw, h, 64);
+            c1 = __shfl(cw, h + 1, 64);
+            s1v = __shfl(sw, h + 1, 64);
+        } else {
+            c0 = cl[h];
+            s0v = sl[h];
+            c1 = cl[h + 1];
+            s1v = sl[h + 1];
+        }
         if (i < n4) {
-            const int h = 2 * (i % d4);  // first of the float4's two pairs
-            const float c0 = cl[h], s0v = sl[h], c1 = cl[h + 1], s1v = sl[h + 1];
             f4 o;
             o.x = v[j].x * c0 - v[j].y * s0v;
             o.y = v[j].y * c0 + v[j].x * s0v;
@@ -360,9 +387,11 @@ void run_rope_axes(const char* op, float* q, int64_t inner_q, float* k, int64_t 
     a.inner[1] = inner_k;
     const dim3 grid((unsigned)(N * S), 2);
     const int64_t steps = (std::max(inner_q, inner_k) / 4 + kThreads - 1) / kThreads;
+    const bool wave = dim <= 128;
     auto go = [&](auto rc) {
         constexpr int RV = decltype(rc)::value;
-        k_rope_il_axes<RV><<<grid, kThreads, 0, stream()>>>(a, S, (int)dim, s0, pos, ax);
+        if (wave) k_rope_il_axes<RV, true><<<grid, kThreads, 0, stream()>>>(a, S, (int)dim, s0, pos, ax);
+        else k_rope_il_axes<RV, false><<<grid, kThreads, 0, stream()>>>(a, S, (int)dim, s0, pos, ax);
     };
     if (steps <= 1) go(std::integral_constant<int, 1>());
     else if (steps <= 2) go(std::integral_constant<int, 2>());

@@ -359,15 +359,16 @@ __global__ __launch_bounds__(kThreads) void k_ln_mod_gate_generic(const float* x
     for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows; row += stride) {
         const float* p = x + row * C;
         float* rp = res + row * C;
-        float s = 0.f;
-        for (int64_t i = lane; i < C; i += 64) s += p[i];
-        const float mean = (float)((double)dev::wave_sum(s) / (double)C);
-        float ss = 0.f;
+        // statistics summed in double, as layer_norm's (tensor.cpp:640-647)
+        double s = 0.0;
+        for (int64_t i = lane; i < C; i += 64) s += (double)p[i];
+        const float mean = (float)(dev::wave_sum_d(s) / (double)C);
+        double ss = 0.0;
         for (int64_t i = lane; i < C; i += 64) {
             const float d = p[i] - mean;
-            ss += d * d;
+            ss += (double)d * (double)d;
         }
-        const float rstd = rstd_of(dev::wave_sum(ss), C, eps);
+        const float rstd = rstd_of_d(dev::wave_sum_d(ss), C, eps);
         for (int64_t i = lane; i < C; i += 64) {
             float yv = __fmul_rn((p[i] - mean) * rstd, scale[i] * 1.0f + 1.0f);
             if (shift) yv = yv + shift[i];
