@@ -16,7 +16,8 @@
 // are exact and fold into per-lane constants: the score scale becomes
 // c = log2(e) / sqrt(d) * 2^(e_q + e_k) per query and tile; softmax weights
 // are formed as 2^(s c - m + 14 + e_v - E) (E = the largest e_v of the head,
-// so they stay below 2^14) against values scaled by 2^-e_v, which keeps every
+// m a running reference at most 1.5 below the row max, so they stay below
+// 2^15.5, inside fp16) against values scaled by 2^-e_v, which keeps every
 // tile's P V on the common scale 2^(14 - E); the sum of the weights is
 // carried as 2^14 sum(p), and the output is divided by it (and scaled by 2^E)
 // once at the end. The softmax is the online form (running row max m and
@@ -30,7 +31,7 @@
 // with the head dimension zero-padded to DP (64 or 128) and keys past Skv
 // zero. Rows sit in the order the MFMA fragment reads want them in LDS (16-B
 // chunk c of row r at c ^ swz(r)), so the attention kernel copies a tile from
-// global memory to LDS as one contiguous block (global_load_lds_dwordx4).
+// global memory to LDS as one contiguous block (buffer_load_dwordx4 ... lds).
 // The kernel computes S^T = K Q^T (v_mfma_f32_32x32x16_f16: K tile as the A
 // operand, rows = keys; Q in registers as the B operand, columns = queries),
 // so lane l holds scores of query l%32 only: the softmax statistics are
@@ -42,8 +43,9 @@
 // 8a + 4h + b), so the A operand of O^T is again one 16-B LDS read per lane.
 // Workgroup: 8 waves x 32 queries of one head, in two groups that run half
 // a tile apart (see k_attn_fwd); K and V tiles double-buffered in LDS; the
-// softmax rescale of O is skipped when no row max of the wave changed
-// (exactly alpha = 1).
+// running max a weight is taken against is raised only when a tile's max
+// passes it by 2^1.5 (weights stay below 2^15.5), so O is rescaled on few
+// tiles, and then by exactly the factor between the old and new reference.
 // Head dimensions above 128 take a plain fp32 kernel (one wave per query).
 // Both kernels can store the output rounded to bf16 (sdh_attention_bf16):
 // the operand rounding of the projection that follows (to_out), applied to
@@ -69,6 +71,17 @@ constexpr int kWaves = 8, kThreads = 64 * kWaves;
 constexpr int kBM = 32 * kWaves;            // queries per workgroup
 constexpr float kLog2e = 1.44269504088896341f;
 constexpr float kNoMax = -1e30f;            // running max before any key: finite, so 2^(m - m') never sees inf - inf
+// The running reference m is raised only when a tile's max passes it by
+// kLazy or more: weights then stay below 2^(14 + kLazy) (fp16 holds < 2^16),
+// and O is rescaled only on those tiles.
+constexpr float kLazy = 1.5f;
+// LDS fragment reads of the MFMA loops run kPipe - 1 steps ahead
+constexpr int kPipe = 2;
+// s_waitcnt immediate (gfx9 encoding) that waits on vmcnt only: expcnt and
+// lgkmcnt at their maxima; OR in a vmcnt below 16.
+constexpr int kWaitVmBase = 0x0F70;
+// Word 3 of a raw buffer resource (gfx9: 32-bit data format, no swizzle)
+constexpr int kBufferWord3 = 0x00020000;
 
 // 16-B chunk c of row r of a K tile (rows of DP fp16) sits at c ^ swz_k(r):
 // for 256-B rows (DP = 128) 16 consecutive rows map one logical chunk to 16
@@ -85,6 +98,15 @@ __device__ __host__ __forceinline__ int key_at(int p) { return (p & ~12) | ((p &
 __device__ __forceinline__ void split(float x, _Float16& hi, _Float16& lo) {
     hi = (_Float16)x;
     lo = (_Float16)(x - (float)hi);
+}
+// Softmax weight p in [0, 2^16) into hi + lo: hi keeps p's leading 11 bits
+// (truncated: exact in fp16 for p >= 2^-14), lo = p - hi exactly in fp32,
+// then rounded to fp16 (|lo| < 2^-10 p, so the pair is within 2^-21 p; below
+// 2^-14, where fp16 is subnormal, within 2^-24 absolutely).
+__device__ __forceinline__ void split_weight(float p, _Float16& hi, _Float16& lo) {
+    const float h = __uint_as_float(__float_as_uint(p) & 0xFFFFE000u);
+    hi = (_Float16)h;
+    lo = (_Float16)(p - h);
 }
 
 // Exponent e of a block whose largest magnitude is amax: amax 2^-e lies in
@@ -204,15 +226,14 @@ __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, 
 // ---------------------------------------------------------------------------
 // Fused attention, head dimension padded to DP (64 or 128).
 // 1-D grid of ceil(Sq / 256) * heads * N workgroups; 512 threads = 8 waves of 32 queries.
-// Waves 0-3 (X) and 4-7 (Y) run half a tile apart (waves w and w + 4 share a
-// SIMD): per iteration t, between two barriers,
-//   segment 1:  X: S^T(t) = K(t) Q^T          Y: softmax(t-1), O += V(t-1) P
-//   segment 2:  X: softmax(t), O += V(t) P    Y: S^T(t)
-// so one wave's MFMAs run while the other wave of its SIMD is in its softmax
-// (a single barrier per tile keeps both in the same phase: 760 -> 722 us on
-// the Z-Image layer). K and V have separate double buffers: K(t+1) is loaded
-// after barrier 1 of t (K(t-1)'s last reader, Y's S^T(t-1), is done), V(t+1)
-// after barrier 2 of t (V(t-1)'s last reader, Y's O(t-1), is done).
+// Each wave alternates an MFMA phase (O += V(t-1) P(t-1), then S^T(t) =
+// K(t) Q^T: 96 MFMAs) with a VALU phase (softmax(t)); waves 0-3 (X) and 4-7
+// (Y) run half an iteration apart (waves w and w + 4 share a SIMD), so one
+// wave's MFMAs run while the other computes its softmax. One barrier per
+// iteration; K and V have separate double buffers (see the loop). Measured on
+// the [1,4096,30x128] layer: 7680 cycles per 64-key tile against the 6144 of
+// the MFMA work alone (the earlier two-barrier schedule, softmax and O += V P
+// in one segment against S^T in the other, took 8960).
 // ---------------------------------------------------------------------------
 template <int DP, bool CAUSAL, bool OUT16>
 __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restrict__ Q, const u16* __restrict__ tiles,
@@ -223,8 +244,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
     constexpr int DT = DP / 32;                    // 32-row head-dim tiles of O^T
     constexpr int TILE = 4 * kKT * DP, HALF = TILE / 2;  // fp16 values per packed tile, per K or V part
     constexpr int NLD = HALF * 2 / 16 / kThreads;  // 16-B loads per thread per part
-    __shared__ __attribute__((aligned(1024))) u16 kbuf[2][HALF];
-    __shared__ __attribute__((aligned(1024))) u16 vbuf[2][HALF];
+    // Four separate LDS objects, each named statically where it is read or
+    // filled (the loop below is unrolled by two): the compiler then knows
+    // which LDS-DMA writes a read can alias, and does not make the read of
+    // one buffer wait for the copy into the other.
+    __shared__ __attribute__((aligned(1024))) u16 kbuf0[HALF];
+    __shared__ __attribute__((aligned(1024))) u16 kbuf1[HALF];
+    __shared__ __attribute__((aligned(1024))) u16 vbuf0[HALF];
+    __shared__ __attribute__((aligned(1024))) u16 vbuf1[HALF];
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const bool isY = w >= kWaves / 2;
@@ -242,17 +269,23 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
     const int T = CAUSAL ? min(ntiles, (qend - 1) / kKT + 1) : ntiles;
     const u16* src = tiles + ((int64_t)nb * kv_heads + kh) * ntiles * TILE;
     const int2* ex = exps + ((int64_t)nb * kv_heads + kh) * ntiles;
-    auto issue = [&](int t, int part, u16* dst) {
-        const u16* g = src + (int64_t)t * TILE + part * HALF;
+    // The head's tiles as one buffer (the host checks that they span less
+    // than 2^31 bytes). Tiles are copied to LDS with buffer loads, not
+    // global_load_lds: the compiler counts a FLAT-encoded copy into LDS as
+    // pending on both the vector-memory and the LDS counters, and then waits
+    // for every LDS read in full (lgkmcnt(0)) until the copy has landed.
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, ntiles * TILE * 2, kBufferWord3);
+    auto issue = [&](int t, int part, u16* dst) __attribute__((always_inline)) {
+        const int off = (t * TILE + part * HALF) * 2;  // bytes
 #pragma unroll
         for (int j = 0; j < NLD; ++j) {
-            const int chunk = (j * kWaves + w) * 64;
-            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(g + (chunk + lane) * 8),
-                                             (__attribute__((address_space(3))) void*)(dst + chunk * 8), 16, 0, 0);
+            const int chunk = (j * kWaves + __builtin_amdgcn_readfirstlane(w)) * 64;  // wave-uniform
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(dst + chunk * 8),
+                                                     16, lane * 16, off + chunk * 16, 0, 0);
         }
     };
-    issue(0, 0, kbuf[0]);
-    issue(0, 1, vbuf[0]);
+    issue(0, 0, kbuf0);
 
     // Q fragments (B operand of S^T): query qlane, head dims ds*16 + fh*8 .. +7,
     // scaled by 2^-eq for the query's largest magnitude (lanes l and l^32 hold its two halves)
@@ -303,30 +336,46 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
     float m = kNoMax, lsum = 0.f;
-    f32x16 s[2];  // S^T of the tile in flight (kept across a barrier by Y)
+    f32x16 s[2];      // S^T of the newest tile
+    h8 ph[4], pl[4];  // its softmax weights, split (B operands of O^T += V^T P^T, one per 16-key step)
 
-    auto scores = [&](const u16* Kh) {
+    auto scores = [&](const u16* Kh) __attribute__((always_inline)) {
         const u16* Kl = Kh + kKT * DP;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int i = 0; i < 16; ++i) s[j][i] = 0.f;
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
+        // DS steps; step ds reads the hi/lo K fragments of both 32-key halves
+        // j, kPipe - 1 steps ahead of its MFMAs, and interleaves the two
+        // accumulator chains (each MFMA's predecessor is two issues back)
+        h8 kf[kPipe][2][2];  // [slot][j][hi, lo]
+        auto fetch = [&](int ds) __attribute__((always_inline)) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int r = j * 32 + fr;
                 const int off = r * DP + (((ds * 2 + fh) ^ swz_k<DP>(r)) << 3);
-                const h8 kh8 = *(const h8*)(Kh + off);
-                const h8 kl8 = *(const h8*)(Kl + off);
-                s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh8, qh[ds], s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh8, ql[ds], s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl8, qh[ds], s[j], 0, 0, 0);
+                kf[ds % kPipe][j][0] = *(const h8*)(Kh + off);
+                kf[ds % kPipe][j][1] = *(const h8*)(Kl + off);
             }
+        };
+#pragma unroll
+        for (int i = 0; i < kPipe - 1; ++i) fetch(i);
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            if (ds + kPipe - 1 < DS) fetch(ds + kPipe - 1);
+            __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+            const int sl = ds % kPipe;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[sl][j][0], qh[ds], s[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[sl][j][0], ql[ds], s[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[sl][j][1], qh[ds], s[j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
-    auto softmax_pv = [&](int t, const u16* Vh) {
-        const u16* Vl = Vh + DP * kKT;
+    // softmax of tile t: s -> weights (ph, pl); running max and sum; O rescaled
+    auto softmax = [&](int t) __attribute__((always_inline)) {
         const int k0 = t * kKT;
         const int2 et = ex[t];
         // mask: keys past Skv, and (causal) keys after the query
@@ -347,10 +396,11 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
 #pragma unroll
             for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[j][i]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mnew = fmaxf(m, mx * ct);
-        const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+        const float mt = mx * ct;
+        const float mnew = mt > m + kLazy ? mt : m;
+        const float alpha = __builtin_amdgcn_exp2f(m - mnew);  // exactly 1 when m is kept
         m = mnew;
-        // weights 2^(s ct - m) times 2^(14 + e_v - E), <= 2^14
+        // weights 2^(s ct - m) times 2^(14 + e_v - E), < 2^(14 + kLazy)
         const float shift = (float)(14 + et.y - E) - mnew;
         float rs = 0.f;
 #pragma unroll
@@ -368,53 +418,99 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
 #pragma unroll
                 for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
         }
-        // O^T += V^T P^T over four 16-key steps
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            h8 ph, pl;
+        for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 _Float16 hi, lo;
-                split(s[ks >> 1][(ks & 1) * 8 + e], hi, lo);
-                ph[e] = hi;
-                pl[e] = lo;
+                split_weight(s[ks >> 1][(ks & 1) * 8 + e], hi, lo);
+                ph[ks][e] = hi;
+                pl[ks][e] = lo;
             }
+    };
+    // O^T += V^T P^T in 2 DT steps of (16-key step ks, pair of 32-row tiles
+    // dt, dt + 1): step i reads the pair's hi/lo V fragments kPipe - 1 steps
+    // ahead of its MFMAs, and interleaves the two accumulator chains
+    auto pv = [&](const u16* Vh) __attribute__((always_inline)) {
+        const u16* Vl = Vh + DP * kKT;
+        constexpr int NS = 2 * DT;
+        h8 vf[kPipe][2][2];  // [slot][dt of the pair][hi, lo]
+        auto fetch = [&](int i) __attribute__((always_inline)) {
+            const int ks = i / (DT / 2), d0 = (i % (DT / 2)) * 2;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const int r = dt * 32 + fr;
+            for (int u = 0; u < 2; ++u) {
+                const int r = (d0 + u) * 32 + fr;
                 const int off = r * kKT + (((ks * 2 + fh) ^ swz_v(r)) << 3);
-                const h8 vh8 = *(const h8*)(Vh + off);
-                const h8 vl8 = *(const h8*)(Vl + off);
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh8, ph, o[dt], 0, 0, 0);
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh8, pl, o[dt], 0, 0, 0);
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl8, ph, o[dt], 0, 0, 0);
+                vf[i % kPipe][u][0] = *(const h8*)(Vh + off);
+                vf[i % kPipe][u][1] = *(const h8*)(Vl + off);
             }
+        };
+#pragma unroll
+        for (int i = 0; i < kPipe - 1; ++i) fetch(i);
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            if (i + kPipe - 1 < NS) fetch(i + kPipe - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            const int ks = i / (DT / 2), d0 = (i % (DT / 2)) * 2, sl = i % kPipe;
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+                o[d0 + u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[sl][u][0], ph[ks], o[d0 + u], 0, 0, 0);
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+                o[d0 + u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[sl][u][0], pl[ks], o[d0 + u], 0, 0, 0);
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+                o[d0 + u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[sl][u][1], ph[ks], o[d0 + u], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
     // a wave with no real query, or (causal) whose queries all precede tile t, skips it
     const bool active = qw0 < Sq;
     auto wants = [&](int t) { return active && !(CAUSAL && qw0 + 31 < t * kKT); };
 
-    for (int t = 0; t <= T; ++t) {
-        // barrier 1: K(t) has landed; no wave reads K(t-1) any more
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (t + 1 < T) issue(t + 1, 0, kbuf[(t + 1) & 1]);
+    // Iteration t, one barrier: K(t) and V(t-1) have landed, and no wave
+    // reads K(t-1) or V(t-2) any more, whose buffers then take K(t+1) and
+    // V(t). Each wave alternates an MFMA phase, O += V(t-1) P(t-1) then
+    // S(t) = K(t) Q^T, with a VALU phase, softmax(t); the two waves of a SIMD
+    // (w and w + 4) run half an iteration apart:
+    //   X (waves 0-3):  [O += V P(t-1); S(t)]   softmax(t)
+    //   Y (waves 4-7):  softmax(t-1)            [O += V P(t-1); S(t)]
+    // so one wave's MFMAs run while the other computes its softmax.
+    // Every part is copied unconditionally (past the last tile, a second copy
+    // of tile T-1 into the free buffer): with no branch around the copies
+    // the compiler tracks which buffer each one writes, and an LDS read waits
+    // only for copies into its own buffer. The barrier is a bare s_barrier (a
+    // compiler memory barrier too); the copies of an iteration have a whole
+    // iteration to land.
+    auto land = [&]() __attribute__((always_inline)) {
+        __builtin_amdgcn_s_waitcnt(kWaitVmBase);
+        asm volatile("s_barrier" ::: "memory");
+    };
+    // kc: K(t); vp: V(t-1); kn: K(t-1), to take K(t+1); vn: V(t-2), to take V(t)
+    auto iteration = [&](int t, const u16* kc, const u16* vp, u16* kn, u16* vn) __attribute__((always_inline)) {
+        land();
+        issue(min(t + 1, T - 1), 0, kn);
+        issue(min(t, T - 1), 1, vn);
         if (!isY) {
-            if (t < T && wants(t)) scores(kbuf[t & 1]);
+            if (t >= 1 && wants(t - 1)) pv(vp);
+            if (t < T && wants(t)) {
+                scores(kc);
+                softmax(t);
+            }
         } else {
-            if (t >= 1 && wants(t - 1)) softmax_pv(t - 1, vbuf[(t - 1) & 1]);
+            if (t >= 1 && wants(t - 1)) {
+                softmax(t - 1);
+                pv(vp);
+            }
+            if (t < T && wants(t)) scores(kc);
         }
-        // barrier 2: V(t) has landed; no wave reads V(t-1) any more
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (t + 1 < T) issue(t + 1, 1, vbuf[(t + 1) & 1]);
-        if (!isY) {
-            if (t < T && wants(t)) softmax_pv(t, vbuf[t & 1]);
-        } else {
-            if (t < T && wants(t)) scores(kbuf[t & 1]);
-        }
+    };
+    for (int t = 0; t <= T; t += 2) {
+        iteration(t, kbuf0, vbuf1, kbuf1, vbuf0);
+        if (t + 1 <= T) iteration(t + 1, kbuf1, vbuf0, kbuf0, vbuf1);
     }
+    // the surplus copies must land before the workgroup's LDS is released
+    __builtin_amdgcn_s_waitcnt(kWaitVmBase);
     if (qlane >= Sq) return;
     lsum += __shfl_xor(lsum, 32, 64);
     // the reference scales P by 1/sum (tensor.cpp:761-764); O^T carries 2^(14-E) sum(p v), lsum 2^14 sum(p)
@@ -534,6 +630,7 @@ void run_mfma(const float* q, const float* k, const float* v, void* out, int64_t
     int2* exps = (int2*)(base + (size_t)ntot * tile_bytes);
     const int64_t inner = heads * d, kv_inner = (int64_t)kv_heads * d;
     need(ntiles * 256 <= kMaxGridItems, "sdh_attention", "too many keys for one launch");
+    need(ntiles * (int64_t)tile_bytes < (int64_t(1) << 31), "sdh_attention", "too many keys per head for one launch");
     const dim3 pgrid((unsigned)ntiles, (unsigned)kv_heads, (unsigned)N);
     if (d == DP && kv_inner % 4 == 0 && aligned16(k) && aligned16(v))
         k_attn_pack<DP, true><<<pgrid, 256, 0, stream()>>>(k, v, tiles, exps, (int)Skv, (int)kv_inner, (int)d,
