@@ -604,14 +604,40 @@ class Attention(Workload):
         hq, hk, hv = (R.new(shp, self._head(h, n, 0)) for n in ("q", "k", "v"))
         return (lambda: [R._ptr(R.lib.ref_attention(hq, hk, hv, 1, 0, 1))]), [hq, hk, hv], None
 
+    _ref_cache = {}  # the attention lines share their inputs (same seeds): one reference run
+
     def reference_results(self, R, h):
+        key = tuple(sorted(self.seeds().items()))
+        if key in Attention._ref_cache:
+            return Attention._ref_cache[key]
         o = np.empty((T, 30, 128), np.float32)
         for i in range(30):
             hs = [R.new((1, T, 128), self._head(h, n, i)) for n in ("q", "k", "v")]
             ho = R._ptr(R.lib.ref_attention(*hs, 1, 0, 1))
             o[:, i, :] = _peek(R, ho, (T, 128))
             R.free(ho, *hs)
-        return {"o": o.reshape(1, T, 30 * 128)}
+        Attention._ref_cache[key] = {"o": o.reshape(1, T, 30 * 128)}
+        return Attention._ref_cache[key]
+
+
+class AttentionFp16(Attention):
+    """The opt-in reduced-precision attention (sdh_attention_fp16, no
+    counterpart in the reference) on the same layer and inputs: every product
+    formed once from block-scaled fp16 operands (one MFMA per product, half the
+    packed bytes). Parity against the reference's fp32 attention at abs 1e-2,
+    the error fp16 operands give on unit-variance inputs (the kernel's own
+    rounding bound is checked against a rounded-operand oracle in
+    tests/test_gpu_attention_fp16.py). Not timed on the CPU: the reference has
+    no such mode."""
+
+    name = "attention_fp16"
+    mfma_mult = 1
+    cpu_time = False
+    desc = "opt-in fp16-operand attention (no reference counterpart), q k v [1,4096,30x128], same inputs as attention"
+    results = {"o": ("abs", 1e-2)}
+
+    def step(self, be, s):
+        be.attention_fp16(s["q"], s["k"], s["v"], s["o"], 1, self.S, self.S, self.H, self.H, self.d, False)
 
 
 class ZImageStep(Workload):
@@ -649,6 +675,29 @@ class ZImageStep(Workload):
 
         m = sdhip.ZImage.random(dim=self.D, heads=self.heads, ffn=self.F, layers=self.layers, seed=7)
         try:
+            ms = m.time(self.H, self.W, self.L, self.cap_dim, steps, warmup)
+            params = m.params()
+        finally:
+            m.close()
+        return dict(event_ms=ms, wall_ms=ms, nsets=1, footprint=0, params=params)
+
+
+class ZImageStepFp16Attention(ZImageStep):
+    """The same step with the opt-in fp16-operand attention
+    (ZImageTransformer::set_fp16_attention, no counterpart in the reference);
+    its forward stays within the DiT's 2e-2 of the reference's CPU forward
+    (tests/test_gpu_attention_fp16.py, measured 2.4e-3 with BF16 weights, as
+    with the default attention)."""
+
+    name = "zimage_step_1024_fp16_attention"
+    desc = "Z-Image DiT step at 1024x1024 as zimage_step_1024, attention from fp16 operands (opt-in)"
+
+    def measure(self, steps, warmup):
+        import sdhip
+
+        m = sdhip.ZImage.random(dim=self.D, heads=self.heads, ffn=self.F, layers=self.layers, seed=7)
+        try:
+            m.set_fp16_attention(True)
             ms = m.time(self.H, self.W, self.L, self.cap_dim, steps, warmup)
             params = m.params()
         finally:
@@ -717,7 +766,7 @@ def all_workloads():
         RmsModBf16(),
         RmsGatedAdd(),
     ] + [Layout(n) for n in Layout.SPECS] + [Linear(k) for k in ("linear_bf16", "linear_swiglu", "linear_swiglu_unfused")] + [
-        Attention(), ZImageStep()]
+        Attention(), AttentionFp16(), ZImageStep(), ZImageStepFp16Attention()]
 
 
 # ------------------------------------------------------------------ GPU timing
@@ -876,7 +925,8 @@ KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
     "k_unary<4>": "copy_calibration", "k_add_rms": "add_rms_norm", "k_swiglu": "swiglu",
     "k_rope_il_reg": "rope_qk", "k_rope_il_axes": "rope_qk_axes", "k_ln_mod_gate": "ln_modulate_gate", "k_softmax_block": "softmax_rows",
     "k_upsample2x_vec": "upsample_nearest2x", "k_concat_vec": "concat_channels", "k_patchify": "patchify2d",
-    "k_qknorm_rope_il": "qknorm_rope", "k_attn_fwd": "attention", "k_rms_mod_bf16": "rms_norm_modulate_bf16",
+    "k_qknorm_rope_il": "qknorm_rope", "k_attn_fwd<128, false, false, true>": "attention",
+    "k_attn_fwd<128, false, false, false>": "attention_fp16", "k_rms_mod_bf16": "rms_norm_modulate_bf16",
     "k_rms_gated_add": "rms_norm_gated_add", "copyBuffer": "blit_calibration",
 }
 

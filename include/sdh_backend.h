@@ -224,6 +224,18 @@ int sdh_attention(const float* q, const float* k, const float* v, float* out, in
  * that sequence. out [N, Sq, heads*d] uint16. */
 int sdh_attention_bf16(const float* q, const float* k, const float* v, uint16_t* out, int64_t N, int64_t Sq,
                        int64_t Skv, int heads, int kv_heads, int64_t d, int causal);
+/* OPT-IN REDUCED PRECISION, no counterpart in the reference: attention as
+ * sdh_attention (out float32) or sdh_attention_bf16 (out_bf16 != 0, out the
+ * uint16 bf16 bits), with every product formed once from fp16 operands: q
+ * per row, k and v per 64-key tile scaled by a power of two that brings the
+ * block's largest magnitude into [2^13, 2^14), then rounded to fp16 (11
+ * significant bits); the softmax weights rounded to fp16 likewise; fp32
+ * accumulation and softmax statistics. A third of sdh_attention's MFMA work
+ * and half its packed bytes; the error is that of fp16 operands (about 2^-12
+ * relative per element), for callers whose tolerance allows it (a diffusion
+ * step's 2e-2). Head dimensions above 128 run the fp32 kernel. */
+int sdh_attention_fp16(const float* q, const float* k, const float* v, void* out, int out_bf16, int64_t N,
+                       int64_t Sq, int64_t Skv, int heads, int kv_heads, int64_t d, int causal);
 
 /* ---- activations ----------------------------------------------------------- */
 /* backend_cuda.h:61 swiglu(); tensor.h:191. y = gate / (1 + exp(-gate)) * up. */

@@ -24,12 +24,19 @@
 // sum); masked scores (kv > q when causal, kv past the keys) contribute
 // exactly zero.
 //
+// sdh_attention_fp16 (opt-in, no counterpart in the reference) keeps the
+// block scaling but forms each product once, hi_a hi_b: every operand
+// rounded to 11 significant bits relative to its block's largest magnitude,
+// one MFMA per product, half the packed bytes. Its error is that of fp16
+// operands (about 2^-12 relative per element), not the reference's fp32.
+//
 // Layout. A pack kernel splits k and v of each key/value head into 64-key
 // tiles of library scratch, each one contiguous block:
 //   [K hi: 64 keys x DP][K lo][V^T hi: DP x 64 keys][V^T lo]   (fp16)
 // plus the tile's two exponents (e_k, e_v) in a side array,
 // with the head dimension zero-padded to DP (64 or 128) and keys past Skv
-// zero. Rows sit in the order the MFMA fragment reads want them in LDS (16-B
+// zero (the fp16 variant packs [K][V^T] only). Rows sit in the order the
+// MFMA fragment reads want them in LDS (16-B
 // chunk c of row r at c ^ swz(r)), so the attention kernel copies a tile from
 // global memory to LDS as one contiguous block (buffer_load_dwordx4 ... lds).
 // The kernel computes S^T = K Q^T (v_mfma_f32_32x32x16_f16: K tile as the A
@@ -124,7 +131,7 @@ __device__ __forceinline__ float pow2(int e) { return __uint_as_float((unsigned)
 // the exponents (e_k, e_v) of every tile. One workgroup per (tile, kv head,
 // batch); 256 threads. VEC: d == DP and 16-B aligned rows (float4 loads).
 // ---------------------------------------------------------------------------
-template <int DP, bool VEC>
+template <int DP, bool VEC, bool SPLIT>
 __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, const float* __restrict__ V,
                                                    u16* __restrict__ tiles, int2* __restrict__ exps, int Skv,
                                                    int kv_inner, int d, int ntiles, int kv_heads) {
@@ -138,7 +145,8 @@ __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, 
     const int64_t row0 = (int64_t)nb * Skv + (int64_t)t * kKT;
     const int64_t col0 = (int64_t)kh * d;
     const int64_t tile = ((int64_t)nb * kv_heads + kh) * ntiles + t;
-    u16* out = tiles + tile * 4 * (kKT * DP);
+    constexpr int PARTS = SPLIT ? 4 : 2;  // [K hi][K lo][V^T hi][V^T lo], or [K][V^T] rounded to fp16
+    u16* out = tiles + tile * PARTS * (kKT * DP);
     const int nrows = min(kKT, Skv - t * kKT);
     // K chunks into registers: slot i holds logical chunk (i % CPR) ^ swz of row i / CPR
     float kx[KCH][8];
@@ -204,10 +212,10 @@ __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, 
             lo[e] = b;
         }
         *(h8*)(out + r * DP + p * 8) = hi;
-        *(h8*)(out + kKT * DP + r * DP + p * 8) = lo;
+        if constexpr (SPLIT) *(h8*)(out + kKT * DP + r * DP + p * 8) = lo;
     }
     // V^T: row = head-dim index, 8 chunks of 8 key positions
-    u16* vt = out + 2 * kKT * DP;
+    u16* vt = out + (PARTS / 2) * kKT * DP;
     for (int i = threadIdx.x; i < DP * 8; i += 256) {
         const int r = i / 8, p = i % 8, c = p ^ swz_v(r);
         h8 hi, lo;
@@ -219,7 +227,7 @@ __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, 
             lo[e] = b;
         }
         *(h8*)(vt + r * kKT + p * 8) = hi;
-        *(h8*)(vt + DP * kKT + r * kKT + p * 8) = lo;
+        if constexpr (SPLIT) *(h8*)(vt + DP * kKT + r * kKT + p * 8) = lo;
     }
 }
 
@@ -235,14 +243,14 @@ __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, 
 // the MFMA work alone (the earlier two-barrier schedule, softmax and O += V P
 // in one segment against S^T in the other, took 8960).
 // ---------------------------------------------------------------------------
-template <int DP, bool CAUSAL, bool OUT16>
+template <int DP, bool CAUSAL, bool OUT16, bool SPLIT>
 __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restrict__ Q, const u16* __restrict__ tiles,
                                                           const int2* __restrict__ exps, void* __restrict__ O, int Sq,
                                                           int Skv, int inner, int d, int group, int kv_heads,
                                                           int ntiles, float c2, int qvec, int nqb, int heads) {
     constexpr int DS = DP / 16;                    // 16-wide head-dim steps of S^T = K Q^T
     constexpr int DT = DP / 32;                    // 32-row head-dim tiles of O^T
-    constexpr int TILE = 4 * kKT * DP, HALF = TILE / 2;  // fp16 values per packed tile, per K or V part
+    constexpr int TILE = (SPLIT ? 4 : 2) * kKT * DP, HALF = TILE / 2;  // fp16 values per packed tile, per K or V part
     constexpr int NLD = HALF * 2 / 16 / kThreads;  // 16-B loads per thread per part
     // Four separate LDS objects, each named statically where it is read or
     // filled (the loop below is unrolled by two): the compiler then knows
@@ -319,7 +327,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
                 _Float16 hi, lo;
                 split(x[ds][e] * sc, hi, lo);
                 qh[ds][e] = hi;
-                ql[ds][e] = lo;
+                ql[ds][e] = lo;  // unused without SPLIT
             }
     }
     // E: the largest value exponent among the tiles this workgroup reads
@@ -355,7 +363,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
                 const int r = j * 32 + fr;
                 const int off = r * DP + (((ds * 2 + fh) ^ swz_k<DP>(r)) << 3);
                 kf[ds % kPipe][j][0] = *(const h8*)(Kh + off);
-                kf[ds % kPipe][j][1] = *(const h8*)(Kl + off);
+                if constexpr (SPLIT) kf[ds % kPipe][j][1] = *(const h8*)(Kl + off);
             }
         };
 #pragma unroll
@@ -367,10 +375,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
             const int sl = ds % kPipe;
 #pragma unroll
             for (int j = 0; j < 2; ++j) s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[sl][j][0], qh[ds], s[j], 0, 0, 0);
+            if constexpr (SPLIT) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[sl][j][0], ql[ds], s[j], 0, 0, 0);
+                for (int j = 0; j < 2; ++j)
+                    s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[sl][j][0], ql[ds], s[j], 0, 0, 0);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[sl][j][1], qh[ds], s[j], 0, 0, 0);
+                for (int j = 0; j < 2; ++j)
+                    s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[sl][j][1], qh[ds], s[j], 0, 0, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -422,10 +434,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                _Float16 hi, lo;
-                split_weight(s[ks >> 1][(ks & 1) * 8 + e], hi, lo);
-                ph[ks][e] = hi;
-                pl[ks][e] = lo;
+                if constexpr (SPLIT) {
+                    _Float16 hi, lo;
+                    split_weight(s[ks >> 1][(ks & 1) * 8 + e], hi, lo);
+                    ph[ks][e] = hi;
+                    pl[ks][e] = lo;
+                } else {
+                    ph[ks][e] = (_Float16)s[ks >> 1][(ks & 1) * 8 + e];
+                }
             }
     };
     // O^T += V^T P^T in 2 DT steps of (16-key step ks, pair of 32-row tiles
@@ -442,7 +458,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
                 const int r = (d0 + u) * 32 + fr;
                 const int off = r * kKT + (((ks * 2 + fh) ^ swz_v(r)) << 3);
                 vf[i % kPipe][u][0] = *(const h8*)(Vh + off);
-                vf[i % kPipe][u][1] = *(const h8*)(Vl + off);
+                if constexpr (SPLIT) vf[i % kPipe][u][1] = *(const h8*)(Vl + off);
             }
         };
 #pragma unroll
@@ -455,12 +471,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const float* __restric
 #pragma unroll
             for (int u = 0; u < 2; ++u)
                 o[d0 + u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[sl][u][0], ph[ks], o[d0 + u], 0, 0, 0);
+            if constexpr (SPLIT) {
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
-                o[d0 + u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[sl][u][0], pl[ks], o[d0 + u], 0, 0, 0);
+                for (int u = 0; u < 2; ++u)
+                    o[d0 + u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[sl][u][0], pl[ks], o[d0 + u], 0, 0, 0);
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
-                o[d0 + u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[sl][u][1], ph[ks], o[d0 + u], 0, 0, 0);
+                for (int u = 0; u < 2; ++u)
+                    o[d0 + u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[sl][u][1], ph[ks], o[d0 + u], 0, 0, 0);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -619,12 +637,12 @@ bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
     return x < y + nb && y < x + na;
 }
 
-template <int DP, bool OUT16>
+template <int DP, bool OUT16, bool SPLIT>
 void run_mfma(const float* q, const float* k, const float* v, void* out, int64_t N, int64_t Sq, int64_t Skv,
               int heads, int kv_heads, int64_t d, bool causal, float c2) {
     const int64_t ntiles = (Skv + kKT - 1) / kKT;
     const int64_t ntot = N * kv_heads * ntiles;
-    const size_t tile_bytes = (size_t)4 * kKT * DP * 2;
+    const size_t tile_bytes = (size_t)(SPLIT ? 4 : 2) * kKT * DP * 2;
     char* base = (char*)scratch((size_t)ntot * (tile_bytes + sizeof(int2)));
     u16* tiles = (u16*)base;
     int2* exps = (int2*)(base + (size_t)ntot * tile_bytes);
@@ -633,21 +651,21 @@ void run_mfma(const float* q, const float* k, const float* v, void* out, int64_t
     need(ntiles * (int64_t)tile_bytes < (int64_t(1) << 31), "sdh_attention", "too many keys per head for one launch");
     const dim3 pgrid((unsigned)ntiles, (unsigned)kv_heads, (unsigned)N);
     if (d == DP && kv_inner % 4 == 0 && aligned16(k) && aligned16(v))
-        k_attn_pack<DP, true><<<pgrid, 256, 0, stream()>>>(k, v, tiles, exps, (int)Skv, (int)kv_inner, (int)d,
+        k_attn_pack<DP, true, SPLIT><<<pgrid, 256, 0, stream()>>>(k, v, tiles, exps, (int)Skv, (int)kv_inner, (int)d,
                                                            (int)ntiles, kv_heads);
     else
-        k_attn_pack<DP, false><<<pgrid, 256, 0, stream()>>>(k, v, tiles, exps, (int)Skv, (int)kv_inner, (int)d,
+        k_attn_pack<DP, false, SPLIT><<<pgrid, 256, 0, stream()>>>(k, v, tiles, exps, (int)Skv, (int)kv_inner, (int)d,
                                                             (int)ntiles, kv_heads);
     launched("sdh_attention");
     const int qvec = d == DP && inner % 4 == 0 && aligned16(q) && (OUT16 ? ((uintptr_t)out & 7) == 0 : aligned16(out));
     const int64_t nqb = (Sq + kBM - 1) / kBM, nblk = nqb * heads * N;
     need(nblk * kThreads <= kMaxGridItems, "sdh_attention", "too many query blocks for one launch");
     if (causal)
-        k_attn_fwd<DP, true, OUT16><<<(unsigned)nblk, kThreads, 0, stream()>>>(
+        k_attn_fwd<DP, true, OUT16, SPLIT><<<(unsigned)nblk, kThreads, 0, stream()>>>(
             q, tiles, exps, out, (int)Sq, (int)Skv, (int)inner, (int)d, heads / kv_heads, kv_heads, (int)ntiles, c2,
             qvec, (int)nqb, heads);
     else
-        k_attn_fwd<DP, false, OUT16><<<(unsigned)nblk, kThreads, 0, stream()>>>(
+        k_attn_fwd<DP, false, OUT16, SPLIT><<<(unsigned)nblk, kThreads, 0, stream()>>>(
             q, tiles, exps, out, (int)Sq, (int)Skv, (int)inner, (int)d, heads / kv_heads, kv_heads, (int)ntiles, c2,
             qvec, (int)nqb, heads);
     launched("sdh_attention");
@@ -655,8 +673,8 @@ void run_mfma(const float* q, const float* k, const float* v, void* out, int64_t
 
 // out is float32, or bf16 (uint16) when out16
 void run_attention(const float* q, const float* k, const float* v, void* out, bool out16, int64_t N, int64_t Sq,
-                   int64_t Skv, int heads, int kv_heads, int64_t d, bool causal) {
-    const char* op = out16 ? "sdh_attention_bf16" : "sdh_attention";
+                   int64_t Skv, int heads, int kv_heads, int64_t d, bool causal, bool fp16 = false) {
+    const char* op = fp16 ? "sdh_attention_fp16" : out16 ? "sdh_attention_bf16" : "sdh_attention";
     if (kv_heads <= 0) kv_heads = heads;  // tensor.cpp:777
     need(N >= 0 && Sq >= 0 && Skv >= 0, op, "negative size");
     need(heads > 0 && d > 0, op, "heads and d must be positive");
@@ -684,12 +702,21 @@ void run_attention(const float* q, const float* k, const float* v, void* out, bo
     const float scale = 1.0f / std::sqrt((float)d);  // tensor.cpp:784
     const float c2 = scale * kLog2e;
     if (d <= 128) {
-        if (d <= 64)
-            out16 ? run_mfma<64, true>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2)
-                  : run_mfma<64, false>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2);
-        else
-            out16 ? run_mfma<128, true>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2)
-                  : run_mfma<128, false>(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal, c2);
+        auto go = [&](auto dp, auto o16, auto sp) {
+            run_mfma<decltype(dp)::value, decltype(o16)::value, decltype(sp)::value>(q, k, v, out, N, Sq, Skv, heads,
+                                                                                    kv_heads, d, causal, c2);
+        };
+        using D64 = std::integral_constant<int, 64>;
+        using D128 = std::integral_constant<int, 128>;
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        if (d <= 64) {
+            if (fp16) out16 ? go(D64(), T_(), F_()) : go(D64(), F_(), F_());
+            else out16 ? go(D64(), T_(), T_()) : go(D64(), F_(), T_());
+        } else {
+            if (fp16) out16 ? go(D128(), T_(), F_()) : go(D128(), F_(), F_());
+            else out16 ? go(D128(), T_(), T_()) : go(D128(), F_(), T_());
+        }
     } else {
         const int64_t gx = (Sq + kGenWaves - 1) / kGenWaves;
         need(gx * 64 * kGenWaves <= kMaxGridItems, op, "too many queries for one launch");
@@ -722,6 +749,12 @@ int sdh_attention(const float* q, const float* k, const float* v, float* out, in
 int sdh_attention_bf16(const float* q, const float* k, const float* v, uint16_t* out, int64_t N, int64_t Sq,
                        int64_t Skv, int heads, int kv_heads, int64_t d, int causal) {
     return guarded([&] { run_attention(q, k, v, out, true, N, Sq, Skv, heads, kv_heads, d, causal != 0); });
+}
+
+int sdh_attention_fp16(const float* q, const float* k, const float* v, void* out, int out_bf16, int64_t N,
+                       int64_t Sq, int64_t Skv, int heads, int kv_heads, int64_t d, int causal) {
+    return guarded(
+        [&] { run_attention(q, k, v, out, out_bf16 != 0, N, Sq, Skv, heads, kv_heads, d, causal != 0, true); });
 }
 
 }  // extern "C"

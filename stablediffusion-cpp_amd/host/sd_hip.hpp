@@ -94,6 +94,12 @@ inline void attention_bf16(const float* q, const float* k, const float* v, uint1
     detail::check(sdh_attention_bf16(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal ? 1 : 0),
                   "hip::attention_bf16");
 }
+// opt-in: attention from block-scaled fp16 operands (no reference counterpart); out fp32 or bf16 bits
+inline void attention_fp16(const float* q, const float* k, const float* v, void* out, bool out_bf16, int64_t N,
+                           int64_t Sq, int64_t Skv, int heads, int kv_heads, int64_t d, bool causal) {
+    detail::check(sdh_attention_fp16(q, k, v, out, out_bf16 ? 1 : 0, N, Sq, Skv, heads, kv_heads, d, causal ? 1 : 0),
+                  "hip::attention_fp16");
+}
 // backend_cuda.h:60-61
 inline void geglu(const float* x, float* y, int64_t rows, int64_t D) {
     detail::check(sdh_geglu(x, y, rows, D), "hip::geglu");

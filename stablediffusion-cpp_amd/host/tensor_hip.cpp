@@ -477,7 +477,7 @@ Tensor conv2d(const Tensor& x, const Tensor& W, const Tensor* b, int stride, int
 // tensor.cpp:776-790: the reference's shape checks and messages, device branch
 namespace {
 Tensor attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal, int kv_heads,
-                      bool bf16) {
+                      bool bf16, bool fp16_products = false) {
     if (kv_heads <= 0) kv_heads = heads;
     const int64_t N = q.dim(0), Sq = q.dim(1), inner = q.dim(2), Skv = k.dim(1), kv_inner = k.dim(2);
     if (inner % heads != 0 || heads % kv_heads != 0) throw std::runtime_error("attention: heads mismatch");
@@ -489,11 +489,18 @@ Tensor attention_impl(const Tensor& q, const Tensor& k, const Tensor& v, int hea
     need_hip(q, "attention");
     if (bf16) {
         Tensor out = Tensor::empty_bf16({N, Sq, inner});
-        sd::hip::attention_bf16(q.dptr(), k.dptr(), v.dptr(), out.dptr16(), N, Sq, Skv, heads, kv_heads, d, causal);
+        if (fp16_products)
+            sd::hip::attention_fp16(q.dptr(), k.dptr(), v.dptr(), out.dptr16(), true, N, Sq, Skv, heads, kv_heads, d,
+                                    causal);
+        else
+            sd::hip::attention_bf16(q.dptr(), k.dptr(), v.dptr(), out.dptr16(), N, Sq, Skv, heads, kv_heads, d, causal);
         return out;
     }
     Tensor out = Tensor::empty({N, Sq, inner}, Device::HIP);
-    sd::hip::attention(q.dptr(), k.dptr(), v.dptr(), out.dptr(), N, Sq, Skv, heads, kv_heads, d, causal);
+    if (fp16_products)
+        sd::hip::attention_fp16(q.dptr(), k.dptr(), v.dptr(), out.dptr(), false, N, Sq, Skv, heads, kv_heads, d, causal);
+    else
+        sd::hip::attention(q.dptr(), k.dptr(), v.dptr(), out.dptr(), N, Sq, Skv, heads, kv_heads, d, causal);
     return out;
 }
 }  // namespace
@@ -504,6 +511,11 @@ Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, int heads, b
 
 Tensor attention_bf16(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal, int kv_heads) {
     return attention_impl(q, k, v, heads, causal, kv_heads, true);
+}
+
+Tensor attention_fp16(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal, int kv_heads,
+                      bool out_bf16) {
+    return attention_impl(q, k, v, heads, causal, kv_heads, out_bf16, true);
 }
 
 // ---- the Z-Image block's fused ops ----

@@ -140,6 +140,10 @@ Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, int heads, b
 // attention rounded to BF16 (the input of the block's to_out projection)
 Tensor attention_bf16(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal = false,
                       int kv_heads = 0);
+// opt-in, no counterpart in the reference: attention from block-scaled fp16
+// operands (sdh_attention_fp16), FP32 or (out_bf16) BF16 result
+Tensor attention_fp16(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal = false,
+                      int kv_heads = 0, bool out_bf16 = false);
 
 // ---- softmax (tensor.h:236) ----
 // Same parameters as the reference; x is a DEVICE pointer here (rows x cols

@@ -7,6 +7,7 @@
 #include "zimage_hip.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cctype>
 #include <chrono>
 #include <cmath>
@@ -129,6 +130,7 @@ Tensor as_sequence(Tensor rows) {
 
 struct ZImageTransformer::Impl {
     Config cfg;
+    std::atomic<bool> fp16_attention{false};  // opt-in: attention from block-scaled fp16 operands
     int64_t dim = 0, head_dim = 0;
     int channels = 0;
     Proj patch_embed, text_embed, t_in, t_out, head_mod, head_out;
@@ -140,7 +142,7 @@ struct ZImageTransformer::Impl {
     mutable std::mutex rotary_mu;      // the cache below is filled by const forward calls
     mutable std::map<std::tuple<int64_t, int64_t, int64_t>, std::pair<Tensor, Tensor>> rotary_cache;
 
-    explicit Impl(const Config& c) : cfg(c) {}
+    explicit Impl(const Config& c) : cfg(c), fp16_attention(c.fp16_attention) {}
 
     Proj bind_proj(const Weights& w, const std::string& name) const {
         return Proj{&w.get(name + ".weight"), w.try_get(name + ".bias")};
@@ -293,7 +295,10 @@ struct ZImageTransformer::Impl {
     Tensor attend(const BlockBinding& b, const Tensor& in, const Tensor& cos, const Tensor& sin) const {
         Tensor q = project(in, b, kProjQ), k = project(in, b, kProjK), v = project(in, b, kProjV);
         qknorm_rope_(q, k, head_dim, b.norm[kNormQ], b.norm[kNormK], kQkNormEps, cos, sin, true);
-        Tensor o = b.fused_bf16 ? attention_bf16(q, k, v, cfg.heads, false) : attention(q, k, v, cfg.heads, false);
+        Tensor o = fp16_attention.load(std::memory_order_relaxed)
+                       ? attention_fp16(q, k, v, cfg.heads, false, 0, b.fused_bf16)
+                   : b.fused_bf16 ? attention_bf16(q, k, v, cfg.heads, false)
+                                  : attention(q, k, v, cfg.heads, false);
         return project(o, b, kProjOut);
     }
 
@@ -363,6 +368,7 @@ ZImageTransformer::ZImageTransformer(const Weights& w, const Config& cfg) : impl
 ZImageTransformer::~ZImageTransformer() = default;
 
 int ZImageTransformer::in_channels() const { return impl_->channels; }
+void ZImageTransformer::set_fp16_attention(bool on) { impl_->fp16_attention.store(on, std::memory_order_relaxed); }
 int64_t ZImageTransformer::dim() const { return impl_->dim; }
 
 Tensor ZImageTransformer::forward(const Tensor& latent, float t, const Tensor& text) const {
@@ -507,6 +513,10 @@ int sdhm_zimage_time(void* model, int64_t H, int64_t W, int64_t L, int64_t cap_d
         *ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() /
               (steps > 0 ? steps : 1);
     });
+}
+
+int sdhm_zimage_set_fp16_attention(void* model, int on) {
+    return guard([&] { static_cast<Model*>(model)->m->set_fp16_attention(on != 0); });
 }
 
 int64_t sdhm_zimage_params(void* model) { return (int64_t) static_cast<Model*>(model)->w.total_params(); }

@@ -40,6 +40,11 @@ public:
         float rope_theta = 256.0f;
         float t_scale = 1000.0f;
         int axes_dims[3] = {32, 48, 48};
+        // Opt-in, no counterpart in the reference: attention from block-scaled
+        // fp16 operands (sdh_attention_fp16), a third of the MFMA work, for a
+        // step whose tolerance allows it; off gives the reference's fp32
+        // attention numerics.
+        bool fp16_attention = false;
     };
     // Tensor shapes of a model, for filling Weights with random values.
     struct Shapes {
@@ -63,6 +68,9 @@ public:
     // [0, 1]; text: [1, L, cap_dim] device tensor of text hidden states.
     // Returns a [1, C, H, W] device tensor. Safe to call from several threads.
     Tensor forward(const Tensor& latent, float t, const Tensor& text) const;
+
+    // Switches the attention numerics of later forward calls (Config::fp16_attention).
+    void set_fp16_attention(bool on);
 
     int in_channels() const;
     int64_t dim() const;
@@ -94,6 +102,8 @@ int sdhm_zimage_forward(void* model, const float* x, int64_t C, int64_t H, int64
 // synchronised steps).
 int sdhm_zimage_time(void* model, int64_t H, int64_t W, int64_t L, int64_t cap_dim, int steps, int warmup,
                      double* ms);
+// Opt-in attention from block-scaled fp16 operands for later forwards (on != 0).
+int sdhm_zimage_set_fp16_attention(void* model, int on);
 int64_t sdhm_zimage_params(void* model);
 void sdhm_zimage_free(void* model);
 }

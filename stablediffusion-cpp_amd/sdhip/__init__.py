@@ -91,6 +91,7 @@ SIGNATURES = {
     "sdh_to_bf16": [_vp, _vp, _i64],
     "sdh_attention": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
     "sdh_attention_bf16": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
+    "sdh_attention_fp16": [_vp, _vp, _vp, _vp, C.c_int, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
     "sdh_upsample_nearest2x": [_vp, _vp, _i64, _i64, _i64],
     "sdh_concat_channels": [_vp, _vp, _vp, _i64, _i64, _i64, _i64],
     "sdh_nchw_to_nlc": [_vp, _vp, _i64, _i64, _i64],
@@ -303,6 +304,13 @@ class Backend:
         self.call("sdh_attention_bf16", _p(q), _p(k), _p(v), _p(out16), N, Sq, Skv, heads, kv_heads, d,
                   int(bool(causal)))
 
+    def attention_fp16(self, q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal=False, out_bf16=False):
+        """Opt-in reduced precision attention (no reference counterpart): every
+        product from block-scaled fp16 operands; out float32, or the bf16 bits
+        (uint16) when out_bf16."""
+        self.call("sdh_attention_fp16", _p(q), _p(k), _p(v), _p(out), int(bool(out_bf16)), N, Sq, Skv, heads,
+                  kv_heads, d, int(bool(causal)))
+
     def swiglu(self, g, u, y, n):
         self.call("sdh_swiglu", _p(g), _p(u), _p(y), n)
 
@@ -405,6 +413,7 @@ _MODEL_SIGNATURES = {
                             C.POINTER(C.c_void_p)], _int),
     "sdhm_zimage_forward": ([C.c_void_p, _vp, _i64, _i64, _i64, _fl, _vp, _i64, _i64, _vp], _int),
     "sdhm_zimage_time": ([C.c_void_p, _i64, _i64, _i64, _i64, _int, _int, C.POINTER(C.c_double)], _int),
+    "sdhm_zimage_set_fp16_attention": ([C.c_void_p, _int], _int),
     "sdhm_zimage_params": ([C.c_void_p], _i64),
     "sdhm_zimage_free": ([C.c_void_p], None),
     "sdhm_last_error": ([], C.c_char_p),
@@ -464,6 +473,11 @@ class ZImage:
                                                      float(t), cap.ctypes.data, cap.shape[1], cap.shape[2],
                                                      out.ctypes.data))
         return out
+
+    def set_fp16_attention(self, on=True):
+        """Opt-in (no reference counterpart): later forwards run attention from
+        block-scaled fp16 operands (sdh_attention_fp16)."""
+        self._check(_model_lib().sdhm_zimage_set_fp16_attention(self.h, int(bool(on))))
 
     def time(self, H, W, L, cap_dim, steps, warmup):
         ms = C.c_double()
