@@ -909,7 +909,7 @@ def parity(got, want, results):
 # ------------------------------------------------------------------ traffic (rocprof pmc)
 def read_traffic(name):
     """HBM bytes per launch from profiles/hbm_traffic.txt (rocprofv3 --pmc
-    FETCH_SIZE and WRITE_SIZE runs, scaled by the plain-copy calibration)."""
+    runs of the L2-to-memory request counters by size; see rocprof_summary)."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
     if not os.path.exists(path):
         return None
@@ -1055,6 +1055,7 @@ def rocprof_summary(trace_dir, read_dir=None, write_dir=None):
 
         text += ("\nHBM traffic per dispatch from the L2/EA request counters by size (read = 128 n128 + 64 n64 + "
                  "32 n32; write = 64 n64 + 32 n32); no calibration factor.\n\n")
+        mapped = set()
         text += ("| kernel | grid | read bytes | write bytes | HBM bytes per dispatch | requests of no listed size |\n"
                  "|---|---|---|---|---|---|\n")
         for k in sorted(rd, key=lambda k: -read_bytes(rd[k])[0]):
@@ -1065,7 +1066,8 @@ def rocprof_summary(trace_dir, read_dir=None, write_dir=None):
             tb = int(round(rb + wb))
             text += f"| `{k[0]}` | {k[1]} | {rb:,.0f} | {wb:,.0f} | {tb:,} | {other:.0f} |\n"
             wl = next((v for kk, v in KERNEL_OF.items() if k[0].startswith(kk)), None)
-            if wl:
+            if wl and wl not in mapped:  # rows run largest first: a workload's own launch, not a stray one
+                mapped.add(wl)
                 traffic_lines.append(f"{wl} kernel={k[0]} grid={k[1]} read_bytes={rb:.0f} write_bytes={wb:.0f} "
                                      f"traffic_bytes={tb}")
         for wl in all_workloads():
