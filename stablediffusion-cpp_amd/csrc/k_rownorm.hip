@@ -384,7 +384,12 @@ __global__ __launch_bounds__(kThreads) void k_ln_mod_gate_generic(const float* x
 // applies to its A (backend_cuda.cu:183-188), with the same fp32 products in
 // the same order, so the bits equal those of the three-op sequence. The bf16
 // row is the A operand of the projections that follow.
-template <int V, bool HAS_G, bool HAS_S>
+// PAIR (rows of exactly 64 V float4, y 16-byte aligned): lanes 2i and 2i+1
+// swap one bf16x4 (a DPP exchange), so every lane stores 16 contiguous bytes,
+// the even lane two consecutive float4s' results of step j, the odd lane
+// those of step j + 1; the loads and the sum keep the one-wave order, so
+// rstd, and the output, are bit-equal to the unpaired form's.
+template <int V, bool HAS_G, bool HAS_S, bool PAIR = false>
 __global__ __launch_bounds__(kThreads) void k_rms_mod_bf16(const float* __restrict__ x, uint2* __restrict__ y,
                                                           int64_t rows, int C, const float* __restrict__ gamma,
                                                           const float* __restrict__ scale, float eps) {
@@ -404,15 +409,31 @@ __global__ __launch_bounds__(kThreads) void k_rms_mod_bf16(const float* __restri
 #pragma unroll
     for (int j = 0; j < V; ++j) q += dev::hsum(v[j] * v[j]);
     const float rstd = rstd_of(dev::wave_sum(q), C, eps);
-#pragma unroll
-    for (int j = 0; j < V; ++j) {
+    auto out = [&](int j) __attribute__((always_inline)) {
         const int idx = lane + 64 * j;
-        if (idx < n4) {
-            f4 o = v[j] * rstd;
-            if constexpr (HAS_G) o = o * ((const f4*)gamma)[idx];
-            if constexpr (HAS_S) o = o * ((const f4*)scale)[idx];
-            dev::st_stream(yr + idx, dev::bf16x4(o));
+        f4 o = v[j] * rstd;
+        if constexpr (HAS_G) o = o * ((const f4*)gamma)[idx];
+        if constexpr (HAS_S) o = o * ((const f4*)scale)[idx];
+        return dev::bf16x4(o);
+    };
+    if constexpr (PAIR) {
+        const bool odd = lane & 1;
+        // quad_perm(1, 0, 3, 2): each lane reads its pair partner
+        auto swap = [](unsigned u) { return (unsigned)__builtin_amdgcn_mov_dpp((int)u, 0xB1, 0xF, 0xF, false); };
+#pragma unroll
+        for (int j = 0; j + 1 < V; j += 2) {
+            const uint2 b0 = out(j), b1 = out(j + 1);
+            const uint2 send = odd ? b0 : b1;
+            const uint2 r = {swap(send.x), swap(send.y)};
+            const dev::u4v w = odd ? dev::u4v{r.x, r.y, b1.x, b1.y} : dev::u4v{b0.x, b0.y, r.x, r.y};
+            const int pos = odd ? lane - 1 + 64 * (j + 1) : lane + 64 * j;  // in uint2 units, even
+            __builtin_nontemporal_store(w, reinterpret_cast<dev::u4v*>(yr + pos));
         }
+        if constexpr (V & 1) dev::st_stream(yr + lane + 64 * (V - 1), out(V - 1));
+    } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+            if (lane + 64 * j < n4) dev::st_stream(yr + lane + 64 * j, out(j));
     }
 }
 
@@ -683,7 +704,10 @@ void run_rms_mod_bf16(const float* x, uint16_t* y, int64_t rows, int64_t C, cons
         with_v(pick_v(C / 4), [&](auto vc) {
             constexpr int V = decltype(vc)::value;
             uint2* yy = (uint2*)y;
-            if (gamma && scale)
+            if (gamma && scale && C == 256 * V && ((uintptr_t)y & 15) == 0)
+                k_rms_mod_bf16<V, true, true, true><<<grid, kThreads, 0, stream()>>>(x, yy, rows, (int)C, gamma, scale,
+                                                                                   eps);
+            else if (gamma && scale)
                 k_rms_mod_bf16<V, true, true><<<grid, kThreads, 0, stream()>>>(x, yy, rows, (int)C, gamma, scale, eps);
             else if (gamma)
                 k_rms_mod_bf16<V, true, false><<<grid, kThreads, 0, stream()>>>(x, yy, rows, (int)C, gamma, scale, eps);

@@ -224,6 +224,7 @@ __device__ __forceinline__ float hsum(const f4& v) { return (v.x + v.y) + (v.z +
 __device__ __forceinline__ f4 ld_stream(const f4* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_stream(f4* p, f4 v) { __builtin_nontemporal_store(v, p); }
 typedef unsigned u2v __attribute__((ext_vector_type(2)));
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void st_stream(uint2* p, uint2 v) {
     __builtin_nontemporal_store(u2v{v.x, v.y}, reinterpret_cast<u2v*>(p));
 }
