@@ -602,8 +602,17 @@ def test_zero_and_copy(be):
 
 
 def test_arena_reuse(be):
-    before = be.memory_stats()[1]
-    for _ in range(5):
-        d = be.empty((1 << 20,))
-        d.free()
-    assert be.memory_stats()[1] == before
+    import gc
+
+    # earlier tests' arrays are freed when the collector finds them: collect
+    # first, and keep it off while the bytes in use are compared
+    gc.collect()
+    gc.disable()
+    try:
+        before = be.memory_stats()[1]
+        for _ in range(5):
+            d = be.empty((1 << 20,))
+            d.free()
+        assert be.memory_stats()[1] == before
+    finally:
+        gc.enable()

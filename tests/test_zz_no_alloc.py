@@ -62,11 +62,15 @@ def test_noalloc_equals_group_norm_silu(be, orc):
         cases.append((shape, groups, eps, x, g, b, dx, dg, db, want.download(), be.empty(shape)))
     be.synchronize()
     gc.collect()  # buffers dropped earlier are freed now, not between the two readings
-    before = be.memory_stats()
-    for shape, groups, eps, x, g, b, dx, dg, db, want, dy in cases:  # back to back, shrinking
-        _call(be, "sdh_group_norm_silu_noalloc", dx, dy, shape, groups, dg, db, eps)
-    be.synchronize()
-    after = be.memory_stats()
+    gc.disable()
+    try:
+        before = be.memory_stats()
+        for shape, groups, eps, x, g, b, dx, dg, db, want, dy in cases:  # back to back, shrinking
+            _call(be, "sdh_group_norm_silu_noalloc", dx, dy, shape, groups, dg, db, eps)
+        be.synchronize()
+        after = be.memory_stats()
+    finally:
+        gc.enable()
     for shape, groups, eps, x, g, b, dx, dg, db, want, dy in cases:
         got = dy.download()
         print(shape, "max |noalloc - default|", float(np.max(np.abs(got - want))), flush=True)
