@@ -671,6 +671,57 @@ void run_mfma(const float* q, const float* k, const float* v, void* out, int64_t
     launched("sdh_attention");
 }
 
+// Head dimensions above 128 on long sequences (the VAE's one-head attention
+// over 512 channels, modules.cpp:133-141): the score matrix, as the
+// reference's device path forms it (backend_cuda.cu:550-586), on the fp32
+// library GEMM: per (batch, head) and block of query rows, S = q_h k_g^T,
+// the scaled (causal) row softmax in place, then O_h = P v_g as a GEMM
+// against v^T (v transposed once per batch). fp32 products and sums
+// throughout. The score block is bounded to kScoreBytes (causal: one block,
+// so the mask's row index is the query's). False, with nothing queued, when
+// the operands do not suit the library GEMM (alignment, Skv % 4) or the
+// causal block would not fit: the caller then runs the one-wave kernel.
+constexpr int64_t kScoreBytes = int64_t(1) << 30;
+
+bool run_attention_gemm(const char* op, const float* q, const float* k, const float* v, void* out, bool out16,
+                        int64_t N, int64_t Sq, int64_t Skv, int heads, int kv_heads, int64_t d, bool causal,
+                        float scale) {
+    const int64_t inner = heads * d, kv_inner = (int64_t)kv_heads * d;
+    if (d % 4 || Skv % 4 || !aligned16(q) || !aligned16(k) || !aligned16(v) || (!out16 && !aligned16(out)))
+        return false;
+    const int64_t rb = causal ? Sq : std::max<int64_t>(1, std::min<int64_t>(Sq, kScoreBytes / (Skv * 4)));
+    if (rb * Skv * 4 > 4 * kScoreBytes) return false;
+    const size_t vt_n = (size_t)(Skv * kv_inner), sc_n = (size_t)(rb * Skv), o_n = out16 ? (size_t)(N * Sq * inner) : 0;
+    float* vt = (float*)scratch((vt_n + sc_n + o_n) * 4 + 512);
+    float* sc = vt + ((vt_n + 63) & ~size_t(63));
+    float* o32 = out16 ? sc + ((sc_n + 63) & ~size_t(63)) : (float*)out;
+    const int group = heads / kv_heads;
+    bool first = true;
+    for (int64_t n = 0; n < N; ++n) {
+        transpose_device(op, v + n * Skv * kv_inner, vt, 1, Skv, kv_inner);  // [Skv, kv_inner] -> [kv_inner, Skv]
+        for (int h = 0; h < heads; ++h) {
+            const int g = h / group;
+            for (int64_t q0 = 0; q0 < Sq; q0 += rb) {
+                const int64_t m = std::min(rb, Sq - q0);
+                const bool ok = blaslt_gemm(true, m, Skv, d, q + (n * Sq + q0) * inner + h * d, inner,
+                                            k + n * Skv * kv_inner + g * d, kv_inner, sc, Skv, nullptr, false);
+                if (!ok) {
+                    need(first, op, "the library GEMM has no algorithm for a later block");
+                    return false;  // nothing but the transpose queued; the one-wave kernel takes over
+                }
+                first = false;
+                softmax_rows_device(op, sc, m, Skv, scale, causal);
+                need(blaslt_gemm(true, m, d, Skv, sc, Skv, vt + g * d * Skv, Skv, o32 + (n * Sq + q0) * inner + h * d,
+                                 inner, nullptr, false),
+                     op, "the library GEMM has no algorithm for P v");
+            }
+        }
+    }
+    if (out16) to_bf16_device(op, o32, (uint16_t*)out, N * Sq * inner);
+    launched(op);
+    return true;
+}
+
 // out is float32, or bf16 (uint16) when out16
 void run_attention(const float* q, const float* k, const float* v, void* out, bool out16, int64_t N, int64_t Sq,
                    int64_t Skv, int heads, int kv_heads, int64_t d, bool causal, bool fp16 = false) {
@@ -717,7 +768,8 @@ void run_attention(const float* q, const float* k, const float* v, void* out, bo
             if (fp16) out16 ? go(D128(), T_(), F_()) : go(D128(), F_(), F_());
             else out16 ? go(D128(), T_(), T_()) : go(D128(), F_(), T_());
         }
-    } else {
+    } else if (!(Sq * Skv >= (int64_t(1) << 18) &&
+                 run_attention_gemm(op, q, k, v, out, out16, N, Sq, Skv, heads, kv_heads, d, causal, scale))) {
         const int64_t gx = (Sq + kGenWaves - 1) / kGenWaves;
         need(gx * 64 * kGenWaves <= kMaxGridItems, op, "too many queries for one launch");
         const dim3 grid((unsigned)gx, (unsigned)heads, (unsigned)N);

@@ -134,6 +134,14 @@ void run_gemm_f32(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, 
 }
 
 }  // namespace
+
+void to_bf16_device(const char* op, const float* x, uint16_t* y, int64_t n) {
+    (void)op;
+    if (n <= 0) return;
+    const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, (int64_t)num_cus() * 32);
+    k_to_bf16<<<grid, 256, 0, stream()>>>(x, y, n);
+}
+
 }  // namespace sdh
 
 using namespace sdh;

@@ -218,6 +218,11 @@ void run_patch(const char* op, bool forward, const float* x, float* y, int64_t C
 }
 
 }  // namespace
+
+void transpose_device(const char* op, const float* x, float* y, int64_t B, int64_t R, int64_t K) {
+    run_transpose(op, x, y, B, R, K);
+}
+
 }  // namespace sdh
 
 using namespace sdh;

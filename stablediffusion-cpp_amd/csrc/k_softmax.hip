@@ -204,6 +204,12 @@ void run_softmax(float* x, int64_t rows, int64_t cols, float scale, int causal, 
 }
 
 }  // namespace
+
+void softmax_rows_device(const char* op, float* x, int64_t rows, int64_t cols, float scale, bool causal) {
+    (void)op;
+    run_softmax(x, rows, cols, scale, causal ? 1 : 0, rows > 0 ? rows : 1);
+}
+
 }  // namespace sdh
 
 using namespace sdh;

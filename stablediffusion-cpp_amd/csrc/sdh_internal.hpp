@@ -82,6 +82,12 @@ bool blaslt_gemm(bool f32, int64_t M, int64_t N, int64_t K, const void* P, int64
                  float* C, int64_t ldc, const float* bias, bool accumulate);
 // y = silu(gate) * up over n floats (the SwiGLU kernel of sdh_swiglu, no checks).
 void launch_swiglu(const float* gate, const float* up, float* y, int64_t n);
+// sdh_softmax_rows on [rows, cols] (k_softmax.hip), errors named after `op`.
+void softmax_rows_device(const char* op, float* x, int64_t rows, int64_t cols, float scale, bool causal);
+// [B, R, K] -> [B, K, R] (k_layout.hip), errors named after `op`.
+void transpose_device(const char* op, const float* x, float* y, int64_t B, int64_t R, int64_t K);
+// y[i] = bf16 bits of x[i], the rounding of gemm_nt_bf16's A (k_gemm_f32.hip).
+void to_bf16_device(const char* op, const float* x, uint16_t* y, int64_t n);
 // Zero-initialised per-library device counters (uint32), persistent across
 // calls; kernels that use them leave them at zero when they finish.
 unsigned* counters(size_t count);

@@ -129,3 +129,49 @@ def test_attention_invalid_arguments(be):
     with pytest.raises(sdhip.SdhError) as e:
         be.attention(q, k, k, out, 1, 8, 4, 3, 3, 4, False)  # q holds 4 rows, not 8
     assert e.value.status == sdhip.SDH_ERR_INVALID
+
+
+# Head dimensions above 128 with at least 2^18 scores per head take the
+# score-matrix route (fp32 library GEMM, row softmax, GEMM against v^T); the
+# rest, and Skv not a multiple of 4, the one-wave fp32 kernel. Both are held
+# to the reference's 1e-4.
+WIDE = [  # N, Sq, Skv, heads, kv_heads, d, causal
+    (1, 1024, 1024, 1, 1, 512, False),   # the VAE's one-head attention, smaller image
+    (2, 600, 520, 4, 2, 160, True),      # causal, grouped heads, two batches
+    (1, 700, 1000, 2, 2, 256, False),    # cross-attention, several query blocks of one score block
+    (1, 600, 515, 2, 1, 192, False),     # Skv % 4 != 0: the one-wave kernel
+]
+
+
+@pytest.mark.parametrize("N,Sq,Skv,heads,kvh,d,causal", WIDE)
+def test_attention_wide_heads(be, orc, N, Sq, Skv, heads, kvh, d, causal):
+    q, k, v = _qkv(orc, N, Sq, Skv, heads, kvh, d, 7100 + Sq + d)
+    got = _run(be, q, k, v, heads, kvh, causal)
+    rows = np.arange(0, Sq, 7)
+    want = orc.attention(q, k, v, heads, causal, kvh, rows=rows)
+    err = float(np.max(np.abs(got[:, rows] - want)))
+    print(f"wide attention {N}x{Sq}x{Skv} h{heads}/{kvh} d{d} causal={causal}: max-abs {err:.3g}")
+    assert err <= TOL
+
+
+def test_attention_vae_shape(be, orc):
+    """The FLUX/SD VAE mid-block attention at a 512x512 image: one head over
+    512 channels, 4096 tokens; the bf16 output form is the bf16 rounding of
+    the fp32 one, and the opt-in fp16 entry runs the same fp32 route."""
+    import sdhip
+
+    S, d = 4096, 512
+    q, k, v = _qkv(orc, 1, S, S, 1, 1, d, 7200)
+    got = _run(be, q, k, v, 1, 1, False)
+    rows = np.concatenate([np.arange(0, S, 211), [S - 1]])
+    err = float(np.max(np.abs(got[:, rows] - orc.attention(q, k, v, 1, False, rows=rows))))
+    print(f"VAE attention [1,{S},{d}]: max-abs {err:.3g}")
+    assert err <= TOL
+    dq, dk, dv = be.array(q), be.array(k), be.array(v)
+    o16 = sdhip.DArray(be, (1, S, d), dtype=np.uint16)
+    be.attention_bf16(dq, dk, dv, o16, 1, S, S, 1, 1, d, False)
+    bits = got.view(np.uint32).astype(np.uint64)
+    assert np.array_equal(o16.download(), ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16).astype(np.uint16))
+    of = be.empty((1, S, d))
+    be.attention_fp16(dq, dk, dv, of, 1, S, S, 1, 1, d, False)
+    assert np.array_equal(of.download(), got)
