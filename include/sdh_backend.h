@@ -255,6 +255,10 @@ int sdh_add(float* a, const float* b, int64_t n);
 int sdh_scale(float* x, float s, int64_t n);
 /* backend_cuda.h:70 affine(): x = x * a + b. */
 int sdh_affine(float* x, float a, float b, int64_t n);
+/* FUSED for the Z-Image block: x [2 * pairs, dim] in place, rows 2p become
+ * 1 + x (affine_(scale, 1, 1)) and rows 2p + 1 tanh(x) (tanh_(gate)), the four
+ * ops of zimage.cpp:104-107 in one launch; bits equal those of the ops. */
+int sdh_modulation_rows(float* x, int64_t pairs, int64_t dim);
 /* backend_cuda.h:71 mul_rows(): x[r, :] *= v[:]. */
 int sdh_mul_rows(float* x, const float* v, int64_t rows, int64_t dim);
 /* backend_cuda.h:72 add_rows_scaled(): x[r, :] += g[:] * y[r, :]. */

@@ -59,6 +59,7 @@ STUB(int sdh_gelu(float*, int64_t))
 STUB(int sdh_quick_gelu(float*, int64_t))
 STUB(int sdh_add(float*, const float*, int64_t))
 STUB(int sdh_scale(float*, float, int64_t))
+STUB(int sdh_modulation_rows(float*, int64_t, int64_t))
 STUB(int sdh_affine(float*, float, float, int64_t))
 STUB(int sdh_mul_rows(float*, const float*, int64_t, int64_t))
 STUB(int sdh_add_rows_scaled(float*, const float*, const float*, int64_t, int64_t))

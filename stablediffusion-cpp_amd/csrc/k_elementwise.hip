@@ -58,6 +58,16 @@ __global__ __launch_bounds__(kThreads) void k_unary(f4* __restrict__ x, int64_t 
     if (blockIdx.x == 0 && (int)threadIdx.x < tail) tail_ptr[threadIdx.x] = unary<K>(tail_ptr[threadIdx.x], a, b);
 }
 
+// The adaLN modulation rows of a block, in place: rows 2p (scales) become
+// 1 + x, rows 2p + 1 (gates) tanh(x), with the expressions of affine_ and
+// tanh_ (one launch for the four ops of zimage.cpp:104-107).
+__global__ __launch_bounds__(kThreads) void k_modulation_rows(float* __restrict__ x, int64_t n, int64_t dim) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+        const float v = x[i];
+        x[i] = ((i / dim) & 1) ? unary<U_TANH>(v, 0.f, 0.f) : unary<U_AFFINE>(v, 1.0f, 1.0f);
+    }
+}
+
 template <int K>
 __global__ __launch_bounds__(kThreads) void k_unary_scalar(float* __restrict__ x, int64_t n, float a, float b) {
     for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
@@ -341,6 +351,19 @@ int sdh_quick_gelu(float* x, int64_t n) {
 int sdh_scale(float* x, float s, int64_t n) { return guarded([&] { run_unary<U_SCALE>("sdh_scale", x, n, s, 0.f); }); }
 int sdh_affine(float* x, float a, float b, int64_t n) {
     return guarded([&] { run_unary<U_AFFINE>("sdh_affine", x, n, a, b); });
+}
+
+int sdh_modulation_rows(float* x, int64_t pairs, int64_t dim) {
+    return guarded([&] {
+        const char* op = "sdh_modulation_rows";
+        need(pairs >= 0 && dim >= 0, op, "negative size");
+        const int64_t n = 2 * pairs * dim;
+        if (n == 0) return;
+        ensure_init();
+        check_range(x, (size_t)n * 4, op, "x");
+        k_modulation_rows<<<stride_grid(n), kThreads, 0, stream()>>>(x, n, dim);
+        launched(op);
+    });
 }
 
 int sdh_add(float* a, const float* b, int64_t n) {

@@ -84,6 +84,10 @@ inline void softmax_rows(float* x, int64_t rows, int64_t cols, float scale, bool
     detail::check(sdh_softmax_rows(x, rows, cols, scale, causal ? 1 : 0), "hip::softmax_rows");
 }
 // backend_cuda.h:57-59: q [N, Sq, heads*d]; k, v [N, Skv, kv_heads*d]; out [N, Sq, heads*d]
+// zimage.cpp:104-107 in one launch: x [2 pairs, dim], rows 2p -> 1 + x, rows 2p + 1 -> tanh(x)
+inline void modulation_rows(float* x, int64_t pairs, int64_t dim) {
+    detail::check(sdh_modulation_rows(x, pairs, dim), "hip::modulation_rows");
+}
 inline void attention(const float* q, const float* k, const float* v, float* out, int64_t N, int64_t Sq, int64_t Skv,
                       int heads, int kv_heads, int64_t d, bool causal) {
     detail::check(sdh_attention(q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal ? 1 : 0), "hip::attention");

@@ -263,6 +263,12 @@ void affine_(Tensor& x, float a, float b) {
     sd::hip::affine(x.dptr(), a, b, x.numel());
 }
 
+void modulation_rows_(Tensor& x) {
+    need_hip(x, "modulation_rows_");
+    if (x.ndim() != 2 || x.dim(0) % 2) throw std::runtime_error("modulation_rows_: x must be [2P, D], got " + x.shape_str());
+    sd::hip::modulation_rows(x.dptr(), x.dim(0) / 2, x.dim(1));
+}
+
 // tensor.cpp:889-893
 void mul_rows_(Tensor& x, const Tensor& v) {
     const int64_t dim = x.dim(-1), rows = count_of(x.numel(), dim);

@@ -90,6 +90,9 @@ void quick_gelu_(Tensor& x);
 
 // ---- broadcasts / residual (tensor.h:195-198, :230-232) ----
 void affine_(Tensor& x, float a, float b);
+// x [2 P, D] in place: rows 2p -> 1 + x (affine_(x, 1, 1)), rows 2p + 1 ->
+// tanh(x) (tanh_), one launch (the adaLN modulation of a Z-Image block).
+void modulation_rows_(Tensor& x);
 void mul_rows_(Tensor& x, const Tensor& v);
 void add_rows_scaled_(Tensor& x, const Tensor& y, const Tensor& g);
 void add_channel_bias_(Tensor& x, const Tensor& b);

@@ -327,11 +327,10 @@ struct ZImageTransformer::Impl {
         if (b.modulated) {
             mod = project(*cond, b, kProjMod);
             mod.reshape({4, dim});
+            modulation_rows_(mod);  // 1 + scale, tanh(gate): one launch
             for (int s = 0; s < 2; ++s) {
                 scale[s] = rows_view(mod, 2 * s, 2 * s + 1);
                 gate[s] = rows_view(mod, 2 * s + 1, 2 * s + 2);
-                affine_(scale[s], 1.0f, 1.0f);
-                tanh_(gate[s]);
                 scale[s].reshape({dim});
                 gate[s].reshape({dim});
             }

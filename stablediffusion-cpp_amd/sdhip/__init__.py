@@ -76,6 +76,7 @@ SIGNATURES = {
     "sdh_add": [_vp, _vp, _i64],
     "sdh_scale": [_vp, _fl, _i64],
     "sdh_affine": [_vp, _fl, _fl, _i64],
+    "sdh_modulation_rows": [_vp, _i64, _i64],
     "sdh_mul_rows": [_vp, _vp, _i64, _i64],
     "sdh_add_rows_scaled": [_vp, _vp, _vp, _i64, _i64],
     "sdh_add_channel_bias": [_vp, _vp, _i64, _i64, _i64],
@@ -337,6 +338,10 @@ class Backend:
 
     def affine(self, x, a, b, n):
         self.call("sdh_affine", _p(x), a, b, n)
+
+    def modulation_rows(self, x, pairs, dim):
+        """x [2 * pairs, dim] in place: rows 2p -> 1 + x, rows 2p + 1 -> tanh(x) (zimage.cpp:104-107)."""
+        self.call("sdh_modulation_rows", _p(x), pairs, dim)
 
     def mul_rows(self, x, v, rows, dim):
         self.call("sdh_mul_rows", _p(x), _p(v), rows, dim)

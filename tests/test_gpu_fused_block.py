@@ -147,3 +147,24 @@ def test_attention_bf16(be, orc, N, Sq, Skv, heads, kvh, d, causal):
     be.to_bf16(o, ref16, n)
     got, want = o16.download(), ref16.download()
     assert np.array_equal(got, want), f"{int(np.sum(got != want))} of {got.size} differ"
+
+
+@pytest.mark.parametrize("pairs,dim", [(2, 3840), (2, 37), (3, 8)])
+def test_modulation_rows_equals_affine_and_tanh(be, orc, pairs, dim):
+    """sdh_modulation_rows on [2P, D] equals affine_(row 2p, 1, 1) and
+    tanh_(row 2p + 1), bit for bit (zimage.cpp:104-107)."""
+    x = orc.randn((2 * pairs, dim), 9300 + dim, 0.0, 2.0)
+    dx = be.array(x)
+    be.modulation_rows(dx, pairs, dim)
+    got = dx.download()
+    want = be.array(x)
+    for p in range(pairs):
+        be.affine(_row(be, want, 2 * p, dim), 1.0, 1.0, dim)
+        be.tanh(_row(be, want, 2 * p + 1, dim), dim)
+    assert np.array_equal(got, want.download())
+
+
+def _row(be, arr, r, dim):
+    import sdhip
+
+    return sdhip.DArray(be, (dim,), ptr=arr.ptr + 4 * r * dim, owned=False)
