@@ -400,6 +400,43 @@ class RmsGatedAdd(Workload):
         return run, [hx, ha, hw, hg], lambda outs: {"x": _peek(R, hx, (T, D))}
 
 
+class RmsGatedAddMod(Workload):
+    """The Z-Image block's residual add + RMSNorm + modulate: one sublayer's
+    norm + gated residual and the next sublayer's bf16 input, x read once."""
+    name, kernel = "rms_norm_gated_add_modulate_bf16", "k_rms_gated_add_mod"
+    desc = ("Z-Image block: x += gate * rms_norm(a) * w1, then y16 = bf16(rms_norm(x) * w2 * (1 + scale)) "
+            "(zimage.cpp:124-129); x, a [4096,3840], w1, gate, w2, scale [3840]; eps 1e-5")
+    algo_bytes = 3 * T * D * 4 + T * D * 2 + 4 * D * 4
+    inputs = (("x", (T, D), 0.0, 1.0, 24), ("a", (T, D), 0.0, 3.0, 25), ("w", (D,), 1.0, 0.1, 26),
+              ("g", (D,), 0.0, 0.5, 27), ("w2", (D,), 1.0, 0.1, 22), ("sc", (D,), 1.0, 0.2, 23))
+    results = {"x": ("rel", 1e-4), "y16": ("rel", 1e-2)}
+
+    def make(self, be, i):
+        d = super().make(be, i)
+        d["y16"] = be.array(np.zeros(T * D, np.uint16))
+        return d
+
+    def step(self, be, s):
+        be.rms_norm_gated_add_modulate_bf16(s["x"], s["a"], s["y16"], T, D, s["w"], s["g"], s["w2"], s["sc"], 1e-5)
+
+    def gpu_results(self, be, s):
+        return {"x": s["x"].download().reshape(T, D), "y16": _bf16_to_f32(s["y16"].download()).reshape(T, D)}
+
+    def cpu(self, R, h):
+        hx, ha = R.new((T, D), h["x"]), R.new((T, D), h["a"])
+        hw, hg, hw2, hsc = (R.new((D,), h[k]) for k in ("w", "g", "w2", "sc"))
+
+        def run():
+            y = R._ptr(R.lib.ref_rms_norm(ha, hw, 1e-5))
+            R._chk(R.lib.ref_add_rows_scaled_(hx, y, hg))
+            z = R._ptr(R.lib.ref_rms_norm(hx, hw2, 1e-5))
+            R._chk(R.lib.ref_mul_rows_(z, hsc))
+            return [y, z]
+
+        return run, [hx, ha, hw, hg, hw2, hsc], lambda outs: {
+            "x": _peek(R, hx, (T, D)), "y16": _bf16_to_f32(_bf16_bits(_peek(R, outs[1], (T, D))))}
+
+
 class Softmax(Workload):
     name, kernel = "softmax_rows", "k_softmax"
     desc = "config 5b: in-place row softmax of scores [30,4096,4096] ~N(0,3), scale 1/sqrt(128), non-causal"
@@ -795,6 +832,7 @@ def all_workloads():
         QKNormRope(unfused=True),
         RmsModBf16(),
         RmsGatedAdd(),
+        RmsGatedAddMod(),
     ] + [Layout(n) for n in Layout.SPECS] + [Linear(k) for k in ("linear_bf16", "linear_swiglu", "linear_swiglu_unfused")] + [
         Attention(), AttentionFp16(), AttentionVAE(), ZImageStep(), ZImageStepFp16Attention()]
 
@@ -957,7 +995,8 @@ KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
     "k_upsample2x_vec": "upsample_nearest2x", "k_concat_vec": "concat_channels", "k_patchify": "patchify2d",
     "k_qknorm_rope_il": "qknorm_rope", "k_attn_fwd<128, false, false, true>": "attention",
     "k_attn_fwd<128, false, false, false>": "attention_fp16", "k_rms_mod_bf16": "rms_norm_modulate_bf16",
-    "k_rms_gated_add": "rms_norm_gated_add", "copyBuffer": "blit_calibration",
+    "k_rms_gated_add_mod": "rms_norm_gated_add_modulate_bf16", "k_rms_gated_add": "rms_norm_gated_add",
+    "copyBuffer": "blit_calibration",
 }
 
 

@@ -205,6 +205,16 @@ int sdh_rms_norm_modulate_bf16(const float* x, uint16_t* y, int64_t rows, int64_
  * fp32 results. a is not modified; x and a must not overlap. */
 int sdh_rms_norm_gated_add(float* x, const float* a, int64_t rows, int64_t C, const float* gamma, const float* gate,
                            float eps);
+/* FUSED (residual add + RMSNorm + modulate; zimage.cpp:124-129, :132-135 ->
+ * :114-116): x += gate * rms_norm(a, gamma_out, eps_out), then y = bf16 bits
+ * of rms_norm(x, gamma_in, eps_in) * scale for the updated x: one sublayer's
+ * norm + gated residual and the next sublayer's modulated input in one pass
+ * over x; x and y are bit-equal to sdh_rms_norm_gated_add followed by
+ * sdh_rms_norm_modulate_bf16. gamma_out, gate, gamma_in and scale may be
+ * NULL; x and a must not overlap, nor y either of them. */
+int sdh_rms_norm_gated_add_modulate_bf16(float* x, const float* a, uint16_t* y, int64_t rows, int64_t C,
+                                         const float* gamma_out, const float* gate, const float* gamma_in,
+                                         const float* scale, float eps_out, float eps_in);
 /* FUSED: y = bf16 bits of swiglu(gate, up): swiglu then the bf16 rounding of
  * gemm_nt_bf16's A (the input of the FFN's w2, zimage.cpp:130). */
 int sdh_swiglu_bf16(const float* gate, const float* up, uint16_t* y, int64_t n);

@@ -77,6 +77,8 @@ STUB(int sdh_gemm_nt_bf16_packed(int64_t, int64_t, int64_t, const uint16_t*, int
                                  int64_t, const float*, int))
 STUB(int sdh_rms_norm_modulate_bf16(const float*, uint16_t*, int64_t, int64_t, const float*, const float*, float))
 STUB(int sdh_rms_norm_gated_add(float*, const float*, int64_t, int64_t, const float*, const float*, float))
+STUB(int sdh_rms_norm_gated_add_modulate_bf16(float*, const float*, uint16_t*, int64_t, int64_t, const float*,
+                                              const float*, const float*, const float*, float, float))
 STUB(int sdh_swiglu_bf16(const float*, const float*, uint16_t*, int64_t))
 STUB(int sdh_gemm_nt_f32(int64_t, int64_t, int64_t, const float*, int64_t, const float*, int64_t, float*, int64_t,
                          const float*, int))

@@ -444,7 +444,7 @@ __global__ __launch_bounds__(kThreads) void k_qknorm_rope_il(QKArgs a, int64_t S
     const f4 g = gp ? ((const f4*)gp)[h] : f4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
     for (int j = 0; j < RV; ++j) {
-        const float q = dev::group_sum<L>(dev::hsum(v[j] * v[j]));
+        const float q = dev::group_sum<L>(dev::sumsq4(v[j]));
         const float rstd = dev::rstd_fast(q, 1.0f / (4 * L), eps);  // dim = 4 L
         f4 o = v[j] * rstd;
         if (gp) o = o * g;
@@ -489,7 +489,7 @@ __global__ __launch_bounds__(kThreads) void k_qknorm_rope_half(QKArgs a, int64_t
     const f4 ghi = gp ? ((const f4*)gp)[k + L] : f4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
     for (int j = 0; j < RV; ++j) {
-        const float q = dev::group_sum<L>(dev::hsum(lo[j] * lo[j]) + dev::hsum(hi[j] * hi[j]));
+        const float q = dev::group_sum<L>(dev::sumsq4(lo[j]) + dev::sumsq4(hi[j]));
         const float rstd = dev::rstd_fast(q, 1.0f / (8 * L), eps);  // dim = 8 L
         f4 a0 = lo[j] * rstd, b0 = hi[j] * rstd;
         if (gp) {

@@ -90,7 +90,7 @@ __global__ __launch_bounds__(kThreads) void k_rownorm(const float* __restrict__ 
     } else {
         float q = 0.f;
 #pragma unroll
-        for (int j = 0; j < V; ++j) q += dev::hsum(v[j] * v[j]);
+        for (int j = 0; j < V; ++j) q += dev::sumsq4(v[j]);
         rstd = rstd_of(dev::wave_sum(q), C, eps);
     }
 #pragma unroll
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void k_add_rms(float* __restrict__ x, con
     for (int j = 0; j < V; ++j) {
         const int idx = lane + 64 * j;
         if (idx < n4) dev::st_stream(xr + idx, v[j]);
-        q += dev::hsum(v[j] * v[j]);
+        q += dev::sumsq4(v[j]);
     }
     const float rstd = rstd_of(dev::wave_sum(q), C, eps);
 #pragma unroll
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void k_heads(float* __restrict__ x, int64
     const bool ok = grp < groups;
     f4* p = (f4*)(x + grp * dim) + sub;
     const f4 v = ok ? *p : zero4();
-    const float q = dev::group_sum<L>(dev::hsum(v * v));  // all 64 lanes take part
+    const float q = dev::group_sum<L>(dev::sumsq4(v));  // all 64 lanes take part
     const float rstd = dev::rstd_fast(q, 1.0f / (4 * L), eps);  // dim = 4 L
     f4 o = v * rstd;
     if constexpr (HAS_G) o = o * ((const f4*)gamma)[sub];
@@ -407,7 +407,7 @@ __global__ __launch_bounds__(kThreads) void k_rms_mod_bf16(const float* __restri
     }
     float q = 0.f;
 #pragma unroll
-    for (int j = 0; j < V; ++j) q += dev::hsum(v[j] * v[j]);
+    for (int j = 0; j < V; ++j) q += dev::sumsq4(v[j]);
     const float rstd = rstd_of(dev::wave_sum(q), C, eps);
     auto out = [&](int j) __attribute__((always_inline)) {
         const int idx = lane + 64 * j;
@@ -465,7 +465,7 @@ __global__ __launch_bounds__(kThreads) void k_rms_gated_add(float* __restrict__ 
     }
     float q = 0.f;
 #pragma unroll
-    for (int j = 0; j < V; ++j) q += dev::hsum(v[j] * v[j]);
+    for (int j = 0; j < V; ++j) q += dev::sumsq4(v[j]);
     const float rstd = rstd_of(dev::wave_sum(q), C, eps);
 #pragma unroll
     for (int j = 0; j < V; ++j) {
@@ -517,7 +517,7 @@ __global__ __launch_bounds__(kRowThreads) void k_rms_gated_add_row(float* __rest
         xv[j] = idx < n4 ? dev::ld_stream(xr + idx) : zero4();
     }
 #pragma unroll
-    for (int j = 0; j < V; ++j) hs[p + 4 * j][lane] = dev::hsum(v[j] * v[j]);
+    for (int j = 0; j < V; ++j) hs[p + 4 * j][lane] = dev::sumsq4(v[j]);
     __syncthreads();
     float q = 0.f;
 #pragma unroll
@@ -541,6 +541,160 @@ __global__ __launch_bounds__(kRowThreads) void k_rms_gated_add_row(float* __rest
             dev::st_stream(xr + idx, r);
         }
     }
+}
+
+// ---- residual add + RMSNorm + modulate: one sublayer's end and the next one's input ----
+// x += gate * rms_norm(a, g1), then y16 = bf16(((x * rstd2) * g2) * scale) of
+// the updated row: rms_norm_gated_add then rms_norm_modulate_bf16
+// (zimage.cpp:124-129 and :132-135 -> :114-116), x read once instead of
+// twice. Each half keeps its op's expressions and its sum of squares in the
+// one-wave order (per lane l: float4 l, l + 64, ... in sequence, then the
+// wave tree), so x and y16 are bit-equal to the two ops'. The vectors are
+// optional (null: that product or the gate is left out, as in the two ops).
+
+// x + gate * (a rstd gamma), k_rms_gated_add's expression
+__device__ __forceinline__ f4 gated_add4(const f4& v, const f4& xo, float rstd, const float* g1, const float* gate,
+                                         int idx) {
+#pragma clang fp contract(off)
+    f4 o = v * rstd;
+    if (g1) o = o * ((const f4*)g1)[idx];
+    if (!gate) return xo + o;
+    const f4 g = ((const f4*)gate)[idx];
+    return f4{fmaf(g.x, o.x, xo.x), fmaf(g.y, o.y, xo.y), fmaf(g.z, o.z, xo.z), fmaf(g.w, o.w, xo.w)};
+}
+
+// Stores y16 for V float4 of the updated row (r, zero past the row), lane's
+// float4 at step j being lane + base(j); k_rms_mod_bf16's products. PAIR
+// (n4 % 64 == 0, y 16-byte aligned): k_rms_mod_bf16's paired 16-byte stores.
+template <int V, bool PAIR, class Base>
+__device__ __forceinline__ void store_mod_bf16(uint2* yr, const f4 (&r)[V], float rstd, const float* g2,
+                                               const float* scale, int lane, int n4, Base base) {
+    auto out = [&](int j) __attribute__((always_inline)) {
+        const int idx = lane + base(j);
+        if (idx >= n4) return uint2{0u, 0u};
+        f4 o = r[j] * rstd;
+        if (g2) o = o * ((const f4*)g2)[idx];
+        if (scale) o = o * ((const f4*)scale)[idx];
+        return dev::bf16x4(o);
+    };
+    if constexpr (PAIR) {
+        const bool odd = lane & 1;
+        auto swap = [](unsigned u) { return (unsigned)__builtin_amdgcn_mov_dpp((int)u, 0xB1, 0xF, 0xF, false); };
+#pragma unroll
+        for (int j = 0; j + 1 < V; j += 2) {
+            const uint2 b0 = out(j), b1 = out(j + 1);
+            const uint2 send = odd ? b0 : b1;
+            const uint2 rr = {swap(send.x), swap(send.y)};
+            const dev::u4v w = odd ? dev::u4v{rr.x, rr.y, b1.x, b1.y} : dev::u4v{b0.x, b0.y, rr.x, rr.y};
+            const int pos = odd ? lane - 1 + base(j + 1) : lane + base(j);
+            if (pos < n4) __builtin_nontemporal_store(w, reinterpret_cast<dev::u4v*>(yr + pos));
+        }
+        if constexpr (V & 1) {
+            if (lane + base(V - 1) < n4) dev::st_stream(yr + lane + base(V - 1), out(V - 1));
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+            if (lane + base(j) < n4) dev::st_stream(yr + lane + base(j), out(j));
+    }
+}
+
+// one wave per row (rows of up to 64 V float4), 4 rows per workgroup
+template <int V, bool PAIR>
+__global__ __launch_bounds__(kThreads) void k_rms_gated_add_mod(float* __restrict__ x, const float* __restrict__ a,
+                                                               uint2* __restrict__ y, int64_t rows, int C,
+                                                               const float* __restrict__ g1,
+                                                               const float* __restrict__ gate,
+                                                               const float* __restrict__ g2,
+                                                               const float* __restrict__ scale, float eps1,
+                                                               float eps2) {
+    const int lane = threadIdx.x & 63;
+    const int n4 = C >> 2;
+    const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const f4* ar = (const f4*)(a + row * C);
+    f4* xr = (f4*)(x + row * C);
+    f4 v[V], xv[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * j;
+        v[j] = idx < n4 ? dev::ld_stream(ar + idx) : zero4();
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * j;
+        xv[j] = idx < n4 ? dev::ld_stream(xr + idx) : zero4();
+    }
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) q += dev::sumsq4(v[j]);
+    const float rstd1 = rstd_of(dev::wave_sum(q), C, eps1);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * j;
+        if (idx < n4) {
+            xv[j] = gated_add4(v[j], xv[j], rstd1, g1, gate, idx);
+            dev::st_stream(xr + idx, xv[j]);
+        }
+    }
+    float q2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < V; ++j) q2 += dev::sumsq4(xv[j]);
+    const float rstd2 = rstd_of(dev::wave_sum(q2), C, eps2);
+    store_mod_bf16<V, PAIR>(y + row * n4, xv, rstd2, g2, scale, lane, n4, [](int j) { return 64 * j; });
+}
+
+// one 256-thread workgroup per row (2048 < C <= 8192), wave p lane l holding
+// float4 l + 64 (p + 4 j); both sums of squares in the one-wave order through LDS
+template <int V, bool PAIR>
+__global__ __launch_bounds__(kRowThreads) void k_rms_gated_add_mod_row(float* __restrict__ x,
+                                                                      const float* __restrict__ a,
+                                                                      uint2* __restrict__ y, int C,
+                                                                      const float* __restrict__ g1,
+                                                                      const float* __restrict__ gate,
+                                                                      const float* __restrict__ g2,
+                                                                      const float* __restrict__ scale, float eps1,
+                                                                      float eps2) {
+    __shared__ float hs[2][4 * V][64];  // hs[h][k][l]: squared sum of float4 l + 64 k of a (h = 0), of x (h = 1)
+    const int lane = threadIdx.x & 63, p = threadIdx.x >> 6;
+    const int n4 = C >> 2;
+    const int64_t row = blockIdx.x;
+    const f4* ar = (const f4*)(a + row * C);
+    f4* xr = (f4*)(x + row * C);
+    f4 v[V], xv[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * (p + 4 * j);
+        v[j] = idx < n4 ? dev::ld_stream(ar + idx) : zero4();
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * (p + 4 * j);
+        xv[j] = idx < n4 ? dev::ld_stream(xr + idx) : zero4();
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) hs[0][p + 4 * j][lane] = dev::sumsq4(v[j]);
+    __syncthreads();
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4 * V; ++k) q += hs[0][k][lane];  // zero entries past the row add exactly 0
+    const float rstd1 = rstd_of(dev::wave_sum(q), C, eps1);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int idx = lane + 64 * (p + 4 * j);
+        if (idx < n4) {
+            xv[j] = gated_add4(v[j], xv[j], rstd1, g1, gate, idx);
+            dev::st_stream(xr + idx, xv[j]);
+        }
+        hs[1][p + 4 * j][lane] = dev::sumsq4(xv[j]);
+    }
+    __syncthreads();
+    float q2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4 * V; ++k) q2 += hs[1][k][lane];
+    const float rstd2 = rstd_of(dev::wave_sum(q2), C, eps2);
+    store_mod_bf16<V, PAIR>(y + row * n4, xv, rstd2, g2, scale, lane, n4,
+                            [p](int j) { return 64 * (p + 4 * j); });
 }
 
 // the row-per-workgroup kernels' float4 per lane for a row of n4 float4, or 0
@@ -782,6 +936,60 @@ void run_rms_gated_add(float* x, const float* a, int64_t rows, int64_t C, const 
     launched(op);
 }
 
+void run_rms_gated_add_mod(float* x, const float* a, uint16_t* y, int64_t rows, int64_t C, const float* g1,
+                           const float* gate, const float* g2, const float* scale, float eps1, float eps2) {
+    const char* op = "sdh_rms_norm_gated_add_modulate_bf16";
+    need(rows >= 0 && C >= 0, op, "negative size");
+    if (rows == 0 || C == 0) return;
+    ensure_init();
+    const size_t bytes = (size_t)(rows * C) * 4, ybytes = (size_t)(rows * C) * 2;
+    check_range(x, bytes, op, "x");
+    check_range(a, bytes, op, "a");
+    check_range(y, ybytes, op, "y");
+    for (const float* vec : {g1, gate, g2, scale})
+        if (vec) check_range(vec, (size_t)C * 4, op, "a column vector");
+    need(!overlaps(x, bytes, a, bytes), op, "x overlaps a");
+    need(!overlaps(y, ybytes, x, bytes) && !overlaps(y, ybytes, a, bytes), op, "y overlaps x or a");
+    const int64_t n4 = C / 4;
+    const bool vec = vec_ok(C, {x, a, g1, gate, g2, scale}) && ((uintptr_t)y & 7) == 0;
+    if (!vec) {
+        // the two ops, each on its own general kernel
+        run_rms_gated_add(x, a, rows, C, g1, gate, eps1);
+        run_rms_mod_bf16(x, y, rows, C, g2, scale, eps2);
+        return;
+    }
+    const bool pair = n4 % 64 == 0 && ((uintptr_t)y & 15) == 0;
+    uint2* yy = (uint2*)y;
+    const int rv = pick_row_v(n4);
+    if (rv) {
+        in_pieces(rows, units_per_launch(kRowThreads), [&](int64_t r0, int64_t nr) {
+            const int64_t o = r0 * C;
+            auto go = [&](auto vc, auto pc) {
+                constexpr int V = decltype(vc)::value;
+                constexpr bool P = decltype(pc)::value;
+                k_rms_gated_add_mod_row<V, P><<<(unsigned)nr, kRowThreads, 0, stream()>>>(
+                    x + o, a + o, yy + r0 * n4, (int)C, g1, gate, g2, scale, eps1, eps2);
+            };
+            if (rv == 4) pair ? go(std::integral_constant<int, 4>(), std::true_type()) : go(std::integral_constant<int, 4>(), std::false_type());
+            else pair ? go(std::integral_constant<int, 8>(), std::true_type()) : go(std::integral_constant<int, 8>(), std::false_type());
+        });
+    } else {
+        in_pieces(rows, rows_per_launch(), [&](int64_t r0, int64_t nr) {
+            const int64_t o = r0 * C;
+            with_v(pick_v(n4), [&](auto vc) {
+                constexpr int V = decltype(vc)::value;
+                if (pair)
+                    k_rms_gated_add_mod<V, true><<<exact_grid(nr), kThreads, 0, stream()>>>(
+                        x + o, a + o, yy + r0 * n4, nr, (int)C, g1, gate, g2, scale, eps1, eps2);
+                else
+                    k_rms_gated_add_mod<V, false><<<exact_grid(nr), kThreads, 0, stream()>>>(
+                        x + o, a + o, yy + r0 * n4, nr, (int)C, g1, gate, g2, scale, eps1, eps2);
+            });
+        });
+    }
+    launched(op);
+}
+
 }  // namespace
 }  // namespace sdh
 
@@ -797,6 +1005,12 @@ int sdh_rms_norm_modulate_bf16(const float* x, uint16_t* y, int64_t rows, int64_
 int sdh_rms_norm_gated_add(float* x, const float* a, int64_t rows, int64_t C, const float* gamma, const float* gate,
                            float eps) {
     return guarded([&] { run_rms_gated_add(x, a, rows, C, gamma, gate, eps); });
+}
+
+int sdh_rms_norm_gated_add_modulate_bf16(float* x, const float* a, uint16_t* y, int64_t rows, int64_t C,
+                                         const float* gamma_out, const float* gate, const float* gamma_in,
+                                         const float* scale, float eps_out, float eps_in) {
+    return guarded([&] { run_rms_gated_add_mod(x, a, y, rows, C, gamma_out, gate, gamma_in, scale, eps_out, eps_in); });
 }
 
 int sdh_rms_norm(const float* x, float* y, int64_t rows, int64_t C, const float* gamma, float eps) {

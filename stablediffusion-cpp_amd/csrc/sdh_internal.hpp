@@ -224,6 +224,13 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 __device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
 __device__ __forceinline__ float hsum(const f4& v) { return (v.x + v.y) + (v.z + v.w); }
+// Sum of the squares of a float4 with its rounding fixed: x^2 + y^2 and
+// z^2 + w^2 each as one fused multiply-add, then their sum. The kernels whose
+// results are claimed bit-equal to one another (the RMS norms, their fused
+// forms, QK-norm) form their sums of squares with it, so the compiler's
+// contraction of hsum(v * v), which changes with the surrounding control flow,
+// cannot change their bits.
+__device__ __forceinline__ float sumsq4(const f4& v) { return fmaf(v.x, v.x, v.y * v.y) + fmaf(v.z, v.z, v.w * v.w); }
 
 // Streaming accesses: data touched exactly once per launch is loaded and
 // stored non-temporally so it does not displace reusable lines in L2/MALL.

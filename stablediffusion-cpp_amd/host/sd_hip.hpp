@@ -188,6 +188,13 @@ inline void rms_norm_gated_add(float* x, const float* a, int64_t rows, int64_t C
                                const float* gate, float eps) {
     detail::check(sdh_rms_norm_gated_add(x, a, rows, C, gamma, gate, eps), "hip::rms_norm_gated_add");
 }
+inline void rms_norm_gated_add_modulate_bf16(float* x, const float* a, uint16_t* y, int64_t rows, int64_t C,
+                                            const float* gamma_out, const float* gate, const float* gamma_in,
+                                            const float* scale, float eps_out, float eps_in) {
+    detail::check(sdh_rms_norm_gated_add_modulate_bf16(x, a, y, rows, C, gamma_out, gate, gamma_in, scale, eps_out,
+                                                       eps_in),
+                  "hip::rms_norm_gated_add_modulate_bf16");
+}
 inline void swiglu_bf16(const float* gate, const float* up, uint16_t* y, int64_t n) {
     detail::check(sdh_swiglu_bf16(gate, up, y, n), "hip::swiglu_bf16");
 }

@@ -548,6 +548,25 @@ void rms_norm_gated_add_(Tensor& x, const Tensor& a, const Tensor* gamma, const 
     sd::hip::rms_norm_gated_add(x.dptr(), a.dptr(), rows, C, opt(gamma), opt(gate), eps);
 }
 
+Tensor rms_norm_gated_add_modulate_bf16_(Tensor& x, const Tensor& a, const Tensor* gamma_out, const Tensor* gate,
+                                         const Tensor* gamma_in, const Tensor* scale, float eps) {
+    const char* op = "rms_norm_gated_add_modulate_bf16_";
+    need_hip(x, op);
+    same_device(x, a, op);
+    if (x.numel() != a.numel() || x.dim(-1) != a.dim(-1))
+        throw std::runtime_error("add_rows_scaled_: " + x.shape_str() + " vs " + a.shape_str());
+    const int64_t C = x.dim(-1), rows = count_of(x.numel(), C);
+    for (const Tensor* v : {gamma_out, gate, gamma_in, scale}) {
+        if (!v) continue;
+        same_device(x, *v, op);
+        if (v->numel() != C) throw std::runtime_error(std::string(op) + ": vector length vs " + x.shape_str());
+    }
+    Tensor y = Tensor::empty_bf16(x.shape);
+    sd::hip::rms_norm_gated_add_modulate_bf16(x.dptr(), a.dptr(), y.dptr16(), rows, C, opt(gamma_out), opt(gate),
+                                              opt(gamma_in), opt(scale), eps, eps);
+    return y;
+}
+
 Tensor swiglu_bf16(const Tensor& gate, const Tensor& up) {
     if (gate.numel() != up.numel()) throw std::runtime_error("swiglu: " + gate.shape_str() + " vs " + up.shape_str());
     same_device(gate, up, "swiglu");

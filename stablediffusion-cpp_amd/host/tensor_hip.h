@@ -133,6 +133,10 @@ Tensor conv2d(const Tensor& x, const Tensor& W, const Tensor* b, int stride, int
 Tensor rms_norm_modulate_bf16(const Tensor& x, const Tensor* gamma, const Tensor* scale, float eps);
 // x += *gate * rms_norm(a, gamma, eps), or x += rms_norm(a, gamma, eps) without a gate
 void rms_norm_gated_add_(Tensor& x, const Tensor& a, const Tensor* gamma, const Tensor* gate, float eps);
+// rms_norm_gated_add_(x, a, gamma_out, gate, eps), then
+// rms_norm_modulate_bf16(x, gamma_in, scale, eps) of the updated x, in one pass
+Tensor rms_norm_gated_add_modulate_bf16_(Tensor& x, const Tensor& a, const Tensor* gamma_out, const Tensor* gate,
+                                         const Tensor* gamma_in, const Tensor* scale, float eps);
 // swiglu(gate, up) rounded to BF16 (the input of the FFN's w2)
 Tensor swiglu_bf16(const Tensor& gate, const Tensor& up);
 

@@ -315,33 +315,64 @@ struct ZImageTransformer::Impl {
         return project(hidden, b, kProjDown);
     }
 
-    // One block on rows x ([1, S, dim], a range of the token buffer, updated
-    // in place), rotary rows cos/sin [S, head_dim], conditioning vector cond
-    // (modulated blocks). Each of its two sublayers adds
+    // A block's modulation rows (zimage.cpp:104-107): 1 + scale and tanh(gate)
+    // for the attention and the FFN sublayer; none for unmodulated blocks.
+    struct Modulation {
+        Tensor mod;  // [4, dim]: attention scale, attention gate, FFN scale, FFN gate
+        Tensor scale[2], gate[2];
+        bool on = false;
+        const Tensor* scale_of(int s) const { return on ? &scale[s] : nullptr; }
+        const Tensor* gate_of(int s) const { return on ? &gate[s] : nullptr; }
+    };
+
+    Modulation modulation(const BlockBinding& b, const Tensor* cond) const {
+        Modulation m;
+        if (!b.modulated) return m;
+        m.on = true;
+        m.mod = project(*cond, b, kProjMod);
+        m.mod.reshape({4, dim});
+        modulation_rows_(m.mod);  // 1 + scale, tanh(gate): one launch
+        for (int s = 0; s < 2; ++s) {
+            m.scale[s] = rows_view(m.mod, 2 * s, 2 * s + 1);
+            m.gate[s] = rows_view(m.mod, 2 * s + 1, 2 * s + 2);
+            m.scale[s].reshape({dim});
+            m.gate[s].reshape({dim});
+        }
+        return m;
+    }
+
+    // Closes a sublayer of block b: x += gate * rms_norm(out). With next, also
+    // returns the input of the sublayer that follows (next's norm role nn,
+    // modulated by scale); in one pass over x when both blocks run fused.
+    Tensor close_sublayer(const BlockBinding& b, Tensor& x, const Tensor& out, NormRole n, const Tensor* gate,
+                          const BlockBinding* next, NormRole nn, const Tensor* scale) const {
+        if (next && b.fused_bf16 && next->fused_bf16)
+            return rms_norm_gated_add_modulate_bf16_(x, out, b.norm[n], gate, next->norm[nn], scale, cfg.norm_eps);
+        rms_norm_gated_add_(x, out, b.norm[n], gate, cfg.norm_eps);
+        return next ? sublayer_input(*next, x, nn, scale) : Tensor();
+    }
+
+    // A stack of blocks on rows x ([1, S, dim], a range of the token buffer,
+    // updated in place), rotary rows cos/sin [S, head_dim], conditioning
+    // vector cond (modulated stacks). Each block's two sublayers add
     // gate * rms_norm(sublayer(rms_norm(x) * (1 + scale))) to x, attention
     // first, then the FFN; unmodulated blocks have no scale and gate
-    // (zimage.cpp:90-136).
-    void run(const BlockBinding& b, Tensor& x, const Tensor& cos, const Tensor& sin, const Tensor* cond) const {
-        // the modulation rows: attention scale, attention gate, FFN scale, FFN gate
-        Tensor mod, scale[2], gate[2];
-        if (b.modulated) {
-            mod = project(*cond, b, kProjMod);
-            mod.reshape({4, dim});
-            modulation_rows_(mod);  // 1 + scale, tanh(gate): one launch
-            for (int s = 0; s < 2; ++s) {
-                scale[s] = rows_view(mod, 2 * s, 2 * s + 1);
-                gate[s] = rows_view(mod, 2 * s + 1, 2 * s + 2);
-                scale[s].reshape({dim});
-                gate[s].reshape({dim});
-            }
-        }
-        for (int s = 0; s < 2; ++s) {
-            const bool attn = s == 0;
-            const Tensor* sc = b.modulated ? &scale[s] : nullptr;
-            const Tensor* gt = b.modulated ? &gate[s] : nullptr;
-            Tensor in = sublayer_input(b, x, attn ? kNormAttnIn : kNormFfnIn, sc);
-            Tensor out = attn ? attend(b, in, cos, sin) : feed_forward(b, in);
-            rms_norm_gated_add_(x, out, b.norm[attn ? kNormAttnOut : kNormFfnOut], gt, cfg.norm_eps);
+    // (zimage.cpp:90-136). A sublayer's input is formed where the previous
+    // sublayer closes, the next block's modulation computed one block ahead.
+    void run_stack(const std::vector<BlockBinding>& blocks, Tensor& x, const Tensor& cos, const Tensor& sin,
+                   const Tensor* cond) const {
+        if (blocks.empty()) return;
+        Modulation cur = modulation(blocks[0], cond);
+        Tensor in = sublayer_input(blocks[0], x, kNormAttnIn, cur.scale_of(0));
+        for (size_t i = 0; i < blocks.size(); ++i) {
+            const BlockBinding& b = blocks[i];
+            const BlockBinding* nb = i + 1 < blocks.size() ? &blocks[i + 1] : nullptr;
+            Modulation nxt = nb ? modulation(*nb, cond) : Modulation();
+            Tensor out = attend(b, in, cos, sin);
+            in = close_sublayer(b, x, out, kNormAttnOut, cur.gate_of(0), &b, kNormFfnIn, cur.scale_of(1));
+            out = feed_forward(b, in);
+            in = close_sublayer(b, x, out, kNormFfnOut, cur.gate_of(1), nb, kNormAttnIn, nxt.scale_of(0));
+            cur = std::move(nxt);
         }
     }
 
@@ -385,10 +416,10 @@ Tensor ZImageTransformer::forward(const Tensor& latent, float t, const Tensor& t
         Tensor x = as_sequence(rows_view(seq, split[part], split[part + 1]));
         const Tensor c = rows_view(rot.first, split[part], split[part + 1]);
         const Tensor s = rows_view(rot.second, split[part], split[part + 1]);
-        for (const BlockBinding& b : m.stacks[st]) m.run(b, x, c, s, kStackModulated[st] ? &cond : nullptr);
+        m.run_stack(m.stacks[st], x, c, s, kStackModulated[st] ? &cond : nullptr);
     }
     Tensor all = as_sequence(rows_view(seq, 0, g.rows()));
-    for (const BlockBinding& b : m.stacks[kMainStack]) m.run(b, all, rot.first, rot.second, &cond);
+    m.run_stack(m.stacks[kMainStack], all, rot.first, rot.second, &cond);
     return m.head(seq, cond, g, latent.dim(2), latent.dim(3));
 }
 

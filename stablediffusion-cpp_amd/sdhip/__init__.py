@@ -86,6 +86,7 @@ SIGNATURES = {
     "sdh_gemm_nt_bf16_packed": [_i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, C.c_int],
     "sdh_rms_norm_modulate_bf16": [_vp, _vp, _i64, _i64, _vp, _vp, _fl],
     "sdh_rms_norm_gated_add": [_vp, _vp, _i64, _i64, _vp, _vp, _fl],
+    "sdh_rms_norm_gated_add_modulate_bf16": [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _fl, _fl],
     "sdh_swiglu_bf16": [_vp, _vp, _vp, _i64],
     "sdh_gemm_nt_f32": [_i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, C.c_int],
     "sdh_conv2d": [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, C.c_int, C.c_int, _vp, _i64, _i64],
@@ -368,6 +369,11 @@ class Backend:
 
     def rms_norm_gated_add(self, x, a, rows, C, gamma, gate, eps):
         self.call("sdh_rms_norm_gated_add", _p(x), _p(a), rows, C, _p(gamma), _p(gate), eps)
+
+    def rms_norm_gated_add_modulate_bf16(self, x, a, y16, rows, C, gamma_out, gate, gamma_in, scale, eps_out,
+                                         eps_in=None):
+        self.call("sdh_rms_norm_gated_add_modulate_bf16", _p(x), _p(a), _p(y16), rows, C, _p(gamma_out), _p(gate),
+                  _p(gamma_in), _p(scale), eps_out, eps_out if eps_in is None else eps_in)
 
     def swiglu_bf16(self, g, u, y16, n):
         self.call("sdh_swiglu_bf16", _p(g), _p(u), _p(y16), n)

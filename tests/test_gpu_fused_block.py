@@ -6,6 +6,11 @@ same bf16 rounding), so the bar is exact equality:
     (zimage.cpp:115-116, :128-129, then gemm_nt_bf16's rounding of A);
   * sdh_rms_norm_gated_add == rms_norm -> add_rows_scaled (or add_)
     (zimage.cpp:124-127, :132-135);
+  * sdh_rms_norm_gated_add_modulate_bf16 == sdh_rms_norm_gated_add ->
+    sdh_rms_norm_modulate_bf16 (zimage.cpp:124-129, one sublayer's close and
+    the next one's input);
+  * sdh_modulation_rows == affine_(1, 1) / tanh_ on alternate rows
+    (zimage.cpp:104-107);
   * sdh_swiglu_bf16 == swiglu -> to_bf16 (zimage.cpp:130, the input of w2);
   * sdh_gemm_nt_bf16_packed(bf16 A) == sdh_gemm_nt_bf16(the same values in
     fp32), and within the fp32 accumulation bound of the exact sum for the
@@ -168,3 +173,64 @@ def _row(be, arr, r, dim):
     import sdhip
 
     return sdhip.DArray(be, (dim,), ptr=arr.ptr + 4 * r * dim, owned=False)
+
+
+FUSED_ROWS = [(4224, 3840), (64, 3072), (9, 2080), (70, 512), (33, 1000), (5, 64), (7, 30)]
+
+
+@pytest.mark.parametrize("rows,C", FUSED_ROWS)
+@pytest.mark.parametrize("vecs", [(True, True, True, True), (True, False, True, False), (False, True, False, True)])
+def test_rms_norm_gated_add_modulate_bf16(be, orc, rows, C, vecs):
+    """residual add + RMSNorm + modulate == sdh_rms_norm_gated_add then
+    sdh_rms_norm_modulate_bf16, bit for bit, x and y (every kernel shape:
+    workgroup per row with and without paired stores, wave per row with and
+    without, the two-op path for rows not a multiple of 4)."""
+    has_g1, has_gate, has_g2, has_scale = vecs
+    x = orc.randn((rows, C), 730 + C)
+    a = orc.randn((rows, C), 731 + C, 0.0, 3.0)
+    vec = lambda on, seed, mu, sd: be.array(orc.randn((C,), seed, mu, sd)) if on else None
+    g1, gate = vec(has_g1, 732, 1.0, 0.1), vec(has_gate, 733, 0.0, 0.5)
+    g2, scale = vec(has_g2, 734, 1.0, 0.1), vec(has_scale, 735, 1.0, 0.3)
+    dx, da = be.array(x), be.array(a)
+    y16 = _u16(be, rows * C)
+    be.rms_norm_gated_add_modulate_bf16(dx, da, y16, rows, C, g1, gate, g2, scale, 1e-5, 1e-6)
+    sx = be.array(x)
+    be.rms_norm_gated_add(sx, da, rows, C, g1, gate, 1e-5)
+    s16 = _u16(be, rows * C)
+    be.rms_norm_modulate_bf16(sx, s16, rows, C, g2, scale, 1e-6)
+    got_x, want_x = dx.download(), sx.download()
+    assert np.array_equal(got_x, want_x), f"x: {int(np.sum(got_x != want_x))} of {got_x.size} differ"
+    got, want = y16.download(), s16.download()
+    assert np.array_equal(got, want), f"y: {int(np.sum(got != want))} of {got.size} differ"
+    assert np.array_equal(da.download(), a)  # a is read only
+
+
+def test_rms_norm_gated_add_modulate_bf16_unaligned_y(be, orc):
+    """y 8 bytes past a 16-byte boundary (the unpaired stores)."""
+    import sdhip
+
+    rows, C = 40, 3840
+    x = orc.randn((rows, C), 740)
+    a = orc.randn((rows, C), 741)
+    g = be.array(orc.randn((C,), 742, 1.0, 0.1))
+    s = be.array(orc.randn((C,), 743, 1.0, 0.3))
+    dx, da = be.array(x), be.array(a)
+    buf = _u16(be, rows * C + 4)
+    y16 = sdhip.DArray(be, (rows * C,), ptr=buf.ptr + 8, owned=False, dtype=np.uint16)
+    be.rms_norm_gated_add_modulate_bf16(dx, da, y16, rows, C, g, s, g, s, 1e-5)
+    sx = be.array(x)
+    be.rms_norm_gated_add(sx, da, rows, C, g, s, 1e-5)
+    s16 = _u16(be, rows * C)
+    be.rms_norm_modulate_bf16(sx, s16, rows, C, g, s, 1e-5)
+    assert np.array_equal(dx.download(), sx.download())
+    assert np.array_equal(y16.download(), s16.download())
+
+
+def test_rms_norm_gated_add_modulate_bf16_rejects_overlap(be, orc):
+    import sdhip
+
+    rows, C = 4, 256
+    dx, da = be.array(orc.randn((rows, C), 744)), be.array(orc.randn((rows, C), 745))
+    y_on_a = sdhip.DArray(be, (rows * C,), ptr=da.ptr, owned=False, dtype=np.uint16)
+    with pytest.raises(sdhip.SdhError, match="overlaps"):
+        be.rms_norm_gated_add_modulate_bf16(dx, da, y_on_a, rows, C, None, None, None, None, 1e-5)
