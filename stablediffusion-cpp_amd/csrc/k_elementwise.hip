@@ -357,6 +357,7 @@ int sdh_modulation_rows(float* x, int64_t pairs, int64_t dim) {
     return guarded([&] {
         const char* op = "sdh_modulation_rows";
         need(pairs >= 0 && dim >= 0, op, "negative size");
+        need(dim == 0 || pairs <= (INT64_MAX / 8) / dim, op, "size overflows");
         const int64_t n = 2 * pairs * dim;
         if (n == 0) return;
         ensure_init();

@@ -101,6 +101,18 @@ def main():
     dxw = be.array(xw)
     be.rms_norm_gated_add(dxw, be.array(yw), 40, 3840, be.array(gw), be.array(vw), 1e-5)
     assert_reduction(dxw.download(), orc.add_rows_scaled(xw, orc.rms_norm(yw, gw, 1e-5), vw), "gated_add, wide rows")
+    # residual add + RMSNorm + modulate, narrow and wide rows, against the two ops in the same pieces
+    for xx, yy, gg, vv in ((x, y, dg, dv), (xw, yw, be.array(gw), be.array(vw))):
+        r_, c_ = xx.shape
+        dxf, dyf = be.array(xx), be.array(yy)
+        f16 = be.array(np.zeros(r_ * c_, np.uint16))
+        be.rms_norm_gated_add_modulate_bf16(dxf, dyf, f16, r_, c_, gg, vv, gg, vv, 1e-5)
+        dxs = be.array(xx)
+        be.rms_norm_gated_add(dxs, dyf, r_, c_, gg, vv, 1e-5)
+        s16 = be.array(np.zeros(r_ * c_, np.uint16))
+        be.rms_norm_modulate_bf16(dxs, s16, r_, c_, gg, vv, 1e-5)
+        assert np.array_equal(dxf.download(), dxs.download()), f"gated_add_modulate x, rows of {c_}"
+        assert np.array_equal(f16.download(), s16.download()), f"gated_add_modulate y, rows of {c_}"
     h = orc.randn((3000, 128), 12)
     gh = orc.randn((128,), 13, 1.0, 0.1)
     dh = be.array(h)
