@@ -7,6 +7,7 @@
 #include <unistd.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 #include <utility>
@@ -44,6 +45,8 @@ public:
 private:
     const char* p_;
     const char* end_;
+    int depth_ = 0;  // open objects and arrays; a header nests two or three deep
+    static constexpr int kMaxDepth = 64;
     [[noreturn]] void fail(const char* what) { throw std::runtime_error(std::string("safetensors header: ") + what); }
     void ws() {
         while (p_ < end_ && (*p_ == ' ' || *p_ == '\t' || *p_ == '\n' || *p_ == '\r')) ++p_;
@@ -116,6 +119,7 @@ private:
                     if (cp >= 0xD800 && cp < 0xDC00 && end_ - p_ >= 6 && p_[0] == '\\' && p_[1] == 'u') {
                         p_ += 2;
                         const unsigned lo = hex4();
+                        if (lo < 0xDC00 || lo > 0xDFFF) fail("bad surrogate pair");
                         cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
                     }
                     put_utf8(s, cp);
@@ -131,10 +135,14 @@ private:
         if (p_ >= end_) fail("unexpected end");
         JValue v;
         const char c = *p_;
+        if ((c == '{' || c == '[') && ++depth_ > kMaxDepth) fail("nesting too deep");
         if (c == '{') {
             ++p_;
             v.kind = JValue::Object;
-            if (take('}')) return v;
+            if (take('}')) {
+                --depth_;
+                return v;
+            }
             do {
                 ws();
                 std::string k = string();
@@ -142,13 +150,18 @@ private:
                 v.obj.emplace_back(std::move(k), value());
             } while (take(','));
             expect('}');
+            --depth_;
         } else if (c == '[') {
             ++p_;
             v.kind = JValue::Array;
-            if (take(']')) return v;
+            if (take(']')) {
+                --depth_;
+                return v;
+            }
             do v.arr.push_back(value());
             while (take(','));
             expect(']');
+            --depth_;
         } else if (c == '"') {
             v.kind = JValue::String;
             v.str = string();
@@ -163,10 +176,13 @@ private:
             p_ += 4;
         } else {
             const char* s = p_;
-            while (p_ < end_ && (std::strchr("+-0123456789.eE", *p_) != nullptr)) ++p_;
+            while (p_ < end_ && *p_ != '\0' && std::strchr("+-0123456789.eE", *p_) != nullptr) ++p_;
             if (s == p_) fail("unexpected character");
             v.kind = JValue::Number;
-            v.num = std::stod(std::string(s, p_));
+            const std::string t(s, p_);
+            char* stop = nullptr;
+            v.num = std::strtod(t.c_str(), &stop);
+            if (stop != t.c_str() + t.size()) fail("bad number");
         }
         return v;
     }
