@@ -11,6 +11,8 @@
 #include <cctype>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
+#include <fstream>
 #include <map>
 #include <mutex>
 #include <stdexcept>
@@ -111,6 +113,24 @@ void project_into(const Tensor& x, const Proj& p, Tensor& out, const char* what)
 
 // Rows [from, to) of a [rows, D] device tensor set to a [1, D] token: one
 // copy of the token, then copies of the rows written so far, doubling.
+// With ZIMAGE_TRACE=<prefix> set, named intermediates of a forward are
+// written as <prefix>_trace_<name>.bin (float32 rows) and .json ({"shape":
+// [rows, cols]}), at the points and under the names the reference's
+// forward uses (zimage.cpp:15-26), so the two can be compared stage by
+// stage. Tensors are downloaded only when the variable is set.
+void trace(const char* name, const Tensor& t) {
+    const char* prefix = std::getenv("ZIMAGE_TRACE");
+    if (!prefix || !*prefix) return;
+    const Tensor h = t.is_hip() ? t.to(Device::CPU) : t;
+    const std::string base = std::string(prefix) + "_trace_" + name;
+    std::ofstream bin(base + ".bin", std::ios::binary);
+    bin.write(reinterpret_cast<const char*>(h.ptr()), (std::streamsize)(h.numel() * (int64_t)sizeof(float)));
+    std::ofstream js(base + ".json");
+    const int64_t cols = h.ndim() ? h.dim(-1) : 1;
+    js << "{\"shape\": [" << (cols ? h.numel() / cols : 0) << ", " << cols << "]}";
+    if (!bin || !js) throw std::runtime_error("ZIMAGE_TRACE: cannot write " + base);
+}
+
 void fill_rows(Tensor& buf, int64_t from, int64_t to, const Tensor& token) {
     const int64_t D = buf.dim(-1), n = to - from;
     if (n <= 0) return;
@@ -272,9 +292,11 @@ struct ZImageTransformer::Impl {
     void embed(const Tensor& latent, const Tensor& text, const TokenLayout& g, Tensor& seq) const {
         Tensor img = rows_view(seq, 0, g.img);
         project_into(patchify2d(latent, cfg.patch), patch_embed, img, "the patch embedder");
+        trace("x_embed", img);
         fill_rows(seq, g.img, g.img_rows, *img_pad);
         Tensor txt = rows_view(seq, g.img_rows, g.img_rows + g.txt);
         project_into(rms_norm(text, text_norm, cfg.norm_eps), text_embed, txt, "the text embedder");
+        trace("cap_embed", txt);
         fill_rows(seq, g.img_rows + g.txt, g.rows(), *txt_pad);
     }
 
@@ -359,8 +381,9 @@ struct ZImageTransformer::Impl {
     // first, then the FFN; unmodulated blocks have no scale and gate
     // (zimage.cpp:90-136). A sublayer's input is formed where the previous
     // sublayer closes, the next block's modulation computed one block ahead.
+    // first_trace: the trace name of x after the first block (or null).
     void run_stack(const std::vector<BlockBinding>& blocks, Tensor& x, const Tensor& cos, const Tensor& sin,
-                   const Tensor* cond) const {
+                   const Tensor* cond, const char* first_trace = nullptr) const {
         if (blocks.empty()) return;
         Modulation cur = modulation(blocks[0], cond);
         Tensor in = sublayer_input(blocks[0], x, kNormAttnIn, cur.scale_of(0));
@@ -372,6 +395,7 @@ struct ZImageTransformer::Impl {
             in = close_sublayer(b, x, out, kNormAttnOut, cur.gate_of(0), &b, kNormFfnIn, cur.scale_of(1));
             out = feed_forward(b, in);
             in = close_sublayer(b, x, out, kNormFfnOut, cur.gate_of(1), nb, kNormAttnIn, nxt.scale_of(0));
+            if (i == 0 && first_trace) trace(first_trace, x);
             cur = std::move(nxt);
         }
     }
@@ -387,7 +411,9 @@ struct ZImageTransformer::Impl {
         scale.reshape({dim});
         Tensor y = layer_norm(rows_view(seq, 0, g.img), nullptr, nullptr, kHeadNormEps);
         mul_rows_(y, scale);
-        return unpatchify2d(linear(y, *head_out.W, head_out.b), channels, H, W, cfg.patch);
+        const Tensor tokens = linear(y, *head_out.W, head_out.b);
+        trace("final", tokens);
+        return unpatchify2d(tokens, channels, H, W, cfg.patch);
     }
 };
 
@@ -405,6 +431,7 @@ Tensor ZImageTransformer::forward(const Tensor& latent, float t, const Tensor& t
     const Impl& m = *impl_;
     const TokenLayout g = m.layout(latent, text);
     Tensor cond = m.condition(t);
+    trace("adaln", cond);
     Tensor seq = Tensor::empty({g.rows(), m.dim}, Device::HIP);
     m.embed(latent, text, g, seq);
     const auto& rot = m.rotary(g);
@@ -416,10 +443,13 @@ Tensor ZImageTransformer::forward(const Tensor& latent, float t, const Tensor& t
         Tensor x = as_sequence(rows_view(seq, split[part], split[part + 1]));
         const Tensor c = rows_view(rot.first, split[part], split[part + 1]);
         const Tensor s = rows_view(rot.second, split[part], split[part + 1]);
-        m.run_stack(m.stacks[st], x, c, s, kStackModulated[st] ? &cond : nullptr);
+        m.run_stack(m.stacks[st], x, c, s, kStackModulated[st] ? &cond : nullptr,
+                    part == 0 ? "noise_refiner0" : nullptr);
+        trace(part == 0 ? "noise_refined" : "cap_refined", x);
     }
     Tensor all = as_sequence(rows_view(seq, 0, g.rows()));
-    m.run_stack(m.stacks[kMainStack], all, rot.first, rot.second, &cond);
+    m.run_stack(m.stacks[kMainStack], all, rot.first, rot.second, &cond, "layer0");
+    trace("layers_out", all);
     return m.head(seq, cond, g, latent.dim(2), latent.dim(3));
 }
 

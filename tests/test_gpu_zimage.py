@@ -108,3 +108,49 @@ def test_zimage_full_size_step_is_deterministic(be, orc):
     assert np.all(np.isfinite(a))
     assert np.array_equal(a, b)
     assert 1e-3 < float(np.std(a)) < 1e3
+
+
+TRACE_NAMES = ["adaln", "x_embed", "cap_embed", "noise_refiner0", "noise_refined", "cap_refined", "layer0",
+               "layers_out", "final"]
+
+
+def _read_trace(prefix, name):
+    import json
+    import os
+
+    shape = json.load(open(f"{prefix}_trace_{name}.json"))["shape"]
+    data = np.fromfile(f"{prefix}_trace_{name}.bin", dtype=np.float32)
+    assert data.size == shape[0] * shape[1], (name, shape, data.size)
+    os.remove(f"{prefix}_trace_{name}.json")
+    os.remove(f"{prefix}_trace_{name}.bin")
+    return data.reshape(shape)
+
+
+@pytest.mark.parametrize("H,W,L,t", CASES[1:])
+def test_zimage_trace_matches_reference_stages(be, ref, orc, model, H, W, L, t, tmp_path, monkeypatch):
+    """ZIMAGE_TRACE=<prefix> (zimage.cpp:15-26): the device forward writes the
+    reference's nine named intermediates with the reference's shapes, and each
+    stage agrees with the compiled reference's own trace of the same forward
+    (F32 weights: relative RMS 1e-5 at every stage, the forward's own bar)."""
+    import sdhip
+
+    _, path = model
+    x, cap = zm.inputs(orc, H=H, W=W, L=L)
+    m = sdhip.ZImage.load(path, heads=zm.SHAPES["heads"], keep_bf16=False)
+    try:
+        monkeypatch.setenv("ZIMAGE_TRACE", str(tmp_path / "dev"))
+        got = m.forward(x, t, cap)
+        monkeypatch.setenv("ZIMAGE_TRACE", str(tmp_path / "ref"))
+        want = ref.zimage_forward(path, x, t, cap, zm.SHAPES["heads"], keep_bf16=False)
+        monkeypatch.delenv("ZIMAGE_TRACE")
+        untraced = m.forward(x, t, cap)
+    finally:
+        m.close()
+    assert np.array_equal(got, untraced), "tracing changed the result"
+    assert zm.rel_rms(got, want) <= 1e-5
+    for name in TRACE_NAMES:
+        d, r = _read_trace(tmp_path / "dev", name), _read_trace(tmp_path / "ref", name)
+        assert d.shape == r.shape, (name, d.shape, r.shape)
+        e = zm.rel_rms(d, r)
+        print(f"{name} {d.shape}: relative RMS {e:.3g}")
+        assert e <= 1e-5, name
