@@ -60,6 +60,7 @@
 // separate rounding pass runs.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <type_traits>
 
 #include "sdh_internal.hpp"
@@ -677,11 +678,19 @@ void run_mfma(const float* q, const float* k, const float* v, void* out, int64_t
 // library GEMM: per (batch, head) and block of query rows, S = q_h k_g^T,
 // the scaled (causal) row softmax in place, then O_h = P v_g as a GEMM
 // against v^T (v transposed once per batch). fp32 products and sums
-// throughout. The score block is bounded to kScoreBytes (causal: one block,
+// throughout. The score block is bounded to score_bytes() (causal: one block,
 // so the mask's row index is the query's). False, with nothing queued, when
 // the operands do not suit the library GEMM (alignment, Skv % 4) or the
 // causal block would not fit: the caller then runs the one-wave kernel.
-constexpr int64_t kScoreBytes = int64_t(1) << 30;
+// The score block's budget: SD_CUDA_ATTN_MB megabytes, at least 64, 1024 when
+// unset, as the reference caps its score buffer (backend_cuda.cu:558-561).
+int64_t score_bytes() {
+    static const int64_t v = [] {
+        const char* e = std::getenv("SD_CUDA_ATTN_MB");
+        return (int64_t)(e ? std::max(64, std::atoi(e)) : 1024) << 20;
+    }();
+    return v;
+}
 
 bool run_attention_gemm(const char* op, const float* q, const float* k, const float* v, void* out, bool out16,
                         int64_t N, int64_t Sq, int64_t Skv, int heads, int kv_heads, int64_t d, bool causal,
@@ -689,8 +698,9 @@ bool run_attention_gemm(const char* op, const float* q, const float* k, const fl
     const int64_t inner = heads * d, kv_inner = (int64_t)kv_heads * d;
     if (d % 4 || Skv % 4 || !aligned16(q) || !aligned16(k) || !aligned16(v) || (!out16 && !aligned16(out)))
         return false;
-    const int64_t rb = causal ? Sq : std::max<int64_t>(1, std::min<int64_t>(Sq, kScoreBytes / (Skv * 4)));
-    if (rb * Skv * 4 > 4 * kScoreBytes) return false;
+    const int64_t budget = score_bytes();
+    const int64_t rb = causal ? Sq : std::max<int64_t>(1, std::min<int64_t>(Sq, budget / (Skv * 4)));
+    if (rb * Skv * 4 > 4 * budget) return false;
     const size_t vt_n = (size_t)(Skv * kv_inner), sc_n = (size_t)(rb * Skv), o_n = out16 ? (size_t)(N * Sq * inner) : 0;
     float* vt = (float*)scratch((vt_n + sc_n + o_n) * 4 + 512);
     float* sc = vt + ((vt_n + 63) & ~size_t(63));

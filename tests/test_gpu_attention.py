@@ -175,3 +175,54 @@ def test_attention_vae_shape(be, orc):
     of = be.empty((1, S, d))
     be.attention_fp16(dq, dk, dv, of, 1, S, S, 1, 1, d, False)
     assert np.array_equal(of.download(), got)
+
+
+_BUDGET_CHILD = r"""
+import os, sys
+root = sys.argv[1]
+sys.path[:0] = [os.path.join(root, "stablediffusion-cpp_amd"), os.path.join(root, "oracle"), os.path.join(root, "tests")]
+import numpy as np
+import sdhip
+from oracle import Oracle
+be, orc = sdhip.Backend(), Oracle()
+Sq, Skv, d = 8192, 4096, 256
+q = orc.randn((1, Sq, d), 7300)
+k = orc.randn((1, Skv, d), 7301)
+v = orc.randn((1, Skv, d), 7302)
+dq, dk, dv, do = be.array(q), be.array(k), be.array(v), be.empty((1, Sq, d))
+before = be.memory_stats()[1]
+be.attention(dq, dk, dv, do, 1, Sq, Skv, 1, 1, d, False)
+be.synchronize()
+held = be.memory_stats()[1] - before
+rows = np.concatenate([np.arange(0, Sq, 509), [Sq - 1]])
+err = float(np.max(np.abs(do.download()[:, rows] - orc.attention(q, k, v, 1, False, rows=rows))))
+print(f"held {held} err {err}")
+"""
+
+
+def test_attention_score_budget_env():
+    """SD_CUDA_ATTN_MB bounds the score block of the route for head sizes
+    above 128 as it bounds the reference's score buffer (backend_cuda.cu:
+    558-561; at least 64, 1024 when unset): with 64 the [8192 x 4096] scores
+    (128 MB) are formed in two blocks of 64 MB, so the library's scratch holds
+    64 MB less than with the default, and the result stays within the
+    attention bar either way. Child processes, since the budget is read once."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    held = {}
+    for budget_mb in (None, 64):
+        env = dict(os.environ)
+        env.pop("SD_CUDA_ATTN_MB", None)
+        if budget_mb is not None:
+            env["SD_CUDA_ATTN_MB"] = str(budget_mb)
+        p = subprocess.run([sys.executable, "-c", _BUDGET_CHILD, root], capture_output=True, text=True, env=env,
+                           timeout=240)
+        assert p.returncode == 0, p.stderr[-3000:]
+        h, err = (float(t) for t in p.stdout.split()[1::2])
+        print(f"SD_CUDA_ATTN_MB={budget_mb}: library scratch {h / 2**20:.1f} MiB, max-abs {err:.3g}")
+        assert err <= TOL
+        held[budget_mb] = h
+    assert held[None] - held[64] == 64 << 20
