@@ -244,6 +244,19 @@ int sdh_attention_bf16(const float* q, const float* k, const float* v, uint16_t*
  * and half its packed bytes; the error is that of fp16 operands (about 2^-12
  * relative per element), for callers whose tolerance allows it (a diffusion
  * step's 2e-2). Head dimensions above 128 run the fp32 kernel. */
+/* FUSED (zimage.cpp:117-121): rms_norm_heads_(q), rms_norm_heads_(k), rope_(q),
+ * rope_(k) (as sdh_qknorm_rope, interleaved tables [S, dim]) then attention
+ * (self-attention, heads == kv_heads, not causal): q [N, S, heads*dim] is left
+ * normalised and rotated as sdh_qknorm_rope leaves it; k and v are read only;
+ * out as sdh_attention (out_bf16 == 0, float32) or sdh_attention_bf16
+ * (uint16 bf16 bits), with fp16 != 0 the products of sdh_attention_fp16. For
+ * dim 128 and 16-byte aligned operands one launch normalises and rotates q and
+ * k and packs k and v for the attention kernel (k's normalised rows never
+ * reach memory); q and out are bit-equal to the op sequence. Other shapes
+ * run the sequence on a copy of k. */
+int sdh_qknorm_rope_attention(float* q, const float* k, const float* v, void* out, int out_bf16, int64_t N,
+                              int64_t S, int heads, int64_t dim, const float* gamma_q, const float* gamma_k,
+                              float eps, const float* cos, const float* sin, int fp16);
 int sdh_attention_fp16(const float* q, const float* k, const float* v, void* out, int out_bf16, int64_t N,
                        int64_t Sq, int64_t Skv, int heads, int kv_heads, int64_t d, int causal);
 

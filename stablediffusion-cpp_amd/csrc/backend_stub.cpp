@@ -51,6 +51,8 @@ STUB(int sdh_attention_bf16(const float*, const float*, const float*, uint16_t*,
                              int64_t, int))
 STUB(int sdh_attention_fp16(const float*, const float*, const float*, void*, int, int64_t, int64_t, int64_t, int, int,
                              int64_t, int))
+STUB(int sdh_qknorm_rope_attention(float*, const float*, const float*, void*, int, int64_t, int64_t, int, int64_t,
+                                    const float*, const float*, float, const float*, const float*, int))
 STUB(int sdh_swiglu(const float*, const float*, float*, int64_t))
 STUB(int sdh_geglu(const float*, float*, int64_t, int64_t))
 STUB(int sdh_silu(float*, int64_t))

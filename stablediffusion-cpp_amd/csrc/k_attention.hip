@@ -233,6 +233,122 @@ __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, 
 }
 
 // ---------------------------------------------------------------------------
+// QK-norm + RoPE with the pack (zimage.cpp:117-121: rms_norm_heads_ and rope_
+// on q and k, then attention): for one 64-token tile and one head, q is
+// normalised and rotated in place and written back, k normalised and rotated
+// in registers and packed from there (never written back as fp32), v packed
+// as k_attn_pack packs it. Heads == kv_heads, head dim 128, interleaved
+// rotation with [S, 128] tables. 32 lanes hold a head (lane i: float4 i), so
+// the sum of squares is k_qknorm_rope_il's group_sum<32> and the element
+// math its dev::qk_norm_rope4: q, the tiles and their exponents equal those of
+// sdh_qknorm_rope followed by the pack. k's rows go from registers through
+// LDS into the pack's chunk order.
+template <bool SPLIT>
+__global__ __launch_bounds__(256) void k_qkv_prep(float* __restrict__ Q, const float* __restrict__ K,
+                                                  const float* __restrict__ V, u16* __restrict__ tiles,
+                                                  int2* __restrict__ exps, int S, int inner, int ntiles, int heads,
+                                                  const float* __restrict__ gq, const float* __restrict__ gk,
+                                                  float eps, const float* __restrict__ cs,
+                                                  const float* __restrict__ sn) {
+    constexpr int DP = 128, L = 32;
+    constexpr int RS = 256 / L;              // rows per step (8)
+    constexpr int NS = kKT / RS;             // steps (8)
+    constexpr int CPR = DP / 8;              // 16-B chunks per K row
+    constexpr int KCH = kKT * CPR / 256;     // K chunks per thread
+    constexpr int VCH = kKT * DP / 4 / 256;  // V float4 per thread
+    __shared__ float sk[kKT][DP + 4];
+    __shared__ float sv[kKT][DP + 4];
+    __shared__ float red[2][4];
+    const int t = blockIdx.x, h = blockIdx.y, nb = blockIdx.z;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int hl = threadIdx.x % L, rs = threadIdx.x / L;
+    const int64_t row0 = (int64_t)nb * S + (int64_t)t * kKT;
+    const int64_t col0 = (int64_t)h * DP;
+    const int nrows = min(kKT, S - t * kKT);
+    const f4 one = {1.f, 1.f, 1.f, 1.f};
+    const f4 gq4 = gq ? ((const f4*)gq)[hl] : one;
+    const f4 gk4 = gk ? ((const f4*)gk)[hl] : one;
+    f4 kq[NS], kk[NS];
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const int r = rs + RS * j;
+        const f4 zero = {0.f, 0.f, 0.f, 0.f};
+        kq[j] = r < nrows ? dev::ld_stream((const f4*)(Q + (row0 + r) * inner + col0) + hl) : zero;
+        kk[j] = r < nrows ? dev::ld_stream((const f4*)(K + (row0 + r) * inner + col0) + hl) : zero;
+    }
+    // V tile into LDS (zero beyond the keys)
+    float vmax = 0.f;
+#pragma unroll
+    for (int j = 0; j < VCH; ++j) {
+        const int i = threadIdx.x + j * 256, r = i / (DP / 4), c = (i % (DP / 4)) * 4;
+        f4 x = {0.f, 0.f, 0.f, 0.f};
+        if (r < nrows) x = dev::ld_stream((const f4*)(V + (row0 + r) * inner + col0 + c));
+        *(f4*)&sv[r][c] = x;
+        vmax = fmaxf(vmax, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+    }
+    float kmax = 0.f;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        const int r = rs + RS * j;
+        const int64_t s = (int64_t)t * kKT + min(r, nrows - 1);  // position in the sequence
+        const f4 c = ((const f4*)(cs + s * DP))[hl], sw = ((const f4*)(sn + s * DP))[hl];
+        const float rq = dev::rstd_fast(dev::group_sum<L>(dev::sumsq4(kq[j])), 1.0f / DP, eps);
+        const float rk = dev::rstd_fast(dev::group_sum<L>(dev::sumsq4(kk[j])), 1.0f / DP, eps);
+        if (r < nrows) {
+            dev::st_stream((f4*)(Q + (row0 + r) * inner + col0) + hl, dev::qk_norm_rope4(kq[j], rq, gq != nullptr, gq4, c, sw));
+            const f4 o = dev::qk_norm_rope4(kk[j], rk, gk != nullptr, gk4, c, sw);
+            *(f4*)&sk[r][hl * 4] = o;
+            kmax = fmaxf(kmax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
+        } else {
+            *(f4*)&sk[r][hl * 4] = f4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    kmax = dev::wave_max(kmax);
+    vmax = dev::wave_max(vmax);
+    if (lane == 0) {
+        red[0][w] = kmax;
+        red[1][w] = vmax;
+    }
+    __syncthreads();
+    kmax = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    vmax = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+    const int ek = block_exp(kmax), ev = block_exp(vmax);
+    const int64_t tile = ((int64_t)nb * heads + h) * ntiles + t;
+    if (threadIdx.x == 0) exps[tile] = make_int2(ek, ev);
+    const float sk2 = pow2(-ek), svs = pow2(-ev);
+    constexpr int PARTS = SPLIT ? 4 : 2;
+    u16* out = tiles + tile * PARTS * (kKT * DP);
+#pragma unroll
+    for (int j = 0; j < KCH; ++j) {
+        const int i = threadIdx.x + j * 256, r = i / CPR, p = i % CPR, c = p ^ swz_k<DP>(r);
+        h8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            _Float16 a, b;
+            split(sk[r][c * 8 + e] * sk2, a, b);
+            hi[e] = a;
+            lo[e] = b;
+        }
+        *(h8*)(out + r * DP + p * 8) = hi;
+        if constexpr (SPLIT) *(h8*)(out + kKT * DP + r * DP + p * 8) = lo;
+    }
+    u16* vt = out + (PARTS / 2) * kKT * DP;
+    for (int i = threadIdx.x; i < DP * 8; i += 256) {
+        const int r = i / 8, p = i % 8, c = p ^ swz_v(r);
+        h8 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            _Float16 a, b;
+            split(sv[key_at(c * 8 + e)][r] * svs, a, b);
+            hi[e] = a;
+            lo[e] = b;
+        }
+        *(h8*)(vt + r * kKT + p * 8) = hi;
+        if constexpr (SPLIT) *(h8*)(vt + DP * kKT + r * kKT + p * 8) = lo;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Fused attention, head dimension padded to DP (64 or 128).
 // 1-D grid of ceil(Sq / 256) * heads * N workgroups; 512 threads = 8 waves of 32 queries.
 // Each wave alternates an MFMA phase (O += V(t-1) P(t-1), then S^T(t) =
@@ -638,9 +754,19 @@ bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
     return x < y + nb && y < x + na;
 }
 
+// QK-norm + RoPE folded into the pack (k_qkv_prep); q is written back.
+struct QKPrep {
+    float* q;
+    const float* gq;
+    const float* gk;
+    const float* cs;
+    const float* sn;
+    float eps;
+};
+
 template <int DP, bool OUT16, bool SPLIT>
 void run_mfma(const float* q, const float* k, const float* v, void* out, int64_t N, int64_t Sq, int64_t Skv,
-              int heads, int kv_heads, int64_t d, bool causal, float c2) {
+              int heads, int kv_heads, int64_t d, bool causal, float c2, const QKPrep* prep = nullptr) {
     const int64_t ntiles = (Skv + kKT - 1) / kKT;
     const int64_t ntot = N * kv_heads * ntiles;
     const size_t tile_bytes = (size_t)(SPLIT ? 4 : 2) * kKT * DP * 2;
@@ -651,7 +777,15 @@ void run_mfma(const float* q, const float* k, const float* v, void* out, int64_t
     need(ntiles * 256 <= kMaxGridItems, "sdh_attention", "too many keys for one launch");
     need(ntiles * (int64_t)tile_bytes < (int64_t(1) << 31), "sdh_attention", "too many keys per head for one launch");
     const dim3 pgrid((unsigned)ntiles, (unsigned)kv_heads, (unsigned)N);
-    if (d == DP && kv_inner % 4 == 0 && aligned16(k) && aligned16(v))
+    if constexpr (DP == 128) {
+        if (prep)
+            k_qkv_prep<SPLIT><<<pgrid, 256, 0, stream()>>>(prep->q, k, v, tiles, exps, (int)Skv, (int)kv_inner,
+                                                            (int)ntiles, kv_heads, prep->gq, prep->gk, prep->eps,
+                                                            prep->cs, prep->sn);
+    }
+    if (prep) {
+        need(DP == 128, "sdh_qknorm_rope_attention", "internal: fused preparation needs head dim 128");
+    } else if (d == DP && kv_inner % 4 == 0 && aligned16(k) && aligned16(v))
         k_attn_pack<DP, true, SPLIT><<<pgrid, 256, 0, stream()>>>(k, v, tiles, exps, (int)Skv, (int)kv_inner, (int)d,
                                                            (int)ntiles, kv_heads);
     else
@@ -796,6 +930,69 @@ void run_attention(const float* q, const float* k, const float* v, void* out, bo
     }
 }
 
+// qknorm_rope_ of q and k (zimage.cpp:117-120) then attention (:121), with
+// q left normalised and rotated as sdh_qknorm_rope leaves it, k and v read
+// only. Head dim 128 with heads == kv_heads, Sq == Skv, interleaved [S, 128]
+// tables and aligned operands: one launch prepares q and packs k and v
+// (k_qkv_prep), then the attention kernel; otherwise the same sequence
+// through the separate entry points on a copy of k.
+void run_qknorm_rope_attention(float* q, const float* k, const float* v, void* out, bool out16, int64_t N,
+                               int64_t S, int heads, int64_t dim, const float* gq, const float* gk, float eps,
+                               const float* cs, const float* sn, bool fp16) {
+    const char* op = "sdh_qknorm_rope_attention";
+    need(N >= 0 && S >= 0, op, "negative size");
+    need(heads > 0 && dim > 0 && dim % 2 == 0, op, "heads and dim must be positive, dim even");
+    need(N * S * heads * dim < (1LL << 31), op, "tensor too large (2^31 elements)");
+    if (N == 0 || S == 0) return;
+    ensure_init();
+    const int64_t inner = heads * dim;
+    const size_t bytes = (size_t)(N * S * inner) * 4;
+    check_range(q, bytes, op, "q");
+    check_range(k, bytes, op, "k");
+    check_range(v, bytes, op, "v");
+    check_range(out, out16 ? bytes / 2 : bytes, op, "out");
+    check_range(cs, (size_t)(S * dim) * 4, op, "cos");
+    check_range(sn, (size_t)(S * dim) * 4, op, "sin");
+    if (gq) check_range(gq, (size_t)dim * 4, op, "gamma_q");
+    if (gk) check_range(gk, (size_t)dim * 4, op, "gamma_k");
+    const size_t ob = out16 ? bytes / 2 : bytes;
+    need(!overlaps(out, ob, q, bytes) && !overlaps(out, ob, k, bytes) && !overlaps(out, ob, v, bytes) &&
+             !overlaps(q, bytes, k, bytes) && !overlaps(q, bytes, v, bytes),
+         op, "operands overlap");
+    const bool fused = dim == 128 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(cs) &&
+                       aligned16(sn) && (!gq || aligned16(gq)) && (!gk || aligned16(gk)) &&
+                       (out16 ? ((uintptr_t)out & 7) == 0 : aligned16(out));
+    if (fused) {
+        const QKPrep prep{q, gq, gk, cs, sn, eps};
+        const float c2 = 1.0f / std::sqrt((float)dim) * kLog2e;
+        if (fp16) {
+            if (out16) run_mfma<128, true, false>(q, k, v, out, N, S, S, heads, heads, dim, false, c2, &prep);
+            else run_mfma<128, false, false>(q, k, v, out, N, S, S, heads, heads, dim, false, c2, &prep);
+        } else {
+            if (out16) run_mfma<128, true, true>(q, k, v, out, N, S, S, heads, heads, dim, false, c2, &prep);
+            else run_mfma<128, false, true>(q, k, v, out, N, S, S, heads, heads, dim, false, c2, &prep);
+        }
+        return;
+    }
+    // the op sequence, k normalised on a copy
+    auto ok = [&](int rc) {
+        if (rc != SDH_OK) fail(rc, sdh_last_error());
+    };
+    void* kc = nullptr;
+    ok(sdh_malloc(bytes, &kc));
+    try {
+        ok(sdh_copy(kc, k, bytes));
+        ok(sdh_qknorm_rope(q, inner, (float*)kc, inner, N, S, dim, gq, gk, eps, cs, sn, 1));
+        if (fp16) ok(sdh_attention_fp16(q, (const float*)kc, v, out, out16, N, S, S, heads, heads, dim, 0));
+        else if (out16) ok(sdh_attention_bf16(q, (const float*)kc, v, (uint16_t*)out, N, S, S, heads, heads, dim, 0));
+        else ok(sdh_attention(q, (const float*)kc, v, (float*)out, N, S, S, heads, heads, dim, 0));
+    } catch (...) {
+        sdh_free(kc);
+        throw;
+    }
+    ok(sdh_free(kc));
+}
+
 }  // namespace
 }  // namespace sdh
 
@@ -817,6 +1014,15 @@ int sdh_attention_fp16(const float* q, const float* k, const float* v, void* out
                        int64_t Sq, int64_t Skv, int heads, int kv_heads, int64_t d, int causal) {
     return guarded(
         [&] { run_attention(q, k, v, out, out_bf16 != 0, N, Sq, Skv, heads, kv_heads, d, causal != 0, true); });
+}
+
+int sdh_qknorm_rope_attention(float* q, const float* k, const float* v, void* out, int out_bf16, int64_t N,
+                              int64_t S, int heads, int64_t dim, const float* gamma_q, const float* gamma_k,
+                              float eps, const float* cos, const float* sin, int fp16) {
+    return guarded([&] {
+        run_qknorm_rope_attention(q, k, v, out, out_bf16 != 0, N, S, heads, dim, gamma_q, gamma_k, eps, cos, sin,
+                                  fp16 != 0);
+    });
 }
 
 }  // extern "C"

@@ -409,8 +409,10 @@ void run_rope_axes(const char* op, float* q, int64_t inner_q, float* k, int64_t 
 // head's sum of squares, and a lane's position in the head -- hence its gamma
 // and table entries -- is the same at every step. Per element it applies
 // k_heads' operations (o = x * rstd, then * gamma, with the fp32 rstd_fast)
-// and then k_rope_il_reg's; where the compiler contracts them differently the
-// results differ from the unfused kernels by an ulp or two.
+// and then k_rope_il_reg's, each product and difference rounded on its own
+// (dev::qk_norm_rope4, shared with the attention's fused Q/K preparation);
+// where the compiler contracts the unfused kernels differently the results
+// differ from them by an ulp or two.
 // rotate_half: a lane holds the pair (k, k + dim/8) of float4, L = dim / 8
 // lanes per head. All lanes join the reductions (rows outside the tensor are
 // zeros); only the loads and stores are guarded.
@@ -446,13 +448,7 @@ __global__ __launch_bounds__(kThreads) void k_qknorm_rope_il(QKArgs a, int64_t S
     for (int j = 0; j < RV; ++j) {
         const float q = dev::group_sum<L>(dev::sumsq4(v[j]));
         const float rstd = dev::rstd_fast(q, 1.0f / (4 * L), eps);  // dim = 4 L
-        f4 o = v[j] * rstd;
-        if (gp) o = o * g;
-        f4 r;
-        r.x = o.x * c.x - o.y * sv.x;
-        r.y = o.y * c.x + o.x * sv.x;
-        r.z = o.z * c.z - o.w * sv.z;
-        r.w = o.w * c.z + o.z * sv.z;
+        const f4 r = dev::qk_norm_rope4(v[j], rstd, gp != nullptr, g, c, sv);
         const int i = threadIdx.x + kThreads * j;
         if (i < n4) dev::st_stream(row + i, r);
     }

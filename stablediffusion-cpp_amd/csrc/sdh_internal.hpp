@@ -281,5 +281,21 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 __device__ __forceinline__ float gelu_erf(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
 __device__ __forceinline__ float quick_gelu(float v) { return v / (1.0f + expf(-1.702f * v)); }
 
+// QK-norm then interleaved RoPE of one float4 of a head: o = (v * rstd), then
+// * g when has_g, rotated pairwise, (x, y) by (c.x, s.x) and (z, w) by (c.z, s.z)
+// (the even table entries, tensor.cpp:717-718). Every product and difference
+// is rounded on its own, so each kernel that applies it gives the same bits.
+__device__ __forceinline__ f4 qk_norm_rope4(const f4& v, float rstd, bool has_g, const f4& g, const f4& c,
+                                            const f4& s) {
+#pragma clang fp contract(off)
+    f4 o = v * rstd;
+    if (has_g) o = o * g;
+    f4 r;
+    r.x = o.x * c.x - o.y * s.x;
+    r.y = o.y * c.x + o.x * s.x;
+    r.z = o.z * c.z - o.w * s.z;
+    r.w = o.w * c.z + o.z * s.z;
+    return r;
+}
 }  // namespace dev
 }  // namespace sdh

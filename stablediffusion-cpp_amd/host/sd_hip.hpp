@@ -104,6 +104,14 @@ inline void attention_fp16(const float* q, const float* k, const float* v, void*
     detail::check(sdh_attention_fp16(q, k, v, out, out_bf16 ? 1 : 0, N, Sq, Skv, heads, kv_heads, d, causal ? 1 : 0),
                   "hip::attention_fp16");
 }
+// fused: qknorm_rope of q and k, then attention; q updated in place, k and v read only
+inline void qknorm_rope_attention(float* q, const float* k, const float* v, void* out, bool out_bf16, int64_t N,
+                                  int64_t S, int heads, int64_t dim, const float* gamma_q, const float* gamma_k,
+                                  float eps, const float* cos, const float* sin, bool fp16) {
+    detail::check(sdh_qknorm_rope_attention(q, k, v, out, out_bf16 ? 1 : 0, N, S, heads, dim, gamma_q, gamma_k, eps,
+                                            cos, sin, fp16 ? 1 : 0),
+                  "hip::qknorm_rope_attention");
+}
 // backend_cuda.h:60-61
 inline void geglu(const float* x, float* y, int64_t rows, int64_t D) {
     detail::check(sdh_geglu(x, y, rows, D), "hip::geglu");

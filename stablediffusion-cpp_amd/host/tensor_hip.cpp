@@ -632,6 +632,30 @@ void rope_qk_(Tensor& q, Tensor& k, int64_t dim, const Tensor& cos, const Tensor
 }
 
 // zimage.cpp:117-120 / qwen3.cpp:59-62 in one launch
+Tensor qknorm_rope_attention_(Tensor& q, const Tensor& k, const Tensor& v, int heads, int64_t dim,
+                              const Tensor* gamma_q, const Tensor* gamma_k, float eps, const Tensor& cos,
+                              const Tensor& sin, bool out_bf16, bool fp16_products) {
+    const char* op = "qknorm_rope_attention_";
+    need_hip(q, op);
+    same_device(q, k, op);
+    same_device(q, v, op);
+    for (const Tensor* t : {gamma_q, gamma_k}) {
+        if (!t) continue;
+        same_device(q, *t, op);
+        if (t->numel() != dim) throw std::runtime_error("rms_norm_heads_: weight size mismatch");
+    }
+    const int64_t N = q.dim(0), S = q.dim(1), inner = q.dim(2);
+    if (inner != heads * dim || k.shape != q.shape || v.shape != q.shape)
+        throw std::runtime_error("attention: shape mismatch q" + q.shape_str() + " k" + k.shape_str());
+    if (cos.dim(0) < S || cos.dim(1) != dim || sin.shape != cos.shape)
+        throw std::runtime_error("rope_: table shape mismatch");
+    Tensor out = out_bf16 ? Tensor::empty_bf16({N, S, inner}) : Tensor::empty({N, S, inner}, Device::HIP);
+    sd::hip::qknorm_rope_attention(q.dptr(), k.dptr(), v.dptr(), out_bf16 ? (void*)out.dptr16() : (void*)out.dptr(),
+                                   out_bf16, N, S, heads, dim, opt(gamma_q), opt(gamma_k), eps, cos.dptr(),
+                                   sin.dptr(), fp16_products);
+    return out;
+}
+
 void qknorm_rope_(Tensor& q, Tensor& k, int64_t dim, const Tensor* gamma_q, const Tensor* gamma_k, float eps,
                   const Tensor& cos, const Tensor& sin, bool interleaved) {
     need_hip(q, "qknorm_rope_");

@@ -149,6 +149,12 @@ Tensor attention_bf16(const Tensor& q, const Tensor& k, const Tensor& v, int hea
                       int kv_heads = 0);
 // opt-in, no counterpart in the reference: attention from block-scaled fp16
 // operands (sdh_attention_fp16), FP32 or (out_bf16) BF16 result
+// qknorm_rope_(q, k, ...) (interleaved) then attention(q, k, v, heads): q is
+// left normalised and rotated, k is not modified. BF16 result with out_bf16,
+// the products of attention_fp16 with fp16_products.
+Tensor qknorm_rope_attention_(Tensor& q, const Tensor& k, const Tensor& v, int heads, int64_t dim,
+                              const Tensor* gamma_q, const Tensor* gamma_k, float eps, const Tensor& cos,
+                              const Tensor& sin, bool out_bf16, bool fp16_products = false);
 Tensor attention_fp16(const Tensor& q, const Tensor& k, const Tensor& v, int heads, bool causal = false,
                       int kv_heads = 0, bool out_bf16 = false);
 

@@ -316,11 +316,12 @@ struct ZImageTransformer::Impl {
     // Self-attention with QK-norm and rotary positions, then to_out (zimage.cpp:116-122).
     Tensor attend(const BlockBinding& b, const Tensor& in, const Tensor& cos, const Tensor& sin) const {
         Tensor q = project(in, b, kProjQ), k = project(in, b, kProjK), v = project(in, b, kProjV);
-        qknorm_rope_(q, k, head_dim, b.norm[kNormQ], b.norm[kNormK], kQkNormEps, cos, sin, true);
-        Tensor o = fp16_attention.load(std::memory_order_relaxed)
-                       ? attention_fp16(q, k, v, cfg.heads, false, 0, b.fused_bf16)
-                   : b.fused_bf16 ? attention_bf16(q, k, v, cfg.heads, false)
-                                  : attention(q, k, v, cfg.heads, false);
+        // QK-norm, rotary and attention in one entry point (k's normalised
+        // rows go straight into the attention's packed tiles); the output is
+        // to_out's bf16 A on the fused path
+        const Tensor o = qknorm_rope_attention_(q, k, v, cfg.heads, head_dim, b.norm[kNormQ], b.norm[kNormK],
+                                                kQkNormEps, cos, sin, b.fused_bf16,
+                                                fp16_attention.load(std::memory_order_relaxed));
         return project(o, b, kProjOut);
     }
 

@@ -94,6 +94,8 @@ SIGNATURES = {
     "sdh_attention": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
     "sdh_attention_bf16": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
     "sdh_attention_fp16": [_vp, _vp, _vp, _vp, C.c_int, _i64, _i64, _i64, C.c_int, C.c_int, _i64, C.c_int],
+    "sdh_qknorm_rope_attention": [_vp, _vp, _vp, _vp, C.c_int, _i64, _i64, C.c_int, _i64, _vp, _vp, _fl, _vp, _vp,
+                                  C.c_int],
     "sdh_upsample_nearest2x": [_vp, _vp, _i64, _i64, _i64],
     "sdh_concat_channels": [_vp, _vp, _vp, _i64, _i64, _i64, _i64],
     "sdh_nchw_to_nlc": [_vp, _vp, _i64, _i64, _i64],
@@ -305,6 +307,13 @@ class Backend:
         """As attention, out16 (uint16) holding the bf16 rounding of the result."""
         self.call("sdh_attention_bf16", _p(q), _p(k), _p(v), _p(out16), N, Sq, Skv, heads, kv_heads, d,
                   int(bool(causal)))
+
+    def qknorm_rope_attention(self, q, k, v, out, N, S, heads, dim, gamma_q, gamma_k, eps, cos, sin, out_bf16=False,
+                              fp16=False):
+        """qknorm_rope (interleaved tables) of q and k, then self-attention; q is
+        left normalised and rotated, k and v are read only."""
+        self.call("sdh_qknorm_rope_attention", _p(q), _p(k), _p(v), _p(out), int(bool(out_bf16)), N, S, heads, dim,
+                  _p(gamma_q), _p(gamma_k), eps, _p(cos), _p(sin), int(bool(fp16)))
 
     def attention_fp16(self, q, k, v, out, N, Sq, Skv, heads, kv_heads, d, causal=False, out_bf16=False):
         """Opt-in reduced precision attention (no reference counterpart): every

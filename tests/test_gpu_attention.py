@@ -226,3 +226,47 @@ def test_attention_score_budget_env():
         assert err <= TOL
         held[budget_mb] = h
     assert held[None] - held[64] == 64 << 20
+
+
+QKA_SHAPES = [  # N, S, heads, dim, with gammas (dim 128: the fused preparation; others: the op sequence)
+    (1, 4224, 30, 128, True), (1, 100, 4, 128, True), (2, 65, 3, 128, False), (1, 1, 2, 128, True),
+    (1, 50, 4, 64, True), (1, 33, 2, 80, False),
+]
+
+
+@pytest.mark.parametrize("N,S,heads,dim,gam", QKA_SHAPES)
+@pytest.mark.parametrize("mode", ["f32", "bf16", "fp16"])
+def test_qknorm_rope_attention_equals_sequence(be, orc, N, S, heads, dim, gam, mode):
+    """sdh_qknorm_rope_attention == sdh_qknorm_rope then sdh_attention (or its
+    bf16 / fp16-product forms), bit for bit: the output and q (left normalised
+    and rotated); k and v are not modified."""
+    import sdhip
+
+    inner = heads * dim
+    q = orc.randn((N, S, inner), 9400 + S)
+    k = orc.randn((N, S, inner), 9401 + S, 0.0, 2.0)
+    v = orc.randn((N, S, inner), 9402 + S)
+    cs = orc.randn((S, dim), 9403, 0.0, 0.7)
+    sn = orc.randn((S, dim), 9404, 0.0, 0.7)
+    gq = be.array(orc.randn((dim,), 9405, 1.0, 0.1)) if gam else None
+    gk = be.array(orc.randn((dim,), 9406, 1.0, 0.1)) if gam else None
+    dcs, dsn = be.array(cs), be.array(sn)
+    out16, fp16 = mode != "f32", mode == "fp16"
+
+    def new_out():
+        return sdhip.DArray(be, (N, S, inner), dtype=np.uint16) if out16 else be.empty((N, S, inner))
+
+    dq, dk, dv, o1 = be.array(q), be.array(k), be.array(v), new_out()
+    be.qknorm_rope_attention(dq, dk, dv, o1, N, S, heads, dim, gq, gk, 1e-6, dcs, dsn, out_bf16=out16, fp16=fp16)
+    sq, sk, o2 = be.array(q), be.array(k), new_out()
+    be.qknorm_rope(sq, inner, sk, inner, N, S, dim, gq, gk, 1e-6, dcs, dsn, True)
+    if fp16:
+        be.attention_fp16(sq, sk, dv, o2, N, S, S, heads, heads, dim, False, out_bf16=out16)
+    elif out16:
+        be.attention_bf16(sq, sk, dv, o2, N, S, S, heads, heads, dim, False)
+    else:
+        be.attention(sq, sk, dv, o2, N, S, S, heads, heads, dim, False)
+    assert np.array_equal(dq.download(), sq.download()), "q differs from qknorm_rope's"
+    got, want = o1.download(), o2.download()
+    assert np.array_equal(got, want), f"{int(np.sum(got != want))} of {got.size} outputs differ"
+    assert np.array_equal(dk.download(), k) and np.array_equal(dv.download(), v)
