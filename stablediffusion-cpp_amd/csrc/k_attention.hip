@@ -256,8 +256,7 @@ __global__ __launch_bounds__(256) void k_qkv_prep(float* __restrict__ Q, const f
     constexpr int CPR = DP / 8;              // 16-B chunks per K row
     constexpr int KCH = kKT * CPR / 256;     // K chunks per thread
     constexpr int VCH = kKT * DP / 4 / 256;  // V float4 per thread
-    __shared__ float sk[kKT][DP + 4];
-    __shared__ float sv[kKT][DP + 4];
+    __shared__ float tl[kKT][DP + 4];        // the normalised K tile, then the V tile
     __shared__ float red[2][4];
     const int t = blockIdx.x, h = blockIdx.y, nb = blockIdx.z;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -265,26 +264,20 @@ __global__ __launch_bounds__(256) void k_qkv_prep(float* __restrict__ Q, const f
     const int64_t row0 = (int64_t)nb * S + (int64_t)t * kKT;
     const int64_t col0 = (int64_t)h * DP;
     const int nrows = min(kKT, S - t * kKT);
-    const f4 one = {1.f, 1.f, 1.f, 1.f};
+    const f4 one = {1.f, 1.f, 1.f, 1.f}, zero = {0.f, 0.f, 0.f, 0.f};
     const f4 gq4 = gq ? ((const f4*)gq)[hl] : one;
     const f4 gk4 = gk ? ((const f4*)gk)[hl] : one;
-    f4 kq[NS], kk[NS];
+    f4 kq[NS], kk[NS], vv[VCH];
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
         const int r = rs + RS * j;
-        const f4 zero = {0.f, 0.f, 0.f, 0.f};
         kq[j] = r < nrows ? dev::ld_stream((const f4*)(Q + (row0 + r) * inner + col0) + hl) : zero;
         kk[j] = r < nrows ? dev::ld_stream((const f4*)(K + (row0 + r) * inner + col0) + hl) : zero;
     }
-    // V tile into LDS (zero beyond the keys)
-    float vmax = 0.f;
 #pragma unroll
     for (int j = 0; j < VCH; ++j) {
         const int i = threadIdx.x + j * 256, r = i / (DP / 4), c = (i % (DP / 4)) * 4;
-        f4 x = {0.f, 0.f, 0.f, 0.f};
-        if (r < nrows) x = dev::ld_stream((const f4*)(V + (row0 + r) * inner + col0 + c));
-        *(f4*)&sv[r][c] = x;
-        vmax = fmaxf(vmax, fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+        vv[j] = r < nrows ? dev::ld_stream((const f4*)(V + (row0 + r) * inner + col0 + c)) : zero;
     }
     float kmax = 0.f;
 #pragma unroll
@@ -294,15 +287,19 @@ __global__ __launch_bounds__(256) void k_qkv_prep(float* __restrict__ Q, const f
         const f4 c = ((const f4*)(cs + s * DP))[hl], sw = ((const f4*)(sn + s * DP))[hl];
         const float rq = dev::rstd_fast(dev::group_sum<L>(dev::sumsq4(kq[j])), 1.0f / DP, eps);
         const float rk = dev::rstd_fast(dev::group_sum<L>(dev::sumsq4(kk[j])), 1.0f / DP, eps);
+        f4 o = zero;
         if (r < nrows) {
-            dev::st_stream((f4*)(Q + (row0 + r) * inner + col0) + hl, dev::qk_norm_rope4(kq[j], rq, gq != nullptr, gq4, c, sw));
-            const f4 o = dev::qk_norm_rope4(kk[j], rk, gk != nullptr, gk4, c, sw);
-            *(f4*)&sk[r][hl * 4] = o;
+            dev::st_stream((f4*)(Q + (row0 + r) * inner + col0) + hl,
+                           dev::qk_norm_rope4(kq[j], rq, gq != nullptr, gq4, c, sw));
+            o = dev::qk_norm_rope4(kk[j], rk, gk != nullptr, gk4, c, sw);
             kmax = fmaxf(kmax, fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w))));
-        } else {
-            *(f4*)&sk[r][hl * 4] = f4{0.f, 0.f, 0.f, 0.f};
         }
+        *(f4*)&tl[r][hl * 4] = o;
     }
+    float vmax = 0.f;
+#pragma unroll
+    for (int j = 0; j < VCH; ++j)
+        vmax = fmaxf(vmax, fmaxf(fmaxf(fabsf(vv[j].x), fabsf(vv[j].y)), fmaxf(fabsf(vv[j].z), fabsf(vv[j].w))));
     kmax = dev::wave_max(kmax);
     vmax = dev::wave_max(vmax);
     if (lane == 0) {
@@ -325,13 +322,20 @@ __global__ __launch_bounds__(256) void k_qkv_prep(float* __restrict__ Q, const f
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             _Float16 a, b;
-            split(sk[r][c * 8 + e] * sk2, a, b);
+            split(tl[r][c * 8 + e] * sk2, a, b);
             hi[e] = a;
             lo[e] = b;
         }
         *(h8*)(out + r * DP + p * 8) = hi;
         if constexpr (SPLIT) *(h8*)(out + kKT * DP + r * DP + p * 8) = lo;
     }
+    __syncthreads();  // every K chunk read: the tile now takes V
+#pragma unroll
+    for (int j = 0; j < VCH; ++j) {
+        const int i = threadIdx.x + j * 256, r = i / (DP / 4), c = (i % (DP / 4)) * 4;
+        *(f4*)&tl[r][c] = vv[j];
+    }
+    __syncthreads();
     u16* vt = out + (PARTS / 2) * kKT * DP;
     for (int i = threadIdx.x; i < DP * 8; i += 256) {
         const int r = i / 8, p = i % 8, c = p ^ swz_v(r);
@@ -339,7 +343,7 @@ __global__ __launch_bounds__(256) void k_qkv_prep(float* __restrict__ Q, const f
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             _Float16 a, b;
-            split(sv[key_at(c * 8 + e)][r] * svs, a, b);
+            split(tl[key_at(c * 8 + e)][r] * svs, a, b);
             hi[e] = a;
             lo[e] = b;
         }
