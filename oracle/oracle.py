@@ -620,6 +620,8 @@ class Reference:
             "ref_conv2d": (_vp, [_vp, _vp, _vp, C.c_int, C.c_int]),
             "ref_zimage_forward": (C.c_int, [C.c_char_p, C.c_int, _i64, C.c_int, _f32p, _i64, _i64, _i64, _fl, _f32p,
                                              _i64, _i64, _f32p]),
+            "ref_vae_decode": (C.c_int, [C.c_char_p, _fl, _fl, _f32p, _i64, _i64, _i64, _f32p, _i64,
+                                         C.POINTER(C.c_int64)]),
             "ref_patchify2d": (_vp, [_vp, C.c_int]),
             "ref_unpatchify2d": (_vp, [_vp, _i64, _i64, _i64, C.c_int]),
             "ref_slice_rows": (_vp, [_vp, _i64, _i64]),
@@ -850,6 +852,18 @@ class Reference:
                                               x, x.shape[1], x.shape[2], x.shape[3], float(t), cap, cap.shape[1],
                                               cap.shape[2], out))
         return out
+
+    def vae_decode(self, path, z, scaling, shift):
+        """The reference's VAEDecoder::decode on the CPU (vae.cpp:35-51) with
+        F32 weights loaded by its own Weights::load_safetensors."""
+        z = _f32(z)
+        cap = 1024 * z.shape[2] * z.shape[3]  # up to 16 output channels at 8x per side
+        out = np.empty(cap, np.float32)
+        shape = (C.c_int64 * 4)()
+        self._chk(self.lib.ref_vae_decode(str(path).encode(), float(scaling), float(shift), z, z.shape[1], z.shape[2],
+                                          z.shape[3], out, cap, shape))
+        n = int(np.prod(list(shape)))
+        return out[:n].reshape(tuple(shape)).copy()
 
     # -- layout --
     def _new_op(self, fn, inputs, out_shape, *args):

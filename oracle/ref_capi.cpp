@@ -14,6 +14,7 @@
 #include <string>
 
 #include "tensor.h"
+#include "vae.h"
 #include "zimage.h"
 
 using sd::Tensor;
@@ -128,6 +129,25 @@ int ref_zimage_forward(const char* path, int keep_bf16, int64_t bf16_min_numel, 
         std::memcpy(xt.ptr(), x, (size_t)xt.numel() * sizeof(float));
         std::memcpy(ct.ptr(), cap, (size_t)ct.numel() * sizeof(float));
         Tensor y = m.forward(xt, t, ct);
+        std::memcpy(out, y.ptr(), (size_t)y.numel() * sizeof(float));
+    });
+}
+
+// ---- the VAE decoder, one decode on the CPU (vae.cpp:35-51) ----
+// Weights from a .safetensors file as Weights::load_safetensors(path) loads
+// them (F32); z [1, C, H, W]. Writes the image into out (capacity out_cap
+// floats) and its shape into shape4; returns 0, or -1 with the error.
+int ref_vae_decode(const char* path, float scaling, float shift, const float* z, int64_t C, int64_t H, int64_t W,
+                   float* out, int64_t out_cap, int64_t* shape4) {
+    return guard([&] {
+        sd::Weights w;
+        w.load_safetensors(path);
+        sd::VAEDecoder vae(w, scaling, shift);
+        Tensor zt({1, C, H, W});
+        std::memcpy(zt.ptr(), z, (size_t)zt.numel() * sizeof(float));
+        Tensor y = vae.decode(zt);
+        if (y.ndim() != 4 || y.numel() > out_cap) throw std::runtime_error("ref_vae_decode: output larger than out_cap");
+        for (int i = 0; i < 4; ++i) shape4[i] = y.dim(i);
         std::memcpy(out, y.ptr(), (size_t)y.numel() * sizeof(float));
     });
 }
