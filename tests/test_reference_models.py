@@ -35,6 +35,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 REF_DIR = os.path.join(ROOT, "oracle", "_ref")
 ZIMAGE_EXE = os.path.join(REF_DIR, "test_zimage_sdh")
 VAE_EXE = os.path.join(REF_DIR, "test_vae_sdh")
+TIMING_EXE = os.path.join(REF_DIR, "zimage_reference_timing")
 
 # test_zimage.cpp builds ZImageTransformer with the default Config: 30 heads
 # and rotary axes 32 + 48 + 48, so the head size is 128 and dim 3840.
@@ -137,3 +138,20 @@ def test_reference_vae_test_on_device(vae_case):
     within the reference's own bar against its CPU decode."""
     rc, rel, verdict = _run(VAE_EXE, vae_case[0], vae_case[1], "cuda")
     assert rc == 0 and verdict == "ok" and rel < 1e-3, (rc, rel)
+
+
+@pytest.mark.gpu
+def test_reference_zimage_forward_at_step_shapes_on_device():
+    """The reference's Z-Image forward through backend_hip at the 1024x1024
+    step's token counts and the checkpoint's widths
+    (tests/cpp/zimage_reference_timing.cpp; two main blocks and one refiner
+    of each kind here, to keep the test short): it runs, op by op, and its
+    output is finite and of the input's scale."""
+    _need(TIMING_EXE)
+    print("running zimage_reference_timing cuda 128 128 128 2 1 2", flush=True)
+    r = subprocess.run([TIMING_EXE, "cuda", "128", "128", "128", "2", "1", "2"], capture_output=True, text=True,
+                       timeout=300)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and "finite" in r.stdout and "NOT FINITE" not in r.stdout, r.stdout + r.stderr
+    m = re.search(r"mean \|y\| ([0-9.eE+-]+)", r.stdout)
+    assert m and 0.05 < float(m.group(1)) < 20.0, r.stdout
