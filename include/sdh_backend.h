@@ -234,16 +234,6 @@ int sdh_attention(const float* q, const float* k, const float* v, float* out, in
  * that sequence. out [N, Sq, heads*d] uint16. */
 int sdh_attention_bf16(const float* q, const float* k, const float* v, uint16_t* out, int64_t N, int64_t Sq,
                        int64_t Skv, int heads, int kv_heads, int64_t d, int causal);
-/* OPT-IN REDUCED PRECISION, no counterpart in the reference: attention as
- * sdh_attention (out float32) or sdh_attention_bf16 (out_bf16 != 0, out the
- * uint16 bf16 bits), with every product formed once from fp16 operands: q
- * per row, k and v per 64-key tile scaled by a power of two that brings the
- * block's largest magnitude into [2^13, 2^14), then rounded to fp16 (11
- * significant bits); the softmax weights rounded to fp16 likewise; fp32
- * accumulation and softmax statistics. A third of sdh_attention's MFMA work
- * and half its packed bytes; the error is that of fp16 operands (about 2^-12
- * relative per element), for callers whose tolerance allows it (a diffusion
- * step's 2e-2). Head dimensions above 128 run the fp32 kernel. */
 /* FUSED (zimage.cpp:117-121): rms_norm_heads_(q), rms_norm_heads_(k), rope_(q),
  * rope_(k) (as sdh_qknorm_rope, interleaved tables [S, dim]) then attention
  * (self-attention, heads == kv_heads, not causal): q [N, S, heads*dim] is left
@@ -257,6 +247,16 @@ int sdh_attention_bf16(const float* q, const float* k, const float* v, uint16_t*
 int sdh_qknorm_rope_attention(float* q, const float* k, const float* v, void* out, int out_bf16, int64_t N,
                               int64_t S, int heads, int64_t dim, const float* gamma_q, const float* gamma_k,
                               float eps, const float* cos, const float* sin, int fp16);
+/* OPT-IN REDUCED PRECISION, no counterpart in the reference: attention as
+ * sdh_attention (out float32) or sdh_attention_bf16 (out_bf16 != 0, out the
+ * uint16 bf16 bits), with every product formed once from fp16 operands: q
+ * per row, k and v per 64-key tile scaled by a power of two that brings the
+ * block's largest magnitude into [2^13, 2^14), then rounded to fp16 (11
+ * significant bits); the softmax weights rounded to fp16 likewise; fp32
+ * accumulation and softmax statistics. A third of sdh_attention's MFMA work
+ * and half its packed bytes; the error is that of fp16 operands (about 2^-12
+ * relative per element), for callers whose tolerance allows it (a diffusion
+ * step's 2e-2). Head dimensions above 128 run the fp32 kernel. */
 int sdh_attention_fp16(const float* q, const float* k, const float* v, void* out, int out_bf16, int64_t N,
                        int64_t Sq, int64_t Skv, int heads, int kv_heads, int64_t d, int causal);
 
@@ -322,15 +322,16 @@ int sdh_add_rms_norm(float* x, const float* r, float* y, int64_t rows, int64_t C
 int sdh_group_norm_silu(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups, const float* gamma,
                         const float* beta, float eps);
 /* ALLOCATION-FREE: no counterpart in the reference. For callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc). The same kernels and result as
+ * allocate device memory (tight serving loops, harnesses that forbid
+ * hipMalloc). The same kernels and result as
  * sdh_group_norm_silu, with the scratch they need (team slots and counters,
  * chunk statistics) in a fixed 1 MiB device array per GPU instead of the
  * arena; it calls no hipMalloc, hipFree or allocating routine, so sdh_init
- * must have run first (SDH_ERR_INVALID otherwise). A tensor whose split
- * schedule needs more than the array's 960 KiB of chunk statistics is
- * rejected with SDH_ERR_INVALID; the resident and single-workgroup schedules
- * need at most 17 KiB. Calls that overlap on one GPU share the array and
+ * must have run first (SDH_ERR_INVALID otherwise). The split schedule runs
+ * as many segments at a time as the array's 960 KiB of chunk statistics
+ * holds; a single segment whose statistics exceed it (over about 10^9
+ * floats) is rejected with SDH_ERR_INVALID. The resident and
+ * single-workgroup schedules need at most 17 KiB. Calls that overlap on one GPU share the array and
  * would race; the library's own calls are serialised on its one stream. */
 int sdh_group_norm_silu_noalloc(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups,
                                 const float* gamma, const float* beta, float eps);

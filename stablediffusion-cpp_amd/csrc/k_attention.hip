@@ -947,6 +947,7 @@ void run_qknorm_rope_attention(float* q, const float* k, const float* v, void* o
     need(N >= 0 && S >= 0, op, "negative size");
     need(heads > 0 && dim > 0 && dim % 2 == 0, op, "heads and dim must be positive, dim even");
     need(N * S * heads * dim < (1LL << 31), op, "tensor too large (2^31 elements)");
+    need(N <= 65535 && heads <= 65535, op, "too many batches or heads for one launch");
     if (N == 0 || S == 0) return;
     ensure_init();
     const int64_t inner = heads * dim;

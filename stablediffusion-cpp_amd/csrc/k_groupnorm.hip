@@ -850,16 +850,26 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
         const int64_t budget = gn_block_bytes();
         if (budget > 0) sb = std::max<int64_t>(1, std::min<int64_t>(nseg, budget / (L * 4)));
         sb = std::min<int64_t>(sb, 65535);
+        if (fixed) {
+            // the fixed scratch holds the chunk pairs and statistics of this
+            // many segments at once; larger tensors run in more blocks
+            const int64_t room = (int64_t)(kFixedScratchBytes - kFixedCtlBytes - 256) /
+                                 ((nchunks + 1) * (int64_t)sizeof(float2));
+            if (room < 1)
+                fail(SDH_ERR_INVALID, std::string(op) + ": a segment of " + std::to_string(L) + " floats needs " +
+                                          std::to_string((nchunks + 1) * (int64_t)sizeof(float2)) +
+                                          " bytes of scratch for its chunk statistics; this entry point holds " +
+                                          std::to_string(kFixedScratchBytes - kFixedCtlBytes));
+            sb = std::min<int64_t>(sb, room);
+        }
         const size_t part_bytes = ((size_t)(sb * nchunks) * sizeof(float2) + 255) / 256 * 256;
         const size_t scr_bytes = part_bytes + (size_t)sb * sizeof(float2);
         char* scr = nullptr;
         if (fixed) {
             // every pair and statistic is written before it is read: nothing here must start at zero
             if (scr_bytes > kFixedScratchBytes - kFixedCtlBytes)
-                fail(SDH_ERR_INVALID, std::string(op) + ": " + std::to_string(nseg) + " segments of " +
-                                          std::to_string(L) + " floats need " + std::to_string(scr_bytes) +
-                                          " bytes of scratch; this entry point holds " +
-                                          std::to_string(kFixedScratchBytes - kFixedCtlBytes));
+                fail(SDH_ERR_INVALID, std::string(op) + ": block of " + std::to_string(sb) +
+                                           " segments exceeds the fixed scratch");
             scr = (char*)fixed + kFixedCtlBytes;
         } else {
             scr = (char*)scratch(scr_bytes);

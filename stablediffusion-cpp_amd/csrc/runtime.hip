@@ -168,9 +168,16 @@ struct Runtime {
     size_t counter_count = 0;
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
-    unsigned* check_word = nullptr;  // see arm_device_check
-    const char* check_what = nullptr;
-    void (*check_failure)() = nullptr;
+    // Words that kernels set when a bounded wait expired (see
+    // arm_device_check): one per scratch area that such a launch used since
+    // the last synchronisation, so a second area armed before the host reads
+    // the first does not hide the first's failure.
+    struct ArmedCheck {
+        unsigned* word;
+        const char* what;
+        void (*failure)();
+    };
+    std::vector<ArmedCheck> armed;
 };
 
 Runtime& rt() {
@@ -240,24 +247,29 @@ void range_check_locked(Runtime& r, const void* p, size_t bytes, const char* op,
                               " bytes) is not inside a live backend_hip allocation");
 }
 
-// Reads and clears the word registered by arm_device_check; the stream must
-// be synchronised.
+// Reads and clears every word registered by arm_device_check since the
+// last check; the stream must be synchronised. Reports the first that was
+// set, after clearing them all and running every failed op's callback.
 void device_check_locked(Runtime& r) {
-    if (!r.check_word) return;
-    unsigned* w = r.check_word;
-    r.check_word = nullptr;
-    unsigned v = 0;
-    hip_check(hipMemcpyAsync(&v, w, sizeof v, hipMemcpyDeviceToHost, r.stream), "hipMemcpyAsync(device check)");
-    hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
-    if (v) {
-        const unsigned z = 0;
-        hip_check(hipMemcpyAsync(w, &z, sizeof z, hipMemcpyHostToDevice, r.stream), "hipMemcpyAsync(device check)");
+    if (r.armed.empty()) return;
+    std::vector<Runtime::ArmedCheck> armed;
+    armed.swap(r.armed);
+    const char* failed = nullptr;
+    for (const auto& a : armed) {
+        unsigned v = 0;
+        hip_check(hipMemcpyAsync(&v, a.word, sizeof v, hipMemcpyDeviceToHost, r.stream), "hipMemcpyAsync(device check)");
         hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
-        if (r.check_failure) r.check_failure();
-        fail(SDH_ERR_HIP, std::string(r.check_what) +
+        if (!v) continue;
+        const unsigned z = 0;
+        hip_check(hipMemcpyAsync(a.word, &z, sizeof z, hipMemcpyHostToDevice, r.stream), "hipMemcpyAsync(device check)");
+        hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
+        if (a.failure) a.failure();
+        if (!failed) failed = a.what;
+    }
+    if (failed)
+        fail(SDH_ERR_HIP, std::string(failed) +
                               ": a bounded wait inside the kernel expired; the affected outputs hold NaN (and, for "
                               "a call made in place, the same parts of its input)");
-    }
 }
 
 }  // namespace
@@ -354,9 +366,12 @@ void* workspace(size_t bytes) {
 void arm_device_check(unsigned* word, const char* what, void (*on_failure)()) {
     Runtime& r = rt();
     std::lock_guard<std::mutex> lk(r.mu);
-    r.check_word = word;
-    r.check_what = what;
-    r.check_failure = on_failure;
+    for (auto& a : r.armed)
+        if (a.word == word) {  // the same area again: the word still holds both launches' outcome
+            if (!a.failure) a.failure = on_failure;
+            return;
+        }
+    r.armed.push_back({word, what, on_failure});
 }
 
 unsigned* counters(size_t count) {
@@ -432,7 +447,7 @@ int sdh_shutdown(void) {
         r.scratch_bytes = 0;
         r.counters = nullptr;
         r.counter_count = 0;
-        r.check_word = nullptr;
+        r.armed.clear();
         r.workspace = nullptr;
         r.workspace_bytes = 0;
         for (int i = 0; i < 2; ++i) {

@@ -541,7 +541,7 @@ void rms_norm_gated_add_(Tensor& x, const Tensor& a, const Tensor* gamma, const 
     need_hip(x, "rms_norm_gated_add_");
     same_device(x, a, "rms_norm_gated_add_");
     if (x.numel() != a.numel() || x.dim(-1) != a.dim(-1))
-        throw std::runtime_error("add_rows_scaled_: " + x.shape_str() + " vs " + a.shape_str());
+        throw std::runtime_error("rms_norm_gated_add_: " + x.shape_str() + " vs " + a.shape_str());
     const int64_t C = x.dim(-1), rows = count_of(x.numel(), C);
     if ((gamma && gamma->numel() != C) || (gate && gate->numel() != C))
         throw std::runtime_error("rms_norm_gated_add_: vector length vs " + x.shape_str());
@@ -554,7 +554,7 @@ Tensor rms_norm_gated_add_modulate_bf16_(Tensor& x, const Tensor& a, const Tenso
     need_hip(x, op);
     same_device(x, a, op);
     if (x.numel() != a.numel() || x.dim(-1) != a.dim(-1))
-        throw std::runtime_error("add_rows_scaled_: " + x.shape_str() + " vs " + a.shape_str());
+        throw std::runtime_error(std::string(op) + ": " + x.shape_str() + " vs " + a.shape_str());
     const int64_t C = x.dim(-1), rows = count_of(x.numel(), C);
     for (const Tensor* v : {gamma_out, gate, gamma_in, scale}) {
         if (!v) continue;

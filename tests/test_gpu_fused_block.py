@@ -17,6 +17,10 @@ same bf16 rounding), so the bar is exact equality:
     strided A and the hand-written kernels' shapes.
 Shapes: the Z-Image rows [4224, 3840], small and odd row widths (the generic
 kernels), optional gamma / scale / gate.
+
+The second half of the file checks the same fused entry points against the
+CPU oracle directly (the reference's composition), not only against the
+GPU's op sequence.
 """
 import numpy as np
 import pytest
@@ -234,3 +238,138 @@ def test_rms_norm_gated_add_modulate_bf16_rejects_overlap(be, orc):
     y_on_a = sdhip.DArray(be, (rows * C,), ptr=da.ptr, owned=False, dtype=np.uint16)
     with pytest.raises(sdhip.SdhError, match="overlaps"):
         be.rms_norm_gated_add_modulate_bf16(dx, da, y_on_a, rows, C, None, None, None, None, 1e-5)
+
+
+# ---------------------------------------------------------------- against the oracle
+# The bit-equality tests above compare each fused kernel with the GPU's own
+# op sequence. These compare the fused kernels with the CPU oracle directly
+# (the reference's composition, zimage.cpp:104-107, :122-133, over
+# tensor.cpp:660-679, :889-917, :732-748, :850-853, :884-887):
+#   * x, the gated residual: relative 1e-4 elementwise (a reduction's bar),
+#     cancellation elements within a few ulp of their terms |x| + |gate * an|;
+#   * y16, the next sublayer's bf16 input: the bf16 pattern of the GPU value
+#     and the nearest-even bf16 of the oracle's fp32 value (the oracle's
+#     RMSNorm and modulate applied to the x the kernel produced) differ by at
+#     most one unit in the last place (the fp32 values differ by the
+#     reductions' rounding, which moves a value across a bf16 rounding
+#     boundary at most);
+#   * swiglu_bf16 the same way; modulation rows at max-abs 1e-5.
+
+def _bf16_within_one_ulp(got16, want32, what):
+    want16 = f32_to_bf16(np.ascontiguousarray(want32, np.float32)).reshape(-1)
+    got16 = np.asarray(got16, np.uint16).reshape(-1)
+    # patterns of one sign are ordered like their magnitudes; a sign change
+    # across zero is allowed only between the two smallest patterns
+    d = np.abs(got16.astype(np.int64) - want16.astype(np.int64))
+    sign_flip = (got16 >> 15) != (want16 >> 15)
+    tiny = ((got16 & 0x7FFF) <= 1) & ((want16 & 0x7FFF) <= 1)
+    bad = np.where(sign_flip, ~tiny, d > 1)
+    n_off = int(np.count_nonzero(d != 0))
+    print(f"{what}: {n_off} of {d.size} bf16 values one ulp from the oracle's rounding, "
+          f"{int(np.count_nonzero(bad))} beyond", flush=True)
+    assert not np.any(bad), f"{what}: {int(np.count_nonzero(bad))} bf16 values beyond one ulp of the oracle"
+
+
+def _gated_add_oracle(orc, x, a, g1, gate, eps1):
+    an = orc.rms_norm(a, g1, eps1)
+    if gate is None:
+        return orc.add(x, an), np.abs(x.astype(np.float64)) + np.abs(an.astype(np.float64))
+    return (orc.add_rows_scaled(x, an, gate),
+            np.abs(x.astype(np.float64)) + np.abs(an.astype(np.float64) * gate.astype(np.float64)))
+
+
+ORACLE_ROWS = [(4224, 3840), (33, 1000), (7, 30)]
+
+
+@pytest.mark.parametrize("rows,C", ORACLE_ROWS)
+@pytest.mark.parametrize("vecs", [(True, True, True, True), (False, False, False, False), (True, False, False, True)])
+def test_rms_norm_gated_add_modulate_bf16_vs_oracle(be, orc, rows, C, vecs):
+    """Residual add + RMSNorm + modulate (the north star's fused variant)
+    against the oracle's rms_norm -> add_rows_scaled_ -> rms_norm ->
+    mul_rows_ (zimage.cpp:124-129)."""
+    from tolerances import assert_true_relative
+
+    has_g1, has_gate, has_g2, has_scale = vecs
+    x = orc.randn((rows, C), 760 + C)
+    a = orc.randn((rows, C), 761 + C, 0.0, 3.0)
+    vec = lambda on, seed, mu, sd: orc.randn((C,), seed, mu, sd) if on else None
+    g1, gate = vec(has_g1, 762, 1.0, 0.1), vec(has_gate, 763, 0.0, 0.5)
+    g2, scale = vec(has_g2, 764, 1.0, 0.1), vec(has_scale, 765, 1.0, 0.3)
+    dv = lambda v: be.array(v) if v is not None else None
+    dx, da = be.array(x), be.array(a)
+    y16 = _u16(be, rows * C)
+    be.rms_norm_gated_add_modulate_bf16(dx, da, y16, rows, C, dv(g1), dv(gate), dv(g2), dv(scale), 1e-5, 1e-6)
+    want_x, terms = _gated_add_oracle(orc, x, a, g1, gate, 1e-5)
+    got_x = dx.download().reshape(rows, C)
+    assert_true_relative(got_x, want_x, terms, f"gated add x [{rows},{C}] {vecs}")
+    # y from the x the kernel produced: an element of x that its terms nearly
+    # cancel carries their rounding (checked just above), and y's element is
+    # that x times a row factor, so it carries the same relative error; the
+    # modulate stage itself is pinned on its actual input
+    h = orc.rms_norm(got_x, g2, 1e-6)
+    if has_scale:
+        h = orc.mul_rows(h, scale)
+    _bf16_within_one_ulp(y16.download(), h, f"modulated y16 [{rows},{C}] {vecs}")
+
+
+@pytest.mark.parametrize("rows,C", ORACLE_ROWS)
+@pytest.mark.parametrize("with_gamma,with_gate", [(True, True), (False, False)])
+def test_rms_norm_gated_add_vs_oracle(be, orc, rows, C, with_gamma, with_gate):
+    """x += gate * rms_norm(a) * g against the oracle's rms_norm ->
+    add_rows_scaled_ (zimage.cpp:124-127), or add_ without a gate."""
+    from tolerances import assert_true_relative
+
+    x = orc.randn((rows, C), 770 + C)
+    a = orc.randn((rows, C), 771 + C, 0.0, 3.0)
+    g = orc.randn((C,), 772, 1.0, 0.1) if with_gamma else None
+    gate = orc.randn((C,), 773, 0.0, 0.5) if with_gate else None
+    dx = be.array(x)
+    be.rms_norm_gated_add(dx, be.array(a), rows, C, be.array(g) if with_gamma else None,
+                          be.array(gate) if with_gate else None, 1e-5)
+    want_x, terms = _gated_add_oracle(orc, x, a, g, gate, 1e-5)
+    assert_true_relative(dx.download().reshape(rows, C), want_x, terms, f"rms_norm_gated_add [{rows},{C}]")
+
+
+@pytest.mark.parametrize("rows,C", ORACLE_ROWS)
+@pytest.mark.parametrize("with_gamma,with_scale", [(True, True), (False, False)])
+def test_rms_norm_modulate_bf16_vs_oracle(be, orc, rows, C, with_gamma, with_scale):
+    """RMSNorm * scale -> bf16 against the oracle's rms_norm -> mul_rows_
+    (zimage.cpp:115-116, :128-129), then nearest-even bf16."""
+    x = orc.randn((rows, C), 780 + C, 0.0, 2.0)
+    g = orc.randn((C,), 781, 1.0, 0.1) if with_gamma else None
+    s = orc.randn((C,), 782, 1.0, 0.3) if with_scale else None
+    y16 = _u16(be, rows * C)
+    be.rms_norm_modulate_bf16(be.array(x), y16, rows, C, be.array(g) if with_gamma else None,
+                              be.array(s) if with_scale else None, 1e-5)
+    h = orc.rms_norm(x, g, 1e-5)
+    if with_scale:
+        h = orc.mul_rows(h, s)
+    _bf16_within_one_ulp(y16.download(), h, f"rms_norm_modulate_bf16 [{rows},{C}]")
+
+
+@pytest.mark.parametrize("n", [4224 * 10240, 1001])
+def test_swiglu_bf16_vs_oracle(be, orc, n):
+    """silu(g) * u -> bf16 against the oracle's swiglu (tensor.cpp:732-748),
+    then nearest-even bf16 (zimage.cpp:130, the input of w2)."""
+    g = orc.randn((n,), 790, 0.0, 1.5)
+    u = orc.randn((n,), 791, 0.0, 1.5)
+    y16 = _u16(be, n)
+    be.swiglu_bf16(be.array(g), be.array(u), y16, n)
+    _bf16_within_one_ulp(y16.download(), orc.swiglu(g, u), f"swiglu_bf16 n={n}")
+
+
+@pytest.mark.parametrize("pairs,dim", [(2, 3840), (2, 37)])
+def test_modulation_rows_vs_oracle(be, orc, pairs, dim):
+    """Rows 2p: affine_(1, 1) (1 + scale); rows 2p + 1: tanh_ (gate), against
+    the oracle (zimage.cpp:104-107; tensor.cpp:850-853, :884-887) at the
+    elementwise bar."""
+    from tolerances import assert_elementwise
+
+    x = orc.randn((2 * pairs, dim), 9400 + dim, 0.0, 2.0)
+    dx = be.array(x)
+    be.modulation_rows(dx, pairs, dim)
+    got = dx.download().reshape(2 * pairs, dim)
+    want = np.empty_like(x)
+    want[0::2] = orc.affine(x[0::2], 1.0, 1.0)
+    want[1::2] = orc.tanh(x[1::2])
+    assert_elementwise(got, want, f"modulation_rows [{2 * pairs},{dim}]")

@@ -205,6 +205,40 @@ def test_expired_wait_is_reported():
     assert r.returncode == 0 and "expiry ok" in r.stdout
 
 
+def test_expired_waits_in_two_scratch_areas_both_reported():
+    """SDH_GN_SPIN_LIMIT=0, a library GroupNorm (team slots and flag word in
+    the library's counters) and then an allocation-free one (its own fixed
+    scratch), both resident and both expiring, before one synchronisation:
+    the failure reported is the first call's (the second arming must not
+    hide it), both outputs are NaN, both flag words are cleared (the next
+    synchronisation is clean) and the library keeps working afterwards."""
+    body = (
+        "shape = (1, 256, 256, 256); C = 256; HW = 256 * 256\n"
+        "x = orc.randn(shape, 4610, 0.5, 2.0)\n"
+        "g = be.array(orc.randn((C,), 4611, 1.0, 0.1)); b = be.array(orc.randn((C,), 4612, 0.0, 0.1))\n"
+        "d, o1, o2 = be.array(x), be.empty(shape), be.empty(shape)\n"
+        "be.call('sdh_group_norm_silu', d.ptr, o1.ptr, 1, C, HW, 32, g.ptr, b.ptr, 1e-6)\n"
+        "be.call('sdh_group_norm_silu_noalloc', d.ptr, o2.ptr, 1, C, HW, 32, g.ptr, b.ptr, 1e-6)\n"
+        "try:\n"
+        "    be.synchronize(); print('no error'); sys.exit(1)\n"
+        "except sdhip.SdhError as e:\n"
+        "    assert e.status == sdhip.SDH_ERR_HIP and 'sdh_group_norm_silu: a bounded wait' in str(e), e\n"
+        "be.synchronize()\n"
+        "assert np.isnan(o1.download()).all() and np.isnan(o2.download()).all()\n"
+        "o3, want3 = run(shape, 32, 1e-6, True, 4613)\n"
+        "assert_reduction(o3.download(), want3, 'library call after expiry')\n"
+        "x4 = orc.randn(shape, 4614, 0.5, 2.0); d4, o4 = be.array(x4), be.empty(shape)\n"
+        "be.call('sdh_group_norm_silu_noalloc', d4.ptr, o4.ptr, 1, C, HW, 32, g.ptr, b.ptr, 1e-6)\n"
+        "o5 = be.empty(shape)\n"
+        "be.call('sdh_group_norm_silu', d4.ptr, o5.ptr, 1, C, HW, 32, g.ptr, b.ptr, 1e-6)\n"
+        "assert np.array_equal(o4.download(), o5.download())\n"
+        "be.synchronize()\n"
+        "print('two areas ok')\n"
+    )
+    r = _child({"SDH_GN_SPIN_LIMIT": "0"}, body)
+    assert r.returncode == 0 and "two areas ok" in r.stdout
+
+
 def test_two_processes_at_once():
     """Two child processes run resident GroupNorms at the same time as each
     other, while this process holds its own device context: every result

@@ -86,7 +86,8 @@ def test_noalloc_equals_group_norm_silu(be, orc):
 
 
 def _child(env, body):
-    code = ("import sys, ctypes as C; sys.path.insert(0, %r)\nimport numpy as np, sdhip\n" % PKG_DIR) + body
+    code = ("import sys, ctypes as C; sys.path[:0] = [%r, %r]\nimport numpy as np, sdhip\n"
+            % (PKG_DIR, os.path.join(ROOT, "oracle"))) + body
     r = subprocess.run([sys.executable, "-u", "-c", code], capture_output=True, text=True, timeout=240,
                        env=dict(os.environ, **env))
     print(r.stdout, r.stderr[-2000:])
@@ -95,20 +96,40 @@ def _child(env, body):
 
 def test_noalloc_rejects_before_init_and_oversize():
     """Before sdh_init: SDH_ERR_INVALID naming sdh_init, no device work.
-    Split schedule forced (SDH_GN_RESIDENT=0) on 12800 segments of 65540
-    floats: their chunk statistics need 1,024,000 bytes, more than the
-    983,040 the fixed scratch holds: SDH_ERR_INVALID, nothing launched (the
-    3.4 GB tensor is never written), and the library still works."""
+    Split schedule forced (SDH_GN_RESIDENT=0):
+      * 12800 segments of 65540 floats, whose chunk statistics (1,024,000
+        bytes) exceed the 983,040 the fixed scratch holds, run in two blocks
+        of segments and equal sdh_group_norm_silu (one block, arena scratch)
+        bit for bit; the samples cycle through 7 distinct ones, so a block
+        that read or wrote another block's segments would show;
+      * one segment of 1,006,632,960 floats (122,880 chunks: its own
+        statistics exceed the array) is rejected with SDH_ERR_INVALID before
+        anything is launched, and the library still works."""
     body = (
         "lib = sdhip.load_library(sdhip.LIB_PATH)\n"
         "st = lib.sdh_group_norm_silu_noalloc(None, None, 1, 32, 64, 32, None, None, 1e-6)\n"
         "msg = lib.sdh_last_error().decode()\n"
         "assert st == sdhip.SDH_ERR_INVALID and 'sdh_init' in msg, (st, msg)\n"
+        "from oracle import Oracle\n"
+        "orc = Oracle()\n"
         "be = sdhip.Backend()\n"
         "N, C, HW, groups = 400, 32, 65540, 32\n"
-        "x = be.empty((N, C, HW)); g = be.array(np.ones(C, np.float32)); b = be.array(np.zeros(C, np.float32))\n"
+        "x = be.empty((N, C, HW)); y1 = be.empty((N, C, HW)); y2 = be.empty((N, C, HW))\n"
+        "S = C * HW\n"
+        "samples = [be.array(orc.randn((S,), 9600 + i, 0.3 * i, 1.0 + 0.25 * i)) for i in range(7)]\n"
+        "for n in range(N):\n"
+        "    be.call('sdh_copy', x.ptr + 4 * n * S, samples[n % 7].ptr, 4 * S)\n"
+        "g = be.array(orc.randn((C,), 9610, 1.0, 0.1)); b = be.array(orc.randn((C,), 9611, 0.0, 0.1))\n"
+        "be.call('sdh_group_norm_silu_noalloc', x.ptr, y1.ptr, N, C, HW, groups, g.ptr, b.ptr, 1e-6)\n"
+        "be.call('sdh_group_norm_silu', x.ptr, y2.ptr, N, C, HW, groups, g.ptr, b.ptr, 1e-6)\n"
+        "a1, a2 = y1.download(), y2.download()\n"
+        "assert np.isfinite(a1).all() and np.array_equal(a1, a2), 'blocked noalloc differs'\n"
+        "print('blocked ok', flush=True)\n"
+        "del x, y1, y2, a1, a2\n"
+        "HW1 = 122880 * 8192\n"
+        "big = be.empty((1, 1, HW1))\n"
         "try:\n"
-        "    be.call('sdh_group_norm_silu_noalloc', x.ptr, x.ptr, N, C, HW, groups, g.ptr, b.ptr, 1e-6)\n"
+        "    be.call('sdh_group_norm_silu_noalloc', big.ptr, big.ptr, 1, 1, HW1, 1, g.ptr, b.ptr, 1e-6)\n"
         "    print('accepted'); sys.exit(1)\n"
         "except sdhip.SdhError as e:\n"
         "    assert e.status == sdhip.SDH_ERR_INVALID and 'bytes of scratch' in str(e), e\n"
