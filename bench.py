@@ -23,7 +23,14 @@ steps (both bracketed by a device synchronize).
 
 The CPU baseline is the reference's own tensor.cpp (oracle/_ref, compiled from
 /root/reference) timed in this process on the host's cores; if it is absent,
-the C restatement (oracle/liboracle.so) is timed instead ("port").
+the C restatement (oracle/liboracle.so) is timed instead ("port"). It is timed
+on every BASELINE config line by default (median of 5 runs after one, 3 for
+tensors over 1 GB); --cpu-all adds the other lines.
+
+Ops whose step is shorter than 25 us are launch-bound: a ctypes loop cannot
+issue them as fast as the GPU runs them. Their steps are also captured into
+one graph (sdh_capture_begin) and replayed, and us_per_op is that replay's
+device time; the host-paced figure is kept as us_per_op_host_paced.
 """
 from __future__ import annotations
 
@@ -47,6 +54,9 @@ METRIC = "achieved HBM GB/s (% of peak) per op at Z-Image 1024² shapes; speedup
 T, D, F = 4096, 3840, 10240
 MIN_ROTATION_BYTES = 512_000_000  # 2x the 256 MB Infinity Cache
 MAX_SETS = 32
+# ops whose host-paced step is shorter than this are also timed as one
+# captured graph of the same steps (the GPU's time, not the ctypes loop's)
+GRAPH_BELOW_MS = 0.025
 
 
 # ------------------------------------------------------------------ workloads
@@ -128,6 +138,7 @@ def _peek(R, h, shape):
 
 
 class AddRmsNorm(Workload):
+    config_line = True  # a BASELINE config: the reference CPU path is timed beside it
     name, kernel = "add_rms_norm", "k_add_rms"
     desc = "config 1: x += r; y = rms_norm(x) * w; x, r [4096,3840], w [3840], eps 1e-6"
     algo_bytes = 4 * T * D * 4 + D * 4
@@ -149,6 +160,7 @@ class AddRmsNorm(Workload):
 
 
 class SwiGLU(Workload):
+    config_line = True  # a BASELINE config: the reference CPU path is timed beside it
     name, kernel = "swiglu", "k_swiglu"
     desc = "config 2: y = silu(g) * u; g, u [4096,10240] ~N(0,1.5)"
     algo_bytes = 3 * T * F * 4
@@ -165,6 +177,7 @@ class SwiGLU(Workload):
 
 
 class RopeQK(Workload):
+    config_line = True  # a BASELINE config: the reference CPU path is timed beside it
     name, kernel = "rope_qk", "k_rope_il_reg"
     desc = ("config 3: 3-axis interleaved RoPE in place on q and k [4096,30*128] in one launch, axes (32,48,48), "
             "theta 256, reference-format duplicated cos/sin tables [4096,128]")
@@ -268,6 +281,7 @@ class QKNormRope(Workload):
 
 
 class GNSiLU(Workload):
+    config_line = True  # a BASELINE config: the reference CPU path is timed beside it
     kernel = "k_gn_"
     results = {"y": ("rel", 1e-4)}
 
@@ -299,6 +313,7 @@ class GNSiLU(Workload):
 
 
 class LNModGate(Workload):
+    config_line = True  # a BASELINE config: the reference CPU path is timed beside it
     name, kernel = "ln_modulate_gate", "k_ln_mod_gate"
     desc = ("config 5a: y = layer_norm(x)*(1+scale)+shift; res += tanh(gate)*y (y not stored); x, res [4096,3840]; "
             "scale, shift, gate [3840] ~N(0,0.2); eps 1e-6")
@@ -438,6 +453,7 @@ class RmsGatedAddMod(Workload):
 
 
 class Softmax(Workload):
+    config_line = True  # a BASELINE config: the reference CPU path is timed beside it
     name, kernel = "softmax_rows", "k_softmax"
     desc = "config 5b: in-place row softmax of scores [30,4096,4096] ~N(0,3), scale 1/sqrt(128), non-causal"
     algo_bytes = 2 * 30 * T * T * 4
@@ -860,6 +876,27 @@ def measure_gpu(be, w, steps, warmup, check=False):
     be.synchronize()
     wall = time.perf_counter() - t0
     ev_ms = be.timer_elapsed(0, 1)
+    graph_ms = None
+    if ev_ms / steps < GRAPH_BELOW_MS:
+        # launch-bound: the host's ctypes loop, not the GPU, sets the pace of
+        # the loop above; the same steps captured into one graph run back to
+        # back on the device (sdh_capture_begin), which is the GPU's time
+        be.capture_begin()
+        try:
+            for i in range(steps):
+                w.step(be, sets[i % nsets])
+        finally:
+            g = be.capture_end()
+        try:
+            be.graph_launch(g)  # warm-up replay
+            be.synchronize()
+            be.timer_record(0)
+            be.graph_launch(g)
+            be.timer_record(1)
+            be.synchronize()
+            graph_ms = be.timer_elapsed(0, 1)
+        finally:
+            be.graph_destroy(g)
     got = None
     if host is not None and w.results:
         w.reload(be, sets[0], host)
@@ -868,8 +905,11 @@ def measure_gpu(be, w, steps, warmup, check=False):
     for st in sets:
         for a in st.values():
             a.free()
-    return dict(nsets=nsets, footprint=footprint * nsets, wall_ms=wall * 1e3 / steps, event_ms=ev_ms / steps,
-                got=got, host=host)
+    out = dict(nsets=nsets, footprint=footprint * nsets, wall_ms=wall * 1e3 / steps, event_ms=ev_ms / steps,
+               got=got, host=host)
+    if graph_ms is not None:
+        out.update(host_paced_ms=ev_ms / steps, event_ms=graph_ms / steps, graph=True)
+    return out
 
 
 # ------------------------------------------------------------------ CPU leg: reference timing and parity
@@ -1161,7 +1201,8 @@ def main():
     ap.add_argument("--only", default=None, help="comma list: measure only these workloads (profiling runs)")
     ap.add_argument("--op-steps", type=int, default=20, help="timed steps per op in the per-op table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-all", action="store_true", help="time the reference CPU path for every config")
+    ap.add_argument("--cpu-all", action="store_true",
+                    help="time the reference CPU path on every line (the BASELINE config lines always are)")
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--list", action="store_true")
     ap.add_argument("--rocprof-summary", nargs="+", metavar="DIR",
@@ -1214,6 +1255,9 @@ def main():
         entry = dict(op=w.name, desc=w.desc, algo_bytes=w.algo_bytes, us_per_op=round(r["event_ms"] * 1e3, 2),
                      GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1), rotation_sets=r["nsets"],
                      rotation_MB=round(r["footprint"] / 2**20), traffic_bytes=read_traffic(w.name))
+        if r.get("graph"):
+            entry.update(timing="device: the steps captured into one graph and replayed (sdh_capture_begin)",
+                         us_per_op_host_paced=round(r["host_paced_ms"] * 1e3, 2))
         if w.inputs:
             entry["seeds"] = w.seeds()
         if "params" in r:
@@ -1227,8 +1271,11 @@ def main():
                          mfma_peak=peak_name)
         if r.get("got") is not None:
             heavy = w.algo_bytes > (1 << 30) or (flops or 0) > 1e10
+            # every BASELINE config line carries the reference CPU time by
+            # default; --cpu-all adds the other lines
+            timed = w is head or getattr(w, "config_line", False) or args.cpu_all
             reps = (args.cpu_reps if w is head else
-                    (1 if (flops or 0) > 1e10 else 3 if heavy else args.cpu_reps) if args.cpu_all else 0)
+                    (1 if (flops or 0) > 1e10 else 3 if heavy else args.cpu_reps) if timed else 0)
             c = run_reference(R, w, r["host"], reps)
             if c is not None and c["want"] is not None:
                 per, worst = parity(r["got"], c["want"], w.results)

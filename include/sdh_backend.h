@@ -353,6 +353,21 @@ int sdh_fill_normal(float* x, int64_t n, uint64_t seed, float mean, float std);
 int sdh_timer_record(int slot);
 /* Milliseconds between two recorded slots; waits for the second. */
 int sdh_timer_elapsed(int start_slot, int end_slot, float* ms);
+/* Graph capture of the library stream, for callers that replay a fixed
+ * sequence of ops with no host work between launches (and for timing
+ * launch-bound ops on the device). Between sdh_capture_begin and
+ * sdh_capture_end the ops' launches are recorded, not run; sdh_capture_end
+ * returns an instantiated graph that sdh_graph_launch queues on the library
+ * stream (in order with every other call) and sdh_graph_destroy frees after
+ * waiting for the stream. While capturing, everything that waits on the
+ * stream (upload, download, synchronize, timer readout) and every op whose
+ * scratch would have to grow is refused with SDH_ERR_INVALID: run each op
+ * once before capturing it. The graph keeps the pointers it was captured
+ * with. */
+int sdh_capture_begin(void);
+int sdh_capture_end(void** graph);
+int sdh_graph_launch(void* graph);
+int sdh_graph_destroy(void* graph);
 
 #ifdef __cplusplus
 }

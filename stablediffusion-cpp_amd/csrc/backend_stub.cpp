@@ -99,5 +99,9 @@ STUB(int sdh_unpatchify(const float*, float*, int64_t, int64_t, int64_t, int))
 STUB(int sdh_fill_normal(float*, int64_t, uint64_t, float, float))
 STUB(int sdh_timer_record(int))
 STUB(int sdh_timer_elapsed(int, int, float*))
+STUB(int sdh_capture_begin(void))
+STUB(int sdh_capture_end(void**))
+STUB(int sdh_graph_launch(void*))
+STUB(int sdh_graph_destroy(void*))
 
 }  // extern "C"

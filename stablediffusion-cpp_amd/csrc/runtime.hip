@@ -178,6 +178,10 @@ struct Runtime {
         void (*failure)();
     };
     std::vector<ArmedCheck> armed;
+    // Set between sdh_capture_begin and sdh_capture_end: the stream is being
+    // recorded into a graph, so nothing may wait on it or grow a buffer
+    // that queued work could still be reading.
+    bool capturing = false;
 };
 
 Runtime& rt() {
@@ -245,6 +249,15 @@ void range_check_locked(Runtime& r, const void* p, size_t bytes, const char* op,
     if (inside(r.arena.requested) || inside(r.external)) return;
     fail(SDH_ERR_INVALID, std::string(op) + ": " + what + " (" + std::to_string(bytes) +
                               " bytes) is not inside a live backend_hip allocation");
+}
+
+// Refuses what would wait on the stream (or replace a buffer that queued
+// work may read) while the stream is being recorded into a graph.
+void not_capturing_locked(const Runtime& r, const char* what) {
+    if (r.capturing)
+        fail(SDH_ERR_INVALID, std::string(what) +
+                                  ": not allowed while the library stream is being captured (sdh_capture_begin); "
+                                  "run the op once before capturing so its scratch is sized");
 }
 
 // Reads and clears every word registered by arm_device_check since the
@@ -330,6 +343,7 @@ void* scratch(size_t bytes) {
     Runtime& r = rt();
     std::lock_guard<std::mutex> lk(r.mu);
     if (bytes > r.scratch_bytes) {
+        not_capturing_locked(r, "backend_hip scratch");
         if (r.scratch) {
             // Work queued earlier may still read the old scratch.
             hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
@@ -349,6 +363,7 @@ void* workspace(size_t bytes) {
     Runtime& r = rt();
     std::lock_guard<std::mutex> lk(r.mu);
     if (bytes > r.workspace_bytes) {
+        not_capturing_locked(r, "backend_hip GEMM workspace");
         if (r.workspace) {
             hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
             r.arena.release(r.workspace);
@@ -378,6 +393,7 @@ unsigned* counters(size_t count) {
     Runtime& r = rt();
     std::lock_guard<std::mutex> lk(r.mu);
     if (count > r.counter_count) {
+        not_capturing_locked(r, "backend_hip counters");
         if (r.counters) {
             hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
             device_check_locked(r);  // the registered word may live in the old block
@@ -440,6 +456,7 @@ int sdh_shutdown(void) {
         Runtime& r = rt();
         std::lock_guard<std::mutex> lk(r.mu);
         if (!r.inited) return;
+        not_capturing_locked(r, "sdh_shutdown");
         hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
         r.arena.clear();
         r.external.clear();
@@ -498,6 +515,7 @@ int sdh_upload(void* dst, const void* src, size_t bytes) {
         ensure_init();
         Runtime& r = rt();
         std::lock_guard<std::mutex> lk(r.mu);
+        not_capturing_locked(r, "sdh_upload");
         range_check_locked(r, dst, bytes, "sdh_upload", "dst");
         size_t off = 0;
         int b = 0;
@@ -521,6 +539,7 @@ int sdh_download(void* dst, const void* src, size_t bytes) {
         ensure_init();
         Runtime& r = rt();
         std::lock_guard<std::mutex> lk(r.mu);
+        not_capturing_locked(r, "sdh_download");
         range_check_locked(r, src, bytes, "sdh_download", "src");
         // Pipeline: copy chunk i into staging buffer i%2 while the host drains
         // chunk i-1 from the other buffer.
@@ -565,6 +584,7 @@ int sdh_synchronize(void) {
         Runtime& r = rt();
         std::lock_guard<std::mutex> lk(r.mu);
         if (!r.inited) return;
+        not_capturing_locked(r, "sdh_synchronize");
         hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
         device_check_locked(r);
     });
@@ -612,8 +632,69 @@ int sdh_timer_elapsed(int a, int b, float* ms) {
             fail(SDH_ERR_INVALID, "sdh_timer_elapsed: bad slot or NULL output");
         ensure_init();
         Runtime& r = rt();
+        {
+            std::lock_guard<std::mutex> lk(r.mu);
+            not_capturing_locked(r, "sdh_timer_elapsed");
+        }
         hip_check(hipEventSynchronize(r.timers[b]), "hipEventSynchronize(timer)");
         hip_check(hipEventElapsedTime(ms, r.timers[a], r.timers[b]), "hipEventElapsedTime");
+    });
+}
+
+// Graph capture of the library stream: the launches of the ops called
+// between begin and end are recorded, not run, and replay as one graph with
+// no host work between them. Ops whose scratch would have to grow, and
+// everything that waits on the stream, are refused while capturing.
+int sdh_capture_begin(void) {
+    return guarded([&] {
+        ensure_init();
+        Runtime& r = rt();
+        std::lock_guard<std::mutex> lk(r.mu);
+        if (r.capturing) fail(SDH_ERR_INVALID, "sdh_capture_begin: a capture is already open");
+        hip_check(hipStreamBeginCapture(r.stream, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
+        r.capturing = true;
+    });
+}
+
+int sdh_capture_end(void** graph) {
+    return guarded([&] {
+        if (!graph) fail(SDH_ERR_INVALID, "sdh_capture_end: graph is NULL");
+        *graph = nullptr;
+        Runtime& r = rt();
+        std::lock_guard<std::mutex> lk(r.mu);
+        if (!r.capturing) fail(SDH_ERR_INVALID, "sdh_capture_end: no capture is open");
+        r.capturing = false;
+        hipGraph_t g = nullptr;
+        hip_check(hipStreamEndCapture(r.stream, &g), "hipStreamEndCapture");
+        if (!g) fail(SDH_ERR_HIP, "sdh_capture_end: the capture produced no graph");
+        hipGraphExec_t e = nullptr;
+        const hipError_t ie = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        hip_check(ie, "hipGraphInstantiate");
+        *graph = (void*)e;
+    });
+}
+
+int sdh_graph_launch(void* graph) {
+    return guarded([&] {
+        if (!graph) fail(SDH_ERR_INVALID, "sdh_graph_launch: graph is NULL");
+        ensure_init();
+        Runtime& r = rt();
+        std::lock_guard<std::mutex> lk(r.mu);
+        not_capturing_locked(r, "sdh_graph_launch");
+        hip_check(hipGraphLaunch((hipGraphExec_t)graph, r.stream), "hipGraphLaunch");
+    });
+}
+
+int sdh_graph_destroy(void* graph) {
+    return guarded([&] {
+        if (!graph) return;
+        Runtime& r = rt();
+        std::lock_guard<std::mutex> lk(r.mu);
+        not_capturing_locked(r, "sdh_graph_destroy");
+        // a launch of it may still be queued
+        hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
+        hip_check(hipGraphExecDestroy((hipGraphExec_t)graph), "hipGraphExecDestroy");
     });
 }
 

@@ -109,6 +109,10 @@ SIGNATURES = {
     "sdh_fill_normal": [_vp, _i64, C.c_uint64, _fl, _fl],
     "sdh_timer_record": [_int],
     "sdh_timer_elapsed": [_int, _int, C.POINTER(C.c_float)],
+    "sdh_capture_begin": [],
+    "sdh_capture_end": [C.POINTER(C.c_void_p)],
+    "sdh_graph_launch": [_vp],
+    "sdh_graph_destroy": [_vp],
 }
 _RESTYPES = {
     "sdh_last_error": C.c_char_p,
@@ -261,6 +265,22 @@ class Backend:
         ms = C.c_float()
         self.check(self.lib.sdh_timer_elapsed(a, b, C.byref(ms)))
         return ms.value
+
+    def capture_begin(self):
+        """Starts recording the library stream into a graph (sdh_capture_begin)."""
+        self.check(self.lib.sdh_capture_begin())
+
+    def capture_end(self) -> int:
+        """Ends the recording; returns the instantiated graph's handle."""
+        g = C.c_void_p()
+        self.check(self.lib.sdh_capture_end(C.byref(g)))
+        return g.value
+
+    def graph_launch(self, graph: int):
+        self.check(self.lib.sdh_graph_launch(graph))
+
+    def graph_destroy(self, graph: int):
+        self.check(self.lib.sdh_graph_destroy(graph))
 
     # -- ops on DArrays (argument meaning as include/sdh_backend.h) --
     def group_norm(self, x, y, N, Cc, HW, groups, gamma, beta, eps, silu=False):
