@@ -347,53 +347,52 @@ struct ResArgs {
 
 // UNIFORM: every share is full and lies in one channel (HW % (4096 V) ==
 // 0), so one (a, b) per workgroup.
-template <int V, bool UNIFORM>
-__device__ __forceinline__ void res_load(f4 (&v)[V], const float* x, int64_t base, int n4) {
-    const f4* p = (const f4*)(x + base);
-#pragma unroll
-    for (int j = 0; j < V; ++j) {
-        const int idx = threadIdx.x + kResThreads * j;
-        v[j] = (UNIFORM || idx < n4) ? dev::ld_stream(p + idx) : f4{0.f, 0.f, 0.f, 0.f};
-    }
+// A share's loads go through a buffer descriptor that covers exactly the
+// share's n4 float4 (x + base .. + 16 n4 bytes): one 32-bit offset register
+// per lane instead of a 64-bit address per load (the two register buffers
+// of the pipelined kernel leave no room for eight), and the descriptor's
+// range check returns zeros for the lanes past a short share's end without
+// a branch, and for a whole empty range without touching memory.
+// Non-temporal, like the other streaming kernels.
+//
+// The stores stay ordinary global stores. Measured on MI355X: buffer stores
+// issued while the wave's loads were still outstanding, with the compiler
+// rewriting their offset registers right after them, wrote some lanes'
+// values to the wrong place (lanes 12-15 of every row of 16 in some waves;
+// correct once the stores waited for every load, or as global stores).
+constexpr int kBufWord3 = 0x00020000;  // raw buffer, 32-bit data format
+constexpr int kNonTemporal = 2;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t share_rsrc(const float* base, int n4) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, n4 * 16, kBufWord3);
 }
 
-// Wave 0: waits for the team's (sum, M2) pairs of this round (lane i holds
-// parts i, i + 64, ...; KS slots per lane), merges them in double and
-// leaves (mean, rstd) in *stat.
+template <int V, bool UNIFORM>
+__device__ __forceinline__ void res_load(f4 (&v)[V], const float* x, int64_t base, int n4) {
+    const __amdgpu_buffer_rsrc_t r = share_rsrc(x + base, n4);
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+        v[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)threadIdx.x * 16,
+                                                                           kResThreads * 16 * j, kNonTemporal));
+}
+
+// gamma[ch] or beta[ch] through a buffer load (ch uniform; range: ch + 1 floats).
+__device__ __forceinline__ float coef_load(const float* v, int ch) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(v), (short)0, (ch + 1) * 4, kBufWord3);
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, ch * 4, 0, 0));
+}
+
+
+// The team's merge of this round's pairs, in wave 0: lane i holds parts i,
+// i + 64, ... (KS per lane) as (sv, mv); the pairs merge in double in a
+// fixed order (the split schedule's finalize arithmetic) into (mean, rstd)
+// at *stat. timed_out: a wait expired; the statistics become NaN and the
+// error word is set.
 template <int KS>
-__device__ __forceinline__ void res_team_stats(const ResArgs& a, const u64* slots, int team, int par, unsigned tag,
-                                               int share, float2* stat) {
+__device__ __forceinline__ void res_merge(const ResArgs& a, const float (&sv)[KS], const float (&mv)[KS], int share,
+                                          bool timed_out, float2* stat) {
     const int lane = threadIdx.x;
-    float sv[KS], mv[KS];
-    unsigned pending = 0;
-#pragma unroll
-    for (int k = 0; k < KS; ++k) {
-        sv[k] = 0.f;
-        mv[k] = 0.f;
-        if (lane + 64 * k < a.P) pending |= 1u << k;
-    }
-    const u64* ts = slots + (size_t)team * a.P * 4 + par * 2;
-    bool timed_out = false;
-    for (unsigned it = 0;; ++it) {
-        if (it >= a.spin_limit) {
-            timed_out = true;
-            break;
-        }
-#pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            if (pending & (1u << k)) {
-                const u64* q = ts + (size_t)(lane + 64 * k) * 4;
-                const u64 u = get_slot(q), w = get_slot(q + 1);
-                if ((unsigned)(u >> 32) == tag && (unsigned)(w >> 32) == tag) {
-                    sv[k] = __uint_as_float((unsigned)u);
-                    mv[k] = __uint_as_float((unsigned)w);
-                    pending &= ~(1u << k);
-                }
-            }
-        }
-        if (!__any(pending != 0)) break;
-        __builtin_amdgcn_s_sleep(2);
-    }
     double tot = 0.0;
 #pragma unroll
     for (int k = 0; k < KS; ++k) tot += (double)sv[k];
@@ -419,15 +418,134 @@ __device__ __forceinline__ void res_team_stats(const ResArgs& a, const u64* slot
     }
 }
 
+// Wave 0: waits for the team's pairs of this round with agent-scope vector
+// loads (ts: part i's sum and M2 at ts[2 i], ts[2 i + 1]; lane i holds
+// parts i, i + 64, ...) and merges them. These loads complete in order
+// behind every vector load the wave issued before them.
+template <int KS>
+__device__ __forceinline__ void res_team_stats(const ResArgs& a, const u64* ts, unsigned tag, int share,
+                                               float2* stat) {
+    const int lane = threadIdx.x;
+    float sv[KS], mv[KS];
+    unsigned pending = 0;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+        sv[k] = 0.f;
+        mv[k] = 0.f;
+        if (lane + 64 * k < a.P) pending |= 1u << k;
+    }
+    bool timed_out = false;
+    for (unsigned it = 0;; ++it) {
+        if (it >= a.spin_limit) {
+            timed_out = true;
+            break;
+        }
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            if (pending & (1u << k)) {
+                const u64* q = ts + (size_t)(lane + 64 * k) * 2;
+                const u64 u = get_slot(q), w = get_slot(q + 1);
+                if ((unsigned)(u >> 32) == tag && (unsigned)(w >> 32) == tag) {
+                    sv[k] = __uint_as_float((unsigned)u);
+                    mv[k] = __uint_as_float((unsigned)w);
+                    pending &= ~(1u << k);
+                }
+            }
+        }
+        if (!__any(pending != 0)) break;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    res_merge<KS>(a, sv, mv, share, timed_out, stat);
+}
+
+typedef unsigned su16 __attribute__((ext_vector_type(16)));
+
+// 8 tagged (sum, M2) pairs, 128 bytes at the uniform address p, by two
+// scalar loads that miss the scalar cache. Scalar loads have their own
+// queue and counter (lgkmcnt), so they do not wait behind the CU's
+// outstanding vector loads.
+__device__ __forceinline__ void sload_pairs8(const u64* p, su16& d0, su16& d1) {
+    asm volatile(
+        "s_load_dwordx16 %0, %2, 0x0 glc\n\t"
+        "s_load_dwordx16 %1, %2, 0x40 glc\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(d0), "=&s"(d1)
+        : "s"(p)
+        : "memory");
+}
+
+// Every wave: the team's pairs of this round (layout as res_team_stats)
+// through the scalar path, wave w polling parts 8 w .. 8 w + 7, into
+// pairs[0 .. P) in LDS; an expired wait leaves NaN there and sets the error
+// word. Needs the slots in uncached memory: the L2 keeps no copy of it, so
+// a load that misses the scalar cache sees another XCD's latest store. The
+// caller's barrier publishes pairs[].
+__device__ __forceinline__ void res_gather_scalar(const ResArgs& a, const u64* ts, unsigned tag, float2* pairs) {
+    // the wave index is uniform; readfirstlane lets the compiler keep the
+    // poll address in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+    const int np = min(8, a.P - 8 * wave);
+    if (np <= 0) return;
+    const u64* gp = ts + (size_t)wave * 16;
+    su16 d0, d1;
+    bool timed_out = false;
+    for (unsigned it = 0;; ++it) {
+        if (it >= a.spin_limit) {
+            timed_out = true;
+            break;
+        }
+        sload_pairs8(gp, d0, d1);
+        bool ok = true;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const unsigned t0 = j < 4 ? d0[4 * j + 1] : d1[4 * (j - 4) + 1];
+            const unsigned t1 = j < 4 ? d0[4 * j + 3] : d1[4 * (j - 4) + 3];
+            if (j < np) ok = ok && t0 == tag && t1 == tag;
+        }
+        if (ok) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane < np) {
+        unsigned sb = 0, mb = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const unsigned s0 = j < 4 ? d0[4 * j] : d1[4 * (j - 4)];
+            const unsigned m0 = j < 4 ? d0[4 * j + 2] : d1[4 * (j - 4) + 2];
+            sb = lane == j ? s0 : sb;
+            mb = lane == j ? m0 : mb;
+        }
+        pairs[8 * wave + lane] = timed_out ? make_float2(__builtin_nanf(""), __builtin_nanf(""))
+                                           : make_float2(__uint_as_float(sb), __uint_as_float(mb));
+    }
+    if (timed_out && lane == 0) __hip_atomic_store(a.ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // One round of one workgroup: share statistics from registers, publication,
 // (PREFETCH: the next round's loads into nxt, issued before the wait so
-// they run under it), the team wait, and y from registers.
-template <int V, bool SILU, bool UNIFORM, int KS, bool PREFETCH>
+// they run under it; the caller passes a next segment that exists, so the
+// loads are unconditional and the compiler can wait for this round's
+// channel coefficients without waiting for them), the team wait, and y
+// from registers. SPOLL: the wait reads the slots through the scalar path
+// (res_gather_scalar), so neither the wait nor the stores after it queue
+// behind the prefetch.
+template <int V, bool SILU, bool UNIFORM, int KS, bool PREFETCH, bool SPOLL>
 __device__ __forceinline__ void res_round(const ResArgs& a, f4 (&cur)[V], f4 (&nxt)[V], int seg, int next_seg,
                                           int round, int team, int ticket, int off, int n4, float* sh,
-                                          float2* stat) {
+                                          float2* stat, float2* pairs) {
     constexpr int kShare = kResThreads * V * 4;
     u64* slots = (u64*)(a.ctl + kCtlWords);
+    const int G = (int)gridDim.x;
+    const int gc = (seg % a.groups) * a.cg;
+    // UNIFORM: the share's one channel coefficient pair, loaded ahead of the
+    // prefetch so that waiting for it does not wait for the prefetch (the
+    // compiler counts a wave's vector loads down in issue order), through
+    // the same buffer path as the shares.
+    float g_ch = 0.f, b_ch = 0.f;
+    if constexpr (UNIFORM) {
+        const int ch = gc + off / a.HW;
+        g_ch = coef_load(a.gamma, ch);
+        b_ch = coef_load(a.beta, ch);
+    }
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < V; ++j) s += dev::hsum(cur[j]);  // masked entries are zero
@@ -445,23 +563,41 @@ __device__ __forceinline__ void res_round(const ResArgs& a, f4 (&cur)[V], f4 (&n
     const float M2 = block_sum<kResThreads>(m2, sh);
     const unsigned tag = (unsigned)round + 1;
     const int par = round & 1;
+    // slots: [parity][ticket] (sum, M2); a team's parts are consecutive
     if (threadIdx.x == 0) {
-        u64* mine = slots + ((size_t)ticket * 2 + par) * 2;
+        u64* mine = slots + ((size_t)par * G + ticket) * 2;
         put_slot(mine, sum, tag);
         put_slot(mine + 1, M2, tag);
     }
     if constexpr (PREFETCH) {
-        if (next_seg < a.nseg) res_load<V, UNIFORM>(nxt, a.x, (int64_t)next_seg * a.L + off, n4);
+        // past the team's last segment: an empty range, so no memory access
+        const bool more = next_seg < a.nseg;
+        res_load<V, UNIFORM>(nxt, a.x, (int64_t)(more ? next_seg : seg) * a.L + off, more ? n4 : 0);
     }
-    if (threadIdx.x < 64) res_team_stats<KS>(a, slots, team, par, tag, kShare, stat);
+    const u64* ts = slots + ((size_t)par * G + (size_t)team * a.P) * 2;
+    if constexpr (SPOLL) {
+        res_gather_scalar(a, ts, tag, pairs);
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            float sv[KS], mv[KS];
+#pragma unroll
+            for (int k = 0; k < KS; ++k) {
+                const int i = threadIdx.x + 64 * k;
+                const float2 pr = i < a.P ? pairs[i] : make_float2(0.f, 0.f);
+                sv[k] = pr.x;
+                mv[k] = pr.y;
+            }
+            res_merge<KS>(a, sv, mv, kShare, false, stat);  // an expiry left NaN pairs and set the word
+        }
+    } else {
+        if (threadIdx.x < 64) res_team_stats<KS>(a, ts, tag, kShare, stat);
+    }
     __syncthreads();
     const float meanf = stat->x, rstd = stat->y;
     f4* q = (f4*)(a.y + (int64_t)seg * a.L + off);
-    const int gc = (seg % a.groups) * a.cg;
     if constexpr (UNIFORM) {
-        const int ch = gc + off / a.HW;
-        const float ca = rstd * a.gamma[ch];
-        const float cb = a.beta[ch] - meanf * ca;
+        const float ca = rstd * g_ch;
+        const float cb = b_ch - meanf * ca;
 #pragma unroll
         for (int j = 0; j < V; ++j) dev::st_stream(q + threadIdx.x + kResThreads * j, apply4<SILU>(cur[j], ca, cb));
     } else {
@@ -504,14 +640,15 @@ __device__ __forceinline__ int res_ticket(unsigned* ctl, int* sh_ticket) {
 
 // grid = T * P workgroups of kResThreads; segments team, team + T, ... one
 // round each; P <= 64.
-template <int V, bool SILU, bool UNIFORM>
+template <int V, bool SILU, bool UNIFORM, bool SPOLL>
 __global__ __launch_bounds__(kResThreads) void k_gn_resident(ResArgs a) {
     constexpr int kShare4 = kResThreads * V;
     __shared__ float sh[kResThreads / 64];
     __shared__ float2 stat;
+    __shared__ float2 pairs[SPOLL ? kResMaxTeam : 1];
     __shared__ unsigned last;
     __shared__ int sh_ticket;
-    const int ticket = res_ticket(a.ctl, &sh_ticket);
+    const int ticket = __builtin_amdgcn_readfirstlane(res_ticket(a.ctl, &sh_ticket));
     const int team = ticket / a.P, part = ticket - team * a.P, T = gridDim.x / a.P;
     const int off = part * kShare4 * 4;
     const int n4 = UNIFORM ? kShare4 : min(kShare4, (a.L - off) >> 2);
@@ -519,7 +656,8 @@ __global__ __launch_bounds__(kResThreads) void k_gn_resident(ResArgs a) {
     for (int seg = team; seg < a.nseg; seg += T, ++round) {
         f4 v[V];
         res_load<V, UNIFORM>(v, a.x, (int64_t)seg * a.L + off, n4);
-        res_round<V, SILU, UNIFORM, 1, false>(a, v, v, seg, 0, round, team, ticket, off, n4, sh, &stat);
+        res_round<V, SILU, UNIFORM, 1, false, SPOLL>(a, v, v, seg, 0, round, team, ticket, off, n4, sh, &stat,
+                                                     pairs);
     }
     res_finish(a.ctl, &last);
 }
@@ -527,15 +665,17 @@ __global__ __launch_bounds__(kResThreads) void k_gn_resident(ResArgs a) {
 // The same schedule software-pipelined over two register buffers: round
 // r + 1's share is loaded while round r waits for its team, so the waits
 // (and the share reductions) overlap HBM traffic. P <= 128 (two slots per
-// polling lane).
-template <int V, bool SILU, bool UNIFORM>
+// polling lane). A team's last round prefetches through an empty buffer
+// range (no memory access), so every prefetch is issued unconditionally.
+template <int V, bool SILU, bool UNIFORM, bool SPOLL>
 __global__ __launch_bounds__(kResThreads) void k_gn_resident_pipe(ResArgs a) {
     constexpr int kShare4 = kResThreads * V;
     __shared__ float sh[kResThreads / 64];
     __shared__ float2 stat;
+    __shared__ float2 pairs[SPOLL ? 2 * kResMaxTeam : 1];
     __shared__ unsigned last;
     __shared__ int sh_ticket;
-    const int ticket = res_ticket(a.ctl, &sh_ticket);
+    const int ticket = __builtin_amdgcn_readfirstlane(res_ticket(a.ctl, &sh_ticket));
     const int team = ticket / a.P, part = ticket - team * a.P, T = gridDim.x / a.P;
     const int off = part * kShare4 * 4;
     const int n4 = UNIFORM ? kShare4 : min(kShare4, (a.L - off) >> 2);
@@ -544,10 +684,12 @@ __global__ __launch_bounds__(kResThreads) void k_gn_resident_pipe(ResArgs a) {
     if (seg < a.nseg) res_load<V, UNIFORM>(va, a.x, (int64_t)seg * a.L + off, n4);
     for (int round = 0; seg < a.nseg; round += 2) {
         const int s1 = seg + T;
-        res_round<V, SILU, UNIFORM, 2, true>(a, va, vb, seg, s1, round, team, ticket, off, n4, sh, &stat);
+        res_round<V, SILU, UNIFORM, 2, true, SPOLL>(a, va, vb, seg, s1, round, team, ticket, off, n4, sh, &stat,
+                                                    pairs);
         if (s1 >= a.nseg) break;
         const int s2 = s1 + T;
-        res_round<V, SILU, UNIFORM, 2, true>(a, vb, va, s1, s2, round + 1, team, ticket, off, n4, sh, &stat);
+        res_round<V, SILU, UNIFORM, 2, true, SPOLL>(a, vb, va, s1, s2, round + 1, team, ticket, off, n4, sh, &stat,
+                                                    pairs);
         seg = s2;
     }
     res_finish(a.ctl, &last);
@@ -628,31 +770,37 @@ struct ResKind {
     int V;
 };
 
-// Calls f with the instantiation for (kind, silu, uniform). Instantiated:
-// k_gn_resident V = 4, 8, 16 (16 only uniform: the per-vector channel lookup
-// would spill) and k_gn_resident_pipe V = 4, 8.
+// Calls f with the instantiation for (kind, silu, uniform, spoll).
+// Instantiated: k_gn_resident V = 4, 8, 16 (16 only uniform: the per-vector
+// channel lookup would spill) and k_gn_resident_pipe V = 4, 8; each with
+// scalar (spoll) or vector polls.
 template <class F>
-void with_resident(ResKind k, bool silu, bool uniform, F&& f) {
-    auto go = [&](auto vc, auto pc) {
+void with_resident(ResKind k, bool silu, bool uniform, bool spoll, F&& f) {
+    auto go = [&](auto vc, auto pc, auto sc) {
         constexpr int VV = decltype(vc)::value;
         constexpr bool PP = decltype(pc)::value;
+        constexpr bool SP = decltype(sc)::value;
         if constexpr (PP) {
-            if (silu) uniform ? f(k_gn_resident_pipe<VV, true, true>) : f(k_gn_resident_pipe<VV, true, false>);
-            else uniform ? f(k_gn_resident_pipe<VV, false, true>) : f(k_gn_resident_pipe<VV, false, false>);
+            if (silu) uniform ? f(k_gn_resident_pipe<VV, true, true, SP>) : f(k_gn_resident_pipe<VV, true, false, SP>);
+            else uniform ? f(k_gn_resident_pipe<VV, false, true, SP>) : f(k_gn_resident_pipe<VV, false, false, SP>);
+        } else if constexpr (VV == 16) {
+            if (silu) f(k_gn_resident<16, true, true, SP>);
+            else f(k_gn_resident<16, false, true, SP>);
         } else {
-            if (silu) uniform ? f(k_gn_resident<VV, true, true>) : f(k_gn_resident<VV, true, false>);
-            else uniform ? f(k_gn_resident<VV, false, true>) : f(k_gn_resident<VV, false, false>);
+            if (silu) uniform ? f(k_gn_resident<VV, true, true, SP>) : f(k_gn_resident<VV, true, false, SP>);
+            else uniform ? f(k_gn_resident<VV, false, true, SP>) : f(k_gn_resident<VV, false, false, SP>);
         }
+    };
+    auto go2 = [&](auto vc, auto pc) {
+        if (spoll) go(vc, pc, std::true_type());
+        else go(vc, pc, std::false_type());
     };
     using P1 = std::true_type;
     using P0 = std::false_type;
-    if (k.V == 4) k.pipe ? go(std::integral_constant<int, 4>(), P1()) : go(std::integral_constant<int, 4>(), P0());
-    else if (k.V == 8) k.pipe ? go(std::integral_constant<int, 8>(), P1()) : go(std::integral_constant<int, 8>(), P0());
-    else if (k.V == 16 && !k.pipe && uniform) {
-        if (silu) f(k_gn_resident<16, true, true>);
-        else f(k_gn_resident<16, false, true>);
-    } else
-        fail(SDH_ERR_INVALID, "k_gn_resident: no such instantiation");
+    if (k.V == 4) k.pipe ? go2(std::integral_constant<int, 4>(), P1()) : go2(std::integral_constant<int, 4>(), P0());
+    else if (k.V == 8) k.pipe ? go2(std::integral_constant<int, 8>(), P1()) : go2(std::integral_constant<int, 8>(), P0());
+    else if (k.V == 16 && !k.pipe && uniform) go2(std::integral_constant<int, 16>(), P0());
+    else fail(SDH_ERR_INVALID, "k_gn_resident: no such instantiation");
 }
 
 bool instantiated(ResKind k, bool uniform) { return k.pipe ? (k.V == 4 || k.V == 8) : (k.V != 16 || uniform); }
@@ -673,7 +821,7 @@ int resident_occupancy(ResKind k, bool silu, bool uniform) {
     int& c = cache[k.pipe][k.V == 4 ? 0 : k.V == 8 ? 1 : 2][silu][uniform];
     if (c < 0) {
         c = 0;
-        with_resident(k, silu, uniform, [&](auto kern) {
+        with_resident(k, silu, uniform, true, [&](auto kern) {
             int nb = 0;
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kern), kResThreads, 0) ==
                 hipSuccess)
@@ -727,6 +875,7 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
     static const long force_v = env_long("SDH_GN_RESIDENT_V", 0);
     static const long force_pipe = env_long("SDH_GN_RESIDENT_PIPE", -1);
     static const unsigned spin = (unsigned)std::min<long>(env_long("SDH_GN_SPIN_LIMIT", kSpinLimit), 0x7fffffffL);
+    static const bool scalar_poll = env_long("SDH_GN_SCALAR_POLL", 1) != 0;
     if (mode == 0 || nseg > 0x7fffffffLL) return false;
     struct Plan {
         ResKind k{false, 0};
@@ -765,18 +914,29 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
     const int64_t grid = std::min(pl.T, nseg) * pl.P;
     ResArgs args{x, y, gamma, beta, nullptr, (int)L, (int)HW, (int)cg, groups, (int)nseg, (int)pl.P, spin, eps};
     const size_t ctl_words = (size_t)kCtlWords + (size_t)grid * 8;
+    // scalar polls (plans of several rounds) need the slots in the library's
+    // uncached words (the last poll of a team reads up to 7 parts past its
+    // own: 32 words of slack); the allocation-free entry point's fixed
+    // scratch is ordinary memory, so it keeps the vector polls.
+    // SDH_GN_SCALAR_POLL=0 turns the scalar polls off.
+    bool spoll = false;
     if (fixed) {
         if (ctl_words * sizeof(unsigned) > kFixedCtlBytes)
             fail(SDH_ERR_INVALID, std::string(op) + ": " + std::to_string(grid) +
                                       " resident workgroups need more team slots than the fixed scratch holds");
         args.ctl = (unsigned*)fixed;  // zero at set-up; every launch leaves it zero when it ends
+    } else if (scalar_poll && pl.rounds > 1 && (args.ctl = uncached_words(ctl_words + 32)) != nullptr) {
+        // one round has no prefetch for the wait to pass: the vector poll,
+        // without the scalar path's extra barrier, measured faster there
+        spoll = true;
     } else {
         args.ctl = counters(ctl_words);
     }
     void* argv[] = {&args};
-    with_resident(pl.k, silu, uniform, [&](auto kern) {
+    with_resident(pl.k, silu, uniform, spoll, [&](auto kern) {
         const std::string what = std::string(op) + ": launch of " + std::to_string(grid) + " resident workgroups (" +
-                                 (pl.k.pipe ? "pipelined, " : "") + "V " + std::to_string(pl.k.V) + ", " +
+                                 (pl.k.pipe ? "pipelined, " : "") + (spoll ? "scalar polls, " : "") + "V " +
+                                 std::to_string(pl.k.V) + ", " +
                                  std::to_string(resident_occupancy(pl.k, silu, uniform)) + " per CU)";
         hip_check(hipLaunchKernel(reinterpret_cast<const void*>(kern), dim3((unsigned)grid), dim3(kResThreads), argv,
                                   0, stream()),

@@ -31,6 +31,7 @@ thread_local std::string t_last_error;
 constexpr size_t kAlign = 256;
 constexpr size_t kStageBytes = 8u << 20;  // per staging buffer
 constexpr int kTimerSlots = 16;
+constexpr size_t kUncachedWords = 64u << 10;  // 256 KiB
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -182,6 +183,12 @@ struct Runtime {
     // recorded into a graph, so nothing may wait on it or grow a buffer
     // that queued work could still be reading.
     bool capturing = false;
+    // Uncached device words for cross-workgroup exchange polled through the
+    // scalar path (uncached_words): allocated once, never freed, because
+    // memory of this kind that a kernel has read must outlive the process's
+    // later allocations.
+    unsigned* uncached = nullptr;
+    size_t uncached_count = 0;
 };
 
 Runtime& rt() {
@@ -233,6 +240,18 @@ void init_locked(Runtime& r, size_t arena_bytes) {
     if (first && !r.arena.grow(first))
         fail(SDH_ERR_OOM, "backend_hip: cannot reserve the initial arena segment of " + std::to_string(first) + " bytes");
     gn_fixed_scratch_setup();
+    if (!r.uncached) {
+        // kept across sdh_shutdown and re-initialisation (see Runtime::uncached);
+        // without it the kernels that would poll it poll ordinary memory instead
+        void* p = nullptr;
+        if (hipExtMallocWithFlags(&p, kUncachedWords * sizeof(unsigned), hipDeviceMallocUncached) == hipSuccess && p) {
+            zero_device(p, kUncachedWords * sizeof(unsigned));
+            r.uncached = (unsigned*)p;
+            r.uncached_count = kUncachedWords;
+        } else {
+            (void)hipGetLastError();
+        }
+    }
     r.inited = true;
 }
 
@@ -387,6 +406,13 @@ void arm_device_check(unsigned* word, const char* what, void (*on_failure)()) {
             return;
         }
     r.armed.push_back({word, what, on_failure});
+}
+
+unsigned* uncached_words(size_t count) {
+    Runtime& r = rt();
+    std::lock_guard<std::mutex> lk(r.mu);
+    if (!r.uncached || count > r.uncached_count) return nullptr;
+    return r.uncached;
 }
 
 unsigned* counters(size_t count) {

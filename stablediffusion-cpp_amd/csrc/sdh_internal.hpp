@@ -91,6 +91,12 @@ void to_bf16_device(const char* op, const float* x, uint16_t* y, int64_t n);
 // Zero-initialised per-library device counters (uint32), persistent across
 // calls; kernels that use them leave them at zero when they finish.
 unsigned* counters(size_t count);
+// Zero-initialised device words in uncached memory (the L2 keeps no copy,
+// so a scalar load that misses the scalar cache reads what another XCD
+// stored last), persistent across calls and never freed; kernels that use
+// them leave them at zero when they finish. Null if the block holds fewer
+// than `count` words.
+unsigned* uncached_words(size_t count);
 void launched(const char* op);
 // Registers a device word that the kernel just queued sets nonzero on a
 // failure it cannot return as a status (a bounded wait that expired). The

@@ -5,6 +5,10 @@ once; teams of workgroups hold a segment in registers, exchange per-share
 
 Against the float64 oracle (tensor.cpp:592-625, then silu :843-849) at the
 reductions' relative 1e-4:
+  * plans of several rounds whose shares each lie in one channel (few
+    workgroups per team up to the 4b shape), bit-identical on repeat;
+  * the team wait through the scalar path (uncached slots) and through
+    vector loads (SDH_GN_SCALAR_POLL=0): the same bits;
   * the default choice between the resident and the split schedule;
   * the resident kernels forced (SDH_GN_RESIDENT=2) on every shape, every
     share size (V = 4, 8, 16 float4 per thread: SDH_GN_RESIDENT_V) and each
@@ -163,6 +167,44 @@ def test_resident_plain_or_pipelined_forced(pipe):
     if pipe:
         r = _child({"SDH_GN_RESIDENT": "2", "SDH_GN_RESIDENT_PIPE": "1", "SDH_GN_RESIDENT_V": "4"}, body)
         assert r.returncode == 0 and "pipe ok" in r.stdout
+
+
+# Multi-round resident plans whose shares each lie in one channel, with few
+# workgroups per team: the case in which stores that raced the prefetch
+# showed as wrong lanes (lanes 12-15 of rows of 16) in the first round.
+UNIFORM_ROUNDS = [((4, 64, 256, 256), 32), ((2, 128, 256, 256), 32), ((1, 256, 256, 256), 32),
+                  ((1, 128, 1024, 1024), 32)]
+
+
+@pytest.mark.parametrize("shape,groups", UNIFORM_ROUNDS)
+def test_uniform_shares_over_several_rounds(be, orc, shape, groups):
+    """Against the oracle, and bit-identical on a second call."""
+    a, want = _run(be, orc, shape, groups, 1e-6, True, 4700 + shape[0])
+    assert_reduction(a, want, f"uniform rounds {shape}")
+    b, _ = _run(be, orc, shape, groups, 1e-6, True, 4700 + shape[0])
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_scalar_and_vector_polls_give_the_same_bits():
+    """The team wait read through the scalar path (uncached slots, plans of
+    several rounds, the default) and through agent-scope vector loads
+    (SDH_GN_SCALAR_POLL=0) merge the same pairs in the same order: the
+    outputs are bit-identical, and both match the oracle."""
+    body = (
+        "import hashlib\n"
+        "for shape, groups in %r + [((16, 64, 100, 100), 8), ((4, 96, 300, 300), 3)]:\n"
+        "    o, want = run(shape, groups, 1e-6, True, 4750)\n"
+        "    got = o.download()\n"
+        "    assert_reduction(got, want, f'poll {shape}')\n"
+        "    print('digest', shape, hashlib.sha1(got.tobytes()).hexdigest(), flush=True)\n"
+        "print('polls ok')\n"
+    ) % (UNIFORM_ROUNDS,)
+    outs = []
+    for sp in ("1", "0"):
+        r = _child({"SDH_GN_SCALAR_POLL": sp}, body)
+        assert r.returncode == 0 and "polls ok" in r.stdout
+        outs.append([l for l in r.stdout.splitlines() if l.startswith("digest")])
+    assert outs[0] == outs[1] and len(outs[0]) == len(UNIFORM_ROUNDS) + 2
 
 
 def test_split_schedule_still_reachable():
