@@ -644,57 +644,246 @@ __global__ __launch_bounds__(kThreads) void k_rms_gated_add_mod(float* __restric
     store_mod_bf16<V, PAIR>(y + row * n4, xv, rstd2, g2, scale, lane, n4, [](int j) { return 64 * j; });
 }
 
-// one 256-thread workgroup per row (2048 < C <= 8192), wave p lane l holding
-// float4 l + 64 (p + 4 j); both sums of squares in the one-wave order through LDS
-template <int V, bool PAIR>
-__global__ __launch_bounds__(kRowThreads) void k_rms_gated_add_mod_row(float* __restrict__ x,
-                                                                      const float* __restrict__ a,
-                                                                      uint2* __restrict__ y, int C,
-                                                                      const float* __restrict__ g1,
-                                                                      const float* __restrict__ gate,
-                                                                      const float* __restrict__ g2,
-                                                                      const float* __restrict__ scale, float eps1,
-                                                                      float eps2) {
-    __shared__ float hs[2][4 * V][64];  // hs[h][k][l]: squared sum of float4 l + 64 k of a (h = 0), of x (h = 1)
+// one workgroup of W waves per row, wave p lane l holding float4 l + 64 (p +
+// W j), j < V; both sums of squares in the one-wave order (float4 block k =
+// p + W j in sequence, then the wave tree) through LDS. The column vectors
+// are loaded ahead of the stores that precede their use: g1 and gate before
+// the row, g2 and scale before the x stores. A wave's vector loads and
+// stores are counted down in issue order, so a vector loaded after the x
+// stores would have waited for every one of them to complete before the
+// bf16 row could be formed. The vectors are never null here: the launcher
+// passes a vector of ones for an absent one (an absent gate is the plain
+// add), which leaves every product and sum bit-equal to leaving it out.
+template <int W, int V, bool PAIR>
+__global__ __launch_bounds__(64 * W) void k_rms_gated_add_mod_row(float* __restrict__ x, const float* __restrict__ a,
+                                                                 uint2* __restrict__ y, int C,
+                                                                 const float* __restrict__ g1,
+                                                                 const float* __restrict__ gate,
+                                                                 const float* __restrict__ g2,
+                                                                 const float* __restrict__ scale, float eps1,
+                                                                 float eps2) {
+    __shared__ float hs[2][W * V][64];  // hs[h][k][l]: squared sum of float4 l + 64 k of a (h = 0), of x (h = 1)
     const int lane = threadIdx.x & 63, p = threadIdx.x >> 6;
     const int n4 = C >> 2;
     const int64_t row = blockIdx.x;
     const f4* ar = (const f4*)(a + row * C);
     f4* xr = (f4*)(x + row * C);
+    auto pos = [&](int j) __attribute__((always_inline)) { return lane + 64 * (p + W * j); };
+    // lanes past the row read a valid column vector (their values are never stored)
+    auto col = [&](const float* vec, int j) __attribute__((always_inline)) {
+        return ((const f4*)vec)[min(pos(j), n4 - 1)];
+    };
+    f4 c1[V], cg[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        c1[j] = col(g1, j);
+        cg[j] = col(gate, j);
+    }
     f4 v[V], xv[V];
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-        const int idx = lane + 64 * (p + 4 * j);
-        v[j] = idx < n4 ? dev::ld_stream(ar + idx) : zero4();
-    }
+    for (int j = 0; j < V; ++j) v[j] = pos(j) < n4 ? dev::ld_stream(ar + pos(j)) : zero4();
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-        const int idx = lane + 64 * (p + 4 * j);
-        xv[j] = idx < n4 ? dev::ld_stream(xr + idx) : zero4();
-    }
+    for (int j = 0; j < V; ++j) xv[j] = pos(j) < n4 ? dev::ld_stream(xr + pos(j)) : zero4();
 #pragma unroll
-    for (int j = 0; j < V; ++j) hs[0][p + 4 * j][lane] = dev::sumsq4(v[j]);
+    for (int j = 0; j < V; ++j) hs[0][p + W * j][lane] = dev::sumsq4(v[j]);
     __syncthreads();
     float q = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4 * V; ++k) q += hs[0][k][lane];  // zero entries past the row add exactly 0
+    for (int k = 0; k < W * V; ++k) q += hs[0][k][lane];  // zero entries past the row add exactly 0
     const float rstd1 = rstd_of(dev::wave_sum(q), C, eps1);
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-        const int idx = lane + 64 * (p + 4 * j);
-        if (idx < n4) {
-            xv[j] = gated_add4(v[j], xv[j], rstd1, g1, gate, idx);
-            dev::st_stream(xr + idx, xv[j]);
+#pragma clang fp contract(off)
+        f4 o = v[j] * rstd1;
+        o = o * c1[j];
+        const f4 g = cg[j], xo = xv[j];
+        xv[j] = f4{fmaf(g.x, o.x, xo.x), fmaf(g.y, o.y, xo.y), fmaf(g.z, o.z, xo.z), fmaf(g.w, o.w, xo.w)};
+    }
+    // the second pair of vectors, into the registers the first pair and the a row leave
+    f4 c2[V], cs[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        c2[j] = col(g2, j);
+        cs[j] = col(scale, j);
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        if (pos(j) < n4) {
+            dev::st_stream(xr + pos(j), xv[j]);
+            hs[1][p + W * j][lane] = dev::sumsq4(xv[j]);
+        } else {
+            hs[1][p + W * j][lane] = 0.f;
         }
-        hs[1][p + 4 * j][lane] = dev::sumsq4(xv[j]);
     }
     __syncthreads();
     float q2 = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4 * V; ++k) q2 += hs[1][k][lane];
+    for (int k = 0; k < W * V; ++k) q2 += hs[1][k][lane];
     const float rstd2 = rstd_of(dev::wave_sum(q2), C, eps2);
-    store_mod_bf16<V, PAIR>(y + row * n4, xv, rstd2, g2, scale, lane, n4,
-                            [p](int j) { return 64 * (p + 4 * j); });
+    // y16 = bf16(((x * rstd2) * g2) * scale), k_rms_mod_bf16's products
+    uint2 b[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+#pragma clang fp contract(off)
+        f4 o = xv[j] * rstd2;
+        o = o * c2[j];
+        o = o * cs[j];
+        b[j] = dev::bf16x4(o);
+    }
+    uint2* yr = y + row * n4;
+    if constexpr (PAIR) {
+        // adjacent lanes swap one bf16x4 so every lane stores 16 contiguous bytes
+        const bool odd = lane & 1;
+        auto swap = [](unsigned u) { return (unsigned)__builtin_amdgcn_mov_dpp((int)u, 0xB1, 0xF, 0xF, false); };
+#pragma unroll
+        for (int j = 0; j + 1 < V; j += 2) {
+            const uint2 b0 = b[j], b1 = b[j + 1];
+            const uint2 send = odd ? b0 : b1;
+            const uint2 rr = {swap(send.x), swap(send.y)};
+            const dev::u4v w = odd ? dev::u4v{rr.x, rr.y, b1.x, b1.y} : dev::u4v{b0.x, b0.y, rr.x, rr.y};
+            const int at = odd ? pos(j + 1) - 1 : pos(j);
+            if (at < n4) __builtin_nontemporal_store(w, reinterpret_cast<dev::u4v*>(yr + at));
+        }
+        if constexpr (V & 1) {
+            if (pos(V - 1) < n4) dev::st_stream(yr + pos(V - 1), b[V - 1]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+            if (pos(j) < n4) dev::st_stream(yr + pos(j), b[j]);
+    }
+}
+
+// The same op over R consecutive rows per workgroup, for rows of exactly
+// 64 W V float4 (3840 = 64 x 5 x 3). The four column vectors are loaded once
+// per workgroup and kept in registers: loaded once per row they are 61 KB of
+// L2 reads per 45 KB row of HBM traffic, and measured they, not HBM, bound
+// the one-row-per-workgroup kernel (its byte mix without them: 35 us at
+// [4096, 3840]; with them: 44 us). Row i + 1 is loaded while row i is
+// formed, ahead of row i's stores, through buffer loads over the row, so a
+// workgroup's last prefetch covers an empty range (no memory access) and
+// every load is issued unconditionally. Per row the arithmetic and both
+// sums of squares are k_rms_gated_add_mod_row's, so the results are
+// bit-equal to it and to the two ops.
+template <int W, int V>
+__device__ __forceinline__ void rows_load(f4 (&v)[V], const float* base, bool present) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, present ? 64 * W * V * 16 : 0, 0x00020000);
+    const int lane = threadIdx.x & 63, p = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < V; ++j)
+        v[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, (lane + 64 * p) * 16, 64 * W * 16 * j, 2));
+}
+
+// 1 / rms of a row from its per-block sums of squares h[k][lane] (block k =
+// float4 lane + 64 k): wave 0 adds them per lane in block order, then the
+// wave tree (the one-wave kernels' order), and broadcasts the result through
+// *out; the other waves read one word instead of K per lane. Two barriers:
+// the first publishes h, the second *out. The caller's next write of h comes
+// after the second barrier, which every wave passes after wave 0's reads.
+template <int K>
+__device__ __forceinline__ float rows_rstd(const float (*h)[64], float* out, int C, float eps) {
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        float q = 0.f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) q += h[k][threadIdx.x];
+        const float r = rstd_of(dev::wave_sum(q), C, eps);
+        if (threadIdx.x == 0) *out = r;
+    }
+    __syncthreads();
+    return *out;
+}
+
+template <int W, int V, bool PAIR>
+__device__ __forceinline__ void rows_one(float* __restrict__ x, const float* __restrict__ a, uint2* __restrict__ y,
+                                         int64_t rows, int64_t row, int C, f4 (&v)[V], f4 (&xc)[V], f4 (&an)[V],
+                                         f4 (&xn)[V], int64_t next, const f4 (&c1)[V], const f4 (&cg)[V],
+                                         const f4 (&c2)[V], const f4 (&cs)[V], float eps1, float eps2,
+                                         float (*hs)[W * V][64], float* rs) {
+    const int lane = threadIdx.x & 63, p = threadIdx.x >> 6;
+    constexpr int n4 = 64 * W * V;
+    auto pos = [&](int j) __attribute__((always_inline)) { return lane + 64 * (p + W * j); };
+#pragma unroll
+    for (int j = 0; j < V; ++j) hs[0][p + W * j][lane] = dev::sumsq4(v[j]);
+    const float rstd1 = rows_rstd<W * V>(hs[0], rs, C, eps1);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+#pragma clang fp contract(off)
+        f4 o = v[j] * rstd1;
+        o = o * c1[j];
+        const f4 g = cg[j], xo = xc[j];
+        xc[j] = f4{fmaf(g.x, o.x, xo.x), fmaf(g.y, o.y, xo.y), fmaf(g.z, o.z, xo.z), fmaf(g.w, o.w, xo.w)};
+    }
+    // row `next`, ahead of this row's stores (an empty range past the workgroup's last row)
+    const bool more = next < rows;
+    rows_load<W, V>(an, a + (more ? next : row) * (int64_t)C, more);
+    rows_load<W, V>(xn, x + (more ? next : row) * (int64_t)C, more);
+    f4* xr = (f4*)(x + row * (int64_t)C);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        dev::st_stream(xr + pos(j), xc[j]);
+        hs[1][p + W * j][lane] = dev::sumsq4(xc[j]);
+    }
+    const float rstd2 = rows_rstd<W * V>(hs[1], rs + 1, C, eps2);
+    uint2 b[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+#pragma clang fp contract(off)
+        f4 o = xc[j] * rstd2;
+        o = o * c2[j];
+        o = o * cs[j];
+        b[j] = dev::bf16x4(o);
+    }
+    uint2* yr = y + row * (int64_t)n4;
+    if constexpr (PAIR) {
+        const bool odd = lane & 1;
+        auto swap = [](unsigned u) { return (unsigned)__builtin_amdgcn_mov_dpp((int)u, 0xB1, 0xF, 0xF, false); };
+#pragma unroll
+        for (int j = 0; j + 1 < V; j += 2) {
+            const uint2 b0 = b[j], b1 = b[j + 1];
+            const uint2 send = odd ? b0 : b1;
+            const uint2 rr = {swap(send.x), swap(send.y)};
+            const dev::u4v w = odd ? dev::u4v{rr.x, rr.y, b1.x, b1.y} : dev::u4v{b0.x, b0.y, rr.x, rr.y};
+            __builtin_nontemporal_store(w, reinterpret_cast<dev::u4v*>(yr + (odd ? pos(j + 1) - 1 : pos(j))));
+        }
+        if constexpr (V & 1) dev::st_stream(yr + pos(V - 1), b[V - 1]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j) dev::st_stream(yr + pos(j), b[j]);
+    }
+}
+
+template <int W, int V, bool PAIR, int R>
+__global__ __launch_bounds__(64 * W) void k_rms_gated_add_mod_rows(float* __restrict__ x, const float* __restrict__ a,
+                                                                  uint2* __restrict__ y, int64_t rows, int C,
+                                                                  const float* __restrict__ g1,
+                                                                  const float* __restrict__ gate,
+                                                                  const float* __restrict__ g2,
+                                                                  const float* __restrict__ scale, float eps1,
+                                                                  float eps2) {
+    __shared__ float hs[2][W * V][64];
+    __shared__ float rs[2];
+    const int lane = threadIdx.x & 63, p = threadIdx.x >> 6;
+    const int64_t r0 = (int64_t)blockIdx.x * R;
+    const int64_t end = r0 + R < rows ? r0 + R : rows;  // this workgroup's rows [r0, end)
+    f4 c1[V], cg[V], c2[V], cs[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const int i = lane + 64 * (p + W * j);
+        c1[j] = ((const f4*)g1)[i];
+        cg[j] = ((const f4*)gate)[i];
+        c2[j] = ((const f4*)g2)[i];
+        cs[j] = ((const f4*)scale)[i];
+    }
+    f4 v[V], xa[V], xb[V];
+    rows_load<W, V>(v, a + r0 * (int64_t)C, true);
+    rows_load<W, V>(xa, x + r0 * (int64_t)C, true);
+    for (int64_t row = r0; row < end; row += 2) {
+        rows_one<W, V, PAIR>(x, a, y, end, row, C, v, xa, v, xb, row + 1, c1, cg, c2, cs, eps1, eps2, hs, rs);
+        if (row + 1 >= end) break;
+        rows_one<W, V, PAIR>(x, a, y, end, row + 1, C, v, xb, v, xa, row + 2, c1, cg, c2, cs, eps1, eps2, hs, rs);
+    }
 }
 
 // the row-per-workgroup kernels' float4 per lane for a row of n4 float4, or 0
@@ -962,16 +1151,38 @@ void run_rms_gated_add_mod(float* x, const float* a, uint16_t* y, int64_t rows, 
     uint2* yy = (uint2*)y;
     const int rv = pick_row_v(n4);
     if (rv) {
-        in_pieces(rows, units_per_launch(kRowThreads), [&](int64_t r0, int64_t nr) {
+        // absent column vectors become a vector of ones (bit-equal, see the kernel)
+        const float* one = ones_vector(C);
+        const float *v1 = g1 ? g1 : one, *vg = gate ? gate : one, *v2 = g2 ? g2 : one, *vs = scale ? scale : one;
+        // rows of exactly 960 float4 (C = 3840, the Z-Image width) take the
+        // multi-row kernel: 15 waves, one float4 per lane, 8 rows per workgroup
+        const bool rows15 = n4 == 64 * 15;
+        in_pieces(rows, units_per_launch(rows15 ? 960 / 8 : kRowThreads), [&](int64_t r0, int64_t nr) {
             const int64_t o = r0 * C;
-            auto go = [&](auto vc, auto pc) {
-                constexpr int V = decltype(vc)::value;
+            auto go = [&](auto wc, auto vc, auto pc) {
+                constexpr int W = decltype(wc)::value, V = decltype(vc)::value;
                 constexpr bool P = decltype(pc)::value;
-                k_rms_gated_add_mod_row<V, P><<<(unsigned)nr, kRowThreads, 0, stream()>>>(
-                    x + o, a + o, yy + r0 * n4, (int)C, g1, gate, g2, scale, eps1, eps2);
+                k_rms_gated_add_mod_row<W, V, P><<<(unsigned)nr, 64 * W, 0, stream()>>>(
+                    x + o, a + o, yy + r0 * n4, (int)C, v1, vg, v2, vs, eps1, eps2);
             };
-            if (rv == 4) pair ? go(std::integral_constant<int, 4>(), std::true_type()) : go(std::integral_constant<int, 4>(), std::false_type());
-            else pair ? go(std::integral_constant<int, 8>(), std::true_type()) : go(std::integral_constant<int, 8>(), std::false_type());
+            using I4 = std::integral_constant<int, 4>;
+            using T_ = std::true_type;
+            using F_ = std::false_type;
+            if (rows15) {
+                // measured at [4096, 3840]: 15 waves x 1 float4, 8 rows per
+                // workgroup 39.3 us; 5 x 3 over 8 rows 45 us; 15 x 1 over 4
+                // rows 42 us, over 16 rows 43.6 us; two rows ahead 41.9 us
+                constexpr int R = 8;
+                const unsigned g = (unsigned)((nr + R - 1) / R);
+                if (pair)
+                    k_rms_gated_add_mod_rows<15, 1, true, R><<<g, 960, 0, stream()>>>(
+                        x + o, a + o, yy + r0 * n4, nr, (int)C, v1, vg, v2, vs, eps1, eps2);
+                else
+                    k_rms_gated_add_mod_rows<15, 1, false, R><<<g, 960, 0, stream()>>>(
+                        x + o, a + o, yy + r0 * n4, nr, (int)C, v1, vg, v2, vs, eps1, eps2);
+            }
+            else if (rv == 4) pair ? go(I4(), I4(), T_()) : go(I4(), I4(), F_());
+            else pair ? go(I4(), std::integral_constant<int, 8>(), T_()) : go(I4(), std::integral_constant<int, 8>(), F_());
         });
     } else {
         in_pieces(rows, rows_per_launch(), [&](int64_t r0, int64_t nr) {

@@ -189,6 +189,10 @@ struct Runtime {
     // later allocations.
     unsigned* uncached = nullptr;
     size_t uncached_count = 0;
+    // A vector of 1.0f for kernels that take a missing column vector as ones
+    // (ones_vector).
+    float* ones = nullptr;
+    size_t ones_count = 0;
 };
 
 Runtime& rt() {
@@ -408,6 +412,33 @@ void arm_device_check(unsigned* word, const char* what, void (*on_failure)()) {
     r.armed.push_back({word, what, on_failure});
 }
 
+__global__ void k_fill_ones(float* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 1.0f;
+}
+
+const float* ones_vector(size_t n) {
+    Runtime& r = rt();
+    std::lock_guard<std::mutex> lk(r.mu);
+    if (n > r.ones_count) {
+        not_capturing_locked(r, "backend_hip ones vector");
+        if (r.ones) {
+            hip_check(hipStreamSynchronize(r.stream), "hipStreamSynchronize");
+            r.arena.release(r.ones);
+        }
+        const size_t cnt = round_up(std::max(n, (size_t)4096), 64);
+        r.ones = (float*)r.arena.alloc(cnt * sizeof(float));
+        if (!r.ones) {
+            r.ones_count = 0;
+            fail(SDH_ERR_OOM, "backend_hip: arena exhausted allocating the ones vector");
+        }
+        k_fill_ones<<<(unsigned)std::min<size_t>((cnt + 255) / 256, 1024), 256, 0, r.stream>>>(r.ones, cnt);
+        hip_check(hipGetLastError(), "k_fill_ones");
+        r.ones_count = cnt;
+    }
+    return r.ones;
+}
+
 unsigned* uncached_words(size_t count) {
     Runtime& r = rt();
     std::lock_guard<std::mutex> lk(r.mu);
@@ -490,6 +521,8 @@ int sdh_shutdown(void) {
         r.scratch_bytes = 0;
         r.counters = nullptr;
         r.counter_count = 0;
+        r.ones = nullptr;
+        r.ones_count = 0;
         r.armed.clear();
         r.workspace = nullptr;
         r.workspace_bytes = 0;

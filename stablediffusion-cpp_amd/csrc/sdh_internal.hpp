@@ -97,6 +97,9 @@ unsigned* counters(size_t count);
 // them leave them at zero when they finish. Null if the block holds fewer
 // than `count` words.
 unsigned* uncached_words(size_t count);
+// At least n floats of 1.0f on the device, library-owned and persistent (for
+// kernels that take a missing column vector as ones).
+const float* ones_vector(size_t n);
 void launched(const char* op);
 // Registers a device word that the kernel just queued sets nonzero on a
 // failure it cannot return as a status (a bounded wait that expired). The
