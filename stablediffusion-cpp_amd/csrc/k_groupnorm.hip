@@ -321,6 +321,7 @@ __global__ __launch_bounds__(kThreads) void k_gn_apply(const float* __restrict__
 // synchronisation, and from then on this process runs the split schedule
 // instead (an in-place call, y == x, has then lost the expired shares of x).
 constexpr int kResThreads = 1024;
+
 constexpr int kResMaxTeam = 64;  // workgroups per segment per slot of a polling lane
 constexpr int kCtlWords = 64;     // ctl[0] finished workgroups, ctl[1] error word, ctl[2] ticket; slots from ctl + 64
 constexpr unsigned kSpinLimit = 1u << 20;  // polls of about 1 us: a wait ends within about a second
@@ -339,7 +340,8 @@ struct ResArgs {
     float* y;
     const float* gamma;
     const float* beta;
-    unsigned* ctl;
+    unsigned* ctl;  // ctl[0] finished workgroups, ctl[1] error word, ctl[2] ticket
+    u64* slots;     // the team slots: [parity][workgroup] (sum, M2); uncached for scalar polls
     int L, HW, cg, groups, nseg, P;
     unsigned spin_limit;
     float eps;
@@ -367,13 +369,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t share_rsrc(const float* base, 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, n4 * 16, kBufWord3);
 }
 
-template <int V, bool UNIFORM>
+template <int V, bool UNIFORM, int TPB = kResThreads>
 __device__ __forceinline__ void res_load(f4 (&v)[V], const float* x, int64_t base, int n4) {
     const __amdgpu_buffer_rsrc_t r = share_rsrc(x + base, n4);
 #pragma unroll
     for (int j = 0; j < V; ++j)
-        v[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)threadIdx.x * 16,
-                                                                           kResThreads * 16 * j, kNonTemporal));
+        v[j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)threadIdx.x * 16, TPB * 16 * j,
+                                                                           kNonTemporal));
 }
 
 // gamma[ch] or beta[ch] through a buffer load (ch uniform; range: ch + 1 floats).
@@ -528,12 +530,12 @@ __device__ __forceinline__ void res_gather_scalar(const ResArgs& a, const u64* t
 // from registers. SPOLL: the wait reads the slots through the scalar path
 // (res_gather_scalar), so neither the wait nor the stores after it queue
 // behind the prefetch.
-template <int V, bool SILU, bool UNIFORM, int KS, bool PREFETCH, bool SPOLL>
+template <int V, bool SILU, bool UNIFORM, int KS, bool PREFETCH, bool SPOLL, int TPB = kResThreads>
 __device__ __forceinline__ void res_round(const ResArgs& a, f4 (&cur)[V], f4 (&nxt)[V], int seg, int next_seg,
                                           int round, int team, int ticket, int off, int n4, float* sh,
                                           float2* stat, float2* pairs) {
-    constexpr int kShare = kResThreads * V * 4;
-    u64* slots = (u64*)(a.ctl + kCtlWords);
+    constexpr int kShare = TPB * V * 4;
+    u64* slots = a.slots;
     const int G = (int)gridDim.x;
     const int gc = (seg % a.groups) * a.cg;
     // UNIFORM: the share's one channel coefficient pair, loaded ahead of the
@@ -549,18 +551,18 @@ __device__ __forceinline__ void res_round(const ResArgs& a, f4 (&cur)[V], f4 (&n
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < V; ++j) s += dev::hsum(cur[j]);  // masked entries are zero
-    const float sum = block_sum<kResThreads>(s, sh);
+    const float sum = block_sum<TPB>(s, sh);
     const float mc = sum / (float)(n4 * 4);
     float m2 = 0.f;
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-        const int idx = threadIdx.x + kResThreads * j;
+        const int idx = threadIdx.x + TPB * j;
         if (UNIFORM || idx < n4) {
             const f4 d = cur[j] - mc;
             m2 += dev::hsum(d * d);
         }
     }
-    const float M2 = block_sum<kResThreads>(m2, sh);
+    const float M2 = block_sum<TPB>(m2, sh);
     const unsigned tag = (unsigned)round + 1;
     const int par = round & 1;
     // slots: [parity][ticket] (sum, M2); a team's parts are consecutive
@@ -572,7 +574,7 @@ __device__ __forceinline__ void res_round(const ResArgs& a, f4 (&cur)[V], f4 (&n
     if constexpr (PREFETCH) {
         // past the team's last segment: an empty range, so no memory access
         const bool more = next_seg < a.nseg;
-        res_load<V, UNIFORM>(nxt, a.x, (int64_t)(more ? next_seg : seg) * a.L + off, more ? n4 : 0);
+        res_load<V, UNIFORM, TPB>(nxt, a.x, (int64_t)(more ? next_seg : seg) * a.L + off, more ? n4 : 0);
     }
     const u64* ts = slots + ((size_t)par * G + (size_t)team * a.P) * 2;
     if constexpr (SPOLL) {
@@ -599,11 +601,11 @@ __device__ __forceinline__ void res_round(const ResArgs& a, f4 (&cur)[V], f4 (&n
         const float ca = rstd * g_ch;
         const float cb = b_ch - meanf * ca;
 #pragma unroll
-        for (int j = 0; j < V; ++j) dev::st_stream(q + threadIdx.x + kResThreads * j, apply4<SILU>(cur[j], ca, cb));
+        for (int j = 0; j < V; ++j) dev::st_stream(q + threadIdx.x + TPB * j, apply4<SILU>(cur[j], ca, cb));
     } else {
 #pragma unroll
         for (int j = 0; j < V; ++j) {
-            const int idx = threadIdx.x + kResThreads * j;
+            const int idx = threadIdx.x + TPB * j;
             if (idx < n4) {
                 const int ch = gc + (int)((unsigned)(off + idx * 4) / (unsigned)a.HW);
                 const float ca = rstd * a.gamma[ch];
@@ -617,13 +619,12 @@ __device__ __forceinline__ void res_round(const ResArgs& a, f4 (&cur)[V], f4 (&n
 // Every workgroup has taken its ticket and finished its reads of the slots
 // before it counts itself finished; the last one clears the slots of this
 // launch, the ticket and the counter.
-__device__ __forceinline__ void res_finish(unsigned* ctl, unsigned* last) {
-    u64* slots = (u64*)(ctl + kCtlWords);
+__device__ __forceinline__ void res_finish(unsigned* ctl, u64* slots, unsigned* last) {
     if (threadIdx.x == 0)
         *last = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
     __syncthreads();
     if (*last) {
-        for (unsigned i = threadIdx.x; i < gridDim.x * 4; i += kResThreads)
+        for (unsigned i = threadIdx.x; i < gridDim.x * 4; i += blockDim.x)
             __hip_atomic_store(slots + i, (u64)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (threadIdx.x == 0 || threadIdx.x == 2)
             __hip_atomic_store(ctl + threadIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -659,7 +660,7 @@ __global__ __launch_bounds__(kResThreads) void k_gn_resident(ResArgs a) {
         res_round<V, SILU, UNIFORM, 1, false, SPOLL>(a, v, v, seg, 0, round, team, ticket, off, n4, sh, &stat,
                                                      pairs);
     }
-    res_finish(a.ctl, &last);
+    res_finish(a.ctl, a.slots, &last);
 }
 
 // The same schedule software-pipelined over two register buffers: round
@@ -692,7 +693,7 @@ __global__ __launch_bounds__(kResThreads) void k_gn_resident_pipe(ResArgs a) {
                                                     pairs);
         seg = s2;
     }
-    res_finish(a.ctl, &last);
+    res_finish(a.ctl, a.slots, &last);
 }
 
 // ---- generic (any HW / alignment): one workgroup per segment, three strided
@@ -912,7 +913,8 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
     if (!pl.k.V) return false;
     const bool uniform = HW % ((int64_t)kResThreads * 4 * pl.k.V) == 0;
     const int64_t grid = std::min(pl.T, nseg) * pl.P;
-    ResArgs args{x, y, gamma, beta, nullptr, (int)L, (int)HW, (int)cg, groups, (int)nseg, (int)pl.P, spin, eps};
+    ResArgs args{x, y, gamma, beta, nullptr, nullptr, (int)L, (int)HW, (int)cg, groups, (int)nseg, (int)pl.P,
+                 spin, eps};
     const size_t ctl_words = (size_t)kCtlWords + (size_t)grid * 8;
     // scalar polls (plans of several rounds) need the slots in the library's
     // uncached words (the last poll of a team reads up to 7 parts past its
@@ -925,12 +927,21 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
             fail(SDH_ERR_INVALID, std::string(op) + ": " + std::to_string(grid) +
                                       " resident workgroups need more team slots than the fixed scratch holds");
         args.ctl = (unsigned*)fixed;  // zero at set-up; every launch leaves it zero when it ends
-    } else if (scalar_poll && pl.rounds > 1 && (args.ctl = uncached_words(ctl_words + 32)) != nullptr) {
-        // one round has no prefetch for the wait to pass: the vector poll,
-        // without the scalar path's extra barrier, measured faster there
-        spoll = true;
+        args.slots = (u64*)(args.ctl + kCtlWords);
     } else {
+        // the counters (ticket, finish, error word) in ordinary memory: an
+        // atomic on uncached memory goes to the memory controller, and one
+        // per workgroup on one word serialises there
         args.ctl = counters(ctl_words);
+        args.slots = (u64*)(args.ctl + kCtlWords);
+        if (scalar_poll && pl.rounds > 1) {
+            // one round has no prefetch for the wait to pass: the vector
+            // poll, without the scalar path's extra barrier, measured faster
+            if (unsigned* w = uncached_words((size_t)grid * 8 + 32)) {
+                args.slots = (u64*)w;
+                spoll = true;
+            }
+        }
     }
     void* argv[] = {&args};
     with_resident(pl.k, silu, uniform, spoll, [&](auto kern) {
