@@ -1041,9 +1041,9 @@ KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
 
 
 # Resident workgroups per CU of the gfx950 build of each resident GroupNorm
-# kernel (its VGPR count at 1024 threads): k_gn_resident V=4 (59-62 VGPRs)
-# 2, V=8 (70-94) 1, V=16 (107) 1; k_gn_resident_pipe V=4 (80-89) 1, V=8
-# (112-124) 1.
+# kernel (its VGPR count at 1024 threads; the library plans with the
+# vector-poll variants): k_gn_resident V=4 (60-62 VGPRs) 2, V=8 (76-89) 1,
+# V=16 (112) 1; k_gn_resident_pipe V=4 (82-86) 1, V=8 (114-126) 1.
 GN_RESIDENT_OCC = {(False, 4): 2, (False, 8): 1, (False, 16): 1, (True, 4): 1, (True, 8): 1}
 
 

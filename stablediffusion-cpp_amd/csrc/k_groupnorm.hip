@@ -808,21 +808,22 @@ bool instantiated(ResKind k, bool uniform) { return k.pipe ? (k.V == 4 || k.V ==
 
 // Resident workgroups per CU of one instantiation (0 if none); cached (calls
 // are serialised by the op lock).
-int resident_occupancy(ResKind k, bool silu, bool uniform) {
-    static int cache[2][3][2][2];
+int resident_occupancy(ResKind k, bool silu, bool uniform, bool spoll = false) {
+    static int cache[2][3][2][2][2];
     static bool filled = false;
     if (!filled) {
         for (auto& a : cache)
             for (auto& b : a)
                 for (auto& c : b)
-                    for (int& d : c) d = -1;
+                    for (auto& d : c)
+                        for (int& e : d) e = -1;
         filled = true;
     }
     if (!instantiated(k, uniform)) return 0;
-    int& c = cache[k.pipe][k.V == 4 ? 0 : k.V == 8 ? 1 : 2][silu][uniform];
+    int& c = cache[k.pipe][k.V == 4 ? 0 : k.V == 8 ? 1 : 2][silu][uniform][spoll];
     if (c < 0) {
         c = 0;
-        with_resident(k, silu, uniform, true, [&](auto kern) {
+        with_resident(k, silu, uniform, spoll, [&](auto kern) {
             int nb = 0;
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kern), kResThreads, 0) ==
                 hipSuccess)
@@ -934,7 +935,10 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
         // per workgroup on one word serialises there
         args.ctl = counters(ctl_words);
         args.slots = (u64*)(args.ctl + kCtlWords);
-        if (scalar_poll && pl.rounds > 1) {
+        // plans are made with the vector-poll kernels' occupancy; the scalar
+        // one must hold as many workgroups per CU (its grid is the same)
+        if (scalar_poll && pl.rounds > 1 &&
+            resident_occupancy(pl.k, silu, uniform, true) >= resident_occupancy(pl.k, silu, uniform)) {
             // one round has no prefetch for the wait to pass: the vector
             // poll, without the scalar path's extra barrier, measured faster
             if (unsigned* w = uncached_words((size_t)grid * 8 + 32)) {
@@ -948,7 +952,7 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
         const std::string what = std::string(op) + ": launch of " + std::to_string(grid) + " resident workgroups (" +
                                  (pl.k.pipe ? "pipelined, " : "") + (spoll ? "scalar polls, " : "") + "V " +
                                  std::to_string(pl.k.V) + ", " +
-                                 std::to_string(resident_occupancy(pl.k, silu, uniform)) + " per CU)";
+                                 std::to_string(resident_occupancy(pl.k, silu, uniform, spoll)) + " per CU)";
         hip_check(hipLaunchKernel(reinterpret_cast<const void*>(kern), dim3((unsigned)grid), dim3(kResThreads), argv,
                                   0, stream()),
                   what.c_str());
