@@ -140,10 +140,11 @@ def test_rms_norm_heads(be, orc, groups, dim, affine):
     assert_reduction(dx.download(), orc.rms_norm_heads(x, dim, w, 1e-5), f"rms_norm_heads [{groups},{dim}]")
 
 
-@pytest.mark.parametrize("rows,C", [(T, D), (7, 64), (3, 70), (1, 9000)])
+@pytest.mark.parametrize("rows,C", [(T, D), (13, D), (1, D), (7, 64), (3, 70), (1, 9000)])
 @pytest.mark.parametrize("affine", [True, False])
 def test_add_rms_norm(be, orc, rows, C, affine):
-    """Config 1: fused residual add + RMSNorm vs add_ then rms_norm."""
+    """Config 1: fused residual add + RMSNorm vs add_ then rms_norm (also a
+    few rows, and one row, at the config width)."""
     x = orc.randn((rows, C), _seed("arn_x", rows, C))
     r = orc.randn((rows, C), _seed("arn_r", rows, C))
     w = orc.randn((C,), _seed("arn_w", C), 1.0, 0.1) if affine else None
