@@ -754,8 +754,8 @@ __global__ __launch_bounds__(64 * W) void k_rms_gated_add_mod_row(float* __restr
     }
 }
 
-// The same op over R consecutive rows per workgroup, for rows of exactly
-// 64 W V float4 (3840 = 64 x 5 x 3). The four column vectors are loaded once
+// The same op over consecutive rows per workgroup, for rows of exactly
+// 64 W V float4 (3840 = 64 x 15 x 1). The four column vectors are loaded once
 // per workgroup and kept in registers: loaded once per row they are 61 KB of
 // L2 reads per 45 KB row of HBM traffic, and measured they, not HBM, bound
 // the one-row-per-workgroup kernel (its byte mix without them: 35 us at
@@ -854,7 +854,10 @@ __device__ __forceinline__ void rows_one(float* __restrict__ x, const float* __r
     }
 }
 
-template <int W, int V, bool PAIR, int R>
+// Workgroup b of G takes rows [b rows / G, (b + 1) rows / G): G at most one
+// round of resident workgroups, so every workgroup starts at once and each
+// runs rows / G rows, give or take one.
+template <int W, int V, bool PAIR>
 __global__ __launch_bounds__(64 * W) void k_rms_gated_add_mod_rows(float* __restrict__ x, const float* __restrict__ a,
                                                                   uint2* __restrict__ y, int64_t rows, int C,
                                                                   const float* __restrict__ g1,
@@ -865,8 +868,8 @@ __global__ __launch_bounds__(64 * W) void k_rms_gated_add_mod_rows(float* __rest
     __shared__ float hs[2][W * V][64];
     __shared__ float rs[2];
     const int lane = threadIdx.x & 63, p = threadIdx.x >> 6;
-    const int64_t r0 = (int64_t)blockIdx.x * R;
-    const int64_t end = r0 + R < rows ? r0 + R : rows;  // this workgroup's rows [r0, end)
+    const int64_t r0 = (int64_t)blockIdx.x * rows / gridDim.x;
+    const int64_t end = (int64_t)(blockIdx.x + 1) * rows / gridDim.x;  // this workgroup's rows [r0, end)
     f4 c1[V], cg[V], c2[V], cs[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {
@@ -884,6 +887,21 @@ __global__ __launch_bounds__(64 * W) void k_rms_gated_add_mod_rows(float* __rest
         if (row + 1 >= end) break;
         rows_one<W, V, PAIR>(x, a, y, end, row + 1, C, v, xb, v, xa, row + 2, c1, cg, c2, cs, eps1, eps2, hs, rs);
     }
+}
+
+// Workgroups of k_rms_gated_add_mod_rows<15, 1, pair> the GPU holds at once
+// (resident per CU x CUs; 2 x 256 on MI355X); cached.
+int64_t rows15_slots(bool pair) {
+    static int64_t cache[2] = {0, 0};
+    int64_t& c = cache[pair];
+    if (!c) {
+        int nb = 0;
+        const void* k = pair ? reinterpret_cast<const void*>(k_rms_gated_add_mod_rows<15, 1, true>)
+                             : reinterpret_cast<const void*>(k_rms_gated_add_mod_rows<15, 1, false>);
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 960, 0) != hipSuccess || nb < 1) nb = 1;
+        c = (int64_t)nb * num_cus();
+    }
+    return c;
 }
 
 // the row-per-workgroup kernels' float4 per lane for a row of n4 float4, or 0
@@ -1169,16 +1187,18 @@ void run_rms_gated_add_mod(float* x, const float* a, uint16_t* y, int64_t rows, 
             using T_ = std::true_type;
             using F_ = std::false_type;
             if (rows15) {
-                // measured at [4096, 3840]: 15 waves x 1 float4, 8 rows per
-                // workgroup 39.3 us; 5 x 3 over 8 rows 45 us; 15 x 1 over 4
-                // rows 42 us, over 16 rows 43.6 us; two rows ahead 41.9 us
-                constexpr int R = 8;
-                const unsigned g = (unsigned)((nr + R - 1) / R);
+                // measured at [4096, 3840]: 15 waves x 1 float4 over 8 rows
+                // per workgroup (512 workgroups: two per CU, one round)
+                // 39.3 us; 5 x 3 over 8 rows 45 us; 15 x 1 over 4 rows (two
+                // rounds) 42 us, over 16 rows (one workgroup per CU) 43.6 us;
+                // two rows ahead 41.9 us. So: one round of resident
+                // workgroups, the rows shared out evenly.
+                const unsigned g = (unsigned)std::min<int64_t>(nr, rows15_slots(pair));
                 if (pair)
-                    k_rms_gated_add_mod_rows<15, 1, true, R><<<g, 960, 0, stream()>>>(
+                    k_rms_gated_add_mod_rows<15, 1, true><<<g, 960, 0, stream()>>>(
                         x + o, a + o, yy + r0 * n4, nr, (int)C, v1, vg, v2, vs, eps1, eps2);
                 else
-                    k_rms_gated_add_mod_rows<15, 1, false, R><<<g, 960, 0, stream()>>>(
+                    k_rms_gated_add_mod_rows<15, 1, false><<<g, 960, 0, stream()>>>(
                         x + o, a + o, yy + r0 * n4, nr, (int)C, v1, vg, v2, vs, eps1, eps2);
             }
             else if (rv == 4) pair ? go(I4(), I4(), T_()) : go(I4(), I4(), F_());

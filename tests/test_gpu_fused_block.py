@@ -179,7 +179,7 @@ def _row(be, arr, r, dim):
     return sdhip.DArray(be, (dim,), ptr=arr.ptr + 4 * r * dim, owned=False)
 
 
-FUSED_ROWS = [(4224, 3840), (64, 3072), (9, 2080), (70, 512), (33, 1000), (5, 64), (7, 30)]
+FUSED_ROWS = [(4224, 3840), (600, 3840), (128, 3840), (1, 3840), (64, 3072), (9, 2080), (70, 512), (33, 1000), (5, 64), (7, 30)]
 
 
 @pytest.mark.parametrize("rows,C", FUSED_ROWS)
@@ -278,7 +278,7 @@ def _gated_add_oracle(orc, x, a, g1, gate, eps1):
             np.abs(x.astype(np.float64)) + np.abs(an.astype(np.float64) * gate.astype(np.float64)))
 
 
-ORACLE_ROWS = [(4224, 3840), (33, 1000), (7, 30)]
+ORACLE_ROWS = [(4224, 3840), (128, 3840), (13, 3840), (33, 1000), (7, 30)]
 
 
 @pytest.mark.parametrize("rows,C", ORACLE_ROWS)
