@@ -155,7 +155,7 @@ def test_add_rms_norm(be, orc, rows, C, affine):
     assert_reduction(dy.download(), y_ref, "add_rms_norm norm")
 
 
-@pytest.mark.parametrize("rows,C", [(T, D), (9, 64), (3, 70), (2, 9000)])
+@pytest.mark.parametrize("rows,C", [(T, D), (600, D), (13, D), (1, D), (9, 64), (3, 70), (2, 9000)])
 @pytest.mark.parametrize("shift", [True, False])
 @pytest.mark.parametrize("store_y", [True, False])
 def test_ln_modulate_gate(be, orc, rows, C, shift, store_y):
