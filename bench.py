@@ -1047,50 +1047,51 @@ KERNEL_OF = {  # kernel (template) name -> workload whose step launches it
 GN_RESIDENT_OCC = {(False, 4): 2, (False, 8): 1, (False, 16): 1, (True, 4): 1, (True, 8): 1}
 
 
+def gn_split_chunk(nseg, L):
+    """run_gn's split_chunk: the largest of 8192, 4096 and 2048 floats that
+    gives 768 workgroups per pass, else 2048."""
+    for c in (8192, 4096):
+        if nseg * -(-L // c) >= 768:
+            return c
+    return 2048
+
+
 def gn_dispatches(shape, groups=32, cus=256):
     """(kernel prefix, grid work-items) of the launches that carry a GroupNorm
     workload's HBM traffic, following run_gn's choice of schedule: one
-    k_gn_single launch for segments up to 65536 floats, unless a segment
-    holds more than 24576 floats and one resident round takes the tensor;
-    else the resident plan of run_gn_resident when its policy takes the
-    tensor (one launch of k_gn_resident or k_gn_resident_pipe); else
-    k_gn_partial and k_gn_apply over 8192-float chunks (k_gn_finalize moves a
-    few KB and is left out)."""
+    k_gn_single launch for segments up to 24576 floats; else, for x of at
+    least 64 MB, the resident plan of run_gn_resident (one launch of
+    k_gn_resident or k_gn_resident_pipe); else k_gn_partial and k_gn_apply
+    over chunks of gn_split_chunk floats (k_gn_finalize moves a few KB and
+    is left out)."""
     N, Cc = shape[0], shape[1]
     HW = int(np.prod(shape[2:]))
     L, nseg = Cc // groups * HW, N * groups
-    best = {}
-    for pipe in (False, True):
-        for V in (4, 8, 16):
-            share = 4096 * V
-            P = -(-L // share)
-            if (pipe, V) not in GN_RESIDENT_OCC or P > (128 if pipe else 64) or (V == 16 and HW % share):
-                continue
-            T = GN_RESIDENT_OCC[(pipe, V)] * cus // P
-            if T == 0:
-                continue
-            rounds = -(-nseg // T)
-            key = "pipe" if pipe else "plain"
-            if key not in best or rounds < best[key][0]:
-                best[key] = (rounds, pipe, P, T)
-            if not pipe and rounds == 1 and "one" not in best:
-                best["one"] = (rounds, pipe, P, T)
-    if "pipe" in best and best["pipe"][0] == 1:  # run_gn_resident prefers a one-round pipelined plan
-        best["one"] = best["pipe"]
-    large = nseg * L * 4 >= 64 << 20
-    split_wgs = nseg * -(-L // 8192)
-    if L <= 65536:
-        plan = best.get("one") if L > 24576 and split_wgs < 1024 else None
-        if not plan:
-            n4 = L // 4
-            tpb = 256 if n4 <= 2048 else 1024
-            return [("k_gn_single", nseg * tpb)]
-    else:
-        plan = (best.get("pipe") or best.get("plain")) if large else (best.get("one") if split_wgs < 1024 else None)
-    if plan:
-        _, pipe, P, T = plan
-        return [("k_gn_resident_pipe<" if pipe else "k_gn_resident<", min(T, nseg) * P * 1024)]
-    grid = (L + 8191) // 8192 * 256 * nseg
+    if L <= 24576:
+        n4 = L // 4
+        tpb = 256 if n4 <= 2048 else 1024
+        return [("k_gn_single", nseg * tpb)]
+    if nseg * L * 4 >= 64 << 20:
+        best = {}
+        for pipe in (False, True):
+            for V in (4, 8, 16):
+                share = 4096 * V
+                P = -(-L // share)
+                if (pipe, V) not in GN_RESIDENT_OCC or P > (128 if pipe else 64) or (V == 16 and HW % share):
+                    continue
+                T = GN_RESIDENT_OCC[(pipe, V)] * cus // P
+                if T == 0:
+                    continue
+                rounds = -(-nseg // T)
+                key = "pipe" if pipe else "plain"
+                if key not in best or rounds < best[key][0]:
+                    best[key] = (rounds, pipe, P, T)
+        plan = best.get("pipe") or best.get("plain")
+        if plan:
+            _, pipe, P, T = plan
+            return [("k_gn_resident_pipe<" if pipe else "k_gn_resident<", min(T, nseg) * P * 1024)]
+    chunk = gn_split_chunk(nseg, L)
+    grid = -(-L // chunk) * (256 if chunk == 8192 else 64) * nseg
     return [("k_gn_partial", grid), ("k_gn_apply", grid)]
 
 

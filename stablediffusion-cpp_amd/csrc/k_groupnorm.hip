@@ -8,16 +8,18 @@
 // a = rstd * gamma[c], then SiLU as x / (1 + exp(-x)).
 //
 // Three schedules:
-//   * single: one workgroup (256 or 1024 threads) per segment when the
-//     segment fits in its registers (<= 65536 floats). One HBM read, one
-//     write. Used by the SD 1.5 shapes up to 24576 floats per segment;
-//     longer segments of few-segment tensors take one resident round.
+//   * single: one workgroup (256 or 1024 threads) per segment of at most
+//     24576 floats, held in its registers. One HBM read, one write. Longer
+//     segments take the split schedule below 64 MB of x, the resident one
+//     above.
 //   * resident (larger segments, large tensors): teams of workgroups hold a
 //     segment in registers across a team wait, so x is read once (two
 //     streams); pipelined over two register buffers when a team has several
 //     rounds. Described at k_gn_resident; run_gn_resident says when it is
 //     chosen.
-//   * split: the segment is cut into chunks of kChunk floats.
+//   * split: the segment is cut into chunks of 8192, 4096 or 2048 floats
+//     (split_chunk: the largest that gives the pass enough workgroups).
+//     SDH_GN_SPLIT=1 takes it for every aligned shape (a test knob).
 //       pass A (k_gn_partial): one workgroup per chunk computes the chunk's
 //         sum and its M2 around the chunk mean from registers and stores the
 //         pair. No atomics: cross-workgroup publication through device-scope
@@ -66,11 +68,13 @@ constexpr int kMaxDevices = 64;
 unsigned char* g_fixed_scratch[kMaxDevices] = {};
 
 constexpr int kThreads = 256;
-constexpr int kChunkV = 8;                               // float4 per thread per chunk
-constexpr int64_t kChunk = (int64_t)kThreads * 4 * kChunkV;  // floats per chunk (8192)
+// Split schedule chunks: TPB work-items x CV float4 each. The largest chunk
+// is 8192 floats (256 x 8); smaller ones (4096 = 64 x 16, 2048 = 64 x 8)
+// give shapes with few segments more workgroups (split_chunk).
 constexpr int64_t kGnBlockMB = 0;
-// Segments longer than this (up to 65536 floats) try one resident round
-// before the single-workgroup schedule (run_gn_resident).
+// Segments up to this many floats take the single-workgroup schedule
+// (measured: [2,640,32,32], 20480 floats, 7.6 us single, 7.5-7.7 split;
+// [2,320,32,32] 5.6 single, 9.8 split); longer ones the split or resident.
 constexpr int64_t kSmallResidentMin = 24576;
 
 // SiLU on the hardware exp2 and reciprocal: x * rcp(1 + 2^(-x log2 e)). Its
@@ -148,34 +152,36 @@ __global__ __launch_bounds__(TPB) void k_gn_single(const float* __restrict__ x, 
 // Pass A. grid = (chunks per segment, segments). Ordinary loads: measured
 // faster here than non-temporal ones (4a 17 vs 21 us), although the traffic
 // counters show pass B's re-read is not served from L2.
-__global__ __launch_bounds__(kThreads) void k_gn_partial(const float* __restrict__ x, int64_t L, int64_t nchunks,
-                                                        float2* __restrict__ part) {
-    __shared__ float sh[kThreads / 64];
+template <int TPB, int CV>
+__global__ __launch_bounds__(TPB) void k_gn_partial(const float* __restrict__ x, int64_t L, int64_t nchunks,
+                                                   float2* __restrict__ part) {
+    constexpr int64_t CH = (int64_t)TPB * 4 * CV;  // floats per chunk
+    __shared__ float sh[TPB / 64];
     const int64_t seg = blockIdx.y, chunk = blockIdx.x;
-    const int64_t off = chunk * kChunk;
-    const int64_t cnt = L - off < kChunk ? L - off : kChunk;
+    const int64_t off = chunk * CH;
+    const int64_t cnt = L - off < CH ? L - off : CH;
     const f4* p = (const f4*)(x + seg * L + off);
     const int n4 = (int)(cnt >> 2);
-    f4 v[kChunkV];
+    f4 v[CV];
     float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < kChunkV; ++j) {
-        const int idx = threadIdx.x + kThreads * j;
+    for (int j = 0; j < CV; ++j) {
+        const int idx = threadIdx.x + TPB * j;
         v[j] = idx < n4 ? p[idx] : f4{0.f, 0.f, 0.f, 0.f};
         s += dev::hsum(v[j]);
     }
-    const float sum = block_sum<kThreads>(s, sh);
+    const float sum = block_sum<TPB>(s, sh);
     const float mc = sum / (float)cnt;
     float m2 = 0.f;
 #pragma unroll
-    for (int j = 0; j < kChunkV; ++j) {
-        const int idx = threadIdx.x + kThreads * j;
+    for (int j = 0; j < CV; ++j) {
+        const int idx = threadIdx.x + TPB * j;
         if (idx < n4) {
             const f4 d = v[j] - mc;
             m2 += dev::hsum(d * d);
         }
     }
-    const float M2 = block_sum<kThreads>(m2, sh);
+    const float M2 = block_sum<TPB>(m2, sh);
     if (threadIdx.x == 0) part[seg * nchunks + chunk] = make_float2(sum, M2);
 }
 
@@ -189,7 +195,7 @@ __device__ __forceinline__ double wave_dsum(double v) {
 // butterfly): M2 = sum_i M2_i + n_i (mean_i - mean)^2. One wave per segment,
 // no LDS and no barrier. grid = segments, 64 threads.
 __global__ __launch_bounds__(64) void k_gn_finalize(const float2* __restrict__ part, int64_t L, int64_t nchunks,
-                                                   float2* __restrict__ stats, float eps) {
+                                                   int64_t chunk, float2* __restrict__ stats, float eps) {
     const int64_t seg = blockIdx.x;
     const float2* pp = part + seg * nchunks;
     double tot = 0.0;
@@ -198,7 +204,7 @@ __global__ __launch_bounds__(64) void k_gn_finalize(const float2* __restrict__ p
     double m2t = 0.0;
     for (int64_t i = threadIdx.x; i < nchunks; i += 64) {
         const float2 pr = pp[i];
-        const double ni = (double)(L - i * kChunk < kChunk ? L - i * kChunk : kChunk);
+        const double ni = (double)(L - i * chunk < chunk ? L - i * chunk : chunk);
         const double dm = (double)pr.x / ni - mean;
         m2t += (double)pr.y + ni * dm * dm;
     }
@@ -207,8 +213,8 @@ __global__ __launch_bounds__(64) void k_gn_finalize(const float2* __restrict__ p
 }
 
 // Pass B. grid = (chunks per segment, segments), same mapping as pass A.
-// UNIFORM: HW % kChunk == 0, so every chunk is full and lies inside one
-// channel (channel = chunk / (HW / kChunk)): no masks, one set of affine
+// UNIFORM: HW % chunk == 0, so every chunk is full and lies inside one
+// channel (channel = chunk / (HW / chunk)): no masks, one set of affine
 // coefficients per workgroup. Otherwise each vector finds its channel with
 // 32-bit arithmetic (a vector never straddles channels since HW % 4 == 0;
 // segments are < 2^31 floats on this path). Index math stays 32-bit: a
@@ -220,28 +226,46 @@ __global__ __launch_bounds__(64) void k_gn_finalize(const float2* __restrict__ p
 // kernel would store. The pair loads are issued before the x loads: loads
 // complete in order, so the merge runs while the x loads are in flight
 // instead of after them.
-template <bool SILU, bool UNIFORM, bool MERGE>
-__global__ __launch_bounds__(kThreads) void k_gn_apply(const float* __restrict__ x, float* __restrict__ y, int64_t L,
+template <int TPB, int CV, bool SILU, bool UNIFORM, bool MERGE>
+__global__ __launch_bounds__(TPB) void k_gn_apply(const float* __restrict__ x, float* __restrict__ y, int64_t L,
                                                       int HW, int chunks_per_ch, int cg, int groups, int seg0,
                                                       const float2* __restrict__ stats,
                                                       const float2* __restrict__ part, int nchunks, float eps,
                                                       const float* __restrict__ gamma,
                                                       const float* __restrict__ beta) {
+    constexpr int64_t CH = (int64_t)TPB * 4 * CV;  // floats per chunk
     const int seg = blockIdx.y, chunk = blockIdx.x;
-    const int off = chunk * (int)kChunk;
+    const int off = chunk * (int)CH;
     const f4* p = (const f4*)(x + (int64_t)seg * L + off);
     f4* q = (f4*)(y + (int64_t)seg * L + off);
     const int lane = threadIdx.x & 63;
     float2 st = make_float2(0.f, 0.f);
     if constexpr (MERGE) st = lane < nchunks ? part[(int64_t)seg * nchunks + lane] : make_float2(0.f, 0.f);
     else st = stats[seg];
-    const int cnt = UNIFORM ? (int)kChunk : (int)(L - off < kChunk ? L - off : kChunk);
+    const int cnt = UNIFORM ? (int)CH : (int)(L - off < CH ? L - off : CH);
     const int n4 = cnt >> 2;
-    f4 v[kChunkV];
+    const int gc = ((seg0 + seg) % groups) * cg;
+    // chunks that cross channels: each float4's channel pair, loaded with
+    // the chunk pairs ahead of the x loads (after the merge its latency
+    // would follow the merge); a lane past the chunk reads its last float4's
+    float gj[UNIFORM ? 1 : CV], bj[UNIFORM ? 1 : CV];
+    if constexpr (!UNIFORM) {
 #pragma unroll
-    for (int j = 0; j < kChunkV; ++j) {
-        const int idx = threadIdx.x + kThreads * j;
-        if (UNIFORM || idx < n4) v[j] = dev::ld_stream(p + idx);
+        for (int j = 0; j < CV; ++j) {
+            const int idx = min((int)threadIdx.x + TPB * j, n4 - 1);
+            const int ch = gc + (int)((unsigned)(off + idx * 4) / (unsigned)HW);
+            gj[j] = gamma[ch];
+            bj[j] = beta[ch];
+        }
+    }
+    // unconditional loads (a lane past the chunk re-reads its last float4):
+    // loads under a mask split the kernel into blocks between which the
+    // compiler shuffled the row through 200+ VGPRs
+    f4 v[CV];
+#pragma unroll
+    for (int j = 0; j < CV; ++j) {
+        const int idx = threadIdx.x + TPB * j;
+        v[j] = dev::ld_stream(p + (UNIFORM ? idx : min(idx, n4 - 1)));
     }
     float meanf, rstd;
     if constexpr (MERGE) {
@@ -249,8 +273,8 @@ __global__ __launch_bounds__(kThreads) void k_gn_apply(const float* __restrict__
         const double mean = wave_dsum(tot) / (double)L;
         double m2t = 0.0;
         if (lane < nchunks) {
-            const int64_t o = (int64_t)lane * kChunk;
-            const double ni = (double)(L - o < kChunk ? L - o : kChunk);
+            const int64_t o = (int64_t)lane * CH;
+            const double ni = (double)(L - o < CH ? L - o : CH);
             const double dm = (double)st.x / ni - mean;
             m2t = (double)st.y + ni * dm * dm;
         }
@@ -261,21 +285,19 @@ __global__ __launch_bounds__(kThreads) void k_gn_apply(const float* __restrict__
         meanf = st.x;
         rstd = st.y;
     }
-    const int gc = ((seg0 + seg) % groups) * cg;
     if constexpr (UNIFORM) {
         const int ch = gc + chunk / chunks_per_ch;
         const float a = rstd * gamma[ch];
         const float b = beta[ch] - meanf * a;
 #pragma unroll
-        for (int j = 0; j < kChunkV; ++j) dev::st_stream(q + threadIdx.x + kThreads * j, apply4<SILU>(v[j], a, b));
+        for (int j = 0; j < CV; ++j) dev::st_stream(q + threadIdx.x + TPB * j, apply4<SILU>(v[j], a, b));
     } else {
 #pragma unroll
-        for (int j = 0; j < kChunkV; ++j) {
-            const int idx = threadIdx.x + kThreads * j;
+        for (int j = 0; j < CV; ++j) {
+            const int idx = threadIdx.x + TPB * j;
             if (idx < n4) {
-                const int ch = gc + (int)((unsigned)(off + idx * 4) / (unsigned)HW);
-                const float a = rstd * gamma[ch];
-                const float b = beta[ch] - meanf * a;
+                const float a = rstd * gj[j];
+                const float b = bj[j] - meanf * a;
                 dev::st_stream(q + idx, apply4<SILU>(v[j], a, b));
             }
         }
@@ -765,6 +787,21 @@ long env_long(const char* name, long dflt) {
     return (end && *end == 0 && v >= 0) ? v : dflt;
 }
 
+// The split schedule's chunk for nseg segments of L floats: the largest of
+// 8192, 4096 and 2048 floats that still gives 768 workgroups per pass, else
+// 2048. Measured (graph replays, GroupNorm + SiLU, 32 groups), chunk 8192
+// against the one chosen: [2,320,64,64] 9.6 vs 8.6 us (2048),
+// [2,640,64,64] 12.3 vs 11.8 us (4096), [2,1280,32,32] 9.5 vs 9.3 us (2048);
+// [1,512,120,120] keeps 8192 (928 workgroups): 14.6 us, against 16.7 with
+// 4096. SDH_GN_CHUNK forces one of them.
+int64_t split_chunk(int64_t nseg, int64_t L) {
+    static const long force = env_long("SDH_GN_CHUNK", 0);
+    if (force == 2048 || force == 4096 || force == 8192) return force;
+    for (int64_t c : {int64_t(8192), int64_t(4096)})
+        if (nseg * ((L + c - 1) / c) >= 768) return c;
+    return 2048;
+}
+
 // One resident kernel: pipelined or not, V float4 per thread.
 struct ResKind {
     bool pipe;
@@ -837,25 +874,19 @@ int resident_occupancy(ResKind k, bool silu, bool uniform, bool spoll = false) {
 
 // The resident schedule for segments of L floats (HW % 4 == 0, 16-byte
 // aligned, L < 2^31), when it is expected to beat the split schedule
-// (measured on MI355X, GroupNorm + SiLU, 32 groups):
-//   * x of at least 64 MB: the split schedule's re-read comes from HBM; the
-//     k_gn_resident_pipe plan with the fewest rounds (smaller share on
-//     ties; else k_gn_resident's), e.g. [1,128,1024,1024] 247 -> 187 us,
-//     [1,256,256,256] 29.6 -> 25.8 us;
-//   * smaller x when one round of k_gn_resident covers it and the split
-//     schedule would run fewer than 1024 workgroups per pass (too few to
-//     fill the GPU): [2,640,64,64] 18.8 -> 12.7 us; with one_round_only
-//     (segments of kSmallResidentMin + 1 to 65536 floats, ahead of the
-//     single-workgroup schedule) only this case: [2,320,64,64] 11.5 ->
-//     9.3 us, [2,1280,32,32] 11.6 -> 9.4 us, [2,960,32,32] 9.5 -> 8.6 us,
-//     while [2,640,32,32] (20480 floats: shares of 16384 + 4096) measured
-//     7.6 single against 7.9 resident. Otherwise the split
-//     schedule, which re-reads from L2 at these sizes, is as fast or faster
-//     ([1,512,128,128] 15.6 vs 16.2 us; [2,320,128,128], two unbalanced
-//     rounds, 18.8 vs 22.3 us).
+// (measured on MI355X, GroupNorm + SiLU, 32 groups): x of at least 64 MB,
+// where the split schedule's re-read comes from HBM; the
+// k_gn_resident_pipe plan with the fewest rounds (smaller share on ties;
+// else k_gn_resident's), e.g. [1,128,1024,1024] 247 -> 181 us,
+// [1,256,256,256] 29.6 -> 25.8 us. Below 64 MB the split schedule with
+// chunks sized to the tensor (split_chunk) measured as fast or faster than
+// one resident round, which an earlier, slower split took: [2,320,64,64]
+// 10.9 -> 8.6 us, [2,640,64,64] 14.1 -> 11.8 us, [2,1280,32,32] 10.7 -> 9.3
+// us, [2,960,32,32] 9.5 -> 8.2 us (graph replays); [2,1280,64,64] (84 MB)
+// 18.4 resident against 18.5 split.
 // False: use the split schedule. Knobs for tests and tuning:
-// SDH_GN_RESIDENT=0 never, =2 always when a plan exists (the plan chosen as
-// for large x); SDH_GN_RESIDENT_V=4|8|16 fixes the share;
+// SDH_GN_RESIDENT=0 never, =2 always when a plan exists (one round for
+// segments of 24577-65536 floats, else the plan chosen as for large x); SDH_GN_RESIDENT_V=4|8|16 fixes the share;
 // SDH_GN_RESIDENT_PIPE=0|1 allows only the plain or only the pipelined
 // kernel; SDH_GN_ONE_ROUND_PIPE=0 keeps the plain kernel's plan for one
 // round (the pipelined plan measured 2-7 % faster there: [2,640,64,64]
@@ -901,16 +932,14 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
         }
     }
     const bool large = nseg * L * 4 >= (int64_t(64) << 20);
-    const int64_t split_wgs = nseg * ((L + kChunk - 1) / kChunk);
     // one round: the pipelined kernel's plan when it also covers the tensor
     // in one round (shares of 8 float4 where the plain one has 4: fewer
     // workgroups, each holding more in flight), else the plain kernel's
     if (best_pipe.k.V && best_pipe.rounds == 1 && env_long("SDH_GN_ONE_ROUND_PIPE", 1)) best_one = best_pipe;
     Plan pl;
     if (one_round_only) {
-        if (best_one.k.V && split_wgs < 1024) pl = best_one;
+        if (best_one.k.V && mode == 2) pl = best_one;
     } else if (large || mode == 2) pl = best_pipe.k.V ? best_pipe : best_plain;
-    else if (best_one.k.V && split_wgs < 1024) pl = best_one;
     if (!pl.k.V) return false;
     const bool uniform = HW % ((int64_t)kResThreads * 4 * pl.k.V) == 0;
     const int64_t grid = std::min(pl.T, nseg) * pl.P;
@@ -988,12 +1017,13 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
     }
     const int64_t cg = C / groups, L = cg * HW, nseg = N * groups;
     const bool vec = HW % 4 == 0 && aligned16(x) && aligned16(y) && L < (1LL << 31);
-    // segments of 24577-65536 floats: a resident round spreads each over
-    // 2-4 workgroups, where the single schedule runs one per segment
-    if (vec && L > kSmallResidentMin && L <= (int64_t)1024 * 4 * 16 && gn_block_bytes() == 0 &&
+    static const bool force_split = env_long("SDH_GN_SPLIT", 0) != 0;
+    // segments of 24577-65536 floats: one resident round only when forced
+    // (SDH_GN_RESIDENT=2); the split schedule otherwise
+    if (!force_split && vec && L > kSmallResidentMin && L <= (int64_t)1024 * 4 * 16 && gn_block_bytes() == 0 &&
         run_gn_resident(op, silu, x, y, L, HW, cg, groups, nseg, gamma, beta, eps, true, fixed))
         return;
-    if (vec && L <= (int64_t)1024 * 4 * 16 && nseg <= 0x7fffffffLL) {
+    if (!force_split && vec && L <= kSmallResidentMin && nseg <= 0x7fffffffLL) {
         const int64_t n4 = L / 4;
         auto go = [&](auto tc, auto vc) {
             constexpr int TPB = decltype(tc)::value, V = decltype(vc)::value;
@@ -1011,14 +1041,13 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
         else if (n4 <= 1024) go(I(), std::integral_constant<int, 4>());
         else if (n4 <= 2048) go(I(), std::integral_constant<int, 8>());
         else if (n4 <= 4096) go(K(), std::integral_constant<int, 4>());
-        else if (n4 <= 8192) go(K(), std::integral_constant<int, 8>());
-        else if (n4 <= 12288) go(K(), std::integral_constant<int, 12>());
-        else go(K(), std::integral_constant<int, 16>());
-    } else if (vec && gn_block_bytes() == 0 &&
+        else go(K(), std::integral_constant<int, 8>());  // n4 <= 6144
+    } else if (!force_split && vec && gn_block_bytes() == 0 &&
                run_gn_resident(op, silu, x, y, L, HW, cg, groups, nseg, gamma, beta, eps, false, fixed)) {
         return;
     } else if (vec) {
-        const int64_t nchunks = (L + kChunk - 1) / kChunk;
+        const int64_t chunk = split_chunk(nseg, L);
+        const int64_t nchunks = (L + chunk - 1) / chunk;
         // segments per block: the apply pass re-reads a block right after
         // the partial pass read it, while it is still cached
         int64_t sb = nseg;
@@ -1051,38 +1080,43 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
         }
         float2* part = (float2*)scr;
         float2* stats = (float2*)(scr + part_bytes);
-        const bool uniform = HW % kChunk == 0;
-        const int cpc = uniform ? (int)(HW / kChunk) : 1;
-        for (int64_t s0 = 0; s0 < nseg; s0 += sb) {
-            const int64_t k = std::min<int64_t>(sb, nseg - s0);
-            const float* xb = x + s0 * L;
-            float* yb = y + s0 * L;
-            const dim3 grid((unsigned)nchunks, (unsigned)k);
-            k_gn_partial<<<grid, kThreads, 0, stream()>>>(xb, L, nchunks, part);
-            launched(op);
-            const bool merge = nchunks <= 64;  // one chunk pair per lane: merged inside pass B
-            if (!merge) {
-                k_gn_finalize<<<(unsigned)k, 64, 0, stream()>>>(part, L, nchunks, stats, eps);
+        const bool uniform = HW % chunk == 0;
+        const int cpc = uniform ? (int)(HW / chunk) : 1;
+        const bool merge = nchunks <= 64;  // one chunk pair per lane: merged inside pass B
+        auto passes = [&](auto tc, auto vc) {
+            constexpr int TPB = decltype(tc)::value, CV = decltype(vc)::value;
+            for (int64_t s0 = 0; s0 < nseg; s0 += sb) {
+                const int64_t k = std::min<int64_t>(sb, nseg - s0);
+                const float* xb = x + s0 * L;
+                float* yb = y + s0 * L;
+                const dim3 grid((unsigned)nchunks, (unsigned)k);
+                k_gn_partial<TPB, CV><<<grid, TPB, 0, stream()>>>(xb, L, nchunks, part);
                 launched(op);
+                if (!merge) {
+                    k_gn_finalize<<<(unsigned)k, 64, 0, stream()>>>(part, L, nchunks, chunk, stats, eps);
+                    launched(op);
+                }
+                const int seg0 = (int)(s0 % groups);
+                auto apply = [&](auto sc, auto uc) {
+                    constexpr bool S = decltype(sc)::value, U = decltype(uc)::value;
+                    if (merge)
+                        k_gn_apply<TPB, CV, S, U, true><<<grid, TPB, 0, stream()>>>(
+                            xb, yb, L, (int)HW, cpc, (int)cg, groups, seg0, stats, part, (int)nchunks, eps, gamma, beta);
+                    else
+                        k_gn_apply<TPB, CV, S, U, false><<<grid, TPB, 0, stream()>>>(
+                            xb, yb, L, (int)HW, cpc, (int)cg, groups, seg0, stats, part, (int)nchunks, eps, gamma, beta);
+                };
+                using T_ = std::true_type;
+                using F_ = std::false_type;
+                if (silu) uniform ? apply(T_(), T_()) : apply(T_(), F_());
+                else uniform ? apply(F_(), T_()) : apply(F_(), F_());
+                if (s0 + sb < nseg) launched(op);
             }
-            const int seg0 = (int)(s0 % groups);
-            auto apply = [&](auto sc, auto uc) {
-                constexpr bool S = decltype(sc)::value, U = decltype(uc)::value;
-                if (merge)
-                    k_gn_apply<S, U, true><<<grid, kThreads, 0, stream()>>>(xb, yb, L, (int)HW, cpc, (int)cg, groups,
-                                                                            seg0, stats, part, (int)nchunks, eps,
-                                                                            gamma, beta);
-                else
-                    k_gn_apply<S, U, false><<<grid, kThreads, 0, stream()>>>(xb, yb, L, (int)HW, cpc, (int)cg, groups,
-                                                                             seg0, stats, part, (int)nchunks, eps,
-                                                                             gamma, beta);
-            };
-            using T_ = std::true_type;
-            using F_ = std::false_type;
-            if (silu) uniform ? apply(T_(), T_()) : apply(T_(), F_());
-            else uniform ? apply(F_(), T_()) : apply(F_(), F_());
-            if (s0 + sb < nseg) launched(op);
-        }
+        };
+        using I = std::integral_constant<int, 64>;
+        if (chunk == 8192) passes(std::integral_constant<int, 256>(), std::integral_constant<int, 8>());
+        else if (chunk == 4096) passes(I(), std::integral_constant<int, 16>());
+        else passes(I(), std::integral_constant<int, 8>());
     } else {
         need(nseg <= 0x7fffffffLL, op, "too many groups");
         if (silu)

@@ -16,7 +16,9 @@ reductions' relative 1e-4:
     several rounds per team, shares that span channels or end short;
   * in place, repeated and interleaved with the other GroupNorm schedules,
     bit-identical on repeated calls (the merge order is fixed);
-  * the split schedule still reachable with SDH_GN_RESIDENT=0;
+  * the split schedule still reachable with SDH_GN_RESIDENT=0, and with
+    each chunk size forced (SDH_GN_CHUNK) and every shape forced onto it
+    (SDH_GN_SPLIT=1);
   * two processes running it at the same time (besides this one);
   * the failure path, forced from the host: SDH_GN_SPIN_LIMIT=0 expires
     every wait at once, so every workgroup writes NaN and exits, and the
@@ -41,7 +43,7 @@ ORACLE_DIR = os.path.join(ROOT, "oracle")
 SHAPES = [  # shape, groups, eps
     ((1, 512, 128, 128), 32, 1e-6),  # config 4a: split by default; forced: V = 4, one round
     ((1, 256, 256, 256), 32, 1e-6),  # 64 MB: resident (pipelined) by default
-    ((2, 640, 64, 64), 32, 1e-6),    # few split workgroups: one resident round by default
+    ((2, 640, 64, 64), 32, 1e-6),    # 21 MB: split, 4096-float chunks; forced: one resident round
     ((3, 512, 128, 128), 32, 1e-6),  # 96 segments: three rounds of 32 teams
     ((1, 96, 100, 100), 3, 1e-6),    # shares span channels, last share short
     ((2, 64, 129, 132), 8, 1e-5),    # plane of 17028 floats: shares cross channel ends
@@ -307,30 +309,51 @@ def test_two_processes_at_once():
     assert all(rc == 0 and "concurrent ok" in out for rc, out, _ in outs)
 
 
-# Segments of 24577-65536 floats: one resident round ahead of the
-# single-workgroup schedule when the split would run fewer than 1024
-# workgroups (SD 1.5 UNet shapes); shares of 16384 floats, the last short.
+# Segments of 24577-65536 floats (SD 1.5 UNet shapes): the split schedule
+# by default, with chunks of 2048 or 4096 floats so that a pass has enough
+# workgroups; one resident round only when forced (SDH_GN_RESIDENT=2,
+# shares of 16384 floats, the last short). [2,640,32,32] (20480 floats)
+# stays on the single-workgroup kernel.
 SMALL_SEG_SHAPES = [((2, 320, 64, 64), 32, 1e-5), ((2, 1280, 32, 32), 32, 1e-5), ((2, 960, 32, 32), 32, 1e-5),
-                    ((1, 64, 128, 128), 32, 1e-6), ((2, 512, 64, 64), 32, 1e-5), ((2, 96, 30, 36), 3, 1e-6)]
+                    ((1, 64, 128, 128), 32, 1e-6), ((2, 512, 64, 64), 32, 1e-5), ((2, 96, 30, 36), 3, 1e-6),
+                    ((2, 640, 32, 32), 32, 1e-5)]
 
 
 @pytest.mark.parametrize("shape,groups,eps", SMALL_SEG_SHAPES)
 @pytest.mark.parametrize("silu", [True, False])
-def test_small_segments_resident_round(be, orc, shape, groups, eps, silu):
+def test_small_segments_default_schedule(be, orc, shape, groups, eps, silu):
     got, want = _run(be, orc, shape, groups, eps, silu, 5200 + shape[1])
     assert_reduction(got, want, f"small-segment group_norm {shape} g{groups} silu={silu}")
 
 
-def test_small_segments_single_schedule_still_reachable():
-    """SDH_GN_RESIDENT=0: the same shapes on the single-workgroup kernels
-    (V = 8, 12 and 16 float4 per thread of 1024), which larger batches of
-    these shapes still take."""
+def test_small_segments_resident_round_forced():
+    """SDH_GN_RESIDENT=2: one resident round on the same shapes (those of
+    more than 24576 floats per segment)."""
     body = (
         "for shape, groups, eps in %r:\n"
         "    for silu in (True, False):\n"
         "        o, want = run(shape, groups, eps, silu, 5300)\n"
-        "        assert_reduction(o.download(), want, f'single {shape} {silu}')\n"
-        "print('single ok')\n"
+        "        assert_reduction(o.download(), want, f'one round {shape} {silu}')\n"
+        "print('one round ok')\n"
     ) % (SMALL_SEG_SHAPES,)
-    r = _child({"SDH_GN_RESIDENT": "0"}, body)
-    assert r.returncode == 0 and "single ok" in r.stdout
+    r = _child({"SDH_GN_RESIDENT": "2"}, body)
+    assert r.returncode == 0 and "one round ok" in r.stdout
+
+
+@pytest.mark.parametrize("chunk", [2048, 4096, 8192])
+def test_split_each_chunk_size(chunk):
+    """SDH_GN_SPLIT=1 with SDH_GN_CHUNK forced: every shape on the split
+    schedule at each chunk size: chunks inside one channel or crossing
+    channel ends, a short last chunk, merges inside pass B (at most 64
+    chunks per segment) or in the finalize launch (more)."""
+    shapes = SMALL_SEG_SHAPES + [((1, 512, 128, 128), 32, 1e-6), ((1, 96, 100, 100), 3, 1e-6),
+                                 ((1, 16, 300, 300), 2, 1e-6), ((2, 1280, 8, 8), 32, 1e-5)]
+    body = (
+        "for shape, groups, eps in %r:\n"
+        "    for silu in (True, False):\n"
+        "        o, want = run(shape, groups, eps, silu, 5400)\n"
+        "        assert_reduction(o.download(), want, f'split %d {shape} {silu}')\n"
+        "print('split ok')\n"
+    ) % (shapes, chunk)
+    r = _child({"SDH_GN_SPLIT": "1", "SDH_GN_CHUNK": str(chunk)}, body)
+    assert r.returncode == 0 and "split ok" in r.stdout
