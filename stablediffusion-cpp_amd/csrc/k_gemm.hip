@@ -73,21 +73,24 @@ __device__ __forceinline__ unsigned bf16_bits(float f) {
 
 // A fp32 [M, lda] -> P bf16 [M, K] (dense rows). One thread per 8 elements;
 // grid.y walks rows (K % 8 == 0, lda % 4 == 0, A 16-byte aligned).
-__global__ __launch_bounds__(kGT) void k_pack_bf16(const float* __restrict__ A, int64_t lda, u32x4* __restrict__ P,
-                                                  int64_t M, int K) {
-    const int kg = K >> 3;
-    const int g = blockIdx.x * kGT + threadIdx.x;
-    if (g >= kg) return;
-    for (int64_t m = blockIdx.y; m < M; m += gridDim.y) {
-        const f4* p = (const f4*)(A + m * lda) + 2 * g;
-        const f4 a = dev::ld_stream(p), b = dev::ld_stream(p + 1);
-        u32x4 o;
-        o.x = bf16_bits(a.x) | (bf16_bits(a.y) << 16);
-        o.y = bf16_bits(a.z) | (bf16_bits(a.w) << 16);
-        o.z = bf16_bits(b.x) | (bf16_bits(b.y) << 16);
-        o.w = bf16_bits(b.z) | (bf16_bits(b.w) << 16);
-        P[m * kg + g] = o;  // re-read by the GEMM right after: ordinary store
-    }
+// Rows r0 .. r0 + rows of A rounded to bf16 into the dense P: one thread per
+// 8 columns (two float4 in, one 16-B vector out), flat over the rows in
+// one-wave workgroups (many small workgroups stream best on MI355X);
+// rows * (K / 8) < 2^31 per launch.
+constexpr int kPackThreads = 64;
+__global__ __launch_bounds__(kPackThreads) void k_pack_bf16(const float* __restrict__ A, int64_t lda,
+                                                           u32x4* __restrict__ P, unsigned n8, unsigned kg) {
+    const unsigned i = blockIdx.x * kPackThreads + threadIdx.x;
+    if (i >= n8) return;
+    const unsigned m = i / kg, g = i - m * kg;
+    const f4* p = (const f4*)(A + (int64_t)m * lda) + 2 * g;
+    const f4 a = dev::ld_stream(p), b = dev::ld_stream(p + 1);
+    u32x4 o;
+    o.x = bf16_bits(a.x) | (bf16_bits(a.y) << 16);
+    o.y = bf16_bits(a.z) | (bf16_bits(a.w) << 16);
+    o.z = bf16_bits(b.x) | (bf16_bits(b.y) << 16);
+    o.w = bf16_bits(b.z) | (bf16_bits(b.w) << 16);
+    P[i] = o;  // re-read by the GEMM right after: ordinary store
 }
 
 // P bf16 [M, K] dense; B0 (and B1 for SwiGLU) bf16 [N, ldb]. EPI E_LINEAR:
@@ -492,9 +495,12 @@ void run_gemm(const char* op, int64_t M, int64_t N, int64_t K, const float* A, i
         const size_t pbytes = ((size_t)(M * K) * 2 + 255) / 256 * 256, gbytes = (size_t)(M * N) * 4;
         char* base = (char*)scratch(pbytes + (swi_lt ? 2 * gbytes : 0));
         u16* P = (u16*)base;
-        const int kg = (int)(K / 8);
-        const unsigned gy = (unsigned)std::min<int64_t>(M, 65535);
-        k_pack_bf16<<<dim3(blocks_for(kg, kGT), gy), kGT, 0, stream()>>>(A, lda, (u32x4*)P, M, (int)K);
+        const int64_t kg = K / 8;
+        in_pieces(M, std::max<int64_t>(1, ((int64_t)1 << 31) / kg - 1), [&](int64_t m0, int64_t nm) {
+            const unsigned n8 = (unsigned)(nm * kg);
+            k_pack_bf16<<<blocks_for(n8, kPackThreads), kPackThreads, 0, stream()>>>(
+                A + m0 * lda, lda, (u32x4*)P + m0 * kg, n8, (unsigned)kg);
+        });
         launched(op);
         if constexpr (EPI == E_LINEAR) {
             if (lt && blaslt_gemm(false, M, N, K, P, K, B0, ldb, C, ldc, bias, accumulate)) {
