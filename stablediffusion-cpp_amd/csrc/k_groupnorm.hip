@@ -213,9 +213,10 @@ __global__ __launch_bounds__(64) void k_gn_finalize(const float2* __restrict__ p
 }
 
 // Pass B. grid = (chunks per segment, segments), same mapping as pass A.
-// UNIFORM: HW % chunk == 0, so every chunk is full and lies inside one
-// channel (channel = chunk / (HW / chunk)): no masks, one set of affine
-// coefficients per workgroup. Otherwise each vector finds its channel with
+// UNIFORM: HW is a multiple of the chunk size CH, so every chunk is full
+// and lies inside one channel (channel = chunk index / (HW / CH)): no
+// masks, one set of affine coefficients per workgroup. Otherwise each
+// vector finds its channel with
 // 32-bit arithmetic (a vector never straddles channels since HW % 4 == 0;
 // segments are < 2^31 floats on this path). Index math stays 32-bit: a
 // 64-bit division here expands into a software routine that doubled the
@@ -228,11 +229,10 @@ __global__ __launch_bounds__(64) void k_gn_finalize(const float2* __restrict__ p
 // instead of after them.
 template <int TPB, int CV, bool SILU, bool UNIFORM, bool MERGE>
 __global__ __launch_bounds__(TPB) void k_gn_apply(const float* __restrict__ x, float* __restrict__ y, int64_t L,
-                                                      int HW, int chunks_per_ch, int cg, int groups, int seg0,
-                                                      const float2* __restrict__ stats,
-                                                      const float2* __restrict__ part, int nchunks, float eps,
-                                                      const float* __restrict__ gamma,
-                                                      const float* __restrict__ beta) {
+                                                 int HW, int chunks_per_ch, int cg, int groups, int seg0,
+                                                 const float2* __restrict__ stats, const float2* __restrict__ part,
+                                                 int nchunks, float eps, const float* __restrict__ gamma,
+                                                 const float* __restrict__ beta) {
     constexpr int64_t CH = (int64_t)TPB * 4 * CV;  // floats per chunk
     const int seg = blockIdx.y, chunk = blockIdx.x;
     const int off = chunk * (int)CH;
@@ -247,7 +247,8 @@ __global__ __launch_bounds__(TPB) void k_gn_apply(const float* __restrict__ x, f
     const int gc = ((seg0 + seg) % groups) * cg;
     // chunks that cross channels: each float4's channel pair, loaded with
     // the chunk pairs ahead of the x loads (after the merge its latency
-    // would follow the merge); a lane past the chunk reads its last float4's
+    // would follow the merge); a lane past the chunk reads the pair of the
+    // chunk's last float4
     float gj[UNIFORM ? 1 : CV], bj[UNIFORM ? 1 : CV];
     if constexpr (!UNIFORM) {
 #pragma unroll
@@ -886,7 +887,8 @@ int resident_occupancy(ResKind k, bool silu, bool uniform, bool spoll = false) {
 // 18.4 resident against 18.5 split.
 // False: use the split schedule. Knobs for tests and tuning:
 // SDH_GN_RESIDENT=0 never, =2 always when a plan exists (one round for
-// segments of 24577-65536 floats, else the plan chosen as for large x); SDH_GN_RESIDENT_V=4|8|16 fixes the share;
+// segments of 24577-65536 floats, else the plan chosen as for large x);
+// SDH_GN_RESIDENT_V=4|8|16 fixes the share;
 // SDH_GN_RESIDENT_PIPE=0|1 allows only the plain or only the pipelined
 // kernel; SDH_GN_ONE_ROUND_PIPE=0 keeps the plain kernel's plan for one
 // round (the pipelined plan measured 2-7 % faster there: [2,640,64,64]
