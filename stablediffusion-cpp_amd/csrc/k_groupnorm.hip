@@ -216,9 +216,9 @@ __global__ __launch_bounds__(64) void k_gn_finalize(const float2* __restrict__ p
 // UNIFORM: HW is a multiple of the chunk size CH, so every chunk is full
 // and lies inside one channel (channel = chunk index / (HW / CH)): no
 // masks, one set of affine coefficients per workgroup. Otherwise each
-// vector finds its channel with
-// 32-bit arithmetic (a vector never straddles channels since HW % 4 == 0;
-// segments are < 2^31 floats on this path). Index math stays 32-bit: a
+// vector finds its channel with 32-bit arithmetic (a vector never
+// straddles channels since HW % 4 == 0; segments are < 2^31 floats on this
+// path). Index math stays 32-bit: a
 // 64-bit division here expands into a software routine that doubled the
 // kernel's VGPR count and cost a third of its bandwidth.
 // MERGE (segments of at most 64 chunks): no finalize launch; every wave
