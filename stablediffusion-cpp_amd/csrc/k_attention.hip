@@ -156,12 +156,12 @@ __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, 
     for (int j = 0; j < KCH; ++j) {
         const int i = threadIdx.x + j * 256, r = i / CPR, c = (i % CPR) ^ swz_k<DP>(r);
         if constexpr (VEC) {
-            f4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
-            if (r < nrows) {
-                const f4* p = (const f4*)(K + (row0 + r) * kv_inner + col0 + c * 8);
-                a = p[0];
-                b = p[1];
-            }
+            // unconditional loads (rows past the keys re-read the last row,
+            // zeroed after the load): a load under a mask splits the kernel
+            // into blocks that cost registers
+            const f4* p = (const f4*)(K + (row0 + min(r, nrows - 1)) * kv_inner + col0 + c * 8);
+            f4 a = dev::ld_stream(p), b = dev::ld_stream(p + 1);
+            if (r >= nrows) a = b = f4{0.f, 0.f, 0.f, 0.f};
             kx[j][0] = a.x; kx[j][1] = a.y; kx[j][2] = a.z; kx[j][3] = a.w;
             kx[j][4] = b.x; kx[j][5] = b.y; kx[j][6] = b.z; kx[j][7] = b.w;
         } else {
@@ -180,7 +180,8 @@ __global__ __launch_bounds__(256) void k_attn_pack(const float* __restrict__ K, 
         const int i = threadIdx.x + j * 256, r = i / (DP / 4), c = (i % (DP / 4)) * 4;
         f4 x = {0.f, 0.f, 0.f, 0.f};
         if constexpr (VEC) {
-            if (r < nrows) x = *(const f4*)(V + (row0 + r) * kv_inner + col0 + c);
+            x = dev::ld_stream((const f4*)(V + (row0 + min(r, nrows - 1)) * kv_inner + col0 + c));
+            if (r >= nrows) x = f4{0.f, 0.f, 0.f, 0.f};
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
