@@ -268,17 +268,22 @@ __global__ __launch_bounds__(256) void k_qkv_prep(float* __restrict__ Q, const f
     const f4 one = {1.f, 1.f, 1.f, 1.f}, zero = {0.f, 0.f, 0.f, 0.f};
     const f4 gq4 = gq ? ((const f4*)gq)[hl] : one;
     const f4 gk4 = gk ? ((const f4*)gk)[hl] : one;
+    // Loads are unconditional: rows past the sequence end (the last tile)
+    // re-read its last row, and only what is stored or packed is masked
+    // (a load under a mask splits the kernel into blocks that cost
+    // registers).
     f4 kq[NS], kk[NS], vv[VCH];
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        const int r = rs + RS * j;
-        kq[j] = r < nrows ? dev::ld_stream((const f4*)(Q + (row0 + r) * inner + col0) + hl) : zero;
-        kk[j] = r < nrows ? dev::ld_stream((const f4*)(K + (row0 + r) * inner + col0) + hl) : zero;
+        const int r = min(rs + RS * j, nrows - 1);
+        kq[j] = dev::ld_stream((const f4*)(Q + (row0 + r) * inner + col0) + hl);
+        kk[j] = dev::ld_stream((const f4*)(K + (row0 + r) * inner + col0) + hl);
     }
 #pragma unroll
     for (int j = 0; j < VCH; ++j) {
         const int i = threadIdx.x + j * 256, r = i / (DP / 4), c = (i % (DP / 4)) * 4;
-        vv[j] = r < nrows ? dev::ld_stream((const f4*)(V + (row0 + r) * inner + col0 + c)) : zero;
+        const f4 a = dev::ld_stream((const f4*)(V + (row0 + min(r, nrows - 1)) * inner + col0 + c));
+        vv[j] = r < nrows ? a : zero;  // keys past the sequence pack as zero
     }
     float kmax = 0.f;
 #pragma unroll
