@@ -261,12 +261,14 @@ __global__ __launch_bounds__(TPB) void k_gn_apply(const float* __restrict__ x, f
     }
     // unconditional loads (a lane past the chunk re-reads its last float4):
     // loads under a mask split the kernel into blocks between which the
-    // compiler shuffled the row through 200+ VGPRs
+    // compiler shuffled the row through 200+ VGPRs. Ordinary loads, like
+    // pass A's: the chunk is re-read from the caches (4a 14.80 against 14.92
+    // us with non-temporal ones)
     f4 v[CV];
 #pragma unroll
     for (int j = 0; j < CV; ++j) {
         const int idx = threadIdx.x + TPB * j;
-        v[j] = dev::ld_stream(p + (UNIFORM ? idx : min(idx, n4 - 1)));
+        v[j] = p[UNIFORM ? idx : min(idx, n4 - 1)];
     }
     float meanf, rstd;
     if constexpr (MERGE) {
