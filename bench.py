@@ -31,6 +31,11 @@ Ops whose step is shorter than 25 us are launch-bound: a ctypes loop cannot
 issue them as fast as the GPU runs them. Their steps are also captured into
 one graph (sdh_capture_begin) and replayed, and us_per_op is that replay's
 device time; the host-paced figure is kept as us_per_op_host_paced.
+
+The headline takes exactly --warmup untimed steps. Every other line warms up
+for at least 30 ms of its own steps (and at least 3 of them): the CPU leg of
+the line before leaves the GPU idle for seconds, and a few steps do not bring
+its clocks back to their loaded level.
 """
 from __future__ import annotations
 
@@ -57,6 +62,13 @@ MAX_SETS = 32
 # ops whose host-paced step is shorter than this are also timed as one
 # captured graph of the same steps (the GPU's time, not the ctypes loop's)
 GRAPH_BELOW_MS = 0.025
+# per-op lines: the warm-up runs for at least this long (and at least its
+# step count), in batches with a synchronisation after each, so the GPU's
+# clocks are back at their loaded level after the CPU leg of the line before
+# left the GPU idle for seconds (4b: 191 us per op over the first 20 steps
+# after 5 warm-up steps, 181 us once settled)
+OP_WARM_S = 0.03
+OP_WARM_BATCH = 8
 
 
 # ------------------------------------------------------------------ workloads
@@ -854,20 +866,28 @@ def all_workloads():
 
 
 # ------------------------------------------------------------------ GPU timing
-def measure_gpu(be, w, steps, warmup, check=False):
-    """Times `steps` steps over rotating buffer sets. With check, set 0's
-    inputs are downloaded before the timed steps, and afterwards, outside the
-    timed region, set 0 is reloaded from them, stepped once and its results
-    returned for the parity check."""
+def measure_gpu(be, w, steps, warmup, check=False, min_warm_s=0.0):
+    """Times `steps` steps over rotating buffer sets, after `warmup` untimed
+    steps (continued in batches until `min_warm_s` seconds have passed). With
+    check, set 0's inputs are downloaded before the timed steps, and
+    afterwards, outside the timed region, set 0 is reloaded from them, stepped
+    once and its results returned for the parity check."""
     first = w.make(be, 0)
     host = w.host_inputs(first) if check and w.results else None
     footprint = sum(a.nbytes for a in first.values())
     nsets = max(2, min(MAX_SETS, math.ceil(MIN_ROTATION_BYTES / max(footprint, 1))))
     sets = [first] + [w.make(be, i) for i in range(1, nsets)]
     be.synchronize()
+    t_warm = time.perf_counter()
     for i in range(warmup):
         w.step(be, sets[i % nsets])
     be.synchronize()
+    i = warmup
+    while time.perf_counter() - t_warm < min_warm_s:
+        for _ in range(OP_WARM_BATCH):
+            w.step(be, sets[i % nsets])
+            i += 1
+        be.synchronize()
     t0 = time.perf_counter()
     be.timer_record(0)
     for i in range(steps):
@@ -1251,7 +1271,7 @@ def main():
         if hasattr(w, "measure"):  # a whole model step, timed by the model library itself
             r = w.measure(max(3, min(steps, 10)), 2)
         else:
-            r = measure_gpu(be, w, steps, warm, check=R is not None)
+            r = measure_gpu(be, w, steps, warm, check=R is not None, min_warm_s=0.0 if w is head else OP_WARM_S)
         gbs = w.algo_bytes / (r["event_ms"] * 1e-3) / 1e9
         entry = dict(op=w.name, desc=w.desc, algo_bytes=w.algo_bytes, us_per_op=round(r["event_ms"] * 1e3, 2),
                      GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1), rotation_sets=r["nsets"],
