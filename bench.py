@@ -32,10 +32,13 @@ issue them as fast as the GPU runs them. Their steps are also captured into
 one graph (sdh_capture_begin) and replayed, and us_per_op is that replay's
 device time; the host-paced figure is kept as us_per_op_host_paced.
 
-The headline takes exactly --warmup untimed steps. Every other line warms up
-for at least 30 ms of its own steps (and at least 3 of them): the CPU leg of
-the line before leaves the GPU idle for seconds, and a few steps do not bring
-its clocks back to their loaded level.
+Every line is measured on the GPU first, back to back, and the CPU legs and
+parity checks run after the last one: a CPU leg between two measurements
+leaves the GPU idle for seconds, and the next line would time its clocks
+coming back up (measured: 4b 191 us per op over the first 20 steps after 5
+warm-up steps, 181 us once settled). The headline takes exactly --warmup
+untimed steps; every other line warms up for at least 30 ms of its own steps
+(and at least 3 of them).
 """
 from __future__ import annotations
 
@@ -64,9 +67,7 @@ MAX_SETS = 32
 GRAPH_BELOW_MS = 0.025
 # per-op lines: the warm-up runs for at least this long (and at least its
 # step count), in batches with a synchronisation after each, so the GPU's
-# clocks are back at their loaded level after the CPU leg of the line before
-# left the GPU idle for seconds (4b: 191 us per op over the first 20 steps
-# after 5 warm-up steps, 181 us once settled)
+# clocks are at their loaded level when the timed steps start
 OP_WARM_S = 0.03
 OP_WARM_BATCH = 8
 
@@ -1264,6 +1265,11 @@ def main():
 
     ops = []
     head_res, head_cpu, head_err = None, None, None
+    # every GPU measurement first, back to back, then the CPU legs: a CPU leg
+    # between two measurements leaves the GPU idle for seconds, and the next
+    # line (the headline too, whose warm-up is exactly --warmup steps) would
+    # time the GPU's clocks coming back up
+    measured = []
     for n in names:
         w = wls[n]
         steps = args.steps if w is head else args.op_steps
@@ -1272,6 +1278,9 @@ def main():
             r = w.measure(max(3, min(steps, 10)), 2)
         else:
             r = measure_gpu(be, w, steps, warm, check=R is not None, min_warm_s=0.0 if w is head else OP_WARM_S)
+        measured.append((w, r))
+        print(f"# gpu {w.name:22s} {r['event_ms'] * 1e3:10.2f} us", file=sys.stderr, flush=True)
+    for w, r in measured:
         gbs = w.algo_bytes / (r["event_ms"] * 1e-3) / 1e9
         entry = dict(op=w.name, desc=w.desc, algo_bytes=w.algo_bytes, us_per_op=round(r["event_ms"] * 1e3, 2),
                      GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1), rotation_sets=r["nsets"],
