@@ -27,10 +27,13 @@ the C restatement (oracle/liboracle.so) is timed instead ("port"). It is timed
 on every BASELINE config line by default (median of 5 runs after one, 3 for
 tensors over 1 GB); --cpu-all adds the other lines.
 
-Ops whose step is shorter than 25 us are launch-bound: a ctypes loop cannot
-issue them as fast as the GPU runs them. Their steps are also captured into
-one graph (sdh_capture_begin) and replayed, and us_per_op is that replay's
-device time; the host-paced figure is kept as us_per_op_host_paced.
+Ops whose step is shorter than 10 us are launch-bound: a ctypes loop (5-7 us
+per call) cannot issue them as fast as the GPU runs them. Their steps are also
+captured into one graph (sdh_capture_begin) and replayed, and us_per_op is
+that replay's device time; the host-paced figure is kept as
+us_per_op_host_paced. Ops of 10-25 us are replayed too, and keep the
+host-paced figure, the GPU being the bound there, with the replay's as
+us_per_op_graph.
 
 Every line is measured on the GPU first, back to back, and the CPU legs and
 parity checks run after the last one: a CPU leg between two measurements
@@ -62,9 +65,14 @@ METRIC = "achieved HBM GB/s (% of peak) per op at Z-Image 1024² shapes; speedup
 T, D, F = 4096, 3840, 10240
 MIN_ROTATION_BYTES = 512_000_000  # 2x the 256 MB Infinity Cache
 MAX_SETS = 32
-# ops whose host-paced step is shorter than this are also timed as one
-# captured graph of the same steps (the GPU's time, not the ctypes loop's)
-GRAPH_BELOW_MS = 0.025
+# ops whose host-paced step is shorter than GRAPH_ALSO_MS are also timed as
+# one captured graph of the same steps; below GRAPH_BELOW_MS the graph's time
+# is the line's figure (the ctypes loop, 5-7 us per call, cannot keep the GPU
+# busy), above it the host-paced loop's (the GPU is then the bound, and a
+# replay adds the graph's own per-node cost: GroupNorm 4a 12.0 us host-paced,
+# 12.8 us replayed), with the other figure kept beside it
+GRAPH_BELOW_MS = 0.010
+GRAPH_ALSO_MS = 0.025
 # per-op lines: the warm-up runs for at least this long (and at least its
 # step count), in batches with a synchronisation after each, so the GPU's
 # clocks are at their loaded level when the timed steps start
@@ -898,7 +906,7 @@ def measure_gpu(be, w, steps, warmup, check=False, min_warm_s=0.0):
     wall = time.perf_counter() - t0
     ev_ms = be.timer_elapsed(0, 1)
     graph_ms = None
-    if ev_ms / steps < GRAPH_BELOW_MS:
+    if ev_ms / steps < GRAPH_ALSO_MS:
         # launch-bound: the host's ctypes loop, not the GPU, sets the pace of
         # the loop above; the same steps captured into one graph run back to
         # back on the device (sdh_capture_begin), which is the GPU's time
@@ -929,7 +937,10 @@ def measure_gpu(be, w, steps, warmup, check=False, min_warm_s=0.0):
     out = dict(nsets=nsets, footprint=footprint * nsets, wall_ms=wall * 1e3 / steps, event_ms=ev_ms / steps,
                got=got, host=host)
     if graph_ms is not None:
-        out.update(host_paced_ms=ev_ms / steps, event_ms=graph_ms / steps, graph=True)
+        if ev_ms / steps < GRAPH_BELOW_MS:
+            out.update(host_paced_ms=ev_ms / steps, event_ms=graph_ms / steps, graph=True)
+        else:
+            out.update(graph_ms=graph_ms / steps)
     return out
 
 
@@ -1080,8 +1091,10 @@ def gn_split_chunk(nseg, L):
 def gn_dispatches(shape, groups=32, cus=256):
     """(kernel prefix, grid work-items) of the launches that carry a GroupNorm
     workload's HBM traffic, following run_gn's choice of schedule: one
-    k_gn_single launch for segments up to 24576 floats; else, for x of at
-    least 64 MB, the resident plan of run_gn_resident (one launch of
+    k_gn_single launch for segments up to 24576 floats; else, for x under
+    64 MB cut into whole 4096-float chunks that each lie in one channel (at
+    most 64 per segment), one k_gn_pipe launch of two workgroups per chunk;
+    else, for x of at least 64 MB, the resident plan of run_gn_resident (one launch of
     k_gn_resident or k_gn_resident_pipe); else k_gn_partial and k_gn_apply
     over chunks of gn_split_chunk floats (k_gn_finalize moves a few KB and
     is left out)."""
@@ -1092,6 +1105,8 @@ def gn_dispatches(shape, groups=32, cus=256):
         n4 = L // 4
         tpb = 256 if n4 <= 2048 else 1024
         return [("k_gn_single", nseg * tpb)]
+    if HW % 4096 == 0 and L // 4096 <= 64 and nseg * (L // 4096) < 4096:
+        return [("k_gn_pipe", 2 * nseg * (L // 4096) * 256)]
     if nseg * L * 4 >= 64 << 20:
         best = {}
         for pipe in (False, True):
@@ -1288,6 +1303,9 @@ def main():
         if r.get("graph"):
             entry.update(timing="device: the steps captured into one graph and replayed (sdh_capture_begin)",
                          us_per_op_host_paced=round(r["host_paced_ms"] * 1e3, 2))
+        elif r.get("graph_ms") is not None:
+            entry.update(timing="host-paced loop (the GPU is the bound above 10 us per step)",
+                         us_per_op_graph=round(r["graph_ms"] * 1e3, 2))
         if w.inputs:
             entry["seeds"] = w.seeds()
         if "params" in r:

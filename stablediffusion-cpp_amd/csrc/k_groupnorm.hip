@@ -57,6 +57,16 @@
 static constexpr size_t kFixedScratchBytes = size_t(1) << 20;
 static __device__ __align__(256) unsigned char scratch[kFixedScratchBytes];
 
+// Exchange area of the pipelined schedule (k_gn_pipe), used by both
+// GroupNorm entry points (one stream keeps their launches in order): the
+// tagged chunk pairs (2 words per chunk, at most kPipeMaxChunks chunks), then
+// the captured launches' counter and an error word. A file-scope array like
+// `scratch`, so the allocation-free entry point allocates nothing for it;
+// zeroed at set-up. Host code uses the address hipGetSymbolAddress returns
+// (sdh::gn_fixed_scratch_setup).
+static constexpr int kPipeMaxChunks = 4096;
+static __device__ __align__(256) unsigned long long pipe_area[2 * kPipeMaxChunks + 32];
+
 namespace sdh {
 namespace {
 
@@ -66,6 +76,14 @@ constexpr size_t kFixedCtlBytes = size_t(64) << 10;
 constexpr int kMaxDevices = 64;
 // Device address of `scratch` per device, from gn_fixed_scratch_setup.
 unsigned char* g_fixed_scratch[kMaxDevices] = {};
+// Device address of `pipe_area` per device, likewise, and the tag of the
+// last pipelined launch made directly (not captured) on that device.
+unsigned long long* g_pipe_area[kMaxDevices] = {};
+unsigned g_pipe_tag[kMaxDevices] = {};
+// The capture (capture_generation) the last captured pipelined call was
+// recorded in, and how many such calls it has recorded.
+unsigned g_pipe_cap_gen[kMaxDevices] = {};
+unsigned g_pipe_cap_calls[kMaxDevices] = {};
 
 constexpr int kThreads = 256;
 // Split schedule chunks: TPB work-items x CV float4 each. The largest chunk
@@ -765,6 +783,226 @@ __global__ __launch_bounds__(kThreads) void k_gn_generic(const float* x, float* 
     }
 }
 
+// ---- pipelined schedule --------------------------------------------------------
+// Tensors under 64 MB whose segments are whole 4096-float chunks lying in one
+// channel (HW % 4096 == 0, at most 64 chunks per segment): the split
+// schedule's two passes in ONE launch. Workgroups come in units of gsz
+// segments: a stats unit (one workgroup per chunk: the chunk's sum and M2
+// around its mean, published as two tagged 64-bit words) and, later in
+// blockIdx order, the same segments' apply unit (merges the segment's pairs
+// in double in chunk order, then y = silu(x a + b) for its chunk). The order
+// is S(0) .. S(lag-1), then S(g + lag), A(g) alternating, then the last A
+// units: with lag units of stats ahead of each apply unit, about one round
+// of resident workgroups, an apply workgroup is dispatched when a stats
+// workgroup of the round before ends, by which time its segment's pairs are
+// out, and it re-reads its chunk from the caches while later chunks stream
+// in from HBM. Reads and writes overlap as in a copy, where the split
+// schedule's second pass starts only after its first has drained. Dynamic
+// LDS the kernel never touches holds the GPU to kPipeOcc workgroups per CU:
+// with more, apply workgroups dispatched beside their own stats workgroups
+// wait, and re-read x from HBM. Measured at config 4a ([1,512,128,128]): 6
+// per CU 12.1-12.3 us, 5 per CU 12.8, 7 per CU 13.3-14.9, the split schedule
+// 14.4-14.8; lag 4 / 5 / 6 / 7 units of 256 chunks: 13.1 / 12.4 / 12.2-12.5 /
+// 13.0 us.
+//
+// Tags. Every launch tags its pairs with a value no earlier launch used, so
+// pairs left by earlier launches never match: a direct call takes the next
+// value of a host counter (1 .. 2^31 - 1; the pairs are cleared when it
+// wraps), passed as an argument. A captured call's arguments are replayed
+// unchanged, so its tag is 2^31 + 64 E + k: E a device counter that a
+// one-workgroup kernel advances before the first pipelined call of each
+// capture (and before every 64th), k the call's place among them. Each
+// replay thus advances E once per 64 calls. (A counter advanced within the
+// launch itself would need every workgroup to have read it before it moves:
+// a word per workgroup and one reader of them all, measured 2.4 us more at
+// 4a; an atomic load or store per workgroup alone costs 0.6 us; the separate
+// kernel costs about 2 us per replay.)
+//
+// Waits. An apply workgroup's wave 0 polls the segment's pairs (one pair
+// per lane). When x and y do not overlap, a pair still missing after
+// `polls` polls is computed by the apply workgroup itself from x, with the
+// same function the stats workgroup uses (pipe_pair), so the bits are the
+// same; no apply workgroup then waits on another for long, whatever order
+// the dispatcher or another process's work imposes. In place (y == x) the
+// chunk may already be overwritten, so the wait is bounded (polls) and on
+// expiry the workgroup writes NaN and sets ctl[1], which the host reports at
+// the next synchronisation (and then leaves this schedule for the rest of
+// the process), as for the resident schedule.
+constexpr int kPipeTPB = 256, kPipeCV = 4;
+constexpr int kPipeChunk = kPipeTPB * 4 * kPipeCV;  // 4096 floats
+constexpr int kPipeOcc = 6;                         // workgroups per CU
+constexpr unsigned kPipePolls = 256;                // polls before a missing pair is computed here
+constexpr int kPipeUnitChunks = 256;                // chunks per unit, at most
+
+struct PipeArgs {
+    const float* x;
+    float* y;
+    const float* gamma;
+    const float* beta;
+    u64* slots;          // [segment][chunk][sum, M2], tagged
+    unsigned* ctl;       // ctl[0] captured launches' counter, ctl[1] error word
+    unsigned tag;        // this launch's tag, or 0: 2^31 + 64 ctl[0] + k (captured)
+    unsigned k;          // a captured call's place among those sharing ctl[0]
+    int L, HW, cg, groups, cps, gsz, ngroups, lag;
+    unsigned polls;      // polls before a missing pair is computed here (in place: before the wait fails)
+    int selfhelp;        // x and y do not overlap
+    float eps;
+};
+
+// Before the first of up to 64 captured launches: advances the counter their
+// tags are formed from.
+__global__ void k_gn_pipe_epoch(unsigned* ctl) {
+    if (threadIdx.x == 0) ctl[0] = (ctl[0] + 1u) & 0x1ffffffu;
+}
+
+// A chunk's float4 for this thread (t + 256 j), and its (sum, M2 around the
+// chunk mean). Stats workgroups and apply workgroups computing a missing
+// pair both use these, so a pair has the same bits whoever forms it.
+__device__ __forceinline__ void pipe_load(const float* c, f4 (&v)[kPipeCV]) {
+    const f4* p = (const f4*)c;
+#pragma unroll
+    for (int j = 0; j < kPipeCV; ++j) v[j] = p[threadIdx.x + kPipeTPB * j];
+}
+// Workgroup sum over shuffles (measured 0.3 us faster per 4a launch than the
+// DPP tree of block_sum), the four waves' totals added in wave order.
+__device__ __forceinline__ float pipe_sum(float v, float* sh) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    __syncthreads();  // sh may still be read by the previous sum
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (sh[0] + sh[1]) + (sh[2] + sh[3]);
+}
+__device__ __forceinline__ void pipe_pair(const f4 (&v)[kPipeCV], float* sh, float& sum, float& m2) {
+    static_assert(kPipeTPB == 256, "four waves");
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPipeCV; ++j) s += dev::hsum(v[j]);
+    sum = pipe_sum(s, sh);
+    const float mc = sum / (float)kPipeChunk;
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < kPipeCV; ++j) q += dev::sumsq4(v[j] - mc);
+    m2 = pipe_sum(q, sh);
+}
+
+template <bool SILU>
+__global__ __launch_bounds__(kPipeTPB) void k_gn_pipe(PipeArgs a) {
+    __shared__ float sh[kPipeTPB / 64];
+    __shared__ float fix[2][64];
+    __shared__ float stat[2];
+    __shared__ unsigned long long miss;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    // the kernel before a captured launch wrote ctl[0]; kernel boundaries make it visible
+    const unsigned tag = a.tag ? a.tag : 0x80000000u | (*(volatile const unsigned*)a.ctl << 6) | a.k;
+    // unit u of the order S(0) .. S(lg-1), {S(g + lg), A(g)} ..., A(ngroups-lg) .. A(ngroups-1)
+    const int per = a.gsz * a.cps;
+    const int u = (int)blockIdx.x / per, r = (int)blockIdx.x - u * per;
+    const int lg = min(a.lag, a.ngroups), mid = lg + 2 * (a.ngroups - lg);
+    bool apply;
+    int grp;
+    if (u < lg) {
+        apply = false;
+        grp = u;
+    } else if (u < mid) {
+        const int k = u - lg;
+        apply = k & 1;
+        grp = (k >> 1) + (apply ? 0 : lg);
+    } else {
+        apply = true;
+        grp = a.ngroups - lg + (u - mid);
+    }
+    const int sseg = r / a.cps, chunk = r - sseg * a.cps, seg = grp * a.gsz + sseg;
+    const float* xs = a.x + (int64_t)seg * a.L;
+    u64* sl = a.slots + (int64_t)seg * a.cps * 2;
+    f4 v[kPipeCV];
+    if (!apply) {
+        pipe_load(xs + chunk * kPipeChunk, v);
+        float s, q;
+        pipe_pair(v, sh, s, q);
+        if (threadIdx.x == 0) {
+            put_slot(sl + 2 * chunk, s, tag);
+            put_slot(sl + 2 * chunk + 1, q, tag);
+        }
+        return;
+    }
+    u64 ps = 0, pm = 0;
+    if (w == 0 && lane < a.cps) {
+        ps = get_slot(sl + 2 * lane);
+        pm = get_slot(sl + 2 * lane + 1);
+    }
+    {
+        const f4* p = (const f4*)(xs + chunk * kPipeChunk);
+#pragma unroll
+        for (int j = 0; j < kPipeCV; ++j) v[j] = dev::ld_stream(p + threadIdx.x + kPipeTPB * j);
+    }
+    if (w == 0) {
+        auto missing = [&] {
+            return __ballot(lane < a.cps && ((unsigned)(ps >> 32) != tag || (unsigned)(pm >> 32) != tag));
+        };
+        u64 m = missing();
+        for (unsigned n = 0; m && n < a.polls; ++n) {
+            __builtin_amdgcn_s_sleep(2);
+            if (lane < a.cps) {
+                ps = get_slot(sl + 2 * lane);
+                pm = get_slot(sl + 2 * lane + 1);
+            }
+            m = missing();
+        }
+        if (lane == 0) miss = m;
+    }
+    __syncthreads();
+    const u64 m = miss;
+    bool failed = false;
+    if (m) {
+        if (a.selfhelp) {
+            for (u64 mm = m; mm; mm &= mm - 1) {
+                const int c = __builtin_ctzll(mm);
+                f4 vc[kPipeCV];
+                pipe_load(xs + c * kPipeChunk, vc);
+                float s, q;
+                pipe_pair(vc, sh, s, q);
+                if (threadIdx.x == 0) {
+                    fix[0][c] = s;
+                    fix[1][c] = q;
+                }
+            }
+            __syncthreads();
+        } else {
+            failed = true;
+            if (threadIdx.x == 0) __hip_atomic_store(a.ctl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (w == 0) {
+        // k_gn_finalize's merge, one pair per lane
+        float s = 0.f, q = 0.f;
+        if (lane < a.cps) {
+            const bool f = (m >> lane) & 1;
+            s = f ? fix[0][lane] : __uint_as_float((unsigned)ps);
+            q = f ? fix[1][lane] : __uint_as_float((unsigned)pm);
+        }
+        const double mean = wave_dsum(lane < a.cps ? (double)s : 0.0) / (double)a.L;
+        double m2t = 0.0;
+        if (lane < a.cps) {
+            const double dm = (double)s / (double)kPipeChunk - mean;
+            m2t = (double)q + (double)kPipeChunk * dm * dm;
+        }
+        const double m2 = wave_dsum(m2t);
+        if (lane == 0) {
+            stat[0] = (float)mean;
+            stat[1] = failed ? __builtin_nanf("") : (float)(1.0 / sqrt(m2 / (double)a.L + (double)a.eps));
+        }
+    }
+    __syncthreads();
+    const float meanf = stat[0], rstd = stat[1];
+    const int ch = (seg % a.groups) * a.cg + (chunk * kPipeChunk) / a.HW;
+    const float ga = rstd * a.gamma[ch];
+    const float gb = a.beta[ch] - meanf * ga;
+    f4* q = (f4*)(a.y + (int64_t)seg * a.L + chunk * kPipeChunk);
+#pragma unroll
+    for (int j = 0; j < kPipeCV; ++j) dev::st_stream(q + threadIdx.x + kPipeTPB * j, apply4<SILU>(v[j], ga, gb));
+}
+
 // Bytes of input per block of the split schedule (SDH_GN_BLOCK_MB; 0 = the
 // whole tensor in one block, the default). Blocks exist for the grid's
 // 65535-segment limit; smaller blocks, so that the apply pass would re-read
@@ -994,6 +1232,103 @@ bool run_gn_resident(const char* op, bool silu, const float* x, float* y, int64_
     return true;
 }
 
+// Set when a pipelined launch's bounded wait expired (in place only): later
+// calls in this process take the other schedules.
+bool g_pipe_off = false;
+void pipe_expired() { g_pipe_off = true; }
+
+// Dynamic LDS that holds k_gn_pipe to kPipeOcc workgroups per CU (0: its
+// natural occupancy is already at most that), or -1 when it fits fewer than
+// four (the schedule is then not used); cached.
+int pipe_lds_bytes(bool silu) {
+    static int cache[2] = {-2, -2};
+    static const int occ_want = (int)std::max<long>(1, std::min<long>(env_long("SDH_GN_PIPE_OCC", kPipeOcc), 16));
+    int& c = cache[silu];
+    if (c == -2) {
+        c = -1;
+        int dev = 0, lds = 0;
+        const void* k = silu ? reinterpret_cast<const void*>(k_gn_pipe<true>) : reinterpret_cast<const void*>(k_gn_pipe<false>);
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) == hipSuccess &&
+            lds > 0) {
+            for (int dyn = 0; dyn <= lds; dyn += 256) {
+                int n = 0;
+                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kPipeTPB, (size_t)dyn) != hipSuccess) break;
+                if (n <= occ_want) {
+                    if (n >= std::min(4, occ_want)) c = dyn;
+                    break;
+                }
+                if (dyn == 0) dyn = (lds / (occ_want + 1)) & ~255;  // skip ahead; the loop adds 256
+            }
+        }
+        (void)hipGetLastError();
+    }
+    return c;
+}
+
+bool run_gn_pipe(const char* op, bool silu, const float* x, float* y, int64_t L, int64_t HW, int64_t cg, int groups,
+                 int64_t nseg, const float* gamma, const float* beta, float eps) {
+    static const bool on = env_long("SDH_GN_PIPE", 1) != 0;
+    static const long resident_mode = env_long("SDH_GN_RESIDENT", 1);
+    static const unsigned spin = (unsigned)std::min<long>(env_long("SDH_GN_SPIN_LIMIT", kSpinLimit), 0x7fffffffL);
+    if (!on || g_pipe_off || resident_mode == 2 || gn_block_bytes() != 0) return false;
+    if (HW % kPipeChunk != 0 || L % kPipeChunk != 0) return false;
+    const int64_t cps = L / kPipeChunk;
+    // 64 MB and more: the resident schedule (x read once)
+    if (cps < 1 || cps > 64 || nseg * cps >= kPipeMaxChunks) return false;
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    u64* area = dev >= 0 && dev < kMaxDevices ? g_pipe_area[dev] : nullptr;
+    if (!area) return false;
+    const int dyn = pipe_lds_bytes(silu);
+    if (dyn < 0) return false;
+    int occ = 0;
+    const void* kern = silu ? reinterpret_cast<const void*>(k_gn_pipe<true>) : reinterpret_cast<const void*>(k_gn_pipe<false>);
+    hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, kPipeTPB, (size_t)dyn), "occupancy");
+    // units: the most segments whose chunks stay within kPipeUnitChunks; lag:
+    // about one round of resident workgroups, in units
+    int64_t gsz = 1;
+    for (int64_t d = 2; d <= nseg && d * cps <= kPipeUnitChunks; ++d)
+        if (nseg % d == 0) gsz = d;
+    const int64_t unit = gsz * cps, ngroups = nseg / gsz;
+    const int64_t rounds = (int64_t)std::max(occ, 1) * num_cus();
+    static const long force_lag = env_long("SDH_GN_PIPE_LAG", 0);
+    const int64_t lag = force_lag > 0 ? force_lag : std::max<int64_t>(1, (rounds + unit / 2) / unit);
+    const size_t bytes = (size_t)(nseg * L) * 4;
+    const uintptr_t xa = (uintptr_t)x, ya = (uintptr_t)y;
+    const bool disjoint = xa + bytes <= ya || ya + bytes <= xa;
+    unsigned* ctl = (unsigned*)(area + 2 * kPipeMaxChunks);
+    unsigned tag = 0, k = 0;
+    if (capturing()) {
+        const unsigned gen = capture_generation();
+        if (g_pipe_cap_gen[dev] != gen) {
+            g_pipe_cap_gen[dev] = gen;
+            g_pipe_cap_calls[dev] = 0;
+        }
+        k = g_pipe_cap_calls[dev]++ % 64;
+        if (k == 0) {
+            k_gn_pipe_epoch<<<1, 64, 0, stream()>>>(ctl);
+            launched(op);
+        }
+    } else {
+        unsigned& t = g_pipe_tag[dev];
+        if (t == 0x7fffffffu) {  // every tag used: no pair may match a reused one
+            zero_device(area, 2 * kPipeMaxChunks * sizeof(u64));
+            t = 0;
+        }
+        tag = ++t;
+    }
+    PipeArgs args{x, y, gamma, beta, area, ctl, tag, k, (int)L, (int)HW, (int)cg, groups, (int)cps, (int)gsz,
+                  (int)ngroups, (int)std::min<int64_t>(lag, ngroups), disjoint ? std::min(kPipePolls, spin) : spin,
+                  disjoint ? 1 : 0, eps};
+    const unsigned grid = (unsigned)(2 * nseg * cps);
+    void* argv[] = {&args};
+    hip_check(hipLaunchKernel(kern, dim3(grid), dim3(kPipeTPB), argv, (size_t)dyn, stream()),
+              (std::string(op) + ": pipelined launch of " + std::to_string(grid) + " workgroups").c_str());
+    arm_device_check(args.ctl + 1, op, pipe_expired);
+    return true;
+}
+
 // fixed: the allocation-free entry point's scratch, or null for the
 // library's scratch and counters (which may allocate from the arena).
 void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups,
@@ -1027,6 +1362,11 @@ void run_gn(const char* op, bool silu, const float* x, float* y, int64_t N, int6
     if (!force_split && vec && L > kSmallResidentMin && L <= (int64_t)1024 * 4 * 16 && gn_block_bytes() == 0 &&
         run_gn_resident(op, silu, x, y, L, HW, cg, groups, nseg, gamma, beta, eps, true, fixed))
         return;
+    if (!force_split && vec && L > kSmallResidentMin &&
+        run_gn_pipe(op, silu, x, y, L, HW, cg, groups, nseg, gamma, beta, eps)) {
+        launched(op);
+        return;
+    }
     if (!force_split && vec && L <= kSmallResidentMin && nseg <= 0x7fffffffLL) {
         const int64_t n4 = L / 4;
         auto go = [&](auto tc, auto vc) {
@@ -1141,6 +1481,10 @@ void gn_fixed_scratch_setup() {
     hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(::scratch)), "hipGetSymbolAddress(scratch)");
     zero_device(p, kFixedScratchBytes);
     g_fixed_scratch[dev] = (unsigned char*)p;
+    void* q = nullptr;
+    hip_check(hipGetSymbolAddress(&q, HIP_SYMBOL(::pipe_area)), "hipGetSymbolAddress(pipe_area)");
+    zero_device(q, sizeof(::pipe_area));
+    g_pipe_area[dev] = (unsigned long long*)q;
 }
 
 }  // namespace sdh

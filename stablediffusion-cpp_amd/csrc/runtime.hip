@@ -183,6 +183,8 @@ struct Runtime {
     // recorded into a graph, so nothing may wait on it or grow a buffer
     // that queued work could still be reading.
     bool capturing = false;
+    // Incremented by every sdh_capture_begin (capture_generation).
+    unsigned capture_gen = 0;
     // Uncached device words for cross-workgroup exchange polled through the
     // scalar path (uncached_words): allocated once, never freed, because
     // memory of this kind that a kernel has read must outlive the process's
@@ -354,6 +356,16 @@ bool initialized() {
 }
 
 hipStream_t stream() { return rt().stream; }
+bool capturing() {
+    Runtime& r = rt();
+    std::lock_guard<std::mutex> lk(r.mu);
+    return r.capturing;
+}
+unsigned capture_generation() {
+    Runtime& r = rt();
+    std::lock_guard<std::mutex> lk(r.mu);
+    return r.capture_gen;
+}
 int num_cus() { return rt().cus > 0 ? rt().cus : 256; }
 
 void check_range(const void* p, size_t bytes, const char* op, const char* what) {
@@ -712,6 +724,7 @@ int sdh_capture_begin(void) {
         if (r.capturing) fail(SDH_ERR_INVALID, "sdh_capture_begin: a capture is already open");
         hip_check(hipStreamBeginCapture(r.stream, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
         r.capturing = true;
+        ++r.capture_gen;
     });
 }
 

@@ -65,6 +65,11 @@ bool initialized();
 // called by the library's set-up.
 void gn_fixed_scratch_setup();
 hipStream_t stream();
+// True between sdh_capture_begin and sdh_capture_end: launches are being
+// recorded into a graph, to be replayed later.
+bool capturing();
+// Counts the captures begun so far (sdh_capture_begin).
+unsigned capture_generation();
 int num_cus();
 // Throws SDH_ERR_INVALID unless [p, p + bytes) lies inside one live arena
 // block or one registered external range. `what` names the argument.

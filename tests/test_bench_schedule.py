@@ -1,9 +1,11 @@
 """CPU test: bench.py's model of run_gn's schedule choice (gn_dispatches,
 used to find each GroupNorm workload's kernels in a rocprofv3 trace) agrees
 with the library's rule, whose thresholds it reads from the source: single
-kernel up to kSmallResidentMin floats per segment, the resident schedule
-from 64 MB of x, else the split schedule with split_chunk's chunk (the
-largest of 8192, 4096, 2048 floats giving 768 workgroups per pass)."""
+kernel up to kSmallResidentMin floats per segment, the pipelined schedule
+for x under 64 MB in whole 4096-float chunks within one channel (at most 64
+per segment), the resident schedule from 64 MB of x, else the split schedule
+with split_chunk's chunk (the largest of 8192, 4096, 2048 floats giving 768
+workgroups per pass)."""
 import importlib.util
 import os
 import re
@@ -25,15 +27,24 @@ def test_thresholds_match_the_library_source():
     assert re.search(r"nseg \* L \* 4 >= \(int64_t\(64\) << 20\)", src)
     assert re.search(r"if \(nseg \* \(\(L \+ c - 1\) / c\) >= 768\) return c;", src)
     assert "{int64_t(8192), int64_t(4096)}" in src and "return 2048;" in src
+    assert "constexpr int kPipeChunk = kPipeTPB * 4 * kPipeCV;  // 4096 floats" in src
+    assert "constexpr int kPipeTPB = 256, kPipeCV = 4;" in src
+    assert "static constexpr int kPipeMaxChunks = 4096;" in src
+    assert "if (HW % kPipeChunk != 0 || L % kPipeChunk != 0) return false;" in src
+    assert "if (cps < 1 || cps > 64 || nseg * cps >= kPipeMaxChunks) return false;" in src
+    assert "const unsigned grid = (unsigned)(2 * nseg * cps);" in src
 
 
 def test_config_shapes():
     b = _bench()
     assert b.gn_dispatches((2, 1280, 8, 8)) == [("k_gn_single", 64 * 256)]           # 4d
-    assert b.gn_dispatches((2, 320, 64, 64)) == [("k_gn_partial", 81920), ("k_gn_apply", 81920)]  # 4c: 2048
-    assert b.gn_dispatches((1, 512, 128, 128)) == [("k_gn_partial", 262144), ("k_gn_apply", 262144)]  # 4a: 8192
+    assert b.gn_dispatches((2, 320, 64, 64)) == [("k_gn_pipe", 2 * 64 * 10 * 256)]   # 4c: 10 chunks a segment
+    assert b.gn_dispatches((1, 512, 128, 128)) == [("k_gn_pipe", 2 * 32 * 64 * 256)]  # 4a: 64 chunks a segment
     assert b.gn_dispatches((1, 128, 1024, 1024))[0][0] == "k_gn_resident_pipe<"   # 4b
-    assert b.gn_dispatches((2, 640, 64, 64)) == [("k_gn_partial", 64 * 20 * 64), ("k_gn_apply", 64 * 20 * 64)]
+    assert b.gn_dispatches((2, 640, 64, 64)) == [("k_gn_pipe", 2 * 64 * 20 * 256)]
+    # chunks that would cross channels, or more than 64 a segment: the split schedule
+    assert b.gn_dispatches((2, 1280, 32, 32)) == [("k_gn_partial", 64 * 20 * 64), ("k_gn_apply", 64 * 20 * 64)]  # 2048-float chunks
+    assert b.gn_dispatches((1, 64, 384, 384))[0][0] == "k_gn_partial"      # 72 chunks a segment, 38 MB
 
 
 def test_split_chunk_rule():

@@ -19,10 +19,11 @@ from tolerances import assert_reduction
 
 pytestmark = pytest.mark.gpu
 
-GN_SHAPES = [  # the launch-bound GroupNorm configs and one split-schedule shape
+GN_SHAPES = [  # the launch-bound GroupNorm configs, 4a and one split-schedule shape
     ((2, 1280, 8, 8), 1e-5),     # 4d: one workgroup per segment
-    ((2, 320, 64, 64), 1e-5),    # 4c: one resident round (team slots, tickets)
-    ((1, 512, 128, 128), 1e-6),  # 4a: split schedule, two launches
+    ((2, 320, 64, 64), 1e-5),    # 4c: pipelined (tags from the device counter a captured call advances)
+    ((1, 512, 128, 128), 1e-6),  # 4a: pipelined
+    ((2, 1280, 32, 32), 1e-5),   # split schedule, two launches
 ]
 
 

@@ -16,7 +16,8 @@ reductions' relative 1e-4:
     several rounds per team, shares that span channels or end short;
   * in place, repeated and interleaved with the other GroupNorm schedules,
     bit-identical on repeated calls (the merge order is fixed);
-  * the split schedule still reachable with SDH_GN_RESIDENT=0, and with
+  * the split schedule still reachable with SDH_GN_RESIDENT=0 (and
+    SDH_GN_PIPE=0), and with
     each chunk size forced (SDH_GN_CHUNK) and every shape forced onto it
     (SDH_GN_SPLIT=1);
   * two processes running it at the same time (besides this one);
@@ -41,9 +42,9 @@ PKG_DIR = os.path.join(ROOT, "stablediffusion-cpp_amd")
 ORACLE_DIR = os.path.join(ROOT, "oracle")
 
 SHAPES = [  # shape, groups, eps
-    ((1, 512, 128, 128), 32, 1e-6),  # config 4a: split by default; forced: V = 4, one round
+    ((1, 512, 128, 128), 32, 1e-6),  # config 4a: pipelined by default; forced: V = 4, one round
     ((1, 256, 256, 256), 32, 1e-6),  # 64 MB: resident (pipelined) by default
-    ((2, 640, 64, 64), 32, 1e-6),    # 21 MB: split, 4096-float chunks; forced: one resident round
+    ((2, 640, 64, 64), 32, 1e-6),    # 21 MB: pipelined; forced: one resident round
     ((3, 512, 128, 128), 32, 1e-6),  # 96 segments: three rounds of 32 teams
     ((1, 96, 100, 100), 3, 1e-6),    # shares span channels, last share short
     ((2, 64, 129, 132), 8, 1e-5),    # plane of 17028 floats: shares cross channel ends
@@ -210,15 +211,15 @@ def test_scalar_and_vector_polls_give_the_same_bits():
 
 
 def test_split_schedule_still_reachable():
-    """SDH_GN_RESIDENT=0: the three-launch split schedule on the shapes the
-    resident one would take."""
+    """SDH_GN_RESIDENT=0 and SDH_GN_PIPE=0: the split schedule on the shapes
+    the resident and the pipelined ones would take."""
     body = (
         "for shape, groups in (((1, 256, 256, 256), 32), ((2, 640, 64, 64), 32), ((1, 16, 300, 300), 2)):\n"
         "    o, want = run(shape, groups, 1e-6, True, 4500)\n"
         "    assert_reduction(o.download(), want, f'split {shape}')\n"
         "print('split ok')\n"
     )
-    r = _child({"SDH_GN_RESIDENT": "0"}, body)
+    r = _child({"SDH_GN_RESIDENT": "0", "SDH_GN_PIPE": "0"}, body)
     assert r.returncode == 0 and "split ok" in r.stdout
 
 

@@ -3,8 +3,9 @@ sdh_group_norm_silu (no reference counterpart: for callers that cannot
 allocate device memory). Through the C ABI (ctypes):
 
   * bit-identical to sdh_group_norm_silu on the same inputs, for every
-    GroupNorm schedule (resident pipelined, split with chunk statistics,
-    one resident round, single workgroup), called back to back with
+    GroupNorm schedule (resident pipelined, the one-launch pipelined
+    schedule, split with chunk statistics, single workgroup), called back
+    to back with
     shrinking inputs, so each call starts from the fixed scratch the
     previous one left; also in place;
   * the arena's reserved and in-use bytes do not move across those calls;
@@ -32,8 +33,9 @@ PKG_DIR = os.path.join(ROOT, "stablediffusion-cpp_amd")
 # one with a smaller input
 SHAPES = [
     ((1, 128, 512, 512), 32, 1e-6),  # 128 MB: resident, pipelined rounds (team slots in the fixed scratch)
-    ((1, 512, 128, 128), 32, 1e-6),  # config 4a: split schedule (chunk pairs in the fixed scratch)
-    ((2, 320, 64, 64), 32, 1e-5),    # config 4c: one resident round
+    ((1, 512, 128, 128), 32, 1e-6),  # config 4a: pipelined schedule (chunk pairs in the fixed exchange array)
+    ((2, 320, 64, 64), 32, 1e-5),    # config 4c: pipelined schedule
+    ((2, 1280, 32, 32), 32, 1e-5),   # split schedule (chunk pairs in the fixed scratch)
     ((2, 1280, 8, 8), 32, 1e-5),     # config 4d: one workgroup per segment, no scratch
 ]
 
