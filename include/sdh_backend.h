@@ -331,8 +331,12 @@ int sdh_group_norm_silu(const float* x, float* y, int64_t N, int64_t C, int64_t 
  * as many segments at a time as the array's 960 KiB of chunk statistics
  * holds; a single segment whose statistics exceed it (over about 10^9
  * floats) is rejected with SDH_ERR_INVALID. The resident and
- * single-workgroup schedules need at most 17 KiB. Calls that overlap on one GPU share the array and
- * would race; the library's own calls are serialised on its one stream. */
+ * single-workgroup schedules need at most 17 KiB. The one-launch pipelined
+ * schedule (tensors under 64 MB in whole 4096-float chunks) exchanges its
+ * chunk statistics through a second fixed 64 KiB array that
+ * sdh_group_norm_silu uses too. Calls that overlap on one GPU share the
+ * arrays and would race; the library's own calls are serialised on its one
+ * stream. */
 int sdh_group_norm_silu_noalloc(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups,
                                 const float* gamma, const float* beta, float eps);
 /* FUSED adaLN: y = layer_norm(x, no affine, eps) * (1 + scale) + shift;
