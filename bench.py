@@ -1091,10 +1091,11 @@ def gn_split_chunk(nseg, L):
 def gn_dispatches(shape, groups=32, cus=256):
     """(kernel prefix, grid work-items) of the launches that carry a GroupNorm
     workload's HBM traffic, following run_gn's choice of schedule: one
-    k_gn_single launch for segments up to 24576 floats; else, for x under
-    64 MB cut into whole 4096-float chunks that each lie in one channel (at
-    most 64 per segment), one k_gn_pipe launch of two workgroups per chunk;
-    else, for x of at least 64 MB, the resident plan of run_gn_resident (one launch of
+    k_gn_single launch for segments up to 24576 floats; else, for segments
+    cut into whole 4096-float chunks that each lie in one channel (at most
+    64 per segment), k_gn_pipe launches of two workgroups per chunk (the
+    first launch, of at most 2^17 chunks); else, for x of at least 64 MB,
+    the resident plan of run_gn_resident (one launch of
     k_gn_resident or k_gn_resident_pipe); else k_gn_partial and k_gn_apply
     over chunks of gn_split_chunk floats (k_gn_finalize moves a few KB and
     is left out)."""
@@ -1105,8 +1106,9 @@ def gn_dispatches(shape, groups=32, cus=256):
         n4 = L // 4
         tpb = 256 if n4 <= 2048 else 1024
         return [("k_gn_single", nseg * tpb)]
-    if HW % 4096 == 0 and L // 4096 <= 64 and nseg * (L // 4096) < 4096:
-        return [("k_gn_pipe", 2 * nseg * (L // 4096) * 256)]
+    if HW % 4096 == 0 and L // 4096 <= 64:
+        cps = L // 4096
+        return [("k_gn_pipe", 2 * min(nseg, (1 << 17) // cps) * cps * 256)]
     if nseg * L * 4 >= 64 << 20:
         best = {}
         for pipe in (False, True):

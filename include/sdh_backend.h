@@ -332,9 +332,10 @@ int sdh_group_norm_silu(const float* x, float* y, int64_t N, int64_t C, int64_t 
  * holds; a single segment whose statistics exceed it (over about 10^9
  * floats) is rejected with SDH_ERR_INVALID. The resident and
  * single-workgroup schedules need at most 17 KiB. The one-launch pipelined
- * schedule (tensors under 64 MB in whole 4096-float chunks) exchanges its
- * chunk statistics through a second fixed 64 KiB array that
- * sdh_group_norm_silu uses too. Calls that overlap on one GPU share the
+ * schedule (segments of at most 64 whole 4096-float chunks) exchanges its
+ * chunk statistics through a second fixed 2 MiB array that
+ * sdh_group_norm_silu uses too (2^17 chunks a launch; larger tensors take
+ * several launches). Calls that overlap on one GPU share the
  * arrays and would race; the library's own calls are serialised on its one
  * stream. */
 int sdh_group_norm_silu_noalloc(const float* x, float* y, int64_t N, int64_t C, int64_t HW, int groups,

@@ -7,7 +7,10 @@
 // apply step uses the reference's folded form y = x * a + (beta - mean * a),
 // a = rstd * gamma[c], then SiLU as x / (1 + exp(-x)).
 //
-// Three schedules:
+// Four schedules:
+//   * pipelined (segments of 4096-float chunks, at most 64 of them, each in
+//     one channel): the split schedule's two passes in one launch, the apply
+//     workgroups a round behind the stats workgroups. Described at k_gn_pipe.
 //   * single: one workgroup (256 or 1024 threads) per segment of at most
 //     24576 floats, held in its registers. One HBM read, one write. Longer
 //     segments take the split schedule below 64 MB of x, the resident one
@@ -59,12 +62,13 @@ static __device__ __align__(256) unsigned char scratch[kFixedScratchBytes];
 
 // Exchange area of the pipelined schedule (k_gn_pipe), used by both
 // GroupNorm entry points (one stream keeps their launches in order): the
-// tagged chunk pairs (2 words per chunk, at most kPipeMaxChunks chunks), then
+// tagged chunk pairs (2 words per chunk, at most kPipeMaxChunks chunks a
+// launch), then
 // the captured launches' counter and an error word. A file-scope array like
 // `scratch`, so the allocation-free entry point allocates nothing for it;
 // zeroed at set-up. Host code uses the address hipGetSymbolAddress returns
 // (sdh::gn_fixed_scratch_setup).
-static constexpr int kPipeMaxChunks = 4096;
+static constexpr int kPipeMaxChunks = 1 << 17;  // 2 GB of x per launch
 static __device__ __align__(256) unsigned long long pipe_area[2 * kPipeMaxChunks + 32];
 
 namespace sdh {
@@ -784,9 +788,9 @@ __global__ __launch_bounds__(kThreads) void k_gn_generic(const float* x, float* 
 }
 
 // ---- pipelined schedule --------------------------------------------------------
-// Tensors under 64 MB whose segments are whole 4096-float chunks lying in one
-// channel (HW % 4096 == 0, at most 64 chunks per segment): the split
-// schedule's two passes in ONE launch. Workgroups come in units of gsz
+// Segments that are whole 4096-float chunks lying in one channel (HW % 4096
+// == 0, at most 64 chunks per segment), any tensor size: the split
+// schedule's two passes in ONE launch (per kPipeMaxChunks chunks). Workgroups come in units of gsz
 // segments: a stats unit (one workgroup per chunk: the chunk's sum and M2
 // around its mean, published as two tagged 64-bit words) and, later in
 // blockIdx order, the same segments' apply unit (merges the segment's pairs
@@ -803,7 +807,12 @@ __global__ __launch_bounds__(kThreads) void k_gn_generic(const float* x, float* 
 // wait, and re-read x from HBM. Measured at config 4a ([1,512,128,128]): 6
 // per CU 12.1-12.3 us, 5 per CU 12.8, 7 per CU 13.3-14.9, the split schedule
 // 14.4-14.8; lag 4 / 5 / 6 / 7 units of 256 chunks: 13.1 / 12.4 / 12.2-12.5 /
-// 13.0 us.
+// 13.0 us. Larger tensors keep the re-read distance (lag units) and so the
+// cache hits: [4,512,128,128] 46.8 us against 53.5 (split), [8,512,128,128]
+// 90.7 against 97.1 (resident). Longer segments were tried with a finalize
+// workgroup per segment between the stats and apply units and measured
+// slower than the resident schedule ([1,128,512,512] 66 against 50 us,
+// [1,128,1024,1024] 272 against 183), so they are not taken here.
 //
 // Tags. Every launch tags its pairs with a value no earlier launch used, so
 // pairs left by earlier launches never match: a direct call takes the next
@@ -843,7 +852,7 @@ struct PipeArgs {
     unsigned* ctl;       // ctl[0] captured launches' counter, ctl[1] error word
     unsigned tag;        // this launch's tag, or 0: 2^31 + 64 ctl[0] + k (captured)
     unsigned k;          // a captured call's place among those sharing ctl[0]
-    int L, HW, cg, groups, cps, gsz, ngroups, lag;
+    int L, HW, cg, groups, seg0, cps, gsz, ngroups, lag;  // seg0: the group of the launch's first segment
     unsigned polls;      // polls before a missing pair is computed here (in place: before the wait fails)
     int selfhelp;        // x and y do not overlap
     float eps;
@@ -935,7 +944,7 @@ __global__ __launch_bounds__(kPipeTPB) void k_gn_pipe(PipeArgs a) {
     u64* sl = a.slots + (int64_t)seg * a.cps * 2;
     f4 v[kPipeCV];
     if (!apply) {
-        pipe_load(xs + chunk * kPipeChunk, v);
+        pipe_load(xs + (int64_t)chunk * kPipeChunk, v);
         float s, q;
         pipe_pair(v, sh, s, q);
         if (threadIdx.x == 0) {
@@ -950,7 +959,7 @@ __global__ __launch_bounds__(kPipeTPB) void k_gn_pipe(PipeArgs a) {
         pm = get_slot(sl + 2 * lane + 1);
     }
     {
-        const f4* p = (const f4*)(xs + chunk * kPipeChunk);
+        const f4* p = (const f4*)(xs + (int64_t)chunk * kPipeChunk);
 #pragma unroll
         for (int j = 0; j < kPipeCV; ++j) v[j] = dev::ld_stream(p + threadIdx.x + kPipeTPB * j);
     }
@@ -977,7 +986,7 @@ __global__ __launch_bounds__(kPipeTPB) void k_gn_pipe(PipeArgs a) {
             for (u64 mm = m; mm; mm &= mm - 1) {
                 const int c = __builtin_ctzll(mm);
                 f4 vc[kPipeCV];
-                pipe_load(xs + c * kPipeChunk, vc);
+                pipe_load(xs + (int64_t)c * kPipeChunk, vc);
                 float s, q;
                 pipe_pair(vc, sh, s, q);
                 if (threadIdx.x == 0) {
@@ -1013,10 +1022,10 @@ __global__ __launch_bounds__(kPipeTPB) void k_gn_pipe(PipeArgs a) {
     }
     __syncthreads();
     const float meanf = stat[0], rstd = stat[1];
-    const int ch = (seg % a.groups) * a.cg + (chunk * kPipeChunk) / a.HW;
+    const int ch = ((a.seg0 + seg) % a.groups) * a.cg + (chunk * kPipeChunk) / a.HW;
     const float ga = rstd * a.gamma[ch];
     const float gb = a.beta[ch] - meanf * ga;
-    f4* q = (f4*)(a.y + (int64_t)seg * a.L + chunk * kPipeChunk);
+    f4* q = (f4*)(a.y + (int64_t)seg * a.L + (int64_t)chunk * kPipeChunk);
 #pragma unroll
     for (int j = 0; j < kPipeCV; ++j) dev::st_stream(q + threadIdx.x + kPipeTPB * j, apply4<SILU>(v[j], ga, gb));
 }
@@ -1292,8 +1301,8 @@ bool run_gn_pipe(const char* op, bool silu, const float* x, float* y, int64_t L,
     if (!on || g_pipe_off || resident_mode == 2 || gn_block_bytes() != 0) return false;
     if (HW % kPipeChunk != 0 || L % kPipeChunk != 0) return false;
     const int64_t cps = L / kPipeChunk;
-    // 64 MB and more: the resident schedule (x read once)
-    if (cps < 1 || cps > 64 || nseg * cps >= kPipeMaxChunks) return false;
+    // segments of more than 64 chunks: the resident or split schedule
+    if (cps < 1 || cps > 64) return false;
     int dev = 0;
     hip_check(hipGetDevice(&dev), "hipGetDevice");
     u64* area = dev >= 0 && dev < kMaxDevices ? g_pipe_area[dev] : nullptr;
@@ -1303,47 +1312,53 @@ bool run_gn_pipe(const char* op, bool silu, const float* x, float* y, int64_t L,
     int occ = 0;
     const void* kern = silu ? reinterpret_cast<const void*>(k_gn_pipe<true>) : reinterpret_cast<const void*>(k_gn_pipe<false>);
     hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, kPipeTPB, (size_t)dyn), "occupancy");
-    // units: the most segments whose chunks stay within kPipeUnitChunks; lag:
-    // about one round of resident workgroups, in units
-    int64_t gsz = 1;
-    for (int64_t d = 2; d <= nseg && d * cps <= kPipeUnitChunks; ++d)
-        if (nseg % d == 0) gsz = d;
-    const int64_t unit = gsz * cps, ngroups = nseg / gsz;
     const int64_t rounds = (int64_t)std::max(occ, 1) * num_cus();
     static const long force_lag = env_long("SDH_GN_PIPE_LAG", 0);
-    const int64_t lag = force_lag > 0 ? force_lag : std::max<int64_t>(1, (rounds + unit / 2) / unit);
     const size_t bytes = (size_t)(nseg * L) * 4;
     const uintptr_t xa = (uintptr_t)x, ya = (uintptr_t)y;
     const bool disjoint = xa + bytes <= ya || ya + bytes <= xa;
     unsigned* ctl = (unsigned*)(area + 2 * kPipeMaxChunks);
-    unsigned tag = 0, k = 0;
-    if (capturing()) {
-        const unsigned gen = capture_generation();
-        if (g_pipe_cap_gen[dev] != gen) {
-            g_pipe_cap_gen[dev] = gen;
-            g_pipe_cap_calls[dev] = 0;
+    // segments per launch: as many as the exchange area holds
+    const int64_t sb_max = kPipeMaxChunks / cps;
+    for (int64_t s0 = 0; s0 < nseg; s0 += sb_max) {
+        const int64_t sb = std::min(sb_max, nseg - s0);
+        // units: the most segments whose chunks stay within kPipeUnitChunks;
+        // lag: about one round of resident workgroups, in units
+        int64_t gsz = 1;
+        for (int64_t d = 2; d <= sb && d * cps <= kPipeUnitChunks; ++d)
+            if (sb % d == 0) gsz = d;
+        const int64_t unit = gsz * cps, ngroups = sb / gsz;
+        const int64_t lag = force_lag > 0 ? force_lag : std::max<int64_t>(1, (rounds + unit / 2) / unit);
+        unsigned tag = 0, k = 0;
+        if (capturing()) {
+            const unsigned gen = capture_generation();
+            if (g_pipe_cap_gen[dev] != gen) {
+                g_pipe_cap_gen[dev] = gen;
+                g_pipe_cap_calls[dev] = 0;
+            }
+            k = g_pipe_cap_calls[dev]++ % 64;
+            if (k == 0) {
+                k_gn_pipe_epoch<<<1, 64, 0, stream()>>>(ctl);
+                launched(op);
+            }
+        } else {
+            unsigned& t = g_pipe_tag[dev];
+            if (t == 0x7fffffffu) {  // every tag used: no pair may match a reused one
+                zero_device(area, 2 * kPipeMaxChunks * sizeof(u64));
+                t = 0;
+            }
+            tag = ++t;
         }
-        k = g_pipe_cap_calls[dev]++ % 64;
-        if (k == 0) {
-            k_gn_pipe_epoch<<<1, 64, 0, stream()>>>(ctl);
-            launched(op);
-        }
-    } else {
-        unsigned& t = g_pipe_tag[dev];
-        if (t == 0x7fffffffu) {  // every tag used: no pair may match a reused one
-            zero_device(area, 2 * kPipeMaxChunks * sizeof(u64));
-            t = 0;
-        }
-        tag = ++t;
+        PipeArgs args{x + s0 * L, y + s0 * L, gamma, beta, area, ctl, tag, k, (int)L, (int)HW, (int)cg, groups,
+                      (int)(s0 % groups), (int)cps, (int)gsz, (int)ngroups, (int)std::min<int64_t>(lag, ngroups),
+                      disjoint ? std::min(kPipePolls, spin) : spin, disjoint ? 1 : 0, eps};
+        const unsigned grid = (unsigned)(2 * sb * cps);
+        void* argv[] = {&args};
+        hip_check(hipLaunchKernel(kern, dim3(grid), dim3(kPipeTPB), argv, (size_t)dyn, stream()),
+                  (std::string(op) + ": pipelined launch of " + std::to_string(grid) + " workgroups").c_str());
+        if (s0 + sb < nseg) launched(op);
     }
-    PipeArgs args{x, y, gamma, beta, area, ctl, tag, k, (int)L, (int)HW, (int)cg, groups, (int)cps, (int)gsz,
-                  (int)ngroups, (int)std::min<int64_t>(lag, ngroups), disjoint ? std::min(kPipePolls, spin) : spin,
-                  disjoint ? 1 : 0, eps};
-    const unsigned grid = (unsigned)(2 * nseg * cps);
-    void* argv[] = {&args};
-    hip_check(hipLaunchKernel(kern, dim3(grid), dim3(kPipeTPB), argv, (size_t)dyn, stream()),
-              (std::string(op) + ": pipelined launch of " + std::to_string(grid) + " workgroups").c_str());
-    arm_device_check(args.ctl + 1, op, pipe_expired);
+    arm_device_check(ctl + 1, op, pipe_expired);
     return true;
 }
 

@@ -1,14 +1,16 @@
 """GPU tests of GroupNorm's pipelined schedule (k_gn_pipe: one launch in
 which stats workgroups publish each 4096-float chunk's (sum, M2) as tagged
 64-bit words and apply workgroups, later in dispatch order, merge their
-segment's pairs and write y; tensors under 64 MB in whole chunks that each
-lie in one channel, at most 64 per segment).
+segment's pairs and write y; segments of at most 64 whole chunks that each
+lie in one channel, any tensor size, in launches of at most 2^17 chunks).
 
 Against the float64 oracle (tensor.cpp:592-625, then silu :843-849) at the
 reductions' relative 1e-4:
   * every shape class the schedule takes: the FLUX VAE's config 4a, SD 1.5's
-    config 4c, one and several segments per unit, 1-64 chunks per segment,
-    with and without SiLU, groups other than 32;
+    config 4c, one and several segments per unit, 3-64 chunks per segment,
+    tensors of 128 MB, with and without SiLU, groups other than 32;
+  * a tensor of more than 2^17 chunks (two launches): each sample the same
+    bits as a call on that sample alone;
   * bit-identical on repeat, in place and interleaved with the other
     schedules (a launch's tags never match pairs an earlier launch left);
   * the apply workgroups' own computation of a missing pair, forced from the
@@ -32,6 +34,7 @@ import sys
 
 import numpy as np
 import pytest
+import sdhip
 
 from tolerances import assert_reduction
 
@@ -51,6 +54,9 @@ SHAPES = [  # shape, groups, eps: all take the pipelined schedule
     ((3, 96, 64, 64), 32, 1e-5),     # 3 chunks a segment, 96 segments
     ((1, 64, 128, 128), 8, 1e-6),    # 8 groups: 32 chunks a segment, 8 segments
     ((1, 32, 512, 512), 32, 1e-6),   # one channel of 64 chunks a segment (32 MB)
+    ((4, 512, 128, 128), 32, 1e-6),  # 4 x config 4a: 128 segments (128 MB)
+    ((2, 64, 256, 256), 16, 1e-6),   # 16 groups: 64 chunks a segment, 32 segments
+    ((1, 96, 256, 256), 32, 1e-5),   # 48 chunks a segment, 24 MB
 ]
 
 
@@ -87,7 +93,7 @@ def test_pipe_repeat_in_place_and_interleaved(be, orc):
     _gn(be, dx, first, shape, groups, dg, db, eps)
     want = first.download()
     assert_reduction(want, orc.group_norm(x, groups, g, b, eps, silu=True), "pipe 4a")
-    others = [((1, 256, 256, 256), 32), ((2, 1280, 8, 8), 32), ((2, 320, 64, 64), 32), ((2, 640, 32, 32), 32)]
+    others = [((1, 96, 500, 500), 32), ((2, 1280, 8, 8), 32), ((2, 320, 64, 64), 32), ((2, 1280, 32, 32), 32)]
     for rep in range(3):
         for i, (oshape, og) in enumerate(others):  # resident, single, pipelined, split
             ox, ogm, ob = _inputs(be, orc, oshape, 5210 + i)
@@ -99,6 +105,34 @@ def test_pipe_repeat_in_place_and_interleaved(be, orc):
     inplace = be.array(x)
     _gn(be, inplace, inplace, shape, groups, dg, db, eps)
     assert np.array_equal(inplace.download(), want), "in place"
+
+
+def test_pipe_over_several_launches(be):
+    """[66,512,128,128]: 2112 segments of 64 chunks, more than the 2^17
+    chunks one launch takes, so two launches (2048 segments, then 64, whose
+    channels continue from group 0). Samples 0, 63, 64 and 65 (both sides of
+    the cut, and the last) must give the same bits as calls on those samples
+    alone, which take one launch each."""
+    shape, groups, eps = (66, 512, 128, 128), 32, 1e-6
+    C, HW = shape[1], shape[2] * shape[3]
+    per = C * HW * 4  # bytes a sample
+    dx = be.randn(shape, 5300, 0.5, 2.0)
+    dg, db = be.randn((C,), 5301, 1.0, 0.1), be.randn((C,), 5302, 0.0, 0.1)
+    dy = be.empty(shape)
+    be.group_norm(dx, dy, shape[0], C, HW, groups, dg, db, eps, silu=True)
+    be.synchronize()
+    for n0, k in ((0, 1), (63, 2), (65, 1)):
+        sub = (k, C, shape[2], shape[3])
+        xs = sdhip.DArray(be, sub, ptr=dx.ptr + n0 * per, owned=False)
+        ys = sdhip.DArray(be, sub, ptr=dy.ptr + n0 * per, owned=False)
+        alone = be.empty(sub)
+        be.group_norm(xs, alone, k, C, HW, groups, dg, db, eps, silu=True)
+        got, want = ys.download(), alone.download()
+        assert np.isfinite(want).all(), f"samples {n0}..{n0 + k - 1}"
+        assert np.array_equal(got, want), f"samples {n0}..{n0 + k - 1} differ from a call on them alone"
+        alone.free()
+    dx.free()
+    dy.free()
 
 
 def _child_code(body):

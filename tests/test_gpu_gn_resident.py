@@ -24,6 +24,10 @@ reductions' relative 1e-4:
   * the failure path, forced from the host: SDH_GN_SPIN_LIMIT=0 expires
     every wait at once, so every workgroup writes NaN and exits, and the
     next download reports SDH_ERR_HIP.
+The shapes the pipelined schedule would take by default (x in whole
+4096-float chunks that each lie in one channel) run it in the default-
+schedule tests; the tests of the resident kernels themselves force them
+(SDH_GN_RESIDENT=2) or switch the pipelined schedule off (SDH_GN_PIPE=0).
 """
 import os
 import subprocess
@@ -246,7 +250,7 @@ def test_expired_wait_is_reported():
         "assert (a.download() == 2.0).all()\n"
         "print('expiry ok')\n"
     )
-    r = _child({"SDH_GN_SPIN_LIMIT": "0"}, body)
+    r = _child({"SDH_GN_SPIN_LIMIT": "0", "SDH_GN_PIPE": "0"}, body)
     assert r.returncode == 0 and "expiry ok" in r.stdout
 
 
@@ -280,7 +284,7 @@ def test_expired_waits_in_two_scratch_areas_both_reported():
         "be.synchronize()\n"
         "print('two areas ok')\n"
     )
-    r = _child({"SDH_GN_SPIN_LIMIT": "0"}, body)
+    r = _child({"SDH_GN_SPIN_LIMIT": "0", "SDH_GN_PIPE": "0"}, body)
     assert r.returncode == 0 and "two areas ok" in r.stdout
 
 
