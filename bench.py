@@ -40,8 +40,10 @@ parity checks run after the last one: a CPU leg between two measurements
 leaves the GPU idle for seconds, and the next line would time its clocks
 coming back up (measured: 4b 191 us per op over the first 20 steps after 5
 warm-up steps, 181 us once settled). The headline takes exactly --warmup
-untimed steps; every other line warms up for at least 30 ms of its own steps
-(and at least 3 of them).
+untimed steps and times exactly --steps; every other line warms up for at
+least 30 ms of its own steps (and at least 3 of them) and times at least 10 ms
+of steps (at least --op-steps; `timed_steps` in its entry; a captured graph
+at most 256 of them).
 """
 from __future__ import annotations
 
@@ -78,6 +80,14 @@ GRAPH_ALSO_MS = 0.025
 # clocks are at their loaded level when the timed steps start
 OP_WARM_S = 0.03
 OP_WARM_BATCH = 8
+# per-op lines time at least this long (more than --op-steps steps for ops
+# under 500 us): the first launches after the warm-up's synchronisation run
+# slower than the rest (kernel trace: GroupNorm 4b's first 191-204 us against
+# 172-190 us, 4a's first two 0.5-1.7 us slower), a bias of 0.75 us per op
+# over 20 steps of 4b
+OP_TIMED_S = 0.01
+# the captured graph of a launch-bound line holds at most this many steps
+GRAPH_MAX_STEPS = 256
 
 
 # ------------------------------------------------------------------ workloads
@@ -875,9 +885,11 @@ def all_workloads():
 
 
 # ------------------------------------------------------------------ GPU timing
-def measure_gpu(be, w, steps, warmup, check=False, min_warm_s=0.0):
+def measure_gpu(be, w, steps, warmup, check=False, min_warm_s=0.0, min_timed_s=0.0):
     """Times `steps` steps over rotating buffer sets, after `warmup` untimed
-    steps (continued in batches until `min_warm_s` seconds have passed). With
+    steps (continued in batches until `min_warm_s` seconds have passed; with
+    `min_timed_s`, more steps when `steps` would take less than that at the
+    warm-up's pace). With
     check, set 0's inputs are downloaded before the timed steps, and
     afterwards, outside the timed region, set 0 is reloaded from them, stepped
     once and its results returned for the parity check."""
@@ -897,6 +909,9 @@ def measure_gpu(be, w, steps, warmup, check=False, min_warm_s=0.0):
             w.step(be, sets[i % nsets])
             i += 1
         be.synchronize()
+    if min_timed_s > 0 and i > 0:
+        per = (time.perf_counter() - t_warm) / i
+        steps = max(steps, min(100 * steps, math.ceil(min_timed_s / max(per, 1e-9))))
     t0 = time.perf_counter()
     be.timer_record(0)
     for i in range(steps):
@@ -910,9 +925,10 @@ def measure_gpu(be, w, steps, warmup, check=False, min_warm_s=0.0):
         # launch-bound: the host's ctypes loop, not the GPU, sets the pace of
         # the loop above; the same steps captured into one graph run back to
         # back on the device (sdh_capture_begin), which is the GPU's time
+        gsteps = min(steps, GRAPH_MAX_STEPS)
         be.capture_begin()
         try:
-            for i in range(steps):
+            for i in range(gsteps):
                 w.step(be, sets[i % nsets])
         finally:
             g = be.capture_end()
@@ -923,7 +939,7 @@ def measure_gpu(be, w, steps, warmup, check=False, min_warm_s=0.0):
             be.graph_launch(g)
             be.timer_record(1)
             be.synchronize()
-            graph_ms = be.timer_elapsed(0, 1)
+            graph_ms = be.timer_elapsed(0, 1) * steps / gsteps  # per `steps` steps, as ev_ms
         finally:
             be.graph_destroy(g)
     got = None
@@ -935,12 +951,12 @@ def measure_gpu(be, w, steps, warmup, check=False, min_warm_s=0.0):
         for a in st.values():
             a.free()
     out = dict(nsets=nsets, footprint=footprint * nsets, wall_ms=wall * 1e3 / steps, event_ms=ev_ms / steps,
-               got=got, host=host)
+               got=got, host=host, steps=steps)
     if graph_ms is not None:
         if ev_ms / steps < GRAPH_BELOW_MS:
-            out.update(host_paced_ms=ev_ms / steps, event_ms=graph_ms / steps, graph=True)
+            out.update(host_paced_ms=ev_ms / steps, event_ms=graph_ms / steps, graph=True, graph_steps=gsteps)
         else:
-            out.update(graph_ms=graph_ms / steps)
+            out.update(graph_ms=graph_ms / steps, graph_steps=gsteps)
     return out
 
 
@@ -1238,7 +1254,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="swiglu", help="headline workload (default: swiglu = configs[1])")
     ap.add_argument("--only", default=None, help="comma list: measure only these workloads (profiling runs)")
-    ap.add_argument("--op-steps", type=int, default=20, help="timed steps per op in the per-op table")
+    ap.add_argument("--op-steps", type=int, default=20,
+                    help="timed steps per op in the per-op table, at least (ops under 500 us time 10 ms of steps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-all", action="store_true",
                     help="time the reference CPU path on every line (the BASELINE config lines always are)")
@@ -1294,7 +1311,8 @@ def main():
         if hasattr(w, "measure"):  # a whole model step, timed by the model library itself
             r = w.measure(max(3, min(steps, 10)), 2)
         else:
-            r = measure_gpu(be, w, steps, warm, check=R is not None, min_warm_s=0.0 if w is head else OP_WARM_S)
+            r = measure_gpu(be, w, steps, warm, check=R is not None, min_warm_s=0.0 if w is head else OP_WARM_S,
+                            min_timed_s=0.0 if w is head else OP_TIMED_S)
         measured.append((w, r))
         print(f"# gpu {w.name:22s} {r['event_ms'] * 1e3:10.2f} us", file=sys.stderr, flush=True)
     for w, r in measured:
@@ -1302,6 +1320,8 @@ def main():
         entry = dict(op=w.name, desc=w.desc, algo_bytes=w.algo_bytes, us_per_op=round(r["event_ms"] * 1e3, 2),
                      GBps=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1), rotation_sets=r["nsets"],
                      rotation_MB=round(r["footprint"] / 2**20), traffic_bytes=read_traffic(w.name))
+        if r.get("steps") is not None:
+            entry["timed_steps"] = r["graph_steps"] if r.get("graph") else r["steps"]
         if r.get("graph"):
             entry.update(timing="device: the steps captured into one graph and replayed (sdh_capture_begin)",
                          us_per_op_host_paced=round(r["host_paced_ms"] * 1e3, 2))
