@@ -112,7 +112,9 @@ def test_pipe_over_several_launches(be):
     chunks one launch takes, so two launches (2048 segments, then 64, whose
     channels continue from group 0). Samples 0, 63, 64 and 65 (both sides of
     the cut, and the last) must give the same bits as calls on those samples
-    alone, which take one launch each."""
+    alone, which take one launch each. Then the whole call captured in a
+    graph (two captured launches, each with its own place among the
+    capture's calls), replayed twice over new x: the direct call's bits."""
     shape, groups, eps = (66, 512, 128, 128), 32, 1e-6
     C, HW = shape[1], shape[2] * shape[3]
     per = C * HW * 4  # bytes a sample
@@ -131,8 +133,26 @@ def test_pipe_over_several_launches(be):
         assert np.isfinite(want).all(), f"samples {n0}..{n0 + k - 1}"
         assert np.array_equal(got, want), f"samples {n0}..{n0 + k - 1} differ from a call on them alone"
         alone.free()
+    dg2 = be.empty(shape)
+    be.capture_begin()
+    be.group_norm(dx, dg2, shape[0], C, HW, groups, dg, db, eps, silu=True)
+    graph = be.capture_end()
+    try:
+        for rep in range(2):
+            be.check(be.lib.sdh_fill_normal(dx.ptr, dx.size, 5310 + rep, 0.25 * rep, 2.0))
+            be.group_norm(dx, dy, shape[0], C, HW, groups, dg, db, eps, silu=True)
+            be.graph_launch(graph)
+            be.synchronize()
+            for n0 in (0, 63, 64, 65):
+                sub = (1, C, shape[2], shape[3])
+                want = sdhip.DArray(be, sub, ptr=dy.ptr + n0 * per, owned=False).download()
+                got = sdhip.DArray(be, sub, ptr=dg2.ptr + n0 * per, owned=False).download()
+                assert np.isfinite(want).all() and np.array_equal(got, want), f"replay {rep} sample {n0}"
+    finally:
+        be.graph_destroy(graph)
     dx.free()
     dy.free()
+    dg2.free()
 
 
 def _child_code(body):
