@@ -13,8 +13,8 @@
 //     workgroups a round behind the stats workgroups. Described at k_gn_pipe.
 //   * single: one workgroup (256 or 1024 threads) per segment of at most
 //     24576 floats, held in its registers. One HBM read, one write. Longer
-//     segments take the split schedule below 64 MB of x, the resident one
-//     above.
+//     segments that the pipelined schedule does not take: the split schedule
+//     below 64 MB of x, the resident one above.
 //   * resident (larger segments, large tensors): teams of workgroups hold a
 //     segment in registers across a team wait, so x is read once (two
 //     streams); pipelined over two register buffers when a team has several
