@@ -114,7 +114,8 @@ def test_pipe_over_several_launches(be):
     the cut, and the last) must give the same bits as calls on those samples
     alone, which take one launch each. Then the whole call captured in a
     graph (two captured launches, each with its own place among the
-    capture's calls), replayed twice over new x: the direct call's bits."""
+    capture's calls), replayed twice over new x: the direct call's bits;
+    and the call in place over the last x: the same bits again."""
     shape, groups, eps = (66, 512, 128, 128), 32, 1e-6
     C, HW = shape[1], shape[2] * shape[3]
     per = C * HW * 4  # bytes a sample
@@ -150,6 +151,14 @@ def test_pipe_over_several_launches(be):
                 assert np.isfinite(want).all() and np.array_equal(got, want), f"replay {rep} sample {n0}"
     finally:
         be.graph_destroy(graph)
+    # in place over the last x (two launches whose apply workgroups may only wait): dy's bits
+    be.group_norm(dx, dx, shape[0], C, HW, groups, dg, db, eps, silu=True)
+    be.synchronize()
+    for n0 in (0, 63, 64, 65):
+        sub = (1, C, shape[2], shape[3])
+        want = sdhip.DArray(be, sub, ptr=dy.ptr + n0 * per, owned=False).download()
+        got = sdhip.DArray(be, sub, ptr=dx.ptr + n0 * per, owned=False).download()
+        assert np.array_equal(got, want), f"in place, sample {n0}"
     dx.free()
     dy.free()
     dg2.free()
